@@ -1,0 +1,739 @@
+// Selection attention forward: dense K/V, reference pointer tables, and the paged block cache.
+//
+// Reference semantics: cuda_backend/csrc/selection_fwd.cu:1-3 (fp32 softmax state, empty rows
+// give O = 0 and LSE = -inf, natural-log LSE), common.cuh:158-215 (dense / pointer block
+// resolution, partial blocks, pointer 0 = skip), :327-332 (chunk-causal visible prefix),
+// selection_fwd.cu:218 (a query group's chunk is that of its first query).
+//
+// gfx950 design (bf16 / f16): one workgroup = (b, query group, head), 4 waves x 16 queries.
+//   S^T = K Q^T on v_mfma_f32_16x16x32 (A = K rows from LDS, B = Q^T held in registers), so the
+//   S^T accumulator already has the layout of the B operand of O^T = V^T P^T: P goes from the
+//   softmax straight into the PV MFMA with no LDS round trip.  V is staged transposed in LDS
+//   (Vt[d][key]) so the A operand of PV is two 8-byte LDS reads.  Key tiles of 64 tokens are
+//   double-buffered: the next tile's global loads are in flight during the current tile's MFMAs.
+//   fp8 pages are dequantised (x * page scale -> bf16) while staging.
+// fp32 (and any shape the MFMA kernel does not cover) runs a VALU kernel in full fp32.
+#include "omm_common.h"
+
+namespace omm {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+  __device__ __forceinline__ static f32x4 run(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  }
+};
+template <> struct Mfma<f16_t> {
+  __device__ __forceinline__ static f32x4 run(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+    const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  }
+};
+
+// ---- block accessors ---------------------------------------------------------------------
+// A resolved block: nvalid tokens visible from row 0, rows at k + r*sk (elements of its storage
+// type), k == nullptr when the block is skipped.
+struct BlockRef {
+  const void* k;
+  const void* v;
+  int64_t sk, sv;
+  int nvalid;
+  float scale_k, scale_v;
+};
+
+template <typename T>
+struct DenseAcc {
+  using KV = T;
+  View4<const T> k, v;
+  const int32_t* ids;
+  int64_t is0, is1, is2, is3;
+  int N, bs, chunk;
+  bool causal;
+  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int q_chunk) const {
+    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    if (bid < 0) return r;
+    const int64_t t0 = static_cast<int64_t>(bid) * bs;
+    if (t0 >= N) return r;
+    if (causal && t0 / chunk > q_chunk) return r;
+    int64_t n = N - t0 < bs ? N - t0 : bs;
+    if (causal) {
+      const int64_t lim = static_cast<int64_t>(q_chunk + 1) * chunk - t0;
+      n = n < lim ? n : lim;
+    }
+    if (n <= 0) return r;
+    r.k = k.at(b, t0, h, 0);
+    r.v = v.at(b, t0, h, 0);
+    r.sk = k.s1;
+    r.sv = v.s1;
+    r.nvalid = static_cast<int>(n);
+    return r;
+  }
+};
+
+struct PtrAcc {
+  using KV = bf16_t;
+  const int64_t* pk;
+  const int64_t* pv;
+  int64_t s0, s1, s2, s3;
+  int64_t stride_n;
+  int bs;
+  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
+    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+    const int64_t off = b * s0 + g * s1 + h * s2 + t * s3;
+    const int64_t ak = pk[off], av = pv[off];
+    if (ak == 0 || av == 0) return r;
+    r.k = reinterpret_cast<const void*>(static_cast<uintptr_t>(ak));
+    r.v = reinterpret_cast<const void*>(static_cast<uintptr_t>(av));
+    r.sk = r.sv = stride_n;
+    r.nvalid = bs;
+    return r;
+  }
+};
+
+template <typename KVT>
+struct PagedAcc {
+  using KV = KVT;
+  const KVT* pool_k;
+  const KVT* pool_v;
+  const float* sc_k;
+  const float* sc_v;
+  const KVT* host_k;
+  const KVT* host_v;
+  const float* hsc_k;
+  const float* hsc_v;
+  const int32_t* unit;
+  const int32_t* ids;
+  int64_t is0, is1, is2, is3;
+  int max_chunks, n_chunks, chunk_len, P, ppc, D;
+  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
+    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    if (bid < 0) return r;
+    const int cid = bid / ppc, p = bid - cid * ppc;
+    if (cid >= n_chunks || cid >= max_chunks) return r;
+    const int32_t s = unit[static_cast<int64_t>(h) * max_chunks + cid];
+    if (s == -1) return r;
+    const int64_t page = (s >= 0 ? static_cast<int64_t>(s) : static_cast<int64_t>(-2 - s)) * ppc + p;
+    const int64_t off = page * P * D;
+    if (s >= 0) {
+      r.k = pool_k + off;
+      r.v = pool_v + off;
+      if (sc_k != nullptr) { r.scale_k = sc_k[page]; r.scale_v = sc_v[page]; }
+    } else {
+      r.k = host_k + off;
+      r.v = host_v + off;
+      if (hsc_k != nullptr) { r.scale_k = hsc_k[page]; r.scale_v = hsc_v[page]; }
+    }
+    r.sk = r.sv = D;
+    const int rem = chunk_len - p * P;
+    r.nvalid = rem < P ? rem : P;
+    return r;
+  }
+};
+
+// Key tiles of up to 64 tokens over the listed blocks (wave-uniform).
+struct TileIt {
+  int t, tok0, n;  // block slot, first token of the tile within the block, tokens in tile
+  BlockRef br;
+  bool valid;
+};
+
+template <typename Acc>
+__device__ __forceinline__ TileIt first_tile(const Acc& acc, int b, int g, int h, int T, int qc,
+                                             int t) {
+  TileIt it;
+  for (; t < T; ++t) {
+    const BlockRef br = acc.block(b, g, h, t, qc);
+    if (br.k != nullptr && br.nvalid > 0) {
+      it.t = t;
+      it.tok0 = 0;
+      it.br = br;
+      it.n = br.nvalid < 64 ? br.nvalid : 64;
+      it.valid = true;
+      return it;
+    }
+  }
+  it.valid = false;
+  it.t = T;
+  it.tok0 = 0;
+  it.n = 0;
+  it.br = BlockRef{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+  return it;
+}
+
+template <typename Acc>
+__device__ __forceinline__ TileIt next_tile(const Acc& acc, const TileIt& c, int b, int g, int h,
+                                            int T, int qc) {
+  if (c.tok0 + 64 < c.br.nvalid) {
+    TileIt it = c;
+    it.tok0 += 64;
+    const int rem = c.br.nvalid - it.tok0;
+    it.n = rem < 64 ? rem : 64;
+    return it;
+  }
+  return first_tile(acc, b, g, h, T, qc, c.t + 1);
+}
+
+// ---- staging: global -> registers -> LDS -----------------------------------------------------
+// A staging unit is 4 consecutive keys x 8 consecutive dims.
+template <typename KVT> struct Stage;
+
+// 16-bit storage (bf16 / f16): 16-byte loads, stored as is.
+template <typename KVT> struct Stage16 {
+  uint4 k[4], v[4];
+  template <typename QT>
+  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int kq, int dc) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int key = kq * 4 + kk;
+      if (key < n) {
+        const int64_t row = tok0 + key;
+        k[kk] = *reinterpret_cast<const uint4*>(static_cast<const KVT*>(br.k) + row * br.sk + dc * 8);
+        v[kk] = *reinterpret_cast<const uint4*>(static_cast<const KVT*>(br.v) + row * br.sv + dc * 8);
+      } else {
+        k[kk] = make_uint4(0, 0, 0, 0);
+        v[kk] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+};
+template <> struct Stage<bf16_t> : Stage16<bf16_t> {};
+template <> struct Stage<f16_t> : Stage16<f16_t> {};
+
+// fp8 e4m3fn pages: 8-byte loads, dequantised (code * page scale) and rounded to the MFMA type.
+template <> struct Stage<uint8_t> {
+  uint4 k[4], v[4];
+  template <typename QT>
+  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int kq, int dc) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int key = kq * 4 + kk;
+      uint2 ck = make_uint2(0, 0), cv = make_uint2(0, 0);
+      if (key < n) {
+        const int64_t row = tok0 + key;
+        ck = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(br.k) + row * br.sk + dc * 8);
+        cv = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(br.v) + row * br.sv + dc * 8);
+      }
+      k[kk] = dequant8<QT>(ck, br.scale_k);
+      v[kk] = dequant8<QT>(cv, br.scale_v);
+    }
+  }
+  template <typename QT>
+  __device__ __forceinline__ static uint4 dequant8(uint2 c, float s) {
+    const uint32_t w[2] = {c.x, c.y};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = w[i / 2] >> (16 * (i & 1));
+      const float lo = e4m3_to_f32(static_cast<uint8_t>(word & 0xffu)) * s;
+      const float hi = e4m3_to_f32(static_cast<uint8_t>((word >> 8) & 0xffu)) * s;
+      o[i] = Mfma<QT>::pack2(lo, hi);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  }
+};
+
+// 16-bit element i (0..7) of a 16-byte register group.
+__device__ __forceinline__ uint32_t half_of(const uint4& r, int i) {
+  const uint32_t w = (i < 2) ? r.x : (i < 4) ? r.y : (i < 6) ? r.z : r.w;
+  return (i & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+template <int D>
+__device__ __forceinline__ void store_tile(const uint4 (&k)[4], const uint4 (&v)[4], uint16_t* Ks,
+                                           uint16_t* Vt, int kq, int dc) {
+  constexpr int KP = D + 8, VP = 64 + 8;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    *reinterpret_cast<uint4*>(Ks + (kq * 4 + kk) * KP + dc * 8) = k[kk];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint2 w;
+    w.x = half_of(v[0], i) | (half_of(v[1], i) << 16);
+    w.y = half_of(v[2], i) | (half_of(v[3], i) << 16);
+    *reinterpret_cast<uint2*>(Vt + (dc * 8 + i) * VP + kq * 4) = w;
+  }
+}
+
+// ---- MFMA kernel ------------------------------------------------------------------------------
+constexpr int kMfmaThreads = 256;
+
+template <typename QT, typename Acc, int D>
+__global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
+    View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale, int nsub) {
+  constexpr int KP = D + 8, VP = 64 + 8;
+  constexpr int KS = 64 * KP, VS = D * VP;
+  constexpr int SD = D / 32;   // k-steps of QK^T
+  constexpr int ND = D / 16;   // d-tiles of PV
+  constexpr int UNITS = 16 * (D / 8);
+  __shared__ __align__(16) uint16_t lds[2 * (KS + VS)];
+
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  // work item: (b, h, g, sub), XCD-major so one XCD walks consecutive groups of one head
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int sub = wi % nsub; wi /= nsub;
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+
+  const int m0 = g * G + sub * 64;                       // first query of this workgroup
+  const int m_end = min(min(g * G + G, M), m0 + 64);     // exclusive
+  const int qc = (g * G) / chunk;
+  const int my_q = m0 + 16 * w + l16;
+  const bool q_ok = my_q < m_end;
+
+  // Q^T operand: row my_q, dims 32s + 8 j4 .. +7
+  uint4 qb[SD];
+#pragma unroll
+  for (int s = 0; s < SD; ++s)
+    qb[s] = q_ok ? *reinterpret_cast<const uint4*>(q.at(b, my_q, h, 32 * s + 8 * j4))
+                 : make_uint4(0, 0, 0, 0);
+
+  f32x4 o[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m2 = kNegInf, lsum = 0.0f;
+  const float c2 = scale * kLog2e;
+  const bool wave_active = (m0 + 16 * w) < m_end;
+
+  TileIt it = first_tile(acc, b, g, h, T, qc, 0);
+  using KVT = typename Acc::KV;
+  Stage<KVT> st;
+  const int unit = tid;  // one unit per thread when UNITS == 256
+  const int kq = unit / (D / 8), dc = unit % (D / 8);
+  const bool stager = unit < UNITS;
+  int cur = 0;
+  if (it.valid) {
+    if (stager) {
+      st.template load<QT>(it.br, it.tok0, it.n, kq, dc);
+      store_tile<D>(st.k, st.v, lds, lds + KS, kq, dc);
+    }
+  }
+  while (it.valid) {
+    const TileIt nx = next_tile(acc, it, b, g, h, T, qc);
+    if (nx.valid && stager) st.template load<QT>(nx.br, nx.tok0, nx.n, kq, dc);
+    __syncthreads();
+    if (wave_active) {
+      const uint16_t* Ks = lds + cur * (KS + VS);
+      const uint16_t* Vt = Ks + KS;
+      f32x4 s4[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s4[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SD; ++s) {
+          const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
+          s4[t] = Mfma<QT>::run(a, qb[s], s4[t]);
+        }
+      }
+      // mask + online softmax (log2 domain); this lane holds keys 16t + 4 j4 + r of query l16
+      float mt = kNegInf;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * t + 4 * j4 + r;
+          const float x = key < it.n ? s4[t][r] * c2 : kNegInf;
+          s4[t][r] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      const float mnew = fmaxf(m2, mt);
+      const float alpha = (m2 == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m2 - mnew);
+      float ps = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = (s4[t][r] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s4[t][r] - mnew);
+          s4[t][r] = p;
+          ps += p;
+        }
+      lsum = lsum * alpha + ps;
+      m2 = mnew;
+#pragma unroll
+      for (int i = 0; i < ND; ++i) o[i] *= alpha;
+      // O^T += V^T P^T; k-slot s of lane group j4 is key 32u + 4 j4 + s (s < 4) or
+      // 32u + 16 + 4 j4 + (s - 4), for both operands
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint4 pb;
+        pb.x = Mfma<QT>::pack2(s4[2 * u][0], s4[2 * u][1]);
+        pb.y = Mfma<QT>::pack2(s4[2 * u][2], s4[2 * u][3]);
+        pb.z = Mfma<QT>::pack2(s4[2 * u + 1][0], s4[2 * u + 1][1]);
+        pb.w = Mfma<QT>::pack2(s4[2 * u + 1][2], s4[2 * u + 1][3]);
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+          const uint16_t* vr = Vt + (16 * i + l16) * VP + 32 * u + 4 * j4;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+          o[i] = Mfma<QT>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[i]);
+        }
+      }
+    }
+    if (!nx.valid) break;
+    cur ^= 1;
+    if (stager) store_tile<D>(st.k, st.v, lds + cur * (KS + VS), lds + cur * (KS + VS) + KS, kq, dc);
+    it = nx;
+  }
+
+  // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
+  lsum += __shfl_xor(lsum, 16, kWave);
+  lsum += __shfl_xor(lsum, 32, kWave);
+  if (q_ok) {
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    QT* op = out.at(b, my_q, h, 0);
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int d0 = 16 * i + 4 * j4;
+      uint2 w2;
+      w2.x = Mfma<QT>::pack2(o[i][0] * inv, o[i][1] * inv);
+      w2.y = Mfma<QT>::pack2(o[i][2] * inv, o[i][3] * inv);
+      *reinterpret_cast<uint2*>(op + d0) = w2;
+    }
+    if (lse != nullptr && j4 == 0)
+      lse[(static_cast<int64_t>(b) * H + h) * M + my_q] =
+          lsum > 0.0f ? (m2 + __builtin_log2f(lsum)) * kLn2 : kNegInf;
+  }
+}
+
+// ---- VALU kernel (fp32 arithmetic, any head dim <= 256, any strides) -------------------------
+constexpr int kValuKeys = 32;
+
+template <typename KVT> __device__ __forceinline__ float kv_elem(const void* p, int64_t i, float s);
+template <> __device__ __forceinline__ float kv_elem<float>(const void* p, int64_t i, float) {
+  return static_cast<const float*>(p)[i];
+}
+template <> __device__ __forceinline__ float kv_elem<bf16_t>(const void* p, int64_t i, float) {
+  return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float kv_elem<f16_t>(const void* p, int64_t i, float) {
+  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+}
+template <> __device__ __forceinline__ float kv_elem<uint8_t>(const void* p, int64_t i, float s) {
+  // dequantised value as the MFMA path sees it: code * scale rounded to bf16
+  return bf16_bits_to_f32(f32_to_bf16_bits(e4m3_to_f32(static_cast<const uint8_t*>(p)[i]) * s));
+}
+
+template <typename QT, typename Acc, int DQ>
+__global__ __launch_bounds__(256) void sel_fwd_valu_kernel(View4<const QT> q, View4<QT> out,
+                                                           float* __restrict__ lse, Acc acc, int M,
+                                                           int H, int D, int G, int MG, int T,
+                                                           int chunk, float scale, int nsub,
+                                                           int64_t kv_sd) {
+  constexpr int DP = 4 * DQ;
+  __shared__ float Ks[kValuKeys * DP];
+  __shared__ float Vs[kValuKeys * DP];
+  using KVT = typename Acc::KV;
+  const int tid = threadIdx.x;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int sub = wi % nsub; wi /= nsub;
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+  const int m0 = g * G + sub * 64;
+  const int m_end = min(min(g * G + G, M), m0 + 64);
+  const int qc = (g * G) / chunk;
+  const int qi = tid >> 2, part = tid & 3;
+  const int my_q = m0 + qi;
+  const bool q_ok = my_q < m_end;
+  const int d0 = part * DQ;
+
+  float qr[DQ], o[DQ];
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) {
+    const int d = d0 + i;
+    qr[i] = (q_ok && d < D) ? to_f32<QT>(*q.at(b, my_q, h, d)) : 0.0f;
+    o[i] = 0.0f;
+  }
+  float m = kNegInf, l = 0.0f;
+  for (TileIt it = first_tile(acc, b, g, h, T, qc, 0); it.valid;) {
+    // process the tile in sub-tiles of kValuKeys tokens
+    for (int k0 = 0; k0 < it.n; k0 += kValuKeys) {
+      const int nk = min(kValuKeys, it.n - k0);
+      __syncthreads();
+      for (int i = tid; i < kValuKeys * DP; i += 256) {
+        const int kk = i / DP, d = i - kk * DP;
+        float kvv = 0.0f, vvv = 0.0f;
+        if (kk < nk && d < D) {
+          const int64_t row = it.tok0 + k0 + kk;
+          kvv = kv_elem<KVT>(it.br.k, row * it.br.sk + d * kv_sd, it.br.scale_k);
+          vvv = kv_elem<KVT>(it.br.v, row * it.br.sv + d * kv_sd, it.br.scale_v);
+        }
+        Ks[i] = kvv;
+        Vs[i] = vvv;
+      }
+      __syncthreads();
+      float s[kValuKeys];
+#pragma unroll
+      for (int kk = 0; kk < kValuKeys; ++kk) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) a = __builtin_fmaf(qr[i], Ks[kk * DP + d0 + i], a);
+        a += __shfl_xor(a, 1, kWave);
+        a += __shfl_xor(a, 2, kWave);
+        s[kk] = kk < nk ? a * scale : kNegInf;
+      }
+      float mt = kNegInf;
+#pragma unroll
+      for (int kk = 0; kk < kValuKeys; ++kk) mt = fmaxf(mt, s[kk]);
+      const float mnew = fmaxf(m, mt);
+      const float alpha = (m == kNegInf) ? 0.0f : expf(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < DQ; ++i) o[i] *= alpha;
+#pragma unroll
+      for (int kk = 0; kk < kValuKeys; ++kk) {
+        const float p = (s[kk] == kNegInf) ? 0.0f : expf(s[kk] - mnew);
+        l += p;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) o[i] = __builtin_fmaf(p, Vs[kk * DP + d0 + i], o[i]);
+      }
+      m = mnew;
+    }
+    it = next_tile(acc, it, b, g, h, T, qc);
+  }
+  if (q_ok) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int d = d0 + i;
+      if (d < D) *out.at(b, my_q, h, d) = from_f32<QT>(o[i] * inv);
+    }
+    if (lse != nullptr && part == 0)
+      lse[(static_cast<int64_t>(b) * H + h) * M + my_q] = l > 0.0f ? m + logf(l) : kNegInf;
+  }
+}
+
+// ---- launch helpers -------------------------------------------------------------------------
+struct Geom {
+  int B, M, H, D, G, MG, T, nsub;
+  int64_t items;
+};
+
+inline int geom(const omm_view4& q, int64_t MGv, int64_t T, int G, Geom& g) {
+  g.B = static_cast<int>(q.size[0]);
+  g.M = static_cast<int>(q.size[1]);
+  g.H = static_cast<int>(q.size[2]);
+  g.D = static_cast<int>(q.size[3]);
+  g.G = G;
+  g.MG = static_cast<int>(MGv);
+  g.T = static_cast<int>(T);
+  g.nsub = (G + 63) / 64;
+  g.items = static_cast<int64_t>(g.B) * g.H * g.MG * g.nsub;
+  OMM_REQUIRE(g.items <= 2147483647ll, OMM_EUNSUPPORTED, "selection: grid too large");
+  return OMM_OK;
+}
+
+template <typename QT, typename Acc, int D>
+int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
+                const Acc& acc, int chunk, float scale, hipStream_t s) {
+  sel_fwd_mfma_kernel<QT, Acc, D><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
+      make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T, chunk,
+      scale, gm.nsub);
+  return check_launch("selection attention (mfma)");
+}
+
+template <typename QT, typename Acc>
+int launch_valu(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
+                const Acc& acc, int chunk, float scale, int64_t kv_sd, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(gm.items);
+  if (gm.D <= 64) {
+    sel_fwd_valu_kernel<QT, Acc, 16><<<grid, 256, 0, s>>>(make_view<const QT>(q), make_view<QT>(out),
+                                                          lse, acc, gm.M, gm.H, gm.D, gm.G, gm.MG,
+                                                          gm.T, chunk, scale, gm.nsub, kv_sd);
+  } else if (gm.D <= 128) {
+    sel_fwd_valu_kernel<QT, Acc, 32><<<grid, 256, 0, s>>>(make_view<const QT>(q), make_view<QT>(out),
+                                                          lse, acc, gm.M, gm.H, gm.D, gm.G, gm.MG,
+                                                          gm.T, chunk, scale, gm.nsub, kv_sd);
+  } else {
+    sel_fwd_valu_kernel<QT, Acc, 64><<<grid, 256, 0, s>>>(make_view<const QT>(q), make_view<QT>(out),
+                                                          lse, acc, gm.M, gm.H, gm.D, gm.G, gm.MG,
+                                                          gm.T, chunk, scale, gm.nsub, kv_sd);
+  }
+  return check_launch("selection attention (valu)");
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// MFMA path preconditions on q / out (16-byte rows, unit dim stride).
+inline bool qo_mfma_ok(const omm_view4& q, const omm_view4& out) {
+  return q.stride[3] == 1 && out.stride[3] == 1 && aligned16(q.data) && aligned16(out.data) &&
+         q.stride[0] % 8 == 0 && q.stride[1] % 8 == 0 && q.stride[2] % 8 == 0 &&
+         out.stride[0] % 4 == 0 && out.stride[1] % 4 == 0 && out.stride[2] % 4 == 0;
+}
+
+template <typename QT, typename Acc>
+int dispatch(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse, const Acc& acc,
+             int chunk, float scale, bool mfma_ok, int64_t kv_sd, hipStream_t s) {
+  if constexpr (sizeof(QT) == 2) {
+    if (mfma_ok && gm.D == 128) return launch_mfma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
+    if (mfma_ok && gm.D == 64) return launch_mfma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
+  }
+  return launch_valu<QT, Acc>(gm, q, out, lse, acc, chunk, scale, kv_sd, s);
+}
+
+int check_q_out(const char* op, const omm_view4* q, const omm_view4* out) {
+  OMM_REQUIRE(q != nullptr && out != nullptr, OMM_EINVAL, "%s: null q/out", op);
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(q->size[i] == out->size[i], OMM_EINVAL, "%s: out must have q's shape", op);
+  OMM_REQUIRE(q->size[3] >= 1 && q->size[3] <= 256, OMM_EUNSUPPORTED,
+              "%s: head dim must be in [1, 256], got %lld", op, (long long)q->size[3]);
+  return OMM_OK;
+}
+
+template <typename QT>
+int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, const omm_view4& ids,
+                  int bs, int chunk, bool causal, int G, float scale, const omm_view4& out,
+                  float* lse, hipStream_t s) {
+  Geom gm;
+  int rc = geom(q, ids.size[1], ids.size[3], G, gm);
+  if (rc) return rc;
+  DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
+                   static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
+                   ids.stride[2], ids.stride[3], static_cast<int>(k.size[1]), bs,
+                   causal ? chunk : 1, causal};
+  const bool kv_ok = k.stride[3] == 1 && v.stride[3] == 1 && aligned16(k.data) &&
+                     aligned16(v.data) && k.stride[0] % 8 == 0 && k.stride[1] % 8 == 0 &&
+                     k.stride[2] % 8 == 0 && v.stride[0] % 8 == 0 && v.stride[1] % 8 == 0 &&
+                     v.stride[2] % 8 == 0;
+  const bool mfma = sizeof(QT) == 2 && kv_ok && qo_mfma_ok(q, out);
+  // the VALU kernel reads K and V with K's dim stride
+  OMM_REQUIRE(mfma || k.stride[3] == v.stride[3], OMM_EUNSUPPORTED,
+              "selection attention: k and v need the same dim stride");
+  return dispatch<QT>(gm, q, out, lse, acc, causal ? chunk : 1, scale, mfma, k.stride[3], s);
+}
+
+}  // namespace
+}  // namespace omm
+
+extern "C" int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                           const omm_view4* ids, int32_t dtype, int32_t block_size,
+                           int32_t chunk_size, int32_t causal, int32_t group_size, float scale,
+                           const omm_view4* out, float* lse, void* stream) {
+  using namespace omm;
+  int rc = check_q_out("omm_sel_fwd", q, out);
+  if (rc) return rc;
+  OMM_REQUIRE(k != nullptr && v != nullptr && ids != nullptr, OMM_EINVAL, "omm_sel_fwd: null view");
+  const int64_t B = q->size[0], M = q->size[1], H = q->size[2], D = q->size[3];
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(k->size[i] == v->size[i], OMM_EINVAL, "omm_sel_fwd: k and v must have the same shape");
+  OMM_REQUIRE(k->size[0] == B && k->size[2] == H && k->size[3] == D, OMM_EINVAL,
+              "omm_sel_fwd: expected k/v [B,N,H,D] compatible with q");
+  OMM_REQUIRE(group_size >= 1 && block_size >= 1 && chunk_size >= 1, OMM_EINVAL,
+              "omm_sel_fwd: group_size, block_size and chunk_size must be >= 1");
+  const int64_t MG = cdiv64(M, group_size);
+  OMM_REQUIRE(ids->size[0] == B && ids->size[1] == MG && ids->size[2] == H && ids->size[3] >= 1,
+              OMM_EINVAL, "omm_sel_fwd: block_indices must be [%lld,%lld,%lld,T>=1]", (long long)B,
+              (long long)MG, (long long)H);
+  OMM_REQUIRE(k->size[1] <= 2147483647ll && M <= 2147483647ll, OMM_EUNSUPPORTED, "omm_sel_fwd: too long");
+  if (B == 0 || M == 0 || H == 0) return OMM_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case OMM_BF16:
+      return sel_fwd_typed<bf16_t>(*q, *k, *v, *ids, block_size, chunk_size, causal != 0, group_size,
+                                   scale, *out, lse, s);
+    case OMM_F16:
+      return sel_fwd_typed<f16_t>(*q, *k, *v, *ids, block_size, chunk_size, causal != 0, group_size,
+                                  scale, *out, lse, s);
+    case OMM_F32:
+      return sel_fwd_typed<float>(*q, *k, *v, *ids, block_size, chunk_size, causal != 0, group_size,
+                                  scale, *out, lse, s);
+    default: return set_error(OMM_EINVAL, "omm_sel_fwd: unsupported dtype %d", dtype);
+  }
+}
+
+extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr_v,
+                               const int64_t* ptr_stride, int64_t T, int32_t block_size,
+                               int32_t group_size, int64_t stride_bn, int64_t stride_bd,
+                               float scale, const omm_view4* out, float* lse, void* stream) {
+  using namespace omm;
+  int rc = check_q_out("omm_sel_fwd_ptr", q, out);
+  if (rc) return rc;
+  OMM_REQUIRE(ptr_k != nullptr && ptr_v != nullptr && ptr_stride != nullptr, OMM_EINVAL,
+              "omm_sel_fwd_ptr: null pointer table");
+  OMM_REQUIRE(group_size >= 1 && block_size >= 1 && T >= 1, OMM_EINVAL,
+              "omm_sel_fwd_ptr: group_size, block_size and T must be >= 1");
+  OMM_REQUIRE(stride_bn >= 0 && stride_bd >= 0, OMM_EINVAL, "omm_sel_fwd_ptr: negative stride");
+  Geom gm;
+  rc = geom(*q, cdiv64(q->size[1], group_size), T, group_size, gm);
+  if (rc) return rc;
+  if (gm.items == 0) return OMM_OK;
+  PtrAcc acc{ptr_k, ptr_v, ptr_stride[0], ptr_stride[1], ptr_stride[2], ptr_stride[3], stride_bn,
+             block_size};
+  // pointer rows must be 16-byte aligned for the MFMA staging loads (checked per call on the
+  // host only for the strides; addresses of cache chunks are allocator-aligned)
+  const bool mfma = stride_bd == 1 && stride_bn % 8 == 0 && qo_mfma_ok(*q, *out);
+  return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, stride_bd,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
+                                 int32_t group_size, float scale, const omm_view4* out, float* lse,
+                                 void* stream) {
+  using namespace omm;
+  int rc = check_q_out("omm_sel_fwd_paged", q, out);
+  if (rc) return rc;
+  OMM_REQUIRE(ids != nullptr && kv != nullptr, OMM_EINVAL, "omm_sel_fwd_paged: null argument");
+  OMM_REQUIRE(group_size >= 1, OMM_EINVAL, "omm_sel_fwd_paged: group_size must be >= 1");
+  const int64_t MG = cdiv64(q->size[1], group_size);
+  OMM_REQUIRE(ids->size[0] == q->size[0] && ids->size[1] == MG && ids->size[2] == q->size[2] &&
+                  ids->size[3] >= 1,
+              OMM_EINVAL, "omm_sel_fwd_paged: block_indices must be [B, %lld, H, T]", (long long)MG);
+  OMM_REQUIRE(kv->head_dim == q->size[3] && kv->num_heads == q->size[2], OMM_EINVAL,
+              "omm_sel_fwd_paged: cache geometry (H=%d, D=%d) does not match q", kv->num_heads,
+              kv->head_dim);
+  OMM_REQUIRE(kv->page_tokens >= 1 && kv->chunk_len >= 1 &&
+                  kv->pages_per_chunk == cdiv64(kv->chunk_len, kv->page_tokens) &&
+                  kv->unit_table != nullptr,
+              OMM_EINVAL, "omm_sel_fwd_paged: inconsistent cache geometry");
+  Geom gm;
+  rc = geom(*q, MG, ids->size[3], group_size, gm);
+  if (rc) return rc;
+  if (gm.items == 0) return OMM_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool mfma = qo_mfma_ok(*q, *out) && kv->head_dim % 64 == 0;
+  const int32_t* idp = static_cast<const int32_t*>(ids->data);
+  if (kv->dtype == OMM_BF16) {
+    PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
+                         nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
+                         static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
+                         idp, ids->stride[0], ids->stride[1], ids->stride[2], ids->stride[3],
+                         kv->max_chunks, kv->n_chunks, kv->chunk_len, kv->page_tokens,
+                         kv->pages_per_chunk, kv->head_dim};
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
+  }
+  if (kv->dtype == OMM_FP8E4M3) {
+    OMM_REQUIRE(kv->scale_k != nullptr && kv->scale_v != nullptr, OMM_EINVAL,
+                "omm_sel_fwd_paged: fp8 cache without scales");
+    PagedAcc<uint8_t> acc{static_cast<const uint8_t*>(kv->pool_k), static_cast<const uint8_t*>(kv->pool_v),
+                          kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
+                          static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
+                          kv->host_scale_v, kv->unit_table, idp, ids->stride[0], ids->stride[1],
+                          ids->stride[2], ids->stride[3], kv->max_chunks, kv->n_chunks,
+                          kv->chunk_len, kv->page_tokens, kv->pages_per_chunk, kv->head_dim};
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
+  }
+  return set_error(OMM_EINVAL, "omm_sel_fwd_paged: unsupported cache dtype %d", kv->dtype);
+}

@@ -1,0 +1,124 @@
+"""Dense selection attention with the reference's Python signature.
+
+Reference: src/omnimem/nsa/ops/selection/__init__.py:12-100 (facade and validation) and
+cuda_backend/ops.py:90-101 (op adapter).  Forward only: this build serves inference, so a call
+that would need gradients raises instead of returning a tensor without a backward.
+Extension: ``M % group_size`` need not be 0 (the last query group may be ragged).
+"""
+from __future__ import annotations
+
+import math
+import os
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .backend import NSABackendError, get_backend
+
+__all__ = ["selection_attention", "sel_fwd"]
+
+
+def _debug_checks_enabled() -> bool:
+    return os.environ.get("OMNIMEM_NSA_DEBUG", "0") not in ("", "0", "false", "False")
+
+
+def _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size, causal):
+    """Argument checks of the reference facade (nsa/ops/selection/__init__.py:16-44)."""
+    B, M, H, D = q.shape
+    N = k.shape[1]
+    G = group_size
+    assert k.shape == (B, N, H, D), f"expected k {(B, N, H, D)}, got {tuple(k.shape)}"
+    assert v.shape == (B, N, H, D), f"expected v {(B, N, H, D)}, got {tuple(v.shape)}"
+    assert D >= 16, f"expected D >= 16, but got {D}"
+    MG = -(-M // G)
+    assert block_indices.dim() == 4 and block_indices.shape[:3] == (B, MG, H), (
+        f"Expected block_indices {(B, MG, H, '*')}, got {tuple(block_indices.shape)}")
+    if chunk_size <= 0:
+        raise ValueError(f"chunk_size must be > 0, got {chunk_size}")
+    if block_indices.shape[-1] == 0:
+        raise ValueError("top_idx last dim T must be > 0")
+    num_blocks = math.ceil(N / block_size)
+    # One host sync per call, as in the reference; the op-level sel_fwd() skips it.
+    valid_mask = block_indices >= 0
+    if valid_mask.any() and torch.any(block_indices[valid_mask] >= num_blocks):
+        raise ValueError(
+            f"top_idx out of range: expected in [-1, {num_blocks - 1}] "
+            f"but got [{block_indices.min()}, {block_indices.max()}]")
+    return num_blocks
+
+
+def _debug_check_unique(block_indices):
+    ids = block_indices.to(torch.int64)
+    sorted_ids, _ = ids.sort(dim=-1)
+    dup = (sorted_ids[..., 1:] == sorted_ids[..., :-1]) & (sorted_ids[..., 1:] >= 0)
+    if dup.any():
+        raise ValueError("duplicate valid block ids within a row are not allowed (OMNIMEM_NSA_DEBUG)")
+
+
+def _no_grad_needed(*ts):
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts):
+        raise NotImplementedError(
+            "selection attention backward is not part of this build (inference only); "
+            "call under torch.no_grad() or detach the inputs")
+
+
+def sel_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+            block_size: int, chunk_size: int, scale: float, causal: bool, group_size: int,
+            allow_tf32: bool = True, out: Optional[torch.Tensor] = None,
+            lse: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Op-level adapter (counterpart of ``omnimem_nsa::sel_fwd``): returns (out, lse [B,H,M] f32).
+
+    No host synchronisation; ids outside [0, ceil(N/block_size)) are skipped by the kernel."""
+    _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"))
+    if not (q.dtype == k.dtype == v.dtype):
+        raise NSABackendError(f"sel_fwd: q/k/v must share one dtype, got {q.dtype}/{k.dtype}/{v.dtype}")
+    if block_indices.dtype != torch.int32:
+        block_indices = block_indices.to(torch.int32)
+    B, M, H, D = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device)
+    _lib.call("omm_sel_fwd", _lib.view4(q), _lib.view4(k), _lib.view4(v), _lib.view4(block_indices),
+              _lib.dtype_code(q), int(block_size), int(chunk_size), int(bool(causal)),
+              int(group_size), float(scale), _lib.view4(out), lse.data_ptr() if lse.numel() else None,
+              _lib.stream_of(q))
+    return out, lse
+
+
+def selection_attention(
+        q, k, v,
+        block_indices,
+        block_count,
+        block_size,
+        chunk_size=1,
+        scale=None,
+        variant='two-pass',
+        causal=False,
+        return_lse=False,
+        allow_tf32=True,
+        bwd_method='auto',
+        group_size=1,
+):
+    """Selection attention forward, q [B,M,H,D], k/v [B,N,H,D], block_indices [B,M/G,H,T].
+
+    Same arguments, validation and result as the reference (nsa/ops/selection/__init__.py:56);
+    returns out (q dtype) or (out, lse [B,H,M] fp32) with ``return_lse``."""
+    if variant not in ('one-pass', 'two-pass'):
+        raise ValueError(f"Invalid variant: {variant!r}, expected 'one-pass' or 'two-pass'")
+    if group_size < 1:
+        raise ValueError(f"Invalid group_size: {group_size}, expected >= 1")
+    if variant == 'one-pass':
+        raise NotImplementedError(f"{variant=} is not supported")
+    if bwd_method not in ('auto', 'mask', 'inverted'):
+        raise ValueError(f"Unknown bwd_method '{bwd_method}', expected 'auto', 'inverted' or 'mask'")
+    get_backend()
+    _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size, causal)
+    if _debug_checks_enabled():
+        _debug_check_unique(block_indices)
+    _no_grad_needed(q, k, v)
+    sc = scale if scale is not None else q.shape[-1] ** -0.5
+    out, lse = sel_fwd(q, k, v, block_indices, block_size, chunk_size, sc, causal, group_size,
+                       allow_tf32)
+    return (out, lse) if return_lse else out

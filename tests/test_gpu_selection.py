@@ -1,0 +1,140 @@
+"""GPU parity of dense selection attention against the float64 oracle.
+
+Tolerances (BASELINE): bf16/f16 max-abs 2e-2 and mean-abs 1e-3; fp32 1e-4.  Cases cover the
+reference's edge rules (cuda_backend/csrc/common.cuh:158-190, :327-332; selection_fwd.cu:1-3):
+partial last blocks, chunk-causal prefixes, -1 and out-of-range ids, duplicate ids (counted
+twice), groups larger than 64, blocks longer than 64 tokens, the reference's own shape
+(30-token blocks, groups of 15) and BASELINE configs 1 and 3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import nsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.bfloat16: (2e-2, 1e-3), torch.float16: (2e-2, 1e-3), torch.float32: (1e-4, 1e-5)}
+
+
+def _ids(gen, B, MG, H, T, nblocks, minus=0.0, dup=False):
+    ids = torch.empty((B, MG, H, T), dtype=torch.int32)
+    for b in range(B):
+        for g in range(MG):
+            for h in range(H):
+                ids[b, g, h] = torch.randperm(max(nblocks, T), generator=gen)[:T].to(torch.int32)
+    if minus:
+        ids[torch.rand(ids.shape, generator=gen) < minus] = -1
+    if dup:
+        ids[..., 1] = ids[..., 0]
+    return ids
+
+
+def _check(out, lse, want_o, want_l, dtype, rows=None):
+    o = out.float().cpu().numpy().astype(np.float64)
+    l = lse.cpu().numpy().astype(np.float64)
+    if rows is not None:
+        o, want_o = o[:, rows], want_o[:, rows]
+        l, want_l = l[:, :, rows], want_l[:, :, rows]
+    mx, mean = TOL[dtype]
+    err = np.abs(o - want_o)
+    assert err.max() <= mx, f"max-abs {err.max():.3e} > {mx}"
+    assert err.mean() <= mean, f"mean-abs {err.mean():.3e} > {mean}"
+    both_inf = np.isneginf(l) & np.isneginf(want_l)
+    assert np.array_equal(np.isneginf(l), np.isneginf(want_l))
+    if (~both_inf).any():
+        assert np.abs(l[~both_inf] - want_l[~both_inf]).max() <= 1e-3
+
+
+CASES = [
+    # M, N, H, D, G, BS, T, causal, chunk, minus, dup
+    (256, 512, 2, 128, 64, 64, 4, False, 1, 0.0, False),
+    (300, 700, 3, 128, 15, 30, 8, True, 600, 0.1, False),
+    (200, 333, 2, 128, 100, 100, 3, True, 150, 0.0, False),
+    (64, 256, 2, 128, 1, 64, 2, False, 1, 0.0, False),
+    (130, 256, 2, 64, 64, 32, 5, False, 1, 0.2, True),
+    (90, 180, 1, 96, 30, 16, 6, True, 60, 0.0, False),
+    (128, 64, 1, 128, 64, 64, 3, False, 1, 1.0, False),  # every id -1: O = 0, lse = -inf
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("case", CASES)
+def test_sel_fwd_matches_oracle(dtype, case):
+    from omnimem_amd.selection import sel_fwd
+    M, N, H, D, G, BS, T, causal, chunk, minus, dup = case
+    gen = torch.Generator().manual_seed(M * 31 + N + G)
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(dtype)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(dtype)
+    v = torch.randn((1, N, H, D), generator=gen).to(dtype)
+    MG = -(-M // G)
+    nb = -(-N // BS)
+    ids = _ids(gen, 1, MG, H, T, nb + 2, minus, dup)  # a few ids past the end too
+    out, lse = sel_fwd(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), BS, chunk, D ** -0.5, causal, G)
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                           ids.numpy(), G, D ** -0.5,
+                                           O.dense_block_tokens(N, BS, chunk, causal),
+                                           chunk_size=chunk, causal=causal)
+    _check(out, lse, want_o, want_l, dtype)
+
+
+def test_sel_fwd_strided_views():
+    from omnimem_amd.selection import sel_fwd
+    gen = torch.Generator().manual_seed(9)
+    qkv = torch.randn((1, 512, 3, 4, 128), generator=gen).to(torch.bfloat16)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]  # interleaved, as a fused qkv projection
+    ids = _ids(gen, 1, 8, 4, 4, 8)
+    out, lse = sel_fwd(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), 64, 1, 128 ** -0.5, False, 64)
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                           ids.numpy(), 64, 128 ** -0.5,
+                                           O.dense_block_tokens(512, 64, 1, False))
+    _check(out, lse, want_o, want_l, torch.bfloat16)
+
+
+def test_config1_fp32_full_size():
+    """fp32, q [1,1560,12,128], k/v [1,4680,12,128] ~ N(0,1)/sqrt(128),
+    64-token blocks, groups of 64, top-16 causal by 1560-token frames (indices from our top-k)."""
+    from omnimem_amd.index_topk import parallel_nsa_topk, block_pool
+    from omnimem_amd.selection import selection_attention
+    gen = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn((1, L, 12, 128), generator=gen) / 128 ** 0.5 for L in (1560, 4680, 4680))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    # queries are the last frame (offset 2 frames) so all three frames are candidates
+    kc = block_pool(kd, 64)
+    ids = parallel_nsa_topk(qd, kc, 16, block_size=64, chunk_size=1560, causal=False,
+                            group_size=64)
+    out, lse = selection_attention(qd, kd, vd, ids, 16, 64, chunk_size=1560, causal=False,
+                                   return_lse=True, group_size=64)
+    want_o, want_l = O.selection_attention(q.numpy(), k.numpy(), v.numpy(), ids.cpu().numpy(), 64,
+                                           128 ** -0.5, O.dense_block_tokens(4680, 64, 1560, False))
+    _check(out, lse, want_o, want_l, torch.float32)
+
+
+def test_config3_layer_bf16_sampled_groups():
+    """BASELINE config 3 shape for one layer: M = N = 32760, 12 heads, groups of 64, top-16,
+    causal by 4680-token chunks; checked on a sample of 24 query groups (all heads)."""
+    from omnimem_amd.index_topk import parallel_nsa_topk, block_pool
+    from omnimem_amd.selection import sel_fwd
+    gen = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn((1, 32760, 12, 128), generator=gen).to(torch.bfloat16) for _ in range(3))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ids = parallel_nsa_topk(qd, block_pool(kd, 64), 16, block_size=64, chunk_size=4680,
+                            causal=True, group_size=64)
+    out, lse = sel_fwd(qd, kd, vd, ids, 64, 4680, 128 ** -0.5, True, 64)
+    groups = sorted(set([0, 72, 73, 511] + torch.randint(0, 512, (20,), generator=gen).tolist()))
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                           ids.cpu().numpy(), 64, 128 ** -0.5,
+                                           O.dense_block_tokens(32760, 64, 4680, True),
+                                           chunk_size=4680, causal=True, groups=groups)
+    rows = np.concatenate([np.arange(g * 64, min(32760, g * 64 + 64)) for g in groups])
+    _check(out, lse, want_o, want_l, torch.bfloat16, rows=rows)
+
+
+def test_selection_attention_facade_validation():
+    from omnimem_amd.selection import selection_attention
+    q = torch.zeros((1, 64, 1, 16), device=DEV, dtype=torch.bfloat16)
+    ids = torch.full((1, 1, 1, 2), 5, dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError):
+        selection_attention(q, q, q, ids, 2, 64, group_size=64)  # id 5 >= 1 block
+    with pytest.raises(NotImplementedError):
+        selection_attention(q.requires_grad_(), q, q, ids.clamp(max=0), 2, 64, group_size=64)

@@ -1,0 +1,160 @@
+"""GPU parity of block compression, query pooling and top-k against the CPU oracle.
+
+Bit-exact: pooled values, and block indices (given the oracle's fp32 scores, which the kernel
+reproduces operation for operation).  Cases follow the reference's mask modes
+(cuda_backend/csrc/topk.cu:36-97) and BASELINE config 2 at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import nsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _bf16(shape, gen, scale=1.0):
+    return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16)
+
+
+def _img(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("T,group", [(256, 64), (70, 64), (4680, 64), (300, 15), (5, 1)])
+def test_block_pool_bitexact(dtype, T, group):
+    from omnimem_amd.index_topk import block_pool
+    g = torch.Generator().manual_seed(T * 7 + group)
+    x = torch.randn((2, T, 3, 128), generator=g).to(dtype)
+    got = block_pool(x.to(DEV), group).cpu()
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dtype]
+    want = O.pool_mean(_img(x), group, dt)
+    np.testing.assert_array_equal(got.float().numpy(), want)
+
+
+def test_block_pool_strided_input():
+    from omnimem_amd.index_topk import block_pool
+    g = torch.Generator().manual_seed(3)
+    base = torch.randn((1, 128, 4, 2, 64), generator=g).to(torch.bfloat16)
+    x = base[:, :, :, 1, :]  # non-contiguous head stride
+    got = block_pool(x.to(DEV), 30).cpu()
+    np.testing.assert_array_equal(got.float().numpy(), O.pool_mean(_img(x), 30, "bf16"))
+
+
+def _scores_case(seed, B, MG, H, NC, ties=True):
+    rng = np.random.default_rng(seed)
+    if ties:
+        s = rng.integers(-20, 20, size=(B, MG, H, NC)).astype(np.float32) * 0.125
+        s[rng.random(s.shape) < 0.02] = -0.0
+    else:
+        s = rng.standard_normal((B, MG, H, NC)).astype(np.float32)
+    s[rng.random(s.shape) < 0.01] = -np.inf
+    s[rng.random(s.shape) < 0.005] = np.nan
+    return s
+
+
+MASKS = {
+    "causal": dict(block_size=64, group_size=64, chunk_q=256, chunk_k=256, causal=1),
+    "causal_ragged": dict(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1),
+    "ar_awe": dict(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, blocks_per_chunk=74,
+                   q_chunk_offset=5, ex_win=3, causal=0, prog_excl=1),
+    "sink_win": dict(block_size=30, group_size=15, chunk_q=4680, chunk_k=4680, ex_sink=1, ex_win=2,
+                     causal=1, prog_excl=1),
+    "noncausal": dict(block_size=64, group_size=1, chunk_q=64, chunk_k=64, causal=0),
+}
+
+
+@pytest.mark.parametrize("mask", list(MASKS))
+@pytest.mark.parametrize("topk", [1, 16, 64])
+@pytest.mark.parametrize("NC", [37, 512, 5850])
+def test_topk_from_scores_bitexact(mask, topk, NC):
+    from omnimem_amd.index_topk import topk_from_scores
+    mk = MASKS[mask]
+    B, MG, H = 1, 74, 3
+    s = _scores_case(hash((mask, topk, NC)) & 0xFFFF, B, MG, H, NC)
+    G = mk["group_size"]
+    got = topk_from_scores(torch.from_numpy(s).to(DEV), topk, mk["block_size"], mk["chunk_q"] // G
+                           if mk["chunk_q"] % G == 0 else mk["chunk_q"], mk["chunk_k"],
+                           bool(mk["causal"]), ex_win=mk.get("ex_win", 0),
+                           ex_sink=mk.get("ex_sink", 0), prog_excl=bool(mk.get("prog_excl", 0)),
+                           q_chunk_offset=mk.get("q_chunk_offset", 0), group_size=G
+                           if mk["chunk_q"] % G == 0 else 1,
+                           blocks_per_chunk=mk.get("blocks_per_chunk", 0)).cpu().numpy()
+    om = O.Mask(**mk)
+    if mk["chunk_q"] % G != 0:
+        om.group_size = 1
+    want = O.topk_select(s, topk, om)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_topk_tf_mask_bitexact():
+    from omnimem_amd.index_topk import topk_from_scores
+    B, H, chunk, bs = 1, 2, 64, 16
+    MG, NC = 8 * chunk, 8 * chunk // bs
+    s = _scores_case(77, B, MG, H, NC)
+    got = topk_from_scores(torch.from_numpy(s).to(DEV), 16, bs, chunk, chunk, True,
+                           tf_mask=True).cpu().numpy()
+    want = O.topk_select(s, 16, O.Mask(block_size=bs, group_size=1, chunk_q=chunk, chunk_k=chunk,
+                                       causal=1, tf_mask=1, q_half=4, k_half=4))
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,NC,G,chunk,causal,qoff,exw", [
+    (1024, 16, 64, 256, True, 0, 0),
+    (4680, 592, 64, 4680, False, 7, 3),      # AR step: one chunk of queries vs 8 cached chunks
+    (3000, 100, 30, 600, True, 0, 1),
+])
+def test_parallel_nsa_topk_fused_bitexact(dtype, T, NC, G, chunk, causal, qoff, exw):
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(T + NC)
+    B, H, D = 1, 4, 128
+    q = torch.randn((B, T, H, D), generator=g).to(dtype)
+    k = torch.randn((B, NC, H, D), generator=g).to(dtype)
+    bpc = 74 if not causal else 0
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=chunk,
+                            causal=causal, group_size=G, exclude_window_chunks=exw,
+                            progressive_exclude=not causal, q_chunk_offset=qoff,
+                            blocks_per_chunk=bpc).cpu().numpy()
+    dt = "bf16" if dtype == torch.bfloat16 else "f32"
+    qp = O.pool_mean(_img(q), G, dt)
+    want = O.topk(qp, _img(k), 16, D ** -0.5,
+                  O.Mask(block_size=64, group_size=G, chunk_q=chunk, chunk_k=chunk,
+                         blocks_per_chunk=bpc, q_chunk_offset=qoff, ex_win=exw,
+                         causal=int(causal), prog_excl=int(not causal)))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_topk_config2_full_size_bitexact():
+    """q [1,32768,12,128] bf16 pooled by 64, k_cmp [1,512,12,128], top-16,
+    chunk 4680 tokens, causal."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn((1, 32768, 12, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 512, 12, 128), generator=g).to(torch.bfloat16)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=4680,
+                            causal=True, group_size=64).cpu().numpy()
+    qp = O.pool_mean(_img(q), 64, "bf16")
+    want = O.topk(qp, _img(k), 16, 128 ** -0.5,
+                  O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1))
+    np.testing.assert_array_equal(got, want)
+    assert (got >= 0).all()  # every group sees >= 73 blocks
+
+
+def test_grouped_heads_broadcast():
+    from omnimem_amd.index_topk import parallel_nsa_topk_grouped_heads
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((1, 512, 4, 64), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 32, 4, 64), generator=g).to(torch.bfloat16)
+    got = parallel_nsa_topk_grouped_heads(q.to(DEV), k.to(DEV), 2, 8, 16, 128, causal=True,
+                                          group_size=16).cpu().numpy()
+    # head pool (pairs of heads) then query pool, both rounded to bf16
+    qh = O.round_to(_img(q).reshape(1, 512, 2, 2, 64).astype(np.float32).sum(3) / 2, "bf16")
+    kh = O.round_to(_img(k).reshape(1, 32, 2, 2, 64).astype(np.float32).sum(3) / 2, "bf16")
+    want = O.topk(O.pool_mean(qh, 16, "bf16"), kh, 8, 64 ** -0.5,
+                  O.Mask(block_size=16, group_size=16, chunk_q=128, chunk_k=128, causal=1))
+    np.testing.assert_array_equal(got[:, :, 0::2], want)
+    np.testing.assert_array_equal(got[:, :, 1::2], want)
