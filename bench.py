@@ -1,0 +1,218 @@
+"""Benchmark of the NSA selection path on one MI355X.
+
+A step is one pass of the hot path over one layer of BASELINE config 3 (Wan2.1-1.3B shape: one
+81-frame clip = 32760 tokens, 12 heads x 128, bf16, 64-token blocks, groups of 64 queries,
+top-16, causal by 4680-token chunks), inputs resident in HBM:
+
+    k_cmp = block_pool(k, 64)                       # block compression
+    ids   = parallel_nsa_topk(q, k_cmp, 16, ...)    # query pooling + scoring + top-k
+    out   = sel_fwd(q, k, v, ids, ...)              # selection attention forward
+
+All 30 layers of a forward have this shape, so a forward is 30 steps.  ``value`` is the useful
+selection-attention TFLOP/s of the whole step (4 * D * visible selected tokens per query, summed,
+divided by the step time); ``roofline`` is the selection-attention kernel alone, timed with HIP
+events on the stream it runs on.  Config 2 (top-k alone) is timed beside it and reported as
+``topk`` (GB/s of algorithmic bytes).  ``cpu_baseline`` times the reference's PyTorch CPU
+formulation (oracle/cpu_baseline.py) on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "sel-attn TFLOP/s + %MFMA peak; top-k GB/s; ms per AR chunk at 60s cache"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+# config 3, one layer
+M = N = 32760
+H, D, BS, G, TOPK, CHUNK = 12, 128, 64, 64, 16, 4680
+# config 2: 512 query blocks of 64 (32760 tokens + 8 pad), 512 compressed key blocks
+C2_T, C2_NC = 32768, 512
+C2_BYTES = C2_T * H * D * 2 + C2_NC * H * D * 2 + (C2_T // 64) * H * TOPK * 4
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="target duration of the CPU baseline sample")
+    return p.parse_args()
+
+
+def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
+    """4 * D * sum over queries and heads of the visible tokens of their selected blocks.
+
+    ids holds query groups g0, g0+1, ... of a [B, ceil(M/G), H, T] index tensor."""
+    import torch
+    ids = ids.long()
+    B, MG, Hh, T = ids.shape
+    g = torch.arange(g0, g0 + MG, device=ids.device).view(1, MG, 1, 1)
+    qc = (g * G) // chunk
+    t0 = ids * BS
+    n = torch.clamp(N - t0, max=BS)
+    n = torch.minimum(n, (qc + 1) * chunk - t0)
+    ok = (ids >= 0) & (t0 < N) & ((t0 // chunk) <= qc) & (n > 0)
+    n = torch.where(ok, n, torch.zeros_like(n))
+    nq = torch.clamp(M - g * G, max=G)
+    return int((n.sum(-1, keepdim=True) * nq).sum().item()) * 4 * D
+
+
+def cpu_baseline(q, k, v, ids, seconds: float):
+    """Time the reference's CPU formulation on whole query groups of head 0 until ~seconds."""
+    import torch
+    from oracle import cpu_baseline as CB
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(threads)
+    qh, kh, vh = (x[:, :, :1].float().cpu() for x in (q, k, v))
+    idh = ids[:, :, :1].cpu().long()
+    groups_done, flops, t_total = 0, 0, 0.0
+    MG = idh.shape[1]
+    order = torch.randperm(MG, generator=torch.Generator().manual_seed(0)).tolist()
+    for g in order:
+        m0, m1 = g * G, min(M, g * G + G)
+        tok = CB.inflate_indices(idh[:, g:g + 1], BS).expand(-1, m1 - m0, -1, -1)
+        t = time.perf_counter()
+        CB.select_attention_chunked(qh[:, m0:m1], kh, vh, tok, scale=D ** -0.5, causal=True,
+                                    chunk_size=CHUNK)
+        t_total += time.perf_counter() - t
+        flops += useful_flops(idh[:, g:g + 1], M, N, G, BS, CHUNK, D, g0=g)
+        groups_done += 1
+        if t_total >= seconds:
+            break
+    return {
+        "value": round(flops / t_total / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"reference select_attention_torch_chunk formulation (fp32, 32-query chunks) on "
+                  f"{groups_done} random query groups of 64 x head 0 of the config-3 layer, "
+                  f"{t_total:.1f} s; cpu={platform.processor() or platform.machine()}, "
+                  f"nproc={os.cpu_count()}",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the selection path has no "
+              "multi-GPU mode in this build", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from omnimem_amd.index_topk import block_pool, parallel_nsa_topk
+    from omnimem_amd.selection import sel_fwd
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn((1, L, H, D), generator=gen).to(torch.bfloat16).to(dev)
+               for L in (M, N, N))
+    q2 = torch.randn((1, C2_T, H, D), generator=gen).to(torch.bfloat16).to(dev)
+    k2 = torch.randn((1, C2_NC, H, D), generator=gen).to(torch.bfloat16).to(dev)
+    scale = D ** -0.5
+    out = torch.empty_like(q)
+    lse = torch.empty((1, H, M), dtype=torch.float32, device=dev)
+
+    def step(ev=None):
+        kc = block_pool(k, BS)
+        ids = parallel_nsa_topk(q, kc, TOPK, block_size=BS, chunk_size=CHUNK, causal=True,
+                                group_size=G)
+        if ev is not None:
+            ev[0].record()
+        sel_fwd(q, k, v, ids, BS, CHUNK, scale, True, G, out=out, lse=lse)
+        if ev is not None:
+            ev[1].record()
+        return ids
+
+    def topk_step():
+        return parallel_nsa_topk(q2, k2, TOPK, block_size=BS, chunk_size=CHUNK, causal=True,
+                                 group_size=G)
+
+    ids = step()
+    torch.cuda.synchronize()
+    flops = useful_flops(ids, M, N, G, BS, CHUNK, D)
+
+    for _ in range(args.warmup):
+        step()
+        topk_step()
+    torch.cuda.synchronize()
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    sel_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+
+    # config 2: top-k alone (pool + score + select)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        topk_step()
+    e1.record()
+    torch.cuda.synchronize()
+    topk_ms = e0.elapsed_time(e1) / args.steps
+
+    sel_tflops = flops / (sel_ms * 1e-3) / 1e12
+    res = {
+        "metric": METRIC,
+        "value": round(flops / dt / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) q/k/v resident in HBM",
+        "config": {"workload": "config 3, one layer: pool + top-k + selection attention",
+                   "tokens": M, "heads": H, "head_dim": D, "block_size": BS, "group_size": G,
+                   "topk": TOPK, "chunk": CHUNK, "causal": True, "layers_per_forward": 30},
+        "useful_gflop_per_step": round(flops / 1e9, 3),
+        "roofline": {
+            "kernel": "sel_fwd_mfma_kernel",
+            "bound": "mfma",
+            "achieved": round(sel_tflops, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "kernel_ms": round(sel_ms, 4),
+        },
+        "topk": {
+            "workload": "config 2: q [1,32768,12,128] bf16 pooled by 64, k_cmp [1,512,12,128], "
+                        "top-16, causal chunk 4680",
+            "ms": round(topk_ms, 4),
+            "algorithmic_bytes": C2_BYTES,
+            "GB/s": round(C2_BYTES / (topk_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(C2_BYTES / (topk_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        },
+        "ms_per_ar_chunk": None,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(q, k, v, ids, args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

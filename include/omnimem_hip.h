@@ -18,23 +18,11 @@
  *                              in, indices out, so bit-exactness is testable on identical scores
  *   omm_sel_fwd             <- torch.ops.omnimem_nsa.sel_fwd (bindings.cpp:16-19, ops.h:25-29,
  *                              selection_fwd.cu:934-966)
- *   omm_build_ptr_table     <- torch.ops.omnimem_nsa.build_ptr_table (bindings.cpp:12-15,
- *                              ptr_table.cu:59-127)
  *   omm_sel_fwd_ptr         <- torch.ops.omnimem_nsa.sel_fwd_ptr (bindings.cpp:20-23,
  *                              selection_fwd.cu:968-992)
- *   omm_gather_publish_clear<- block-KV K1 (cuda_backend/csrc/block_kv_ops.h:12-16,
- *                              block_kv_gather.cu:80-106)
- *   omm_block_range         <- block-KV K2 (block_kv_ops.h:18-23, block_kv_range.cu:41-91)
- *   omm_dedup_run           <- block-KV K3 (block_kv_ops.h:25-31, block_kv_dedup.cu:134-206)
- *   omm_paged_append        <- MMCache.update_cache chunk_per_head branch
- *                              (models/cache.py:478-502), re-laid out as 64-token pages
  *   omm_sel_fwd_paged       <- selection_attention_padded_ptr_fast
  *                              (nsa/ops/selection/padded_ptr/wrapper.py:458-553) over the paged
  *                              cache, with int32 unit slots instead of raw int64 addresses
- *   omm_unit_touch          <- the LRU touch key set of _touch_lru_and_detect_missing
- *                              (wrapper.py:268-291), computed on the device
- *   omm_copy_units          <- flush_offload D2H (models/cache.py:1086-1117) and the reload H2D
- *                              (wrapper.py:342-361) as one batched copy kernel
  */
 #ifndef OMNIMEM_HIP_H_
 #define OMNIMEM_HIP_H_
@@ -163,14 +151,6 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 float* lse, void* stream);
 
 /* ---- pointer-table selection (a6, reference address contract) ------------------------ */
-/* ptr_x[b,g,h,t] = base_x[h, cid] + b*batch_stride + (bid % bpc)*in_chunk_block_bytes with
- * cid = bid / bpc (bpc > 0) or bid (bpc == 0); 0 when bid < 0, bid >= n_blocks_per_head[h],
- * cid >= max_chunks or base == 0.  ptr_k / ptr_v: int64 contiguous [B, MG, H, T]. */
-int omm_build_ptr_table(const omm_view4* ids, const int64_t* base_k, const int64_t* base_v,
-                        int64_t base_stride_h, int64_t base_stride_c, int32_t max_chunks,
-                        const int32_t* n_blocks_per_head, int64_t batch_stride,
-                        int32_t blocks_per_chunk, int64_t in_chunk_block_bytes, int64_t* ptr_k,
-                        int64_t* ptr_v, void* stream);
 /* bf16 only.  ptr tables: int64 [B, MG, H, T] with element strides ptr_stride; a block is
  * block_size full rows at (address + r*stride_bn + d*stride_bd) elements; 0 = skip. */
 int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr_v,
@@ -179,51 +159,12 @@ int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr
                     float* lse, void* stream);
 
 /* ---- paged block KV cache (a7) ------------------------------------------------------- */
-/* Write chunk cid of every head: k_new / v_new [1, chunk_tokens, H, D] (src_dtype bf16 or f32),
- * chunk_tokens <= chunk_len, into the units unit_table[h][cid] (must be HBM slots).  fp8 pages
- * get scale = amax/448 per (page, head) (1 when amax == 0), q = rne_sat(x * (448/amax)).
- * Tokens of a partial page beyond chunk_tokens are zeroed. */
-int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_view4* v_new,
-                     int32_t src_dtype, int32_t cid, int32_t chunk_tokens, void* stream);
 /* Selection attention over the cache, non-causal.  q: bf16 [1, M, H, D]; ids: int32
  * [1, MG, H, T] of chunk-aligned page ids (page p of chunk c is id c*pages_per_chunk + p,
  * with min(page_tokens, chunk_len - p*page_tokens) valid tokens). */
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
                       void* stream);
-/* Unique (head, chunk) units referenced by ids [1, MG, H, T]: stamp (int32 [H*max_chunks],
- * persistent) marks keys h*max_chunks + cid with epoch; out[0] = count, out[1..] ascending
- * keys (at most cap written).  Replaces the `unique().cpu()` of the reference's LRU touch. */
-int omm_unit_touch(const omm_view4* ids, int32_t num_heads, int32_t max_chunks,
-                   int32_t pages_per_chunk, int32_t* stamp, int32_t epoch, int32_t* counts,
-                   int32_t* out, int32_t cap, void* stream);
-/* Batched unit copies: for i < n, copy unit_bytes from src_base + src_slot[i]*unit_bytes to
- * dst_base + dst_slot[i]*unit_bytes (either side may be the mapped host pool), and the same for
- * the optional second pair (V) and the optional scale arrays (scale_bytes per unit). */
-int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
-                   const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
-                   const int32_t* src_slot, const int32_t* dst_slot, int32_t n,
-                   int64_t unit_bytes, int64_t scale_bytes, void* stream);
-
-/* ---- reference block-store kernels (K1 / K2 / K3) ------------------------------------ */
-/* desc: int64 [6*n_fetch + n_clear] SoA [src_k|src_v|dst_k|dst_v|pub_k|pub_v] x n_fetch then
- * clear x n_clear.  Copies block_bytes from src to dst (K and V), then stores dst into *pub;
- * zeroes the int64 at each clear address.  Returns launched workgroups via *ctas. */
-int omm_gather_publish_clear(const int64_t* desc, int64_t n_fetch, int64_t n_clear,
-                             int64_t block_bytes, int64_t* ctas, void* stream);
-/* table: int64 contiguous [2, H, MB]; n_valid: int32 [H].  table[x, h, first + j] =
- * base_x + h*head_stride_bytes + j*block_bytes (or 0 when clear); n_valid[:] = n_valid_value
- * when >= 0. */
-int omm_block_range(int64_t* table, int32_t* n_valid, int64_t heads, int64_t mb,
-                    int64_t first_bid, int64_t n_blocks, int64_t k_base, int64_t v_base,
-                    int64_t head_stride_bytes, int64_t block_bytes, int64_t n_valid_value,
-                    int32_t write_k, int32_t write_v, int32_t clear, void* stream);
-/* key = (cid*heads + h)*bpc + loc for bid = cid*bpc + loc of flat entry e (h = (e/t) % heads);
- * out[0] = unique total, out[1..] ascending keys (<= cap written).  counts / offsets hold
- * >= ceil(heads*mb / 1024) int32. */
-int omm_dedup_run(const int32_t* block_indices, int64_t n_entries, int32_t* stamp,
-                  int32_t* counts, int32_t* offsets, int32_t* out, int64_t epoch, int64_t mb,
-                  int64_t heads, int64_t t, int64_t bpc, int64_t cap, void* stream);
 
 #ifdef __cplusplus
 }

@@ -66,20 +66,9 @@ PROTOTYPES = {
     "omm_topk": (_i32, [_V, _V, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
     "omm_topk_from_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _M, _vp, _vp, _sz, _vp]),
     "omm_sel_fwd": (_i32, [_V, _V, _V, _V, _i32, _i32, _i32, _i32, _i32, _f32, _V, _vp, _vp]),
-    "omm_build_ptr_table": (_i32, [_V, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _i64, _vp,
-                                   _vp, _vp]),
     "omm_sel_fwd_ptr": (_i32, [_V, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _f32, _V, _vp,
                                _vp]),
-    "omm_paged_append": (_i32, [_P, _V, _V, _i32, _i32, _i32, _vp]),
     "omm_sel_fwd_paged": (_i32, [_V, _V, _P, _i32, _f32, _V, _vp, _vp]),
-    "omm_unit_touch": (_i32, [_V, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp]),
-    "omm_copy_units": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
-                              _vp]),
-    "omm_gather_publish_clear": (_i32, [_vp, _i64, _i64, _i64, ctypes.POINTER(_i64), _vp]),
-    "omm_block_range": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                               _i32, _i32, _i32, _vp]),
-    "omm_dedup_run": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-                             _vp]),
 }
 
 _lib = None

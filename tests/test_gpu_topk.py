@@ -4,6 +4,8 @@ Bit-exact: pooled values, and block indices (given the oracle's fp32 scores, whi
 reproduces operation for operation).  Cases follow the reference's mask modes
 (cuda_backend/csrc/topk.cu:36-97) and BASELINE config 2 at full size.
 """
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -74,7 +76,7 @@ def test_topk_from_scores_bitexact(mask, topk, NC):
     from omnimem_amd.index_topk import topk_from_scores
     mk = MASKS[mask]
     B, MG, H = 1, 74, 3
-    s = _scores_case(hash((mask, topk, NC)) & 0xFFFF, B, MG, H, NC)
+    s = _scores_case(zlib.crc32(f"{mask}/{topk}/{NC}".encode()) & 0xFFFF, B, MG, H, NC)
     G = mk["group_size"]
     got = topk_from_scores(torch.from_numpy(s).to(DEV), topk, mk["block_size"], mk["chunk_q"] // G
                            if mk["chunk_q"] % G == 0 else mk["chunk_q"], mk["chunk_k"],

@@ -281,3 +281,38 @@ def test_quantize_pages_error_bound_and_amax():
 def test_quantize_zero_page():
     codes, scale = O.quantize_pages(np.zeros((64, 8), np.float32), 64)
     assert scale == 1.0 and not codes.any()
+
+
+# ---------------------------------------------------------------- CPU baseline formulation
+def test_cpu_baseline_chunked_matches_float64_oracle():
+    """The timed CPU baseline (reference naive formulation, fp32) agrees with the float64
+    oracle, including -1 ids, a partial last block and the chunk-causal mask."""
+    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(30)
+    B, M, N, H, D, BS, G, C, T = 1, 96, 200, 2, 32, 16, 32, 64, 5
+    q, k, v = (rng.standard_normal((B, L, H, D)).astype(np.float32) for L in (M, N, N))
+    MG = M // G
+    ids = np.stack([rng.permutation(13)[:T] for _ in range(MG * H)]).astype(np.int32)
+    ids = ids.reshape(B, MG, H, T)
+    ids[0, 1, 0, 2] = -1
+    want, _ = O.selection_attention(q, k, v, ids, G, D ** -0.5, O.dense_block_tokens(N, BS, C, True),
+                                    chunk_size=C, causal=True)
+    # the naive path masks per token position; the kernel masks by the group's chunk, so check
+    # groups that do not straddle a chunk boundary (G divides C here)
+    tok = CB.inflate_indices(torch.from_numpy(ids).long(), BS)
+    tok = tok.repeat_interleave(G, dim=1)
+    got = CB.select_attention_chunked(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                      tok, scale=D ** -0.5, causal=True, chunk_size=C).numpy()
+    np.testing.assert_allclose(got, want, atol=2e-5)
+
+
+def test_cpu_baseline_topk_matches_oracle_without_ties():
+    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(31)
+    q = rng.standard_normal((1, 20, 2, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 30, 2, 64)).astype(np.float32)
+    got = CB.topk_scores(torch.from_numpy(q), torch.from_numpy(k), 8, causal=True, chunk_size=256,
+                         block_size=64, group_size=64).numpy()
+    want = O.topk(q, k, 8, 64 ** -0.5, O.Mask(block_size=64, group_size=64, chunk_q=256,
+                                              chunk_k=256, causal=1))
+    np.testing.assert_array_equal(got, want)
