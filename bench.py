@@ -72,25 +72,28 @@ def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
 
 
 def cpu_baseline(q, k, v, ids, seconds: float):
-    """Time the reference's CPU formulation on whole query groups of head 0 until ~seconds."""
+    """Time the reference's CPU formulation on random (query group, head) pairs until ~seconds."""
     import torch
     from oracle import cpu_baseline as CB
     threads = max(1, min(os.cpu_count() or 1, 16))
     torch.set_num_threads(threads)
-    qh, kh, vh = (x[:, :, :1].float().cpu() for x in (q, k, v))
-    idh = ids[:, :, :1].cpu().long()
-    groups_done, flops, t_total = 0, 0, 0.0
-    MG = idh.shape[1]
-    order = torch.randperm(MG, generator=torch.Generator().manual_seed(0)).tolist()
-    for g in order:
+    qc, kc, vc = (x.float().cpu() for x in (q, k, v))
+    idc = ids.cpu().long()
+    MG, Hh = idc.shape[1], idc.shape[2]
+    pairs = torch.randperm(MG * Hh, generator=torch.Generator().manual_seed(0)).tolist()
+    done, flops, t_total = 0, 0, 0.0
+    for p in pairs:
+        g, h = divmod(p, Hh)
         m0, m1 = g * G, min(M, g * G + G)
-        tok = CB.inflate_indices(idh[:, g:g + 1], BS).expand(-1, m1 - m0, -1, -1)
+        qh = qc[:, m0:m1, h:h + 1]
+        kh, vh = kc[:, :, h:h + 1], vc[:, :, h:h + 1]
+        tok = CB.inflate_indices(idc[:, g:g + 1, h:h + 1], BS).expand(-1, m1 - m0, -1, -1)
         t = time.perf_counter()
-        CB.select_attention_chunked(qh[:, m0:m1], kh, vh, tok, scale=D ** -0.5, causal=True,
+        CB.select_attention_chunked(qh, kh, vh, tok, scale=D ** -0.5, causal=True,
                                     chunk_size=CHUNK)
         t_total += time.perf_counter() - t
-        flops += useful_flops(idh[:, g:g + 1], M, N, G, BS, CHUNK, D, g0=g)
-        groups_done += 1
+        flops += useful_flops(idc[:, g:g + 1, h:h + 1], M, N, G, BS, CHUNK, D, g0=g)
+        done += 1
         if t_total >= seconds:
             break
     return {
@@ -99,9 +102,9 @@ def cpu_baseline(q, k, v, ids, seconds: float):
         "cores": threads,
         "kind": "port",
         "sample": f"reference select_attention_torch_chunk formulation (fp32, 32-query chunks) on "
-                  f"{groups_done} random query groups of 64 x head 0 of the config-3 layer, "
-                  f"{t_total:.1f} s; cpu={platform.processor() or platform.machine()}, "
-                  f"nproc={os.cpu_count()}",
+                  f"{done} random (64-query group, head) pairs of the config-3 layer "
+                  f"({100.0 * done / (MG * Hh):.1f}% of the step), {t_total:.1f} s of CPU time; "
+                  f"cpu={platform.processor() or platform.machine()}, nproc={os.cpu_count()}",
     }
 
 
