@@ -14,6 +14,8 @@
  *                              (nsa/ops/index_topk.py:76)
  *   omm_topk                <- torch.ops.omnimem_nsa.topk (cuda_backend/csrc/bindings.cpp:9-11,
  *                              cuda_backend/csrc/ops.h:11-17, cuda_backend/csrc/topk.cu:664-808)
+ *   omm_topk_fused          <- parallel_nsa_topk's query-group pool + the topk op
+ *                              (nsa/ops/index_topk.py:72-105 then topk.cu:664-808) in one pass
  *   omm_topk_from_scores    <- the selection half of the same op (topk.cu:366-438): block scores
  *                              in, indices out, so bit-exactness is testable on identical scores
  *   omm_sel_fwd             <- torch.ops.omnimem_nsa.sel_fwd (bindings.cpp:16-19, ops.h:25-29,
@@ -133,6 +135,16 @@ size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC, in
 int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t topk, float scale,
              const omm_topk_mask* mask, int32_t* out, void* workspace, size_t workspace_bytes,
              void* stream);
+/* q: full-resolution queries [B, T, H, D]; row g pools tokens [g*group_size,
+ * min((g+1)*group_size, T)) exactly as omm_block_pool (fp32 sum in ascending token order, one
+ * division, one rounding to the element type), then scores and selects as omm_topk.  Rows are
+ * pooled inside the top-k kernel when the shape allows (q read once); otherwise into the
+ * workspace first.  out: int32 contiguous [B, ceil(T/group_size), H, topk]. */
+size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int64_t NC,
+                                      int32_t group_size, int32_t topk, int32_t dtype);
+int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t group_size,
+                   int32_t topk, float scale, const omm_topk_mask* mask, int32_t* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
 /* scores: fp32 contiguous [B, MG, H, NC], already scaled; same selection and output as above. */
 int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H, int64_t NC,
                          int32_t topk, const omm_topk_mask* mask, int32_t* out, void* workspace,

@@ -24,6 +24,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Device fill by a kernel (graph-capture safe, unlike a memset node).
 int fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t stream);
+// Mean pooling of runs of `group` tokens (omm_block_pool without argument checks).
+int pool_launch(const omm_view4& x, const omm_view4& out, int32_t dtype, int group,
+                hipStream_t stream);
 
 #define OMM_REQUIRE(cond, code, ...) \
   do {                               \

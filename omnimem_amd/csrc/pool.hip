@@ -113,6 +113,17 @@ int launch_pool(const omm_view4& x, const omm_view4& out, int group, hipStream_t
 }
 
 }  // namespace
+
+int pool_launch(const omm_view4& x, const omm_view4& out, int32_t dtype, int group,
+                hipStream_t stream) {
+  switch (dtype) {
+    case OMM_F32: return launch_pool<float>(x, out, group, stream);
+    case OMM_BF16: return launch_pool<bf16_t>(x, out, group, stream);
+    case OMM_F16: return launch_pool<f16_t>(x, out, group, stream);
+    default: return set_error(OMM_EINVAL, "block pool: unsupported dtype %d", dtype);
+  }
+}
+
 }  // namespace omm
 
 extern "C" int omm_block_pool(const omm_view4* x, const omm_view4* out, int32_t dtype,
@@ -135,11 +146,5 @@ extern "C" int omm_block_pool(const omm_view4* x, const omm_view4* out, int32_t 
               (long long)x->size[0]);
   if (x->size[0] == 0 || x->size[1] == 0 || x->size[2] == 0 || x->size[3] == 0) return OMM_OK;
   OMM_REQUIRE(x->data != nullptr && out->data != nullptr, OMM_EINVAL, "omm_block_pool: null data");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case OMM_F32: return launch_pool<float>(*x, *out, group, s);
-    case OMM_BF16: return launch_pool<bf16_t>(*x, *out, group, s);
-    case OMM_F16: return launch_pool<f16_t>(*x, *out, group, s);
-    default: return set_error(OMM_EINVAL, "omm_block_pool: unsupported dtype %d", dtype);
-  }
+  return pool_launch(*x, *out, dtype, group, static_cast<hipStream_t>(stream));
 }

@@ -2,26 +2,39 @@
 //
 // Reference semantics: cuda_backend/csrc/topk.cu -- visibility rule (:36-97), ordering
 // (score desc, id asc; :3, :100-102), -1 padding and output contract (ops.h:11-12).
-// Design (gfx950): one workgroup = 8 query rows x one column span of one (b, h).
-//   1. scores: the span's compressed keys stream through LDS in 64-column tiles; every thread
-//      owns one column and two rows and accumulates fmaf over d in ascending order, so the fp32
-//      score is a fixed function of its inputs (reproduced bit-for-bit by the C oracle).
-//   2. selection, one wave per row: theta = topk-th largest of the 64 per-lane maxima (one
+//
+// gfx950 design: one workgroup = 16 query rows x one column span of one (b, h), 4 waves.
+//   1. rows: pooled query rows are staged in LDS as fp32.  In the fused mode the workgroup
+//      pools them itself from the full-resolution queries (16-byte loads, fp32 sum in ascending
+//      token order, one division, one rounding to the element type -- the omm_block_pool
+//      arithmetic), so q is read from HBM exactly once.
+//   2. scores: compressed keys stream through LDS in 64-column tiles (16-byte loads, the next
+//      tile's loads in flight during the current tile's arithmetic); lane = column, each wave
+//      owns 4 rows, and every score is fmaf over d ascending from 0, then * scale, so the fp32
+//      score is a fixed function of its inputs (reproduced bit for bit by the C oracle).
+//   3. selection, one wave per row: theta = topk-th largest of the 64 per-lane maxima (one
 //      wave-wide bitonic sort); only keys >= theta survive (at most topk lanes contribute);
 //      each survivor's exact rank among survivors is counted from LDS; rank < topk is written.
-//   Rows whose span is split (long key histories) write packed keys and a merge kernel selects
-//   again over the per-span winners.
+//      Column chunk ids are precomputed once per workgroup in LDS.
+//   Rows whose columns are split over several workgroups (long key histories) write packed
+//   keys and a merge kernel selects again over the per-span winners.
 #include "omm_common.h"
 
 namespace omm {
 namespace {
 
-constexpr int kRG = 8;            // query rows per workgroup
-constexpr int kThreads = 256;     // 4 waves
-constexpr int kTileC = 64;        // key columns per LDS tile
-constexpr int kSurvCap = 512;     // survivor slots per wave
-constexpr int kMaxSpan = 2048;    // columns per workgroup (score buffer 8 x 2048 fp32)
-constexpr int kMaxSplit = 32;
+constexpr int kRG = 16;                 // query rows per workgroup
+constexpr int kThreads = 256;           // 4 waves
+constexpr int kWaves = kThreads / kWave;
+constexpr int kRowsPerWave = kRG / kWaves;
+constexpr int kTileC = 64;              // key columns per LDS tile
+constexpr int kSurvCap = 256;           // survivor slots per wave
+constexpr int kSpanCap = 1024;          // columns per workgroup
+constexpr int kMaxSplit = 64;
+constexpr size_t kLdsBudget = 80 * 1024;  // two workgroups per CU
+constexpr int kStageRegs = 8;           // 16-byte staging registers per thread (K tile)
+
+enum { kModePooled = 0, kModeFused = 1, kModeScores = 2 };
 
 struct MaskDev {
   int bs, G, chunk_q, chunk_k, bpc, qoff, q_half, k_half, ex_win, ex_sink;
@@ -139,8 +152,8 @@ __device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emi
       if (rank < topk) emit(rank, k);
     }
   } else {
-    // too many survivors for the buffer (scores periodic in the lane stride): extract the
-    // maxima one at a time, each a wave-wide max over the keys below the previous one
+    // too many survivors for the buffer: extract the maxima one at a time, each a wave-wide
+    // max over the keys below the previous one
     uint64_t prev = ~0ull;
     int r = 0;
     for (; r < topk; ++r) {
@@ -168,10 +181,12 @@ __device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emi
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// 8 consecutive T from LDS as floats (p 16-byte aligned).
-template <typename T> __device__ __forceinline__ void lds8(const T* p, float (&f)[8]);
-template <> __device__ __forceinline__ void lds8<bf16_t>(const bf16_t* p, float (&f)[8]) {
-  const uint4 r = *reinterpret_cast<const uint4*>(p);
+// ---- element helpers ------------------------------------------------------------------------
+template <typename T> struct Pk { static constexpr int V = 16 / static_cast<int>(sizeof(T)); };
+
+// The V elements of a 16-byte register group as floats.
+template <typename T> __device__ __forceinline__ void unpack(const uint4& r, float* f);
+template <> __device__ __forceinline__ void unpack<bf16_t>(const uint4& r, float* f) {
   const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -179,113 +194,277 @@ template <> __device__ __forceinline__ void lds8<bf16_t>(const bf16_t* p, float 
     f[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
   }
 }
-template <> __device__ __forceinline__ void lds8<f16_t>(const f16_t* p, float (&f)[8]) {
-  const uint4 r = *reinterpret_cast<const uint4*>(p);
+template <> __device__ __forceinline__ void unpack<f16_t>(const uint4& r, float* f) {
   const f16_t* e = reinterpret_cast<const f16_t*>(&r);
 #pragma unroll
   for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(e[i].v);
 }
-template <> __device__ __forceinline__ void lds8<float>(const float* p, float (&f)[8]) {
+template <> __device__ __forceinline__ void unpack<float>(const uint4& r, float* f) {
+  f[0] = __builtin_bit_cast(float, r.x);
+  f[1] = __builtin_bit_cast(float, r.y);
+  f[2] = __builtin_bit_cast(float, r.z);
+  f[3] = __builtin_bit_cast(float, r.w);
+}
+
+// 8 consecutive elements from LDS as floats (p 16-byte aligned).
+template <typename T> __device__ __forceinline__ void lds8(const T* p, float (&f)[8]) {
+  if constexpr (Pk<T>::V == 8) {
+    unpack<T>(*reinterpret_cast<const uint4*>(p), f);
+  } else {
+    unpack<T>(*reinterpret_cast<const uint4*>(p), f);
+    unpack<T>(*reinterpret_cast<const uint4*>(p + 4), f + 4);
+  }
+}
+__device__ __forceinline__ void lds8f(const float* p, float (&f)[8]) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   const float4 b = *reinterpret_cast<const float4*>(p + 4);
   f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
   f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
 }
 
-template <typename T> __host__ __device__ constexpr int kpad() { return 16 / static_cast<int>(sizeof(T)); }
+__host__ __device__ constexpr int round8(int d) { return (d + 7) & ~7; }
+template <typename T> __host__ __device__ constexpr int kpitch(int D) {
+  return round8(D) + Pk<T>::V;  // one 16-byte pad per key row
+}
 
-// Dynamic LDS: sc [kRG][span] f32 | sv [4][kSurvCap] u64 | qs [kRG][DP] f32 | ks [64][DP+pad] T
-template <typename T, bool FROM_SCORES>
-__global__ __launch_bounds__(kThreads) void topk_kernel(
-    View4<const T> q, View4<const T> k, const float* __restrict__ scores, int MG, int H, int D,
-    int NC, int topk, float scale, MaskDev mk, int span, int nsplit, int32_t* __restrict__ out,
-    uint64_t* __restrict__ part) {
+struct Lds {
+  size_t sc, sv, kc, qs, ks, total;
+};
+
+__host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }
+
+inline Lds lds_layout(int span, int D, int esize, bool scores) {
+  Lds l{};
+  size_t off = 0;
+  l.sc = off; off = align16(off + static_cast<size_t>(kRG) * span * 4);
+  l.sv = off; off = align16(off + static_cast<size_t>(kWaves) * kSurvCap * 8);
+  l.kc = off; off = align16(off + static_cast<size_t>(span) * 4);
+  l.qs = off;
+  if (!scores) {
+    off = align16(off + static_cast<size_t>(kRG) * round8(D) * 4);
+    l.ks = off;
+    off = align16(off + static_cast<size_t>(kTileC) * (round8(D) + 16 / esize) * esize);
+  }
+  l.total = off;
+  return l;
+}
+
+// Argument block (passed by value; offsets in bytes into dynamic LDS).
+struct TopkArgs {
+  const void* q;       // pooled rows [B, MG, H, D] or full-resolution tokens [B, T, H, D]
+  int64_t qs0, qs1, qs2, qs3;
+  const void* k;       // [B, NC, H, D]
+  int64_t ks0, ks1, ks2, ks3;
+  const float* scores; // [B, MG, H, NC] (scores mode)
+  int T_len, G;        // fused mode: tokens and tokens per row
+  int MG, H, D, NC, topk;
+  float scale;
+  MaskDev mk;
+  int span, nsplit;
+  int vec;             // 16-byte loads allowed for q and k
+  int32_t* out;
+  uint64_t* part;
+  uint32_t o_sv, o_kc, o_qs, o_ks;
+};
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int V = Pk<T>::V;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-  const int bh = blockIdx.z, b = bh / H, h = bh - b * H;
-  const int row0 = blockIdx.x * kRG, split = blockIdx.y;
+  const int bh = blockIdx.z, b = bh / a.H, h = bh - b * a.H;
+  // heavy (late, causal) row tiles first
+  const int row0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kRG;
+  const int split = blockIdx.y;
+  const MaskDev& mk = a.mk;
 
   int ub = 0;
 #pragma unroll
   for (int r = 0; r < kRG; ++r) {
     const int g = row0 + r;
-    if (g < MG) ub = max(ub, row_ub(mk, row_info(mk, g), NC));
+    if (g < a.MG) ub = max(ub, row_ub(mk, row_info(mk, g), a.NC));
   }
-  const int c_begin = split * span;
-  const int c_end = min(c_begin + span, ub);
+  const int c_begin = split * a.span;
+  const int c_end = min(c_begin + a.span, ub);
   const int n = max(0, c_end - c_begin);
+  const int span = a.span;
 
   float* sc = reinterpret_cast<float*>(smem);
-  uint64_t* sv = reinterpret_cast<uint64_t*>(smem + static_cast<size_t>(kRG) * span * 4);
+  uint64_t* sv = reinterpret_cast<uint64_t*>(smem + a.o_sv);
+  int* kc = reinterpret_cast<int*>(smem + a.o_kc);
+  for (int i = tid; i < n; i += kThreads) kc[i] = col_cid(mk, c_begin + i);
 
-  if constexpr (!FROM_SCORES) {
-    const int DP = (D + 7) & ~7;
-    const int KP = DP + kpad<T>();
-    float* qs = reinterpret_cast<float*>(sv + 4 * kSurvCap);
-    T* ks = reinterpret_cast<T*>(qs + kRG * DP);
-    for (int i = tid; i < kRG * DP; i += kThreads) {
-      const int r = i / DP, d = i - r * DP, g = row0 + r;
-      qs[i] = (g < MG && d < D) ? to_f32<T>(*q.at(b, g, h, d)) : 0.0f;
-    }
-    const int c = tid & (kTileC - 1), rp = tid / kTileC;  // rows 2rp, 2rp+1
-    for (int c0 = c_begin; c0 < c_end; c0 += kTileC) {
-      __syncthreads();
-      for (int i = tid; i < kTileC * DP; i += kThreads) {
-        const int cc = i / DP, d = i - cc * DP, col = c0 + cc;
-        ks[cc * KP + d] = (col < c_end && d < D) ? *k.at(b, col, h, d) : from_f32<T>(0.0f);
-      }
-      __syncthreads();
-      const T* kr = ks + c * KP;
-      const float* q0 = qs + (2 * rp) * DP;
-      const float* q1 = q0 + DP;
-      float a0 = 0.0f, a1 = 0.0f;
-      for (int d = 0; d < DP; d += 8) {
-        float kv[8], x0[8], x1[8];
-        lds8<T>(kr + d, kv);
-        lds8<float>(q0 + d, x0);
-        lds8<float>(q1 + d, x1);
+  if constexpr (MODE != kModeScores) {
+    const int D = a.D, DP = round8(D), KP = kpitch<T>(D);
+    float* qs = reinterpret_cast<float*>(smem + a.o_qs);
+    T* ks = reinterpret_cast<T*>(smem + a.o_ks);
+    const T* qp = static_cast<const T*>(a.q);
+    const T* kp = static_cast<const T*>(a.k);
+
+    // ---- 1. query rows -> LDS (fp32) ----
+    {
+      const int r = tid / 16, p = tid % 16, g = row0 + r;
+      float* qrow = qs + r * DP;
+      if (a.vec) {
+        const int U = D / V;
+        for (int u = p; u < U; u += 16) {
+          float acc[V];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          a0 = __builtin_fmaf(x0[u], kv[u], a0);
-          a1 = __builtin_fmaf(x1[u], kv[u], a1);
+          for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+          if (g < a.MG) {
+            if constexpr (MODE == kModeFused) {
+              const int t0 = g * a.G, t1 = min(t0 + a.G, a.T_len);
+              const T* base = qp + b * a.qs0 + h * a.qs2 + u * V;
+              int t = t0;
+              for (; t + 8 <= t1; t += 8) {
+                uint4 rr[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                  rr[j] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t + j) * a.qs1);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  float f[V];
+                  unpack<T>(rr[j], f);
+#pragma unroll
+                  for (int i = 0; i < V; ++i) acc[i] += f[i];
+                }
+              }
+              for (; t < t1; ++t) {
+                const uint4 rr = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t) * a.qs1);
+                float f[V];
+                unpack<T>(rr, f);
+#pragma unroll
+                for (int i = 0; i < V; ++i) acc[i] += f[i];
+              }
+              const float cnt = static_cast<float>(t1 - t0);
+#pragma unroll
+              for (int i = 0; i < V; ++i) acc[i] = to_f32<T>(from_f32<T>(acc[i] / cnt));
+            } else {
+              const uint4 rr = *reinterpret_cast<const uint4*>(qp + b * a.qs0 + g * a.qs1 + h * a.qs2 + u * V);
+              unpack<T>(rr, acc);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < V; ++i) qrow[u * V + i] = acc[i];
+        }
+      } else {
+        for (int d = p; d < DP; d += 16) {
+          float x = 0.0f;
+          if (g < a.MG && d < D) {
+            if constexpr (MODE == kModeFused) {
+              const int t0 = g * a.G, t1 = min(t0 + a.G, a.T_len);
+              float acc = 0.0f;
+              for (int t = t0; t < t1; ++t)
+                acc += to_f32<T>(qp[b * a.qs0 + static_cast<int64_t>(t) * a.qs1 + h * a.qs2 + d * a.qs3]);
+              x = to_f32<T>(from_f32<T>(acc / static_cast<float>(t1 - t0)));
+            } else {
+              x = to_f32<T>(qp[b * a.qs0 + g * a.qs1 + h * a.qs2 + d * a.qs3]);
+            }
+          }
+          qrow[d] = x;
         }
       }
-      if (c0 + c < c_end) {
-        sc[(2 * rp) * span + (c0 + c - c_begin)] = a0 * scale;
-        sc[(2 * rp + 1) * span + (c0 + c - c_begin)] = a1 * scale;
+    }
+
+    // ---- 2. scores ----
+    // K tile staging: unit = 16 bytes; unit u of the tile is column u / U, part u % U
+    const int U = DP / V;
+    const int units = kTileC * U;
+    uint4 st[kStageRegs];
+    auto load_tile = [&](int c0) {
+#pragma unroll
+      for (int j = 0; j < kStageRegs; ++j) {
+        const int u = tid + j * kThreads;
+        st[j] = make_uint4(0, 0, 0, 0);
+        if (u < units) {
+          const int cc = u / U, pp = u - cc * U, col = c0 + cc;
+          if (col < c_end)
+            st[j] = *reinterpret_cast<const uint4*>(kp + b * a.ks0 + static_cast<int64_t>(col) * a.ks1 +
+                                                    h * a.ks2 + pp * V);
+        }
+      }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+      for (int j = 0; j < kStageRegs; ++j) {
+        const int u = tid + j * kThreads;
+        if (u < units) {
+          const int cc = u / U, pp = u - cc * U;
+          *reinterpret_cast<uint4*>(ks + cc * KP + pp * V) = st[j];
+        }
+      }
+    };
+    if (a.vec && n > 0) load_tile(c_begin);
+    for (int c0 = c_begin; c0 < c_end; c0 += kTileC) {
+      __syncthreads();
+      if (a.vec) {
+        store_tile();
+      } else {
+        for (int i = tid; i < kTileC * DP; i += kThreads) {
+          const int cc = i / DP, d = i - cc * DP, col = c0 + cc;
+          ks[cc * KP + d] = (col < c_end && d < D)
+                                ? kp[b * a.ks0 + static_cast<int64_t>(col) * a.ks1 + h * a.ks2 + d * a.ks3]
+                                : from_f32<T>(0.0f);
+        }
+      }
+      __syncthreads();
+      if (a.vec && c0 + kTileC < c_end) load_tile(c0 + kTileC);  // in flight during the FMAs
+      const T* kr = ks + lane * KP;
+      const float* q0 = qs + (wave * kRowsPerWave) * DP;
+      float acc[kRowsPerWave];
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r) acc[r] = 0.0f;
+      for (int d = 0; d < DP; d += 8) {
+        float kv[8];
+        lds8<T>(kr + d, kv);
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+          float x[8];
+          lds8f(q0 + r * DP + d, x);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[r] = __builtin_fmaf(x[u], kv[u], acc[r]);
+        }
+      }
+      const int col = c0 + lane;
+      if (col < c_end) {
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r)
+          sc[(wave * kRowsPerWave + r) * span + (col - c_begin)] = acc[r] * a.scale;
       }
     }
   } else {
     for (int i = tid; i < kRG * n; i += kThreads) {
       const int r = i / n, j = i - r * n, g = row0 + r;
-      sc[r * span + j] =
-          (g < MG) ? scores[((static_cast<int64_t>(b) * MG + g) * H + h) * NC + c_begin + j] : 0.0f;
+      sc[r * span + j] = (g < a.MG)
+          ? a.scores[((static_cast<int64_t>(b) * a.MG + g) * a.H + h) * a.NC + c_begin + j]
+          : 0.0f;
     }
   }
   __syncthreads();
 
+  // ---- 3. selection: wave w owns rows w, w + 4, w + 8, w + 12 ----
   uint64_t* wsv = sv + wave * kSurvCap;
-  for (int rr = 0; rr < kRG / 4; ++rr) {
-    const int r = wave + 4 * rr, g = row0 + r;
-    if (g >= MG) continue;  // wave-uniform; no workgroup barrier below
+  for (int rr = 0; rr < kRowsPerWave; ++rr) {
+    const int r = wave + kWaves * rr, g = row0 + r;
+    if (g >= a.MG) continue;  // wave-uniform; no workgroup barrier below
     const RowInfo ri = row_info(mk, g);
     const float* srow = sc + r * span;
-    const int64_t orow = (static_cast<int64_t>(b) * MG + g) * H + h;
+    const int64_t orow = (static_cast<int64_t>(b) * a.MG + g) * a.H + h;
+    const int NC = a.NC;
     auto key = [&](int i) -> uint64_t {
-      const int col = c_begin + i;
-      return visible(mk, ri, col_cid(mk, col)) ? make_key(srow[i], col, NC) : 0ull;
+      return visible(mk, ri, kc[i]) ? make_key(srow[i], c_begin + i, NC) : 0ull;
     };
-    if (nsplit == 1) {
-      int32_t* o = out + orow * topk;
-      wave_select(n, topk, key, [&](int rank, uint64_t kk) { o[rank] = key_id(kk, NC); },
+    if (a.nsplit == 1) {
+      int32_t* o = a.out + orow * a.topk;
+      wave_select(n, a.topk, key, [&](int rank, uint64_t kk) { o[rank] = key_id(kk, NC); },
                   [&](int p) { o[p] = -1; }, wsv);
     } else {
-      uint64_t* o = part + (orow * nsplit + split) * topk;
-      wave_select(n, topk, key, [&](int rank, uint64_t kk) { o[rank] = kk; },
+      uint64_t* o = a.part + (orow * a.nsplit + split) * a.topk;
+      wave_select(n, a.topk, key, [&](int rank, uint64_t kk) { o[rank] = kk; },
                   [&](int p) { o[p] = 0ull; }, wsv);
     }
-    (void)lane;
   }
+  (void)lane;
 }
 
 // One wave per row: top-k over the nsplit * topk per-span winners.
@@ -293,9 +472,9 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
                                                               int32_t* __restrict__ out,
                                                               int64_t rows, int nsplit, int topk,
                                                               int NC) {
-  __shared__ uint64_t sv[4 * kSurvCap];
+  __shared__ uint64_t sv[kWaves * kSurvCap];
   const int wave = threadIdx.x / kWave;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
   if (row >= rows) return;  // wave-uniform; no workgroup barrier in this kernel
   const uint64_t* p = part + row * nsplit * topk;
   int32_t* o = out + row * topk;
@@ -305,23 +484,29 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
       sv + wave * kSurvCap);
 }
 
+// ---- host planning ---------------------------------------------------------------------------
+int span_cap(int D, int esize, bool scores) {
+  for (int s = kSpanCap; s > kTileC; s -= kTileC)
+    if (lds_layout(s, D, esize, scores).total <= kLdsBudget) return s;
+  return kTileC;
+}
+
 struct Plan {
   int span, nsplit;
-  size_t ws;
+  size_t ws_part;
 };
 
-Plan make_plan(int64_t B, int64_t MG, int64_t H, int64_t NC, int topk) {
+// fused: one workgroup per row tile (no column split), so q is pooled exactly once
+Plan make_plan(int64_t B, int64_t MG, int64_t H, int64_t NC, int topk, int D, int esize,
+               bool scores, bool fused) {
   Plan p{};
-  const int span_max = kMaxSpan;
-  int nsplit = static_cast<int>(cdiv64(NC, span_max));
+  const int cap = span_cap(D, esize, scores);
+  int nsplit = static_cast<int>(cdiv64(NC, cap));
   if (nsplit < 1) nsplit = 1;
-  // spread long rows over more workgroups when there are few rows
   const int64_t tiles = cdiv64(MG, kRG) * B * H;
-  const int64_t want = 512;
-  if (tiles * nsplit < want) {
-    const int64_t extra = cdiv64(want, tiles);
-    const int64_t by_len = cdiv64(NC, 256);
-    int64_t ns = std::min<int64_t>(extra, by_len);
+  const int64_t want = 512;  // two workgroups per CU
+  if (!fused && tiles * nsplit < want) {
+    const int64_t ns = std::min<int64_t>(cdiv64(want, tiles), cdiv64(NC, 128));
     if (ns > nsplit) nsplit = static_cast<int>(ns);
   }
   nsplit = std::min(nsplit, kMaxSplit);
@@ -329,9 +514,14 @@ Plan make_plan(int64_t B, int64_t MG, int64_t H, int64_t NC, int topk) {
   span = (span + kTileC - 1) & ~(kTileC - 1);
   if (span < kTileC) span = kTileC;
   p.span = span;
-  p.nsplit = nsplit;
-  p.ws = nsplit > 1 ? static_cast<size_t>(B * MG * H) * nsplit * topk * sizeof(uint64_t) : 0;
+  p.nsplit = static_cast<int>(cdiv64(NC, span));
+  if (p.nsplit < 1) p.nsplit = 1;
+  p.ws_part = p.nsplit > 1 ? static_cast<size_t>(B * MG * H) * p.nsplit * topk * sizeof(uint64_t) : 0;
   return p;
+}
+
+bool fused_ok(int64_t B, int64_t MG, int64_t H, int64_t NC, int D, int esize) {
+  return cdiv64(NC, span_cap(D, esize, false)) == 1 && cdiv64(MG, kRG) * B * H >= 256;
 }
 
 int check_mask(const omm_topk_mask* m) {
@@ -352,56 +542,98 @@ MaskDev to_dev(const omm_topk_mask& m) {
                  m.causal != 0, m.tf_mask != 0, m.prog_excl != 0};
 }
 
-template <typename T, bool FS>
-int launch_topk(const omm_view4* q, const omm_view4* k, const float* scores, int64_t B,
-                int64_t MG, int64_t H, int64_t NC, int D, int topk, float scale,
-                const omm_topk_mask& mask, int32_t* out, void* ws, size_t ws_bytes,
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte loads are legal for a [B, L, H, D] view: unit dim stride, D % 8 == 0, every row
+// start 16-byte aligned, and one key tile's units fit the staging registers.
+bool vec_ok(const omm_view4& v, int esize) {
+  const int V = 16 / esize;
+  const int D = static_cast<int>(v.size[3]);
+  return v.stride[3] == 1 && D % 8 == 0 && a16(v.data) && v.stride[0] % V == 0 &&
+         v.stride[1] % V == 0 && v.stride[2] % V == 0 &&
+         kTileC * (D / V) <= kStageRegs * kThreads;
+}
+
+template <typename T, int MODE>
+int launch_core(TopkArgs a, int64_t B, int64_t MG, int64_t H, const Plan& p, int D,
                 hipStream_t stream) {
-  const Plan p = make_plan(B, MG, H, NC, topk);
-  OMM_REQUIRE(p.ws <= ws_bytes && (p.ws == 0 || ws != nullptr), OMM_EWORKSPACE,
-              "top-k: workspace of %zu bytes required, got %zu", p.ws, ws_bytes);
-  size_t smem = static_cast<size_t>(kRG) * p.span * 4 + 4 * kSurvCap * sizeof(uint64_t);
-  if (!FS) {
-    const int DP = (D + 7) & ~7;
-    smem += static_cast<size_t>(kRG) * DP * 4 + static_cast<size_t>(kTileC) * (DP + kpad<T>()) * sizeof(T);
-  }
-  OMM_REQUIRE(smem <= 160 * 1024, OMM_EUNSUPPORTED, "top-k: %zu bytes of LDS needed", smem);
-  if (smem > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<T, FS>),
+  const Lds l = lds_layout(p.span, D, sizeof(T), MODE == kModeScores);
+  OMM_REQUIRE(l.total <= 160 * 1024, OMM_EUNSUPPORTED, "top-k: %zu bytes of LDS needed", l.total);
+  if (l.total > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<T, MODE>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(smem));
+                                             static_cast<int>(l.total));
     if (e != hipSuccess) return set_error(OMM_EHIP, "top-k: LDS attribute: %s", hipGetErrorString(e));
   }
+  a.span = p.span;
+  a.nsplit = p.nsplit;
+  a.o_sv = static_cast<uint32_t>(l.sv);
+  a.o_kc = static_cast<uint32_t>(l.kc);
+  a.o_qs = static_cast<uint32_t>(l.qs);
+  a.o_ks = static_cast<uint32_t>(l.ks);
   const dim3 grid(static_cast<unsigned>(cdiv64(MG, kRG)), static_cast<unsigned>(p.nsplit),
                   static_cast<unsigned>(B * H));
-  View4<const T> qv{}, kv{};
-  if (!FS) {
-    qv = make_view<const T>(*q);
-    kv = make_view<const T>(*k);
-  }
-  uint64_t* part = static_cast<uint64_t*>(ws);
-  topk_kernel<T, FS><<<grid, kThreads, smem, stream>>>(qv, kv, scores, static_cast<int>(MG),
-                                         static_cast<int>(H), D, static_cast<int>(NC), topk,
-                                         scale, to_dev(mask), p.span, p.nsplit, out, part);
+  topk_kernel<T, MODE><<<grid, kThreads, l.total, stream>>>(a);
   int rc = check_launch("top-k");
   if (rc != OMM_OK || p.nsplit == 1) return rc;
   const int64_t rows = B * MG * H;
-  topk_merge_kernel<<<static_cast<unsigned>(cdiv64(rows, 4)), kThreads, 0, stream>>>(
-      part, out, rows, p.nsplit, topk, static_cast<int>(NC));
+  topk_merge_kernel<<<static_cast<unsigned>(cdiv64(rows, kWaves)), kThreads, 0, stream>>>(
+      a.part, a.out, rows, p.nsplit, a.topk, a.NC);
   return check_launch("top-k merge");
 }
 
-int check_sizes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk) {
+template <int MODE>
+int launch_typed(int32_t dtype, TopkArgs a, int64_t B, int64_t MG, int64_t H, const Plan& p,
+                 int D, hipStream_t s) {
+  switch (dtype) {
+    case OMM_F32: return launch_core<float, MODE>(a, B, MG, H, p, D, s);
+    case OMM_BF16: return launch_core<bf16_t, MODE>(a, B, MG, H, p, D, s);
+    case OMM_F16: return launch_core<f16_t, MODE>(a, B, MG, H, p, D, s);
+    default: return set_error(OMM_EINVAL, "top-k: unsupported dtype %d", dtype);
+  }
+}
+
+int esize_of(int32_t dtype) { return dtype == OMM_F32 ? 4 : 2; }
+
+int check_sizes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk, int D, int esize,
+                bool scores) {
   OMM_REQUIRE(B >= 0 && MG >= 0 && H >= 0 && NC >= 0, OMM_EINVAL, "top-k: negative size");
   OMM_REQUIRE(topk >= 1 && topk <= 64, OMM_EUNSUPPORTED, "top-k: topk must be in [1, 64], got %d",
               topk);
-  OMM_REQUIRE(B * H <= 65535 && cdiv64(MG, kRG) <= 2147483647ll, OMM_EUNSUPPORTED,
-              "top-k: B*H must be <= 65535");
-  OMM_REQUIRE(NC <= static_cast<int64_t>(kMaxSpan) * kMaxSplit, OMM_EUNSUPPORTED,
-              "top-k: %lld key blocks exceed the supported %lld", (long long)NC,
-              (long long)kMaxSpan * kMaxSplit);
+  OMM_REQUIRE(B * H <= 65535 && cdiv64(MG, kRG) <= 2147483647ll && MG <= 2147483647ll,
+              OMM_EUNSUPPORTED, "top-k: B*H must be <= 65535");
+  const int64_t cap = static_cast<int64_t>(span_cap(D, esize, scores)) * kMaxSplit;
+  OMM_REQUIRE(NC <= cap, OMM_EUNSUPPORTED, "top-k: %lld key blocks exceed the supported %lld",
+              (long long)NC, (long long)cap);
   return OMM_OK;
 }
+
+TopkArgs base_args(int64_t MG, int64_t H, int64_t NC, int D, int topk, float scale,
+                   const omm_topk_mask& mask, int32_t* out, void* part) {
+  TopkArgs a{};
+  a.MG = static_cast<int>(MG);
+  a.H = static_cast<int>(H);
+  a.D = D;
+  a.NC = static_cast<int>(NC);
+  a.topk = topk;
+  a.scale = scale;
+  a.mk = to_dev(mask);
+  a.out = out;
+  a.part = static_cast<uint64_t*>(part);
+  a.G = 1;
+  return a;
+}
+
+void set_q(TopkArgs& a, const omm_view4& q) {
+  a.q = q.data;
+  a.qs0 = q.stride[0]; a.qs1 = q.stride[1]; a.qs2 = q.stride[2]; a.qs3 = q.stride[3];
+}
+void set_k(TopkArgs& a, const omm_view4& k) {
+  a.k = k.data;
+  a.ks0 = k.stride[0]; a.ks1 = k.stride[1]; a.ks2 = k.stride[2]; a.ks3 = k.stride[3];
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
 }  // namespace omm
@@ -409,7 +641,14 @@ int check_sizes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk) {
 extern "C" size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC,
                                            int32_t topk) {
   if (B <= 0 || MG <= 0 || H <= 0 || NC <= 0 || topk < 1 || topk > 64) return 0;
-  return omm::make_plan(B, MG, H, NC, topk).ws;
+  // the split plan does not depend on the head dim beyond the LDS cap; use the smallest cap
+  // (fp32, D = 256) so the answer covers every dtype and head dim
+  size_t ws = 0;
+  for (int esize : {2, 4})
+    for (int D : {64, 128, 256})
+      for (bool scores : {false, true})
+        ws = std::max(ws, omm::make_plan(B, MG, H, NC, topk, D, esize, scores, false).ws_part);
+  return ws;
 }
 
 extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t topk,
@@ -426,25 +665,96 @@ extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, i
               (long long)k->size[1], (long long)k->size[2], (long long)k->size[3]);
   OMM_REQUIRE(D >= 1 && D <= 256, OMM_EUNSUPPORTED, "omm_topk: head dim must be in [1, 256], got %lld",
               (long long)D);
-  rc = check_sizes(B, MG, H, NC, topk);
+  const int es = esize_of(dtype);
+  rc = check_sizes(B, MG, H, NC, topk, static_cast<int>(D), es, false);
   if (rc) return rc;
   if (B == 0 || MG == 0 || H == 0) return OMM_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (NC == 0) {
-    return fill_i32(out, B * MG * H * topk, -1, s);
+  if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
+  const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
+  OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
+              OMM_EWORKSPACE, "omm_topk: workspace of %zu bytes required, got %zu", p.ws_part,
+              workspace_bytes);
+  TopkArgs a = base_args(MG, H, NC, static_cast<int>(D), topk, scale, *mask, out, workspace);
+  set_q(a, *q);
+  set_k(a, *k);
+  a.vec = vec_ok(*q, es) && vec_ok(*k, es);
+  return launch_typed<kModePooled>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
+}
+
+extern "C" size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D,
+                                                 int64_t NC, int32_t group_size, int32_t topk,
+                                                 int32_t dtype) {
+  using namespace omm;
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || NC <= 0 || group_size < 1 || topk < 1 || topk > 64)
+    return 0;
+  const int64_t MG = cdiv64(T, group_size);
+  const int es = esize_of(dtype);
+  const size_t pooled = align256(static_cast<size_t>(B * MG * H * D) * es);
+  return pooled + omm_topk_workspace_bytes(B, MG, H, NC, topk);
+}
+
+extern "C" int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                              int32_t group_size, int32_t topk, float scale,
+                              const omm_topk_mask* mask, int32_t* out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL,
+              "omm_topk_fused: null argument");
+  OMM_REQUIRE(group_size >= 1, OMM_EINVAL, "omm_topk_fused: group_size must be >= 1, got %d",
+              group_size);
+  int rc = check_mask(mask);
+  if (rc) return rc;
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(q->size[i] >= 0 && q->stride[i] >= 0 && k->stride[i] >= 0, OMM_EINVAL,
+                "omm_topk_fused: negative size or stride");
+  const int64_t B = q->size[0], T = q->size[1], H = q->size[2], D = q->size[3], NC = k->size[1];
+  const int64_t MG = cdiv64(T, group_size);
+  OMM_REQUIRE(k->size[0] == B && k->size[2] == H && k->size[3] == D, OMM_EINVAL,
+              "omm_topk_fused: incompatible q [%lld,%lld,%lld,%lld] and k [%lld,%lld,%lld,%lld]",
+              (long long)B, (long long)T, (long long)H, (long long)D, (long long)k->size[0],
+              (long long)k->size[1], (long long)k->size[2], (long long)k->size[3]);
+  OMM_REQUIRE(D >= 1 && D <= 256, OMM_EUNSUPPORTED,
+              "omm_topk_fused: head dim must be in [1, 256], got %lld", (long long)D);
+  OMM_REQUIRE(T <= 2147483647ll, OMM_EUNSUPPORTED, "omm_topk_fused: too many tokens");
+  const int es = esize_of(dtype);
+  rc = check_sizes(B, MG, H, NC, topk, static_cast<int>(D), es, false);
+  if (rc) return rc;
+  if (B == 0 || MG == 0 || H == 0) return OMM_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
+  OMM_REQUIRE(q->data != nullptr && k->data != nullptr, OMM_EINVAL, "omm_topk_fused: null data");
+
+  const bool vec = vec_ok(*q, es) && vec_ok(*k, es);
+  if (vec && fused_ok(B, MG, H, NC, static_cast<int>(D), es)) {
+    const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, true);
+    TopkArgs a = base_args(MG, H, NC, static_cast<int>(D), topk, scale, *mask, out, nullptr);
+    set_q(a, *q);
+    set_k(a, *k);
+    a.vec = 1;
+    a.T_len = static_cast<int>(T);
+    a.G = group_size;
+    return launch_typed<kModeFused>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
   }
-  switch (dtype) {
-    case OMM_F32:
-      return launch_topk<float, false>(q, k, nullptr, B, MG, H, NC, static_cast<int>(D), topk, scale,
-                                       *mask, out, workspace, workspace_bytes, s);
-    case OMM_BF16:
-      return launch_topk<bf16_t, false>(q, k, nullptr, B, MG, H, NC, static_cast<int>(D), topk,
-                                        scale, *mask, out, workspace, workspace_bytes, s);
-    case OMM_F16:
-      return launch_topk<f16_t, false>(q, k, nullptr, B, MG, H, NC, static_cast<int>(D), topk,
-                                       scale, *mask, out, workspace, workspace_bytes, s);
-    default: return set_error(OMM_EINVAL, "omm_topk: unsupported dtype %d", dtype);
-  }
+  // few rows or a long key history: pool once into the workspace, then the split kernel
+  const size_t pooled_bytes = align256(static_cast<size_t>(B * MG * H * D) * es);
+  const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
+  const size_t need = pooled_bytes + p.ws_part;
+  OMM_REQUIRE(workspace != nullptr && need <= workspace_bytes, OMM_EWORKSPACE,
+              "omm_topk_fused: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+  omm_view4 pooled{};
+  pooled.data = workspace;
+  pooled.size[0] = B; pooled.size[1] = MG; pooled.size[2] = H; pooled.size[3] = D;
+  pooled.stride[3] = 1; pooled.stride[2] = D; pooled.stride[1] = H * D; pooled.stride[0] = MG * H * D;
+  OMM_REQUIRE(MG <= 65535 && B <= 65535, OMM_EUNSUPPORTED, "omm_topk_fused: grid limit");
+  rc = pool_launch(*q, pooled, dtype, group_size, s);
+  if (rc) return rc;
+  TopkArgs a = base_args(MG, H, NC, static_cast<int>(D), topk, scale, *mask, out,
+                         static_cast<unsigned char*>(workspace) + pooled_bytes);
+  set_q(a, pooled);
+  set_k(a, *k);
+  a.vec = vec_ok(pooled, es) && vec_ok(*k, es);
+  return launch_typed<kModePooled>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
 }
 
 extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H,
@@ -455,14 +765,17 @@ extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, 
   OMM_REQUIRE(out != nullptr, OMM_EINVAL, "omm_topk_from_scores: null output");
   int rc = check_mask(mask);
   if (rc) return rc;
-  rc = check_sizes(B, MG, H, NC, topk);
+  rc = check_sizes(B, MG, H, NC, topk, 128, 4, true);
   if (rc) return rc;
   if (B == 0 || MG == 0 || H == 0) return OMM_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (NC == 0) {
-    return fill_i32(out, B * MG * H * topk, -1, s);
-  }
+  if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   OMM_REQUIRE(scores != nullptr, OMM_EINVAL, "omm_topk_from_scores: null scores");
-  return launch_topk<float, true>(nullptr, nullptr, scores, B, MG, H, NC, 0, topk, 0.0f, *mask, out,
-                                  workspace, workspace_bytes, s);
+  const Plan p = make_plan(B, MG, H, NC, topk, 128, 4, true, false);
+  OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
+              OMM_EWORKSPACE, "omm_topk_from_scores: workspace of %zu bytes required, got %zu",
+              p.ws_part, workspace_bytes);
+  TopkArgs a = base_args(MG, H, NC, 128, topk, 0.0f, *mask, out, workspace);
+  a.scores = scores;
+  return launch_core<float, kModeScores>(a, B, MG, H, p, 128, s);
 }

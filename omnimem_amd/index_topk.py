@@ -145,17 +145,21 @@ def parallel_nsa_topk(
     """Top-``block_counts`` compressed-key blocks per query group: int32 [B, ceil(T/G), H, S].
 
     Same arguments and result as the reference (nsa/ops/index_topk.py:43-105); -1 marks slots
-    with no visible block.  Query pooling runs on the HIP pooling kernel."""
+    with no visible block.  Query-group pooling, scoring and selection run in one HIP call."""
     get_backend()
     assert not (tf_mask and q_chunk_offset), \
         "tf_mask assumes a full [clean|noisy] layout; q_chunk_offset must be 0"
+    _lib.require_cuda((q, "q"), (k, "k"))
+    if q.dim() != 4 or k.dim() != 4:
+        raise NSABackendError("parallel_nsa_topk: expected q [B,T,H,K] and k [B,TC,H,K]")
+    if q.dtype != k.dtype:
+        raise NSABackendError(f"topk: q and k must share a dtype, got {q.dtype} vs {k.dtype}")
     B, T, H, K = q.shape
     G = int(group_size)
     if G < 1:
         raise ValueError(f"group_size must be >= 1, got {G}")
-    if G > 1:
-        q = block_pool(q, G)
-    MG = q.shape[1]
+    MG = -(-T // G)
+    NC = k.shape[1]
     if tf_mask:
         assert chunk_size % G == 0 and T % G == 0, "tf_mask requires G | chunk_size and G | T"
         rows = chunk_size // G
@@ -163,29 +167,26 @@ def parallel_nsa_topk(
             f"tf_mask=True requires T ({MG}) divisible by 2*chunk_size ({2 * rows}); "
             f"Q must be laid out as [clean | noisy] with equal halves.")
         kchunk_blocks = chunk_size // block_size
-        assert k.shape[1] % (2 * kchunk_blocks) == 0, (
-            f"tf_mask=True requires TC ({k.shape[1]}) divisible by 2 * (chunk_size_k/block_size) "
+        assert NC % (2 * kchunk_blocks) == 0, (
+            f"tf_mask=True requires TC ({NC}) divisible by 2 * (chunk_size_k/block_size) "
             f"({2 * kchunk_blocks}); K layout must be [clean | noisy] with equal halves.")
-    sc = scale if scale is not None else K ** -0.5
-    NC = k.shape[1]
-    q_half = (MG * G) // (2 * chunk_size) if tf_mask else 0
-    k_half = (NC * block_size) // (2 * chunk_size) if tf_mask else 0
-    _lib.require_cuda((q, "q"), (k, "k"))
-    if q.dtype != k.dtype:
-        raise NSABackendError(f"topk: q and k must share a dtype, got {q.dtype} vs {k.dtype}")
     for name, v in (("block_size", block_size), ("chunk_size", chunk_size),
                     ("exclude_window_chunks", exclude_window_chunks),
                     ("exclude_sink_chunks", exclude_sink_chunks),
                     ("q_chunk_offset", q_chunk_offset)):
         _check_int(name, v)
+    sc = scale if scale is not None else K ** -0.5
+    q_half = (MG * G) // (2 * chunk_size) if tf_mask else 0
+    k_half = (NC * block_size) // (2 * chunk_size) if tf_mask else 0
     m = _mask(block_size, G, chunk_size, chunk_size, causal, exclude_window_chunks,
               exclude_sink_chunks, progressive_exclude, tf_mask, q_chunk_offset, q_half, k_half,
               blocks_per_chunk)
     S = int(block_counts)
     out = torch.empty((B, MG, H, S), dtype=torch.int32, device=q.device)
-    ws_n = _lib.lib().omm_topk_workspace_bytes(B, MG, H, NC, S)
+    dt = _lib.dtype_code(q)
+    ws_n = _lib.lib().omm_topk_fused_workspace_bytes(B, T, H, K, NC, G, S, dt)
     ws = _lib.workspace(ws_n, q.device)
-    _lib.call("omm_topk", _lib.view4(q), _lib.view4(k), _lib.dtype_code(q), S, float(sc), m,
+    _lib.call("omm_topk_fused", _lib.view4(q), _lib.view4(k), dt, G, S, float(sc), m,
               out.data_ptr() if out.numel() else None, ws.data_ptr(), ws_n, _lib.stream_of(q))
     return out
 

@@ -160,3 +160,64 @@ def test_grouped_heads_broadcast():
                   O.Mask(block_size=16, group_size=16, chunk_q=128, chunk_k=128, causal=1))
     np.testing.assert_array_equal(got[:, :, 0::2], want)
     np.testing.assert_array_equal(got[:, :, 1::2], want)
+
+
+def test_topk_fused_config3_ragged_tail_bitexact():
+    """Config 3 shape: T = 32760 (last group 56 tokens) pooled inside the top-k kernel."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(33)
+    q = torch.randn((1, 32760, 12, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 512, 12, 128), generator=g).to(torch.bfloat16)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=4680,
+                            causal=True, group_size=64).cpu().numpy()
+    want = O.topk(O.pool_mean(_img(q), 64, "bf16"), _img(k), 16, 128 ** -0.5,
+                  O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1))
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_topk_fused_many_heads_bitexact(dtype):
+    """64 heads x 4 row tiles: the single-pass fused kernel, every element type."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(34)
+    q = torch.randn((1, 4096, 64, 64), generator=g).to(dtype)
+    k = torch.randn((1, 200, 64, 64), generator=g).to(dtype)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 8, block_size=32, chunk_size=1024,
+                            causal=True, group_size=64, exclude_sink_chunks=1,
+                            exclude_window_chunks=1).cpu().numpy()
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dtype]
+    want = O.topk(O.pool_mean(_img(q), 64, dt), _img(k), 8, 64 ** -0.5,
+                  O.Mask(block_size=32, group_size=64, chunk_q=1024, chunk_k=1024, causal=1,
+                         ex_sink=1, ex_win=1))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_topk_strided_inputs_scalar_staging_bitexact():
+    """Non-unit dim strides on q and k: element-wise staging paths."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(35)
+    qb = torch.randn((1, 640, 3, 96, 2), generator=g).to(torch.bfloat16)
+    kb = torch.randn((1, 50, 3, 96, 2), generator=g).to(torch.bfloat16)
+    q, k = qb[..., 0], kb[..., 1]
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 6, block_size=16, chunk_size=160,
+                            causal=True, group_size=20).cpu().numpy()
+    want = O.topk(O.pool_mean(_img(q), 20, "bf16"), _img(k), 6, 96 ** -0.5,
+                  O.Mask(block_size=16, group_size=20, chunk_q=160, chunk_k=160, causal=1))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_topk_prepooled_op_long_history_split_merge():
+    """Pre-pooled op with a long history: column splits + merge (AR shape, 80 cached chunks)."""
+    from omnimem_amd.index_topk import topk
+    g = torch.Generator().manual_seed(36)
+    q = torch.randn((1, 74, 12, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 80 * 74, 12, 128), generator=g).to(torch.bfloat16)
+    # chunk_size counts pooled rows (74 rows = one 4680-token chunk of queries, chunk 80)
+    got = topk(q.to(DEV), k.to(DEV), 16, 128 ** -0.5, 64, 74, 4680, False, ex_win=3,
+               prog_excl=True, q_chunk_offset=80, group_size=64,
+               blocks_per_chunk=74).cpu().numpy()
+    want = O.topk(_img(q), _img(k), 16, 128 ** -0.5,
+                  O.Mask(block_size=64, group_size=64, chunk_q=74 * 64, chunk_k=4680,
+                         blocks_per_chunk=74, q_chunk_offset=80, ex_win=3, causal=0,
+                         prog_excl=1))
+    np.testing.assert_array_equal(got, want)
