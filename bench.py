@@ -71,6 +71,23 @@ def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
     return int((n.sum(-1, keepdim=True) * nq).sum().item()) * 4 * D
 
 
+PMC_FILE = os.path.join(ROOT, "profiles", "bench_config3_layer_pmc.json")
+
+
+def measured_traffic(kernel_prefix: str):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary of this benchmark (calibrated against a plain copy), or None."""
+    try:
+        with open(PMC_FILE) as f:
+            kernels = json.load(f)["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    for name, v in kernels.items():
+        if name.startswith(kernel_prefix):
+            return v.get("hbm_bytes_scaled")
+    return None
+
+
 def cpu_baseline(q, k, v, ids, seconds: float):
     """Time the reference's CPU formulation on random (query group, head) pairs until ~seconds."""
     import torch
@@ -198,7 +215,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("sel_fwd_mfma_kernel<bf16_t, DenseAcc<bf16_t>, 128>"),
             "kernel_ms": round(sel_ms, 4),
         },
         "topk": {
@@ -208,6 +225,7 @@ def main():
             "algorithmic_bytes": C2_BYTES,
             "GB/s": round(C2_BYTES / (topk_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(C2_BYTES / (topk_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic("topk_kernel<bf16_t, 1>"),
         },
         "ms_per_ar_chunk": None,
         "cpu_baseline": None,

@@ -1,0 +1,617 @@
+// Block KV cache kernels: the paged cache (append with fused block compression and fp8
+// quantisation, batched unit copies for evict / promote), the reference's pointer-table builder,
+// and the reference's block-store kernels K1 (gather + publish + clear), K2 (table range) and
+// K3 (dedup of selected blocks).
+//
+// Reference semantics: cuda_backend/csrc/ptr_table.cu:1-55 (address contract, 0 = skip),
+// block_kv_ops.h:1-31 (K1/K2/K3 contracts), models/cache.py:478-502 (per-head chunk append).
+// Paged layout (new): a unit is one (head, chunk) of one layer, pages_per_chunk pages of
+// page_tokens x head_dim elements, contiguous; units live in HBM slots or in a device-mapped
+// pinned host pool and are addressed through an int32 unit table instead of raw addresses.
+#include "omm_common.h"
+
+namespace omm {
+namespace {
+
+// ---- pointer table (reference address contract) ------------------------------------------------
+__global__ __launch_bounds__(256) void ptr_table_kernel(
+    const int32_t* __restrict__ ids, int64_t is0, int64_t is1, int64_t is2, int64_t is3,
+    const int64_t* __restrict__ base_k, const int64_t* __restrict__ base_v, int64_t bsh,
+    int64_t bsc, int max_chunks, const int32_t* __restrict__ n_blocks, int64_t* __restrict__ pk,
+    int64_t* __restrict__ pv, int MG, int H, int T, int64_t batch_stride, int bpc,
+    int64_t in_chunk_bytes, int64_t total) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int t = static_cast<int>(i % T);
+    const int64_t r1 = i / T;
+    const int h = static_cast<int>(r1 % H);
+    const int64_t r2 = r1 / H;
+    const int g = static_cast<int>(r2 % MG);
+    const int b = static_cast<int>(r2 / MG);
+    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    int64_t ak = 0, av = 0;
+    if (bid >= 0 && bid < n_blocks[h]) {
+      const int64_t cid = bpc > 0 ? bid / bpc : bid;
+      const int64_t off = bpc > 0 ? static_cast<int64_t>(bid % bpc) * in_chunk_bytes : 0;
+      if (cid < max_chunks) {
+        const int64_t bk = base_k[h * bsh + cid * bsc], bv = base_v[h * bsh + cid * bsc];
+        const int64_t delta = static_cast<int64_t>(b) * batch_stride + off;
+        ak = bk != 0 ? bk + delta : 0;
+        av = bv != 0 ? bv + delta : 0;
+      }
+    }
+    pk[i] = ak;
+    pv[i] = av;
+  }
+}
+
+// ---- paged append ----------------------------------------------------------------------------
+struct AppendArgs {
+  const bf16_t* k;     // new chunk [1, S, H, D] (token stride ks1, head stride ks2)
+  const bf16_t* v;
+  int64_t ks1, ks2, vs1, vs2;
+  void* pool_k;
+  void* pool_v;
+  float* scale_k;
+  float* scale_v;
+  const int32_t* unit_table;
+  int32_t* stamp;
+  bf16_t* k_cmp;       // optional [1, NCB, H, D] pooled keys; page p of chunk cid -> row cid*ppc+p
+  int64_t cs1, cs2;
+  int H, D, P, ppc, max_chunks, cid, tokens, lph, epoch;
+};
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& r, float (&f)[8]) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+    f[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint2 quant8(const float (&x)[8], float inv) {
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = fminf(fmaxf(x[i] * inv, -448.0f), 448.0f);
+    w[i / 4] |= static_cast<uint32_t>(f32_to_e4m3(y)) << (8 * (i & 3));
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+// One wave per (page, heads of the wave); lane = (head in wave, 8-dim slice).  Every lane walks
+// the page's tokens in ascending order, so the pooled key is the omm_block_pool arithmetic.
+template <bool FP8>
+__global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
+  const int lane = lane_id();
+  const int hl = lane / a.lph, dc = lane - hl * a.lph;
+  const int h = blockIdx.y * (kWave / a.lph) + hl;
+  const int p = blockIdx.x;
+  const bool active = hl < kWave / a.lph && h < a.H && dc * 8 < a.D;
+  int32_t slot = -1;
+  if (active) slot = a.unit_table[static_cast<int64_t>(h) * a.max_chunks + a.cid];
+  const int t_first = p * a.P;
+  const int nvalid = max(0, min(a.P, a.tokens - t_first));
+  const bool go = active && slot >= 0;
+  const int64_t page = static_cast<int64_t>(slot) * a.ppc + p;
+  const bf16_t* ksrc = a.k + static_cast<int64_t>(h) * a.ks2 + dc * 8;
+  const bf16_t* vsrc = a.v + static_cast<int64_t>(h) * a.vs2 + dc * 8;
+
+  float ksum[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ksum[i] = 0.0f;
+
+  if constexpr (!FP8) {
+    uint4* kd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_k) + page * a.P * a.D + dc * 8);
+    uint4* vd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_v) + page * a.P * a.D + dc * 8);
+    const int64_t row = a.D / 8;  // uint4 per page row
+    if (go) {
+      for (int t = 0; t < a.P; ++t) {
+        uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
+        if (t < nvalid) {
+          kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
+          vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
+          float f[8];
+          unpack_bf16x8(kr, f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ksum[i] += f[i];
+        }
+        kd[t * row] = kr;
+        vd[t * row] = vr;
+      }
+    }
+  } else {
+    float amax_k = 0.0f, amax_v = 0.0f;
+    if (go) {
+      for (int t = 0; t < nvalid; ++t) {
+        const uint4 kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
+        const uint4 vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
+        float fk[8], fv[8];
+        unpack_bf16x8(kr, fk);
+        unpack_bf16x8(vr, fv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ksum[i] += fk[i];
+          amax_k = fmaxf(amax_k, fabsf(fk[i]));
+          amax_v = fmaxf(amax_v, fabsf(fv[i]));
+        }
+      }
+    }
+    // max over the lanes of one head (exact, order-free); all lanes take part in the shuffles
+    for (int m = 1; m < a.lph; m <<= 1) {
+      amax_k = fmaxf(amax_k, __shfl_xor(amax_k, m, kWave));
+      amax_v = fmaxf(amax_v, __shfl_xor(amax_v, m, kWave));
+    }
+    if (go) {
+      const float sk = amax_k > 0.0f ? amax_k / 448.0f : 1.0f;
+      const float ik = amax_k > 0.0f ? 448.0f / amax_k : 1.0f;
+      const float sv = amax_v > 0.0f ? amax_v / 448.0f : 1.0f;
+      const float iv = amax_v > 0.0f ? 448.0f / amax_v : 1.0f;
+      uint2* kd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_k) + page * a.P * a.D + dc * 8);
+      uint2* vd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_v) + page * a.P * a.D + dc * 8);
+      const int64_t row = a.D / 8;  // uint2 per page row
+      for (int t = 0; t < a.P; ++t) {
+        uint2 kq = make_uint2(0, 0), vq = make_uint2(0, 0);
+        if (t < nvalid) {
+          const uint4 kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
+          const uint4 vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
+          float fk[8], fv[8];
+          unpack_bf16x8(kr, fk);
+          unpack_bf16x8(vr, fv);
+          kq = quant8(fk, ik);
+          vq = quant8(fv, iv);
+        }
+        kd[t * row] = kq;
+        vd[t * row] = vq;
+      }
+      if (dc == 0) {
+        a.scale_k[page] = sk;
+        a.scale_v[page] = sv;
+      }
+    }
+  }
+  if (go && a.k_cmp != nullptr) {
+    const float cnt = static_cast<float>(nvalid);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = nvalid > 0 ? f32_to_bf16_bits(ksum[2 * i] / cnt) : 0;
+      const uint16_t hi = nvalid > 0 ? f32_to_bf16_bits(ksum[2 * i + 1] / cnt) : 0;
+      w[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    const int64_t r = static_cast<int64_t>(a.cid) * a.ppc + p;
+    *reinterpret_cast<uint4*>(a.k_cmp + r * a.cs1 + h * a.cs2 + dc * 8) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (go && p == 0 && dc == 0 && a.stamp != nullptr && a.epoch > 0)
+    a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
+}
+
+// ---- batched unit copies (evict to the host pool, promote to HBM) ---------------------------
+constexpr int64_t kCopyPart = 64 * 1024;  // bytes per workgroup
+
+struct CopyArgs {
+  const unsigned char* src_k;
+  unsigned char* dst_k;
+  const unsigned char* src_v;
+  unsigned char* dst_v;
+  const unsigned char* src_sk;
+  unsigned char* dst_sk;
+  const unsigned char* src_sv;
+  unsigned char* dst_sv;
+  const int32_t* src_slot;
+  const int32_t* dst_slot;
+  int64_t unit_bytes, scale_bytes;
+};
+
+__device__ __forceinline__ void copy_range16(const unsigned char* s, unsigned char* d, int64_t n) {
+  const uint4* s4 = reinterpret_cast<const uint4*>(s);
+  uint4* d4 = reinterpret_cast<uint4*>(d);
+  const int64_t n4 = n / 16;
+  constexpr int U = 4;
+  int64_t i = threadIdx.x;
+  for (; i + (U - 1) * blockDim.x < n4; i += U * blockDim.x) {
+    uint4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) r[u] = s4[i + u * blockDim.x];
+#pragma unroll
+    for (int u = 0; u < U; ++u) d4[i + u * blockDim.x] = r[u];
+  }
+  for (; i < n4; i += blockDim.x) d4[i] = s4[i];
+}
+
+__global__ __launch_bounds__(256) void copy_units_kernel(CopyArgs a) {
+  const int64_t i = blockIdx.x;
+  const int64_t part = blockIdx.y;
+  const int64_t so = static_cast<int64_t>(a.src_slot[i]), dof = static_cast<int64_t>(a.dst_slot[i]);
+  const int64_t b0 = part * kCopyPart;
+  const int64_t n = min(kCopyPart, a.unit_bytes - b0);
+  if (n > 0) {
+    copy_range16(a.src_k + so * a.unit_bytes + b0, a.dst_k + dof * a.unit_bytes + b0, n);
+    if (a.src_v != nullptr)
+      copy_range16(a.src_v + so * a.unit_bytes + b0, a.dst_v + dof * a.unit_bytes + b0, n);
+  }
+  if (part == 0 && a.scale_bytes > 0) {
+    for (int64_t j = threadIdx.x; j < a.scale_bytes; j += blockDim.x) {
+      if (a.src_sk != nullptr) a.dst_sk[dof * a.scale_bytes + j] = a.src_sk[so * a.scale_bytes + j];
+      if (a.src_sv != nullptr) a.dst_sv[dof * a.scale_bytes + j] = a.src_sv[so * a.scale_bytes + j];
+    }
+  }
+}
+
+// ---- K1: gather + publish + clear -----------------------------------------------------------
+constexpr int kClearPerWg = 256;
+
+__device__ __forceinline__ void copy_bytes_wg(int64_t src, int64_t dst, int64_t nbytes) {
+  if ((nbytes & 15) == 0 && ((src | dst) & 15) == 0) {
+    copy_range16(reinterpret_cast<const unsigned char*>(src), reinterpret_cast<unsigned char*>(dst),
+                 nbytes);
+  } else {
+    const uint16_t* s = reinterpret_cast<const uint16_t*>(src);
+    uint16_t* d = reinterpret_cast<uint16_t*>(dst);
+    for (int64_t j = threadIdx.x; j < nbytes / 2; j += blockDim.x) d[j] = s[j];
+  }
+}
+
+// desc has no __restrict__: the kernel stores through addresses read out of it
+__global__ __launch_bounds__(256) void gather_publish_clear_kernel(const int64_t* desc,
+                                                                   int64_t n_fetch,
+                                                                   int64_t n_clear,
+                                                                   int64_t block_bytes) {
+  const int64_t w = blockIdx.x;
+  if (w < n_fetch) {
+    const int64_t sk = desc[w], sv = desc[n_fetch + w];
+    const int64_t dk = desc[2 * n_fetch + w], dv = desc[3 * n_fetch + w];
+    const int64_t pk = desc[4 * n_fetch + w], pv = desc[5 * n_fetch + w];
+    copy_bytes_wg(sk, dk, block_bytes);
+    copy_bytes_wg(sv, dv, block_bytes);
+    __syncthreads();  // every lane's share of K and V is written before the addresses publish
+    if (threadIdx.x == 0) {
+      __threadfence();
+      *reinterpret_cast<int64_t*>(pk) = dk;
+      *reinterpret_cast<int64_t*>(pv) = dv;
+    }
+  } else {
+    const int64_t base = (w - n_fetch) * kClearPerWg;
+    for (int64_t j = threadIdx.x; j < kClearPerWg; j += blockDim.x) {
+      const int64_t e = base + j;
+      if (e < n_clear) *reinterpret_cast<int64_t*>(desc[6 * n_fetch + e]) = 0;
+    }
+  }
+}
+
+// ---- K2: table range register / clear ------------------------------------------------------
+__global__ __launch_bounds__(128) void block_range_kernel(int64_t* table, int32_t* n_valid,
+                                                          int64_t heads, int64_t mb,
+                                                          int64_t first, int64_t n,
+                                                          int64_t k_base, int64_t v_base,
+                                                          int64_t head_stride, int64_t block_bytes,
+                                                          int64_t n_valid_value, int write_k,
+                                                          int write_v, int clear) {
+  const int64_t h = blockIdx.x;
+  const int64_t j = static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x;
+  if (j < n) {
+    const int64_t off = h * head_stride + j * block_bytes;
+    if (write_k) table[h * mb + first + j] = clear ? 0 : k_base + off;
+    if (write_v) table[(heads + h) * mb + first + j] = clear ? 0 : v_base + off;
+  }
+  if (blockIdx.y == 0 && threadIdx.x == 0 && n_valid_value >= 0)
+    n_valid[h] = static_cast<int32_t>(n_valid_value);
+}
+
+// ---- K3: dedup of selected (head, block) keys -----------------------------------------------
+constexpr int kDedupTile = 1024;
+constexpr int kDedupThreads = 256;
+constexpr int kDedupMaxTiles = 1 << 15;
+
+__global__ __launch_bounds__(256) void dedup_mark_kernel(const int32_t* __restrict__ ids,
+                                                         int64_t n, int32_t* __restrict__ stamp,
+                                                         int32_t epoch, int32_t mb, int32_t heads,
+                                                         int32_t t, int32_t bpc) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t bid = ids[e];
+    if (bid < 0 || bid >= mb) continue;
+    const int32_t h = static_cast<int32_t>((e / t) % heads);
+    const int32_t cid = bid / bpc, loc = bid - cid * bpc;
+    stamp[(static_cast<int64_t>(cid) * heads + h) * bpc + loc] = epoch;  // duplicates agree
+  }
+}
+
+// hits of one 1024-key tile; thread j owns keys 4j..4j+3
+__device__ __forceinline__ int tile_hits(const int32_t* stamp, int64_t key0, int64_t n_keys,
+                                         int32_t epoch, bool (&hit)[4]) {
+  int c = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t key = key0 + 4 * threadIdx.x + i;
+    hit[i] = key < n_keys && stamp[key] == epoch;
+    c += hit[i] ? 1 : 0;
+  }
+  return c;
+}
+
+// exclusive prefix of v over the workgroup (256 threads, wave64); returns the total via *total
+__device__ __forceinline__ int wg_exclusive_scan(int v, int* lds, int* total) {
+  const int lane = lane_id(), w = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const int y = __shfl_up(x, m, kWave);
+    if (lane >= m) x += y;
+  }
+  if (lane == kWave - 1) lds[w] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+  for (int i = 0; i < kDedupThreads / kWave; ++i) {
+    const int s = lds[i];
+    if (i < w) off += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + x - v;
+}
+
+__global__ __launch_bounds__(256) void dedup_count_kernel(const int32_t* __restrict__ stamp,
+                                                          int32_t* __restrict__ counts,
+                                                          int64_t n_keys, int32_t epoch) {
+  __shared__ int lds[kDedupThreads / kWave];
+  bool hit[4];
+  const int c = tile_hits(stamp, static_cast<int64_t>(blockIdx.x) * kDedupTile, n_keys, epoch, hit);
+  int total;
+  wg_exclusive_scan(c, lds, &total);
+  if (threadIdx.x == 0) counts[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(256) void dedup_scan_kernel(const int32_t* __restrict__ counts,
+                                                         int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ out, int n_tiles) {
+  __shared__ int lds[kDedupThreads / kWave];
+  const int per = (n_tiles + kDedupThreads - 1) / kDedupThreads;
+  const int b = threadIdx.x * per, e = min(b + per, n_tiles);
+  int s = 0;
+  for (int j = b; j < e; ++j) s += counts[j];
+  int total;
+  int run = wg_exclusive_scan(s, lds, &total);
+  for (int j = b; j < e; ++j) {
+    offsets[j] = run;
+    run += counts[j];
+  }
+  if (threadIdx.x == 0) out[0] = total;
+}
+
+__global__ __launch_bounds__(256) void dedup_compact_kernel(const int32_t* __restrict__ stamp,
+                                                            const int32_t* __restrict__ offsets,
+                                                            int32_t* __restrict__ out,
+                                                            int64_t n_keys, int64_t cap,
+                                                            int32_t epoch) {
+  __shared__ int lds[kDedupThreads / kWave];
+  bool hit[4];
+  const int64_t key0 = static_cast<int64_t>(blockIdx.x) * kDedupTile;
+  const int c = tile_hits(stamp, key0, n_keys, epoch, hit);
+  int total;
+  int pos = offsets[blockIdx.x] + wg_exclusive_scan(c, lds, &total);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (hit[i]) {
+      if (pos < cap) out[1 + pos] = static_cast<int32_t>(key0 + 4 * threadIdx.x + i);
+      ++pos;
+    }
+  }
+}
+
+int check_view_i32(const omm_view4* v, const char* what) {
+  OMM_REQUIRE(v != nullptr, OMM_EINVAL, "%s: null view", what);
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(v->size[i] >= 0 && v->stride[i] >= 0, OMM_EINVAL, "%s: negative size or stride", what);
+  return OMM_OK;
+}
+
+}  // namespace
+}  // namespace omm
+
+extern "C" int omm_build_ptr_table(const omm_view4* ids, const int64_t* base_k,
+                                   const int64_t* base_v, int64_t base_stride_h,
+                                   int64_t base_stride_c, int32_t max_chunks,
+                                   const int32_t* n_blocks_per_head, int64_t batch_stride,
+                                   int32_t blocks_per_chunk, int64_t in_chunk_block_bytes,
+                                   int64_t* ptr_k, int64_t* ptr_v, void* stream) {
+  using namespace omm;
+  int rc = check_view_i32(ids, "omm_build_ptr_table");
+  if (rc) return rc;
+  OMM_REQUIRE(blocks_per_chunk >= 0, OMM_EINVAL, "omm_build_ptr_table: blocks_per_chunk must be >= 0");
+  OMM_REQUIRE(blocks_per_chunk == 0 || in_chunk_block_bytes > 0, OMM_EINVAL,
+              "omm_build_ptr_table: in_chunk_block_bytes required for a chunk-level base table");
+  const int64_t total = ids->size[0] * ids->size[1] * ids->size[2] * ids->size[3];
+  if (total == 0) return OMM_OK;
+  OMM_REQUIRE(max_chunks > 0, OMM_EINVAL, "omm_build_ptr_table: empty base table");
+  OMM_REQUIRE(ids->data && base_k && base_v && n_blocks_per_head && ptr_k && ptr_v, OMM_EINVAL,
+              "omm_build_ptr_table: null pointer");
+  OMM_REQUIRE(ids->size[1] <= 2147483647ll && ids->size[2] <= 2147483647ll &&
+                  ids->size[3] <= 2147483647ll,
+              OMM_EUNSUPPORTED, "omm_build_ptr_table: dimension too large");
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(cdiv64(total, 256), 65535));
+  ptr_table_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const int32_t*>(ids->data), ids->stride[0], ids->stride[1], ids->stride[2],
+      ids->stride[3], base_k, base_v, base_stride_h, base_stride_c, max_chunks, n_blocks_per_head,
+      ptr_k, ptr_v, static_cast<int>(ids->size[1]), static_cast<int>(ids->size[2]),
+      static_cast<int>(ids->size[3]), batch_stride, blocks_per_chunk, in_chunk_block_bytes, total);
+  return check_launch("omm_build_ptr_table");
+}
+
+extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
+                                const omm_view4* v_new, int32_t cid, int32_t chunk_tokens,
+                                const omm_view4* k_cmp, int32_t epoch, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(kv != nullptr && k_new != nullptr && v_new != nullptr, OMM_EINVAL,
+              "omm_paged_append: null argument");
+  const int H = kv->num_heads, D = kv->head_dim, P = kv->page_tokens, ppc = kv->pages_per_chunk;
+  OMM_REQUIRE(kv->dtype == OMM_BF16 || kv->dtype == OMM_FP8E4M3, OMM_EINVAL,
+              "omm_paged_append: cache dtype must be bf16 or fp8e4m3");
+  OMM_REQUIRE(H >= 1 && D >= 8 && D <= 256 && D % 8 == 0 && P >= 1 && kv->chunk_len >= 1 &&
+                  ppc == cdiv64(kv->chunk_len, P),
+              OMM_EINVAL, "omm_paged_append: inconsistent cache geometry");
+  OMM_REQUIRE(cid >= 0 && cid < kv->max_chunks, OMM_EINVAL,
+              "omm_paged_append: chunk id %d outside [0, %d)", cid, kv->max_chunks);
+  OMM_REQUIRE(chunk_tokens >= 0 && chunk_tokens <= kv->chunk_len, OMM_EINVAL,
+              "omm_paged_append: %d tokens for a chunk of %d", chunk_tokens, kv->chunk_len);
+  for (const omm_view4* x : {k_new, v_new}) {
+    OMM_REQUIRE(x->size[0] == 1 && x->size[1] == chunk_tokens && x->size[2] == H &&
+                    x->size[3] == D,
+                OMM_EINVAL, "omm_paged_append: k_new / v_new must be [1, %d, %d, %d]", chunk_tokens,
+                H, D);
+    OMM_REQUIRE(x->stride[3] == 1 && x->stride[1] % 8 == 0 && x->stride[2] % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(x->data) & 15u) == 0,
+                OMM_EUNSUPPORTED,
+                "omm_paged_append: k_new / v_new need unit dim stride and 16-byte aligned rows");
+  }
+  OMM_REQUIRE(kv->pool_k && kv->pool_v && kv->unit_table, OMM_EINVAL, "omm_paged_append: null pool");
+  OMM_REQUIRE(kv->dtype == OMM_BF16 || (kv->scale_k && kv->scale_v), OMM_EINVAL,
+              "omm_paged_append: fp8 cache without scale arrays");
+  AppendArgs a{};
+  a.k = static_cast<const bf16_t*>(k_new->data);
+  a.v = static_cast<const bf16_t*>(v_new->data);
+  a.ks1 = k_new->stride[1]; a.ks2 = k_new->stride[2];
+  a.vs1 = v_new->stride[1]; a.vs2 = v_new->stride[2];
+  a.pool_k = kv->pool_k; a.pool_v = kv->pool_v;
+  a.scale_k = kv->scale_k; a.scale_v = kv->scale_v;
+  a.unit_table = kv->unit_table;
+  a.stamp = kv->stamp;
+  if (k_cmp != nullptr && k_cmp->data != nullptr) {
+    OMM_REQUIRE(k_cmp->size[0] == 1 && k_cmp->size[1] >= static_cast<int64_t>(cid + 1) * ppc &&
+                    k_cmp->size[2] == H && k_cmp->size[3] == D && k_cmp->stride[3] == 1 &&
+                    k_cmp->stride[1] % 8 == 0 && k_cmp->stride[2] % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(k_cmp->data) & 15u) == 0,
+                OMM_EINVAL,
+                "omm_paged_append: k_cmp must be a 16-byte aligned [1, >= %lld, %d, %d] bf16 view",
+                (long long)(cid + 1) * ppc, H, D);
+    a.k_cmp = static_cast<bf16_t*>(const_cast<void*>(k_cmp->data));
+    a.cs1 = k_cmp->stride[1]; a.cs2 = k_cmp->stride[2];
+  }
+  a.H = H; a.D = D; a.P = P; a.ppc = ppc; a.max_chunks = kv->max_chunks; a.cid = cid;
+  a.tokens = chunk_tokens;
+  a.lph = D / 8;
+  a.epoch = epoch;
+  // lanes per head must divide the wave
+  OMM_REQUIRE(kWave % a.lph == 0, OMM_EUNSUPPORTED, "omm_paged_append: head dim %d", D);
+  const dim3 grid(static_cast<unsigned>(ppc), static_cast<unsigned>(cdiv64(H, kWave / a.lph)));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kv->dtype == OMM_BF16)
+    paged_append_kernel<false><<<grid, kWave, 0, s>>>(a);
+  else
+    paged_append_kernel<true><<<grid, kWave, 0, s>>>(a);
+  return check_launch("omm_paged_append");
+}
+
+extern "C" int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
+                              const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
+                              const int32_t* src_slot, const int32_t* dst_slot, int32_t n,
+                              int64_t unit_bytes, int64_t scale_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(n >= 0 && unit_bytes > 0 && unit_bytes % 16 == 0 && scale_bytes >= 0, OMM_EINVAL,
+              "omm_copy_units: n >= 0 and unit_bytes a positive multiple of 16 required");
+  if (n == 0) return OMM_OK;
+  OMM_REQUIRE(src_k && dst_k && src_slot && dst_slot, OMM_EINVAL, "omm_copy_units: null pointer");
+  OMM_REQUIRE((src_v == nullptr) == (dst_v == nullptr) && (src_sk == nullptr) == (dst_sk == nullptr) &&
+                  (src_sv == nullptr) == (dst_sv == nullptr),
+              OMM_EINVAL, "omm_copy_units: source and destination pairs must both be given");
+  for (const void* p : {src_k, static_cast<const void*>(dst_k), src_v, static_cast<const void*>(dst_v)})
+    OMM_REQUIRE((reinterpret_cast<uintptr_t>(p) & 15u) == 0, OMM_EINVAL,
+                "omm_copy_units: pools must be 16-byte aligned");
+  CopyArgs a{static_cast<const unsigned char*>(src_k), static_cast<unsigned char*>(dst_k),
+             static_cast<const unsigned char*>(src_v), static_cast<unsigned char*>(dst_v),
+             static_cast<const unsigned char*>(src_sk), static_cast<unsigned char*>(dst_sk),
+             static_cast<const unsigned char*>(src_sv), static_cast<unsigned char*>(dst_sv),
+             src_slot, dst_slot, unit_bytes, scale_bytes};
+  const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>(cdiv64(unit_bytes, kCopyPart)));
+  copy_units_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("omm_copy_units");
+}
+
+extern "C" int omm_gather_publish_clear(const int64_t* desc, int64_t n_fetch, int64_t n_clear,
+                                        int64_t block_bytes, int64_t* ctas, void* stream) {
+  using namespace omm;
+  if (ctas != nullptr) *ctas = 0;
+  if (n_fetch == 0 && n_clear == 0) return OMM_OK;
+  OMM_REQUIRE(n_fetch >= 0 && n_clear >= 0, OMM_EINVAL,
+              "omm_gather_publish_clear: n_fetch=%lld / n_clear=%lld must be >= 0",
+              (long long)n_fetch, (long long)n_clear);
+  OMM_REQUIRE(desc != nullptr, OMM_EINVAL, "omm_gather_publish_clear: null descriptor");
+  OMM_REQUIRE(block_bytes > 0 && block_bytes % 2 == 0, OMM_EINVAL,
+              "omm_gather_publish_clear: block_bytes=%lld must be a positive multiple of 2",
+              (long long)block_bytes);
+  const int64_t wgs = n_fetch + cdiv64(n_clear, kClearPerWg);
+  OMM_REQUIRE(wgs <= 2147483647ll, OMM_EUNSUPPORTED, "omm_gather_publish_clear: grid too large");
+  gather_publish_clear_kernel<<<static_cast<unsigned>(wgs), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      desc, n_fetch, n_clear, block_bytes);
+  const int rc = check_launch("omm_gather_publish_clear");
+  if (rc == OMM_OK && ctas != nullptr) *ctas = wgs;
+  return rc;
+}
+
+extern "C" int omm_block_range(int64_t* table, int32_t* n_valid, int64_t heads, int64_t mb,
+                               int64_t first_bid, int64_t n_blocks, int64_t k_base,
+                               int64_t v_base, int64_t head_stride_bytes, int64_t block_bytes,
+                               int64_t n_valid_value, int32_t write_k, int32_t write_v,
+                               int32_t clear, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(table != nullptr && n_valid != nullptr && heads > 0 && mb > 0, OMM_EINVAL,
+              "omm_block_range: null table or empty geometry");
+  OMM_REQUIRE(n_blocks > 0 && first_bid >= 0 && first_bid + n_blocks <= mb, OMM_EINVAL,
+              "omm_block_range: block range [%lld, %lld) outside [0, %lld)", (long long)first_bid,
+              (long long)(first_bid + n_blocks), (long long)mb);
+  OMM_REQUIRE(n_valid_value <= 2147483647ll, OMM_EINVAL, "omm_block_range: n_valid_value too large");
+  if (!clear) {
+    OMM_REQUIRE(write_k || write_v, OMM_EINVAL, "omm_block_range: nothing to register");
+    OMM_REQUIRE(!write_k || k_base != 0, OMM_EINVAL, "omm_block_range: write_k with k_base == 0");
+    OMM_REQUIRE(!write_v || v_base != 0, OMM_EINVAL, "omm_block_range: write_v with v_base == 0");
+  }
+  const int64_t tiles = cdiv64(n_blocks, 128);
+  OMM_REQUIRE(tiles <= 65535 && heads <= 2147483647ll, OMM_EUNSUPPORTED,
+              "omm_block_range: %lld blocks exceed the grid", (long long)n_blocks);
+  const dim3 grid(static_cast<unsigned>(heads), static_cast<unsigned>(tiles));
+  block_range_kernel<<<grid, 128, 0, static_cast<hipStream_t>(stream)>>>(
+      table, n_valid, heads, mb, first_bid, n_blocks, k_base, v_base, head_stride_bytes,
+      block_bytes, n_valid_value, write_k != 0, write_v != 0, clear != 0);
+  return check_launch("omm_block_range");
+}
+
+extern "C" int omm_dedup_run(const int32_t* block_indices, int64_t n_entries, int32_t* stamp,
+                             int32_t* counts, int32_t* offsets, int32_t* out, int64_t epoch,
+                             int64_t mb, int64_t heads, int64_t t, int64_t bpc, int64_t cap,
+                             void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(mb > 0 && heads > 0 && t > 0 && bpc > 0 && mb % bpc == 0, OMM_EINVAL,
+              "omm_dedup_run: need positive mb/heads/t/bpc with bpc | mb (mb=%lld heads=%lld t=%lld "
+              "bpc=%lld)", (long long)mb, (long long)heads, (long long)t, (long long)bpc);
+  const int64_t n_keys = heads * mb;
+  OMM_REQUIRE(n_keys <= 2147483647ll, OMM_EINVAL, "omm_dedup_run: %lld keys do not fit int32",
+              (long long)n_keys);
+  const int64_t n_tiles = cdiv64(n_keys, kDedupTile);
+  OMM_REQUIRE(n_tiles <= kDedupMaxTiles, OMM_EUNSUPPORTED, "omm_dedup_run: %lld tiles", (long long)n_tiles);
+  OMM_REQUIRE(epoch >= 1 && epoch <= 2147483647ll && cap >= 0, OMM_EINVAL,
+              "omm_dedup_run: epoch must be in [1, INT32_MAX] and cap >= 0");
+  OMM_REQUIRE(n_entries >= 0 && n_entries <= 2147483647ll, OMM_EINVAL,
+              "omm_dedup_run: n_entries out of range");
+  OMM_REQUIRE(stamp && counts && offsets && out && (n_entries == 0 || block_indices), OMM_EINVAL,
+              "omm_dedup_run: null pointer");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned mark = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(cdiv64(n_entries, 256), 1), 8192));
+  dedup_mark_kernel<<<mark, 256, 0, s>>>(block_indices, n_entries, stamp, static_cast<int32_t>(epoch),
+                                         static_cast<int32_t>(mb), static_cast<int32_t>(heads),
+                                         static_cast<int32_t>(t), static_cast<int32_t>(bpc));
+  int rc = check_launch("omm_dedup_run mark");
+  if (rc) return rc;
+  dedup_count_kernel<<<static_cast<unsigned>(n_tiles), kDedupThreads, 0, s>>>(stamp, counts, n_keys,
+                                                                              static_cast<int32_t>(epoch));
+  rc = check_launch("omm_dedup_run count");
+  if (rc) return rc;
+  dedup_scan_kernel<<<1, kDedupThreads, 0, s>>>(counts, offsets, out, static_cast<int>(n_tiles));
+  rc = check_launch("omm_dedup_run scan");
+  if (rc) return rc;
+  dedup_compact_kernel<<<static_cast<unsigned>(n_tiles), kDedupThreads, 0, s>>>(
+      stamp, offsets, out, n_keys, cap, static_cast<int32_t>(epoch));
+  return check_launch("omm_dedup_run compact");
+}
