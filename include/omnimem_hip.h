@@ -22,6 +22,15 @@
  *                              selection_fwd.cu:934-966)
  *   omm_sel_fwd_ptr         <- torch.ops.omnimem_nsa.sel_fwd_ptr (bindings.cpp:20-23,
  *                              selection_fwd.cu:968-992)
+ *   omm_build_ptr_table     <- torch.ops.omnimem_nsa.build_ptr_table (bindings.cpp:12-15,
+ *                              ptr_table.cu:59-127)
+ *   omm_paged_append        <- MMCache.update_cache chunk_per_head branch (models/cache.py:478-502)
+ *                              fused with the K / V block compression
+ *                              (causal_wan_nsa_model.py:479-490)
+ *   omm_copy_units          <- flush_offload D2H (models/cache.py:1086-1117) and the reload H2D
+ *                              (nsa/ops/selection/padded_ptr/wrapper.py:342-361)
+ *   omm_gather_publish_clear, omm_block_range, omm_dedup_run
+ *                           <- block-KV K1 / K2 / K3 (cuda_backend/csrc/block_kv_ops.h:12-31)
  *   omm_sel_fwd_paged       <- selection_attention_padded_ptr_fast
  *                              (nsa/ops/selection/padded_ptr/wrapper.py:458-553) over the paged
  *                              cache, with int32 unit slots instead of raw int64 addresses
@@ -85,18 +94,20 @@ typedef struct omm_topk_mask {
 
 /* Paged block KV cache of one layer.  A unit is one (head, chunk): pages_per_chunk pages of
  * page_tokens tokens x head_dim, stored contiguously at slot s of pool_k / pool_v.  Units not
- * resident in HBM live in a pinned host pool (zero-copy readable by the device). */
+ * resident in HBM live in a pinned host pool that the device reads directly.  The pools may be
+ * shared by all layers (slots are global); unit_table and stamp are per layer. */
 typedef struct omm_paged_kv {
   void* pool_k;               /* [n_slots][pages_per_chunk][page_tokens][head_dim] */
   void* pool_v;
-  float* scale_k;             /* fp8 only: [n_slots][pages_per_chunk] dequant scales */
+  float* scale_k;             /* fp8 only: [n_slots][pages_per_chunk] dequantisation scales */
   float* scale_v;
-  const void* host_k;         /* device-visible pinned host pool, same unit layout */
-  const void* host_v;
-  const float* host_scale_k;
-  const float* host_scale_v;
+  void* host_k;               /* device address of the pinned host pool, same unit layout */
+  void* host_v;
+  float* host_scale_k;        /* fp8 only: [n_host_slots][pages_per_chunk] */
+  float* host_scale_v;
   const int32_t* unit_table;  /* [num_heads][max_chunks]: s >= 0 HBM slot; s <= -2 host slot
                                  (-2 - s); -1 never written */
+  int32_t* stamp;             /* [num_heads][max_chunks] epoch of the last touch, or NULL */
   int32_t num_heads;
   int32_t max_chunks;
   int32_t n_chunks;           /* chunks 0 .. n_chunks-1 are readable */
@@ -163,6 +174,15 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 float* lse, void* stream);
 
 /* ---- pointer-table selection (a6, reference address contract) ------------------------ */
+/* ptr_x[b,g,h,t] = base_x[h, cid] + b*batch_stride + (bid % bpc)*in_chunk_block_bytes with
+ * cid = bid / bpc (bpc > 0) or bid (bpc == 0); 0 when bid < 0, bid >= n_blocks_per_head[h],
+ * cid >= max_chunks or base == 0.  ids: int32 [B, MG, H, T]; base_x: int64 byte addresses with
+ * element strides base_stride_h / base_stride_c; ptr_k / ptr_v: int64 contiguous [B, MG, H, T]. */
+int omm_build_ptr_table(const omm_view4* ids, const int64_t* base_k, const int64_t* base_v,
+                        int64_t base_stride_h, int64_t base_stride_c, int32_t max_chunks,
+                        const int32_t* n_blocks_per_head, int64_t batch_stride,
+                        int32_t blocks_per_chunk, int64_t in_chunk_block_bytes, int64_t* ptr_k,
+                        int64_t* ptr_v, void* stream);
 /* bf16 only.  ptr tables: int64 [B, MG, H, T] with element strides ptr_stride; a block is
  * block_size full rows at (address + r*stride_bn + d*stride_bd) elements; 0 = skip. */
 int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr_v,
@@ -171,12 +191,62 @@ int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr
                     float* lse, void* stream);
 
 /* ---- paged block KV cache (a7) ------------------------------------------------------- */
+/* Write chunk cid of every head from k_new / v_new (bf16 [1, chunk_tokens, H, D], unit dim
+ * stride, 16-byte aligned rows; chunk_tokens <= chunk_len) into the units unit_table[h][cid]
+ * (HBM slots; units whose entry is < 0 are skipped).  Page slots past chunk_tokens are zeroed.
+ * bf16 cache: bytes copied.  fp8 cache: per (page, head) scale = amax/448 (1 when amax == 0),
+ * code = e4m3(clamp(x * (448/amax), +-448)), round to nearest even.  With k_cmp (bf16
+ * [1, >= (cid+1)*pages_per_chunk, H, D]) row cid*pages_per_chunk + p receives the mean of page
+ * p's keys (omm_block_pool arithmetic over its valid tokens; 0 for a page with none), and
+ * v_cmp the same for the values (both optional).  With kv->stamp and epoch > 0,
+ * stamp[h][cid] = epoch.
+ * Reference: MMCache.update_cache, chunk_per_head branch (models/cache.py:478-502) and the K
+ * block compression of causal_wan_nsa_model.py:479-484. */
+int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_view4* v_new,
+                     int32_t cid, int32_t chunk_tokens, const omm_view4* k_cmp,
+                     const omm_view4* v_cmp, int32_t epoch, void* stream);
 /* Selection attention over the cache, non-causal.  q: bf16 [1, M, H, D]; ids: int32
  * [1, MG, H, T] of chunk-aligned page ids (page p of chunk c is id c*pages_per_chunk + p,
- * with min(page_tokens, chunk_len - p*page_tokens) valid tokens). */
+ * with min(page_tokens, chunk_len - p*page_tokens) valid tokens); ids outside the readable
+ * chunks or of units never written are skipped.  With kv->stamp and epoch > 0 every unit read
+ * gets stamp = epoch (the LRU touch of the reference's _touch_lru_and_detect_missing,
+ * nsa/ops/selection/padded_ptr/wrapper.py:253-291, without its host synchronisation). */
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
-                      void* stream);
+                      int32_t epoch, void* stream);
+/* Batched unit copies: for i < n copy unit_bytes from src_k + src_slot[i]*unit_bytes to
+ * dst_k + dst_slot[i]*unit_bytes (either side may be the mapped host pool), the same for the
+ * optional V pair and the optional scale pairs (scale_bytes per unit).  src_slot / dst_slot are
+ * device int32 arrays; entries outside [0, n_src_slots) / [0, n_dst_slots) are skipped.  Reference: flush_offload's D2H copies (models/cache.py:1086-1117) and
+ * the reload H2D of wrapper.py:342-361, as one launch. */
+int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
+                   const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
+                   const int32_t* src_slot, const int32_t* dst_slot, int32_t n,
+                   int32_t n_src_slots, int32_t n_dst_slots, int64_t unit_bytes,
+                   int64_t scale_bytes, void* stream);
+
+/* ---- reference block-store kernels (K1 / K2 / K3) ------------------------------------ */
+/* K1 (cuda_backend/csrc/block_kv_ops.h:12-16, block_kv_gather.cu:14-45): desc is int64
+ * [6*n_fetch + n_clear], SoA [src_k|src_v|dst_k|dst_v|pub_k|pub_v] x n_fetch then the clear
+ * addresses.  Copies block_bytes from src to dst (K and V), then stores dst into *pub; zeroes
+ * the int64 at each clear address.  *ctas receives the workgroups launched. */
+int omm_gather_publish_clear(const int64_t* desc, int64_t n_fetch, int64_t n_clear,
+                             int64_t block_bytes, int64_t* ctas, void* stream);
+/* K2 (block_kv_ops.h:18-23, block_kv_range.cu:13-37): table int64 contiguous [2, heads, mb];
+ * table[x][h][first_bid + j] = base_x + h*head_stride_bytes + j*block_bytes (0 when clear) for
+ * j < n_blocks; n_valid[h] = n_valid_value when >= 0. */
+int omm_block_range(int64_t* table, int32_t* n_valid, int64_t heads, int64_t mb,
+                    int64_t first_bid, int64_t n_blocks, int64_t k_base, int64_t v_base,
+                    int64_t head_stride_bytes, int64_t block_bytes, int64_t n_valid_value,
+                    int32_t write_k, int32_t write_v, int32_t clear, void* stream);
+/* K3 (block_kv_ops.h:25-31, block_kv_dedup.cu:16-206): entry e of the flattened [B, MG, H, t]
+ * block_indices with 0 <= bid < mb is head h = (e / t) % heads and key (cid*heads + h)*bpc +
+ * loc for bid = cid*bpc + loc.  out[0] = number of distinct keys, out[1..] the distinct keys
+ * ascending (at most cap written).  stamp: int32 [heads*mb], persistent between calls (epochs
+ * must differ); counts / offsets: int32 [>= ceil(heads*mb / 1024)]. */
+int omm_dedup_run(const int32_t* block_indices, int64_t n_entries, int32_t* stamp,
+                  int32_t* counts, int32_t* offsets, int32_t* out, int64_t epoch, int64_t mb,
+                  int64_t heads, int64_t t, int64_t bpc, int64_t cap, void* stream);
 
 #ifdef __cplusplus
 }

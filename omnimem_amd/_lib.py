@@ -41,7 +41,7 @@ class PagedKV(ctypes.Structure):
         ("scale_k", ctypes.c_void_p), ("scale_v", ctypes.c_void_p),
         ("host_k", ctypes.c_void_p), ("host_v", ctypes.c_void_p),
         ("host_scale_k", ctypes.c_void_p), ("host_scale_v", ctypes.c_void_p),
-        ("unit_table", ctypes.c_void_p),
+        ("unit_table", ctypes.c_void_p), ("stamp", ctypes.c_void_p),
         ("num_heads", ctypes.c_int32), ("max_chunks", ctypes.c_int32),
         ("n_chunks", ctypes.c_int32), ("chunk_len", ctypes.c_int32),
         ("page_tokens", ctypes.c_int32), ("pages_per_chunk", ctypes.c_int32),
@@ -70,7 +70,17 @@ PROTOTYPES = {
     "omm_sel_fwd": (_i32, [_V, _V, _V, _V, _i32, _i32, _i32, _i32, _i32, _f32, _V, _vp, _vp]),
     "omm_sel_fwd_ptr": (_i32, [_V, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _f32, _V, _vp,
                                _vp]),
-    "omm_sel_fwd_paged": (_i32, [_V, _V, _P, _i32, _f32, _V, _vp, _vp]),
+    "omm_build_ptr_table": (_i32, [_V, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _i64, _vp,
+                                   _vp, _vp]),
+    "omm_paged_append": (_i32, [_P, _V, _V, _i32, _i32, _V, _V, _i32, _vp]),
+    "omm_sel_fwd_paged": (_i32, [_V, _V, _P, _i32, _f32, _V, _vp, _i32, _vp]),
+    "omm_copy_units": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                              _i64, _i64, _vp]),
+    "omm_gather_publish_clear": (_i32, [_vp, _i64, _i64, _i64, ctypes.POINTER(_i64), _vp]),
+    "omm_block_range": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                               _i32, _i32, _i32, _vp]),
+    "omm_dedup_run": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _vp]),
 }
 
 _lib = None

@@ -1,0 +1,495 @@
+"""Paged block KV cache for the NSA selection path (HBM pool + pinned host pool, LRU by bytes).
+
+Reference: ``MMCache`` (src/omnimem/models/cache.py:7-1149), chunk_per_head storage
+(:478-502), ptr tables (:227-347), LRU (:646-741), offload (:970-1142) and the reload path of
+``_touch_lru_and_detect_missing`` (nsa/ops/selection/padded_ptr/wrapper.py:253-362).
+
+Layout.  A *unit* is one (layer, head, chunk): ``pages_per_chunk`` pages of ``page_tokens``
+tokens x ``head_dim`` values, contiguous (chunk-aligned pages; the last page of a 4680-token chunk
+holds 8 valid tokens when pages are 64 tokens).  Units live in one HBM pool shared by every layer
+(``hbm_slots`` units each for K and V) or in a device-mapped pinned host pool that the attention
+kernel reads directly, so a unit that is not in HBM is never a miss that stalls the stream: it is
+read over the host link page by page.  ``unit_table[layer]`` (int32 [H, max_chunks], on the
+device) maps a unit to its slot: s >= 0 HBM, s <= -2 host slot -2-s, -1 never written.
+
+Recency.  Every append and every selection call stamps the units it touches with an epoch on the
+device (no host synchronisation, unlike the reference's ``unique().cpu()`` per call).  At a chunk
+boundary ``flush()`` reads the stamps once, ranks units by (epoch, chunk id) -- the order in which
+the reference's OrderedDict LRU sees them -- and moves units between the pools in one batched
+copy: the most recent units stay in HBM up to ``lru_max_size`` units per (layer, head) (the
+reference's count) or up to the HBM budget (bytes); sink and window chunks always stay.
+
+Streams.  Every method enqueues on the current stream of ``device``; use one stream per cache.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .backend import BlockKVBackendError
+
+__all__ = ["PagedKVCache"]
+
+
+class _HostPool:
+    """Pinned, device-mapped host memory (omm_host_alloc), viewable from torch on the CPU."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.host = ctypes.c_void_p()
+        self.dev = ctypes.c_void_p()
+        if self.nbytes:
+            _lib.call("omm_host_alloc", self.nbytes, ctypes.byref(self.host), ctypes.byref(self.dev),
+                      error=BlockKVBackendError)
+
+    @property
+    def dev_ptr(self) -> int:
+        return int(self.dev.value or 0)
+
+    def cpu_view(self) -> torch.Tensor:
+        if not self.nbytes:
+            return torch.empty(0, dtype=torch.uint8)
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(self.host.value)
+        return torch.frombuffer(buf, dtype=torch.uint8)
+
+    def free(self):
+        if self.host.value:
+            _lib.call("omm_host_free", self.host, error=BlockKVBackendError)
+            self.host = ctypes.c_void_p()
+            self.dev = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class PagedKVCache:
+    """HBM + host paged KV cache of ``num_layers`` layers (see the module docstring).
+
+    dtype: ``torch.bfloat16`` or ``"fp8"`` (OCP e4m3fn codes with one fp32 scale per
+    (page, head) for K and for V).  Capacity: ``hbm_slots`` units per pool, or derived from
+    ``hbm_budget_bytes`` (K + V + scales).  ``host_slots`` defaults to every unit that can exist
+    minus the HBM slots.
+    """
+
+    def __init__(self, num_layers: int, num_heads: int, head_dim: int, max_chunks: int,
+                 chunk_len: int = 4680, page_tokens: int = 64, dtype=torch.bfloat16,
+                 hbm_budget_bytes: Optional[int] = None, hbm_slots: Optional[int] = None,
+                 host_slots: Optional[int] = None, lru_max_size: int = 0,
+                 window_chunks: int = 3, sink_chunks: int = 0, keep_window_kv: bool = True,
+                 device="cuda"):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise BlockKVBackendError("PagedKVCache lives on a GPU")
+        self.L, self.H, self.D = int(num_layers), int(num_heads), int(head_dim)
+        self.max_chunks = int(max_chunks)
+        self.chunk_len, self.P = int(chunk_len), int(page_tokens)
+        self.ppc = -(-self.chunk_len // self.P)
+        self.fp8 = dtype == "fp8" or dtype == torch.float8_e4m3fn
+        if not self.fp8 and dtype != torch.bfloat16:
+            raise BlockKVBackendError(f"cache dtype must be bfloat16 or fp8, got {dtype}")
+        self.elem = 1 if self.fp8 else 2
+        self.unit_elems = self.ppc * self.P * self.D
+        self.unit_bytes = self.unit_elems * self.elem
+        self.scale_bytes = self.ppc * 4 if self.fp8 else 0
+        per_slot = 2 * (self.unit_bytes + self.scale_bytes)
+        total_units = self.L * self.H * self.max_chunks
+        if hbm_slots is None:
+            if hbm_budget_bytes is None:
+                hbm_slots = total_units
+            else:
+                hbm_slots = int(hbm_budget_bytes) // per_slot
+        self.n_slots = int(min(hbm_slots, total_units))
+        if self.n_slots < self.L * self.H:
+            raise BlockKVBackendError(
+                f"HBM pool of {self.n_slots} units cannot hold one chunk of every layer and head "
+                f"({self.L * self.H} units)")
+        if host_slots is None:
+            host_slots = total_units - self.n_slots
+        self.n_host = int(host_slots)
+        self.hbm_budget_bytes = self.n_slots * per_slot
+        self.lru_max_size = int(lru_max_size)
+        self.window, self.sink = int(window_chunks), int(sink_chunks)
+
+        store = torch.uint8 if self.fp8 else torch.bfloat16
+        shape = (self.n_slots, self.ppc, self.P, self.D)
+        self.pool_k = torch.zeros(shape, dtype=store, device=self.device)
+        self.pool_v = torch.zeros(shape, dtype=store, device=self.device)
+        if self.fp8:
+            self.scale_k = torch.ones((self.n_slots, self.ppc), dtype=torch.float32, device=self.device)
+            self.scale_v = torch.ones_like(self.scale_k)
+        else:
+            self.scale_k = self.scale_v = None
+        self._host_k = _HostPool(self.n_host * self.unit_bytes)
+        self._host_v = _HostPool(self.n_host * self.unit_bytes)
+        self._host_sk = _HostPool(self.n_host * self.scale_bytes)
+        self._host_sv = _HostPool(self.n_host * self.scale_bytes)
+
+        H, MC = self.H, self.max_chunks
+        self.unit_table = [torch.full((H, MC), -1, dtype=torch.int32, device=self.device)
+                           for _ in range(self.L)]
+        self.stamp = [torch.zeros((H, MC), dtype=torch.int32, device=self.device)
+                      for _ in range(self.L)]
+        ncb = MC * self.ppc
+        self.k_cmp = [torch.zeros((1, ncb, H, self.D), dtype=torch.bfloat16, device=self.device)
+                      for _ in range(self.L)]
+        self.v_cmp = [torch.zeros_like(self.k_cmp[0]) for _ in range(self.L)]
+        self.keep_window_kv = bool(keep_window_kv) and self.window > 0
+        if self.keep_window_kv:
+            wshape = (self.window, self.chunk_len, H, self.D)
+            self.win_k = [torch.zeros(wshape, dtype=torch.bfloat16, device=self.device)
+                          for _ in range(self.L)]
+            self.win_v = [torch.zeros_like(self.win_k[0]) for _ in range(self.L)]
+        self._table_h = np.full((self.L, H, MC), -1, dtype=np.int32)
+        self._stage = torch.empty((H, MC), dtype=torch.int32).pin_memory()
+        self.n_chunks = [0] * self.L
+        self._epoch = 0
+        self._flush_epoch = 0
+        self._staged_k: Dict[int, Tuple[torch.Tensor, int]] = {}
+        self.reset()
+
+    # ---------------------------------------------------------------- bookkeeping
+    def reset(self):
+        """Forget every chunk (pools keep their memory), as MMCache.reset (models/cache.py:771)."""
+        self._free_hbm = list(range(self.n_slots - 1, -1, -1))
+        self._free_host = list(range(self.n_host - 1, -1, -1))
+        self._table_h.fill(-1)
+        for l in range(self.L):
+            self.unit_table[l].fill_(-1)
+            self.stamp[l].zero_()
+        self.n_chunks = [0] * self.L
+        self._staged_k.clear()
+        self._epoch = 0
+        self._flush_epoch = 0
+        self.stats = {"hits": 0, "misses": 0, "evicted_units": 0, "promoted_units": 0,
+                      "evicted_bytes": 0, "promoted_bytes": 0, "flushes": 0}
+
+    def next_epoch(self) -> int:
+        self._epoch += 1
+        if self._epoch >= 2 ** 31 - 1:
+            raise BlockKVBackendError("epoch counter exhausted; call reset()")
+        return self._epoch
+
+    def _upload_table(self, layer: int):
+        self._stage.copy_(torch.from_numpy(self._table_h[layer]))
+        self.unit_table[layer].copy_(self._stage, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()  # the staging buffer is reused
+
+    def layer_view(self, layer: int) -> _lib.PagedKV:
+        """The omm_paged_kv struct of one layer."""
+        kv = _lib.PagedKV()
+        kv.pool_k, kv.pool_v = self.pool_k.data_ptr(), self.pool_v.data_ptr()
+        if self.fp8:
+            kv.scale_k, kv.scale_v = self.scale_k.data_ptr(), self.scale_v.data_ptr()
+            kv.host_scale_k, kv.host_scale_v = self._host_sk.dev_ptr, self._host_sv.dev_ptr
+        kv.host_k, kv.host_v = self._host_k.dev_ptr, self._host_v.dev_ptr
+        kv.unit_table = self.unit_table[layer].data_ptr()
+        kv.stamp = self.stamp[layer].data_ptr()
+        kv.num_heads, kv.max_chunks, kv.n_chunks = self.H, self.max_chunks, self.n_chunks[layer]
+        kv.chunk_len, kv.page_tokens, kv.pages_per_chunk = self.chunk_len, self.P, self.ppc
+        kv.head_dim = self.D
+        kv.dtype = _lib.OMM_FP8E4M3 if self.fp8 else _lib.OMM_BF16
+        kv.n_slots, kv.n_host_slots = self.n_slots, self.n_host
+        return kv
+
+    # ---------------------------------------------------------------- append
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, cid: int):
+        """Write chunk ``cid`` (k, v: bf16 [1, S, H, D], S <= chunk_len) of one layer.
+
+        Rewriting a chunk (the reference's 4 denoise + 1 context forwards per AR chunk) reuses its
+        units.  Also writes the pooled keys / values of its pages (``k_cmp`` / ``v_cmp``)."""
+        _lib.require_cuda((k, "k"), (v, "v"))
+        if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise BlockKVBackendError("append expects bf16 keys and values")
+        if not (0 <= cid < self.max_chunks):
+            raise BlockKVBackendError(f"chunk id {cid} outside [0, {self.max_chunks})")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != 1 or k.shape[2:] != (self.H, self.D):
+            raise BlockKVBackendError(f"k / v must be [1, S, {self.H}, {self.D}], got "
+                                      f"{tuple(k.shape)} / {tuple(v.shape)}")
+        S = k.shape[1]
+        if S > self.chunk_len:
+            raise BlockKVBackendError(f"{S} tokens exceed the chunk length {self.chunk_len}")
+        if k.stride(3) != 1 or k.stride(1) % 8 or k.stride(2) % 8 or k.data_ptr() % 16:
+            k = k.contiguous()
+        if v.stride(3) != 1 or v.stride(1) % 8 or v.stride(2) % 8 or v.data_ptr() % 16:
+            v = v.contiguous()
+        row = self._table_h[layer, :, cid]
+        if (row < 0).any():
+            need = int((row < 0).sum())
+            if len(self._free_hbm) < need:
+                self._make_room(need)
+            changed = False
+            for h in np.nonzero(row < 0)[0]:
+                if row[h] <= -2:  # host-resident unit being rewritten: bring it home
+                    self._free_host.append(-2 - int(row[h]))
+                row[h] = self._free_hbm.pop()
+                changed = True
+            if changed:
+                self._upload_table(layer)
+        self.n_chunks[layer] = max(self.n_chunks[layer], cid + 1)
+        kv = self.layer_view(layer)
+        _lib.call("omm_paged_append", ctypes.byref(kv), _lib.view4(k), _lib.view4(v), int(cid),
+                  int(S), _lib.view4(self.k_cmp[layer]), _lib.view4(self.v_cmp[layer]),
+                  self.next_epoch(), _lib.stream_of(k), error=BlockKVBackendError)
+        if self.keep_window_kv:
+            w = cid % self.window
+            self.win_k[layer][w, :S].copy_(k[0])
+            self.win_v[layer][w, :S].copy_(v[0])
+
+    def update_cache(self, name: str, hidden_state: torch.Tensor, layer_idx: int, start_id: int):
+        """MMCache-compatible entry (models/cache.py:439): 'k_cache' stages the keys, 'v_cache'
+        commits the chunk; both return the window ([1, tokens, H, D]) like the reference's
+        chunk_per_head branch."""
+        cid = int(start_id) // self.chunk_len
+        if name == "k_cache":
+            self._staged_k[layer_idx] = (hidden_state, cid)
+            if self.keep_window_kv:
+                self.win_k[layer_idx][cid % self.window, :hidden_state.shape[1]].copy_(hidden_state[0])
+                return self.window_kv(layer_idx, upto=cid + 1)[0]
+            return hidden_state
+        if name == "v_cache":
+            if layer_idx not in self._staged_k or self._staged_k[layer_idx][1] != cid:
+                raise BlockKVBackendError("update_cache('v_cache') needs the matching 'k_cache' first")
+            k, _ = self._staged_k.pop(layer_idx)
+            self.append(layer_idx, k, hidden_state, cid)
+            if self.keep_window_kv:
+                return self.window_kv(layer_idx)[1]
+            return hidden_state
+        raise BlockKVBackendError(f"unknown cache name {name!r} (expected 'k_cache' or 'v_cache')")
+
+    def window_kv(self, layer: int, upto: Optional[int] = None):
+        """K and V of the last ``window_chunks`` chunks as [1, tokens, H, D] (chunk order need not
+        be ascending: attention over the window is permutation invariant)."""
+        if not self.keep_window_kv:
+            raise BlockKVBackendError("window K/V are not kept (keep_window_kv=False)")
+        n = self.n_chunks[layer] if upto is None else upto
+        w = min(n, self.window)
+        L = self.chunk_len
+        return (self.win_k[layer][:w].reshape(1, w * L, self.H, self.D),
+                self.win_v[layer][:w].reshape(1, w * L, self.H, self.D))
+
+    def cmp_history(self, layer: int):
+        """Pooled keys / values of every page written so far: [1, n_chunks*ppc, H, D] each."""
+        n = self.n_chunks[layer] * self.ppc
+        return self.k_cmp[layer][:, :n], self.v_cmp[layer][:, :n]
+
+    # ---------------------------------------------------------------- selection
+    def select(self, q: torch.Tensor, block_indices: torch.Tensor, layer: int, group_size: int,
+               softmax_scale: Optional[float] = None, return_lse: bool = False,
+               out: Optional[torch.Tensor] = None):
+        """Selection attention of q (bf16 [1, M, H, D]) over the pages listed in block_indices
+        (int32 [1, ceil(M/G), H, T], page id = chunk * pages_per_chunk + page)."""
+        _lib.require_cuda((q, "q"), (block_indices, "block_indices"))
+        if q.dtype != torch.bfloat16:
+            raise BlockKVBackendError(f"paged selection needs bf16 queries, got {q.dtype}")
+        if block_indices.dtype != torch.int32:
+            block_indices = block_indices.to(torch.int32)
+        B, M, H, D = q.shape
+        scale = softmax_scale if softmax_scale is not None else D ** -0.5
+        if out is None:
+            out = torch.empty_like(q)
+        lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device) if return_lse else None
+        kv = self.layer_view(layer)
+        _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(block_indices), ctypes.byref(kv),
+                  int(group_size), float(scale), _lib.view4(out),
+                  lse.data_ptr() if lse is not None else None, self.next_epoch(),
+                  _lib.stream_of(q), error=BlockKVBackendError)
+        return (out, lse) if return_lse else out
+
+    # ---------------------------------------------------------------- residency
+    def _recency(self):
+        """Host copy of every layer's stamps: int64 [L, H, MC] (one synchronisation)."""
+        st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
+        return st
+
+    def _protected(self) -> np.ndarray:
+        mask = np.zeros((self.L, self.H, self.max_chunks), dtype=bool)
+        c = np.arange(self.max_chunks)
+        for l in range(self.L):
+            n = self.n_chunks[l]
+            prot = (c < min(self.sink, n)) | ((c >= max(0, n - self.window)) & (c < n))
+            mask[l, :, :] = prot[None, :]
+        return mask
+
+    def _plan(self, st: np.ndarray, reserve: int):
+        """Desired HBM set: protected units, then the most recent (epoch, chunk) units."""
+        written = self._table_h != -1
+        prot = self._protected() & written
+        # rank key: epoch * 2^20 + chunk (later epoch, then larger chunk = more recent)
+        key = st * (1 << 20) + np.arange(self.max_chunks)[None, None, :]
+        desired = prot.copy()
+        if self.lru_max_size > 0:
+            for l in range(self.L):
+                for h in range(self.H):
+                    cand = np.nonzero(written[l, h] & ~prot[l, h])[0]
+                    if cand.size == 0:
+                        continue
+                    room = max(0, self.lru_max_size - int(prot[l, h].sum()))
+                    order = cand[np.argsort(-key[l, h, cand], kind="stable")]
+                    desired[l, h, order[:room]] = True
+        cap = self.n_slots - reserve
+        n_prot = int(desired.sum())
+        if n_prot > cap:
+            raise BlockKVBackendError(
+                f"{n_prot} protected / LRU units exceed the {cap} HBM slots left after reserving "
+                f"{reserve} for the next chunk")
+        cand = written & ~desired
+        if self.lru_max_size > 0:
+            # the per-head LRU decides; the budget only caps it
+            cand_idx = np.zeros(0, dtype=np.int64)
+        else:
+            cand_idx = np.flatnonzero(cand)
+        if cand_idx.size:
+            order = cand_idx[np.argsort(-key.reshape(-1)[cand_idx], kind="stable")]
+            flat = desired.reshape(-1)
+            flat[order[:cap - n_prot]] = True
+        return desired
+
+    def _move(self, layer_units, to_host: bool):
+        """Copy units (list of (l, h, c)) between the pools; returns bytes moved."""
+        if not layer_units:
+            return 0
+        src, dst = [], []
+        for (l, h, c) in layer_units:
+            s = int(self._table_h[l, h, c])
+            if to_host:
+                d = self._free_host.pop()
+                src.append(s)
+                dst.append(d)
+                self._table_h[l, h, c] = -2 - d
+                self._free_hbm.append(s)
+            else:
+                hs = -2 - s
+                d = self._free_hbm.pop()
+                src.append(hs)
+                dst.append(d)
+                self._table_h[l, h, c] = d
+                self._free_host.append(hs)
+        dev = self.device
+        s_t = torch.tensor(src, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
+        d_t = torch.tensor(dst, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
+        hk, hv = self._host_k.dev_ptr, self._host_v.dev_ptr
+        pk, pv = self.pool_k.data_ptr(), self.pool_v.data_ptr()
+        if self.fp8:
+            hsk, hsv = self._host_sk.dev_ptr, self._host_sv.dev_ptr
+            psk, psv = self.scale_k.data_ptr(), self.scale_v.data_ptr()
+        else:
+            hsk = hsv = psk = psv = None
+        if to_host:
+            args = (pk, hk, pv, hv, psk, hsk, psv, hsv)
+            limits = (self.n_slots, self.n_host)
+        else:
+            args = (hk, pk, hv, pv, hsk, psk, hsv, psv)
+            limits = (self.n_host, self.n_slots)
+        _lib.call("omm_copy_units", *args, s_t.data_ptr(), d_t.data_ptr(), len(src), *limits,
+                  self.unit_bytes, self.scale_bytes, _lib.stream_of(self.pool_k),
+                  error=BlockKVBackendError)
+        torch.cuda.current_stream(dev).synchronize()  # slot index tensors die with this frame
+        return len(src) * 2 * (self.unit_bytes + self.scale_bytes)
+
+    def _apply(self, desired: np.ndarray):
+        resident = self._table_h >= 0
+        on_host = self._table_h <= -2
+        evict = list(zip(*np.nonzero(resident & ~desired)))
+        promote = list(zip(*np.nonzero(on_host & desired)))
+        if len(evict) > len(self._free_host):
+            raise BlockKVBackendError(
+                f"host pool full: {len(evict)} units to evict, {len(self._free_host)} host slots free")
+        eb = self._move(evict, to_host=True)
+        room = len(self._free_hbm)
+        promote = promote[:room]
+        pb = self._move(promote, to_host=False)
+        for l in sorted({u[0] for u in evict} | {u[0] for u in promote}):
+            self._upload_table(l)
+        self.stats["evicted_units"] += len(evict)
+        self.stats["promoted_units"] += len(promote)
+        self.stats["evicted_bytes"] += eb
+        self.stats["promoted_bytes"] += pb
+        return len(evict), len(promote)
+
+    def _make_room(self, need: int):
+        st = self._recency()
+        desired = self._plan(st, reserve=need)
+        self._apply(desired)
+        if len(self._free_hbm) < need:
+            raise BlockKVBackendError(f"cannot free {need} HBM slots")
+
+    def flush(self, reserve_next_chunk: bool = True) -> dict:
+        """Chunk-boundary residency update (MMCache.flush_offload, models/cache.py:1032): one
+        stamp read, then batched evict / promote copies.  With ``reserve_next_chunk`` the HBM
+        slots of the next chunk of every layer and head are assigned here, so the appends of the
+        next AR step never touch the host.  Returns this flush's counts."""
+        st = self._recency()
+        touched = st > self._flush_epoch
+        written = self._table_h != -1
+        hits = int((touched & (self._table_h >= 0)).sum())
+        misses = int((touched & (self._table_h <= -2)).sum())
+        self.stats["hits"] += hits
+        self.stats["misses"] += misses
+        reserve = self.L * self.H if reserve_next_chunk else 0
+        desired = self._plan(st, reserve=reserve) & written
+        ev, pr = self._apply(desired)
+        if reserve_next_chunk:
+            for l in range(self.L):
+                c = self.n_chunks[l]
+                if c >= self.max_chunks:
+                    continue
+                row = self._table_h[l, :, c]
+                free = np.nonzero(row == -1)[0]
+                if free.size == 0:
+                    continue
+                for h in free:
+                    row[h] = self._free_hbm.pop()
+                self._upload_table(l)
+        self._flush_epoch = self._epoch
+        self.stats["flushes"] += 1
+        return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr}
+
+    def lru_hit_rate_overall(self) -> float:
+        """Fraction of touched units found in HBM (models/cache.py:713)."""
+        tot = self.stats["hits"] + self.stats["misses"]
+        return self.stats["hits"] / tot if tot else 0.0
+
+    # ---------------------------------------------------------------- inspection (tests)
+    def read_unit(self, layer: int, head: int, cid: int):
+        """(K, V[, scale_k, scale_v]) of one unit as CPU tensors, from whichever pool holds it."""
+        s = int(self._table_h[layer, head, cid])
+        if s == -1:
+            raise BlockKVBackendError("unit never written")
+        torch.cuda.current_stream(self.device).synchronize()
+        store = torch.uint8 if self.fp8 else torch.bfloat16
+        shape = (self.ppc, self.P, self.D)
+        if s >= 0:
+            k, v = self.pool_k[s].cpu(), self.pool_v[s].cpu()
+            sc = (self.scale_k[s].cpu(), self.scale_v[s].cpu()) if self.fp8 else ()
+        else:
+            hs = -2 - s
+            ub = self.unit_bytes
+            k = self._host_k.cpu_view()[hs * ub:(hs + 1) * ub].clone().view(store).view(shape)
+            v = self._host_v.cpu_view()[hs * ub:(hs + 1) * ub].clone().view(store).view(shape)
+            sc = ()
+            if self.fp8:
+                sb = self.scale_bytes
+                sc = (self._host_sk.cpu_view()[hs * sb:(hs + 1) * sb].clone().view(torch.float32),
+                      self._host_sv.cpu_view()[hs * sb:(hs + 1) * sb].clone().view(torch.float32))
+        return (k, v) + tuple(sc)
+
+    def where(self, layer: int, head: int, cid: int) -> str:
+        s = int(self._table_h[layer, head, cid])
+        return "none" if s == -1 else ("hbm" if s >= 0 else "host")
+
+    def evict_all(self):
+        """Move every unit to the host pool (failure-injection / parity tests)."""
+        desired = np.zeros_like(self._table_h, dtype=bool)
+        self._apply(desired)
+
+    def close(self):
+        for p in (self._host_k, self._host_v, self._host_sk, self._host_sv):
+            p.free()

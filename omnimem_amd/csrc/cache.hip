@@ -58,7 +58,9 @@ struct AppendArgs {
   int32_t* stamp;
   bf16_t* k_cmp;       // optional [1, NCB, H, D] pooled keys; page p of chunk cid -> row cid*ppc+p
   int64_t cs1, cs2;
-  int H, D, P, ppc, max_chunks, cid, tokens, lph, epoch;
+  bf16_t* v_cmp;       // optional pooled values, same layout
+  int64_t vcs1, vcs2;
+  int H, D, P, ppc, max_chunks, cid, tokens, lph, epoch, n_slots;
 };
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& r, float (&f)[8]) {
@@ -80,6 +82,18 @@ __device__ __forceinline__ uint2 quant8(const float (&x)[8], float inv) {
   return make_uint2(w[0], w[1]);
 }
 
+// 8 pooled sums / count, rounded to bf16 and packed (zeros for an empty page)
+__device__ __forceinline__ uint4 mean8(const float (&sum)[8], float cnt, int n) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t lo = n > 0 ? f32_to_bf16_bits(sum[2 * i] / cnt) : 0;
+    const uint16_t hi = n > 0 ? f32_to_bf16_bits(sum[2 * i + 1] / cnt) : 0;
+    w[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // One wave per (page, heads of the wave); lane = (head in wave, 8-dim slice).  Every lane walks
 // the page's tokens in ascending order, so the pooled key is the omm_block_pool arithmetic.
 template <bool FP8>
@@ -93,14 +107,14 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
   if (active) slot = a.unit_table[static_cast<int64_t>(h) * a.max_chunks + a.cid];
   const int t_first = p * a.P;
   const int nvalid = max(0, min(a.P, a.tokens - t_first));
-  const bool go = active && slot >= 0;
+  const bool go = active && slot >= 0 && slot < a.n_slots;
   const int64_t page = static_cast<int64_t>(slot) * a.ppc + p;
   const bf16_t* ksrc = a.k + static_cast<int64_t>(h) * a.ks2 + dc * 8;
   const bf16_t* vsrc = a.v + static_cast<int64_t>(h) * a.vs2 + dc * 8;
 
-  float ksum[8];
+  float ksum[8], vsum[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ksum[i] = 0.0f;
+  for (int i = 0; i < 8; ++i) ksum[i] = vsum[i] = 0.0f;
 
   if constexpr (!FP8) {
     uint4* kd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_k) + page * a.P * a.D + dc * 8);
@@ -112,10 +126,14 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
         if (t < nvalid) {
           kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
           vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
-          float f[8];
+          float f[8], g[8];
           unpack_bf16x8(kr, f);
+          unpack_bf16x8(vr, g);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ksum[i] += f[i];
+          for (int i = 0; i < 8; ++i) {
+            ksum[i] += f[i];
+            vsum[i] += g[i];
+          }
         }
         kd[t * row] = kr;
         vd[t * row] = vr;
@@ -133,6 +151,7 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           ksum[i] += fk[i];
+          vsum[i] += fv[i];
           amax_k = fmaxf(amax_k, fabsf(fk[i]));
           amax_v = fmaxf(amax_v, fabsf(fv[i]));
         }
@@ -171,19 +190,12 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
       }
     }
   }
-  if (go && a.k_cmp != nullptr) {
-    const float cnt = static_cast<float>(nvalid);
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = nvalid > 0 ? f32_to_bf16_bits(ksum[2 * i] / cnt) : 0;
-      const uint16_t hi = nvalid > 0 ? f32_to_bf16_bits(ksum[2 * i + 1] / cnt) : 0;
-      w[i] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
-    }
-    const int64_t r = static_cast<int64_t>(a.cid) * a.ppc + p;
-    *reinterpret_cast<uint4*>(a.k_cmp + r * a.cs1 + h * a.cs2 + dc * 8) =
-        make_uint4(w[0], w[1], w[2], w[3]);
-  }
+  const float cnt = static_cast<float>(nvalid);
+  const int64_t crow = static_cast<int64_t>(a.cid) * a.ppc + p;
+  if (go && a.k_cmp != nullptr)
+    *reinterpret_cast<uint4*>(a.k_cmp + crow * a.cs1 + h * a.cs2 + dc * 8) = mean8(ksum, cnt, nvalid);
+  if (go && a.v_cmp != nullptr)
+    *reinterpret_cast<uint4*>(a.v_cmp + crow * a.vcs1 + h * a.vcs2 + dc * 8) = mean8(vsum, cnt, nvalid);
   if (go && p == 0 && dc == 0 && a.stamp != nullptr && a.epoch > 0)
     a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
 }
@@ -203,28 +215,31 @@ struct CopyArgs {
   const int32_t* src_slot;
   const int32_t* dst_slot;
   int64_t unit_bytes, scale_bytes;
+  int32_t n_src, n_dst;  // slots in the source / destination pools
 };
 
 __device__ __forceinline__ void copy_range16(const unsigned char* s, unsigned char* d, int64_t n) {
   const uint4* s4 = reinterpret_cast<const uint4*>(s);
   uint4* d4 = reinterpret_cast<uint4*>(d);
   const int64_t n4 = n / 16;
-  constexpr int U = 4;
+  const int64_t st = blockDim.x;
   int64_t i = threadIdx.x;
-  for (; i + (U - 1) * blockDim.x < n4; i += U * blockDim.x) {
-    uint4 r[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) r[u] = s4[i + u * blockDim.x];
-#pragma unroll
-    for (int u = 0; u < U; ++u) d4[i + u * blockDim.x] = r[u];
+  // four 16-byte loads in flight per lane
+  for (; i + 3 * st < n4; i += 4 * st) {
+    const uint4 r0 = s4[i], r1 = s4[i + st], r2 = s4[i + 2 * st], r3 = s4[i + 3 * st];
+    d4[i] = r0;
+    d4[i + st] = r1;
+    d4[i + 2 * st] = r2;
+    d4[i + 3 * st] = r3;
   }
-  for (; i < n4; i += blockDim.x) d4[i] = s4[i];
+  for (; i < n4; i += st) d4[i] = s4[i];
 }
 
 __global__ __launch_bounds__(256) void copy_units_kernel(CopyArgs a) {
   const int64_t i = blockIdx.x;
   const int64_t part = blockIdx.y;
   const int64_t so = static_cast<int64_t>(a.src_slot[i]), dof = static_cast<int64_t>(a.dst_slot[i]);
+  if (so < 0 || so >= a.n_src || dof < 0 || dof >= a.n_dst) return;  // workgroup-uniform
   const int64_t b0 = part * kCopyPart;
   const int64_t n = min(kCopyPart, a.unit_bytes - b0);
   if (n > 0) {
@@ -441,9 +456,23 @@ extern "C" int omm_build_ptr_table(const omm_view4* ids, const int64_t* base_k,
   return check_launch("omm_build_ptr_table");
 }
 
+namespace omm {
+namespace {
+int check_cmp(const omm_view4* c, int64_t rows, int H, int D, const char* what) {
+  OMM_REQUIRE(c->size[0] == 1 && c->size[1] >= rows && c->size[2] == H && c->size[3] == D &&
+                  c->stride[3] == 1 && c->stride[1] % 8 == 0 && c->stride[2] % 8 == 0 &&
+                  (reinterpret_cast<uintptr_t>(c->data) & 15u) == 0,
+              OMM_EINVAL, "omm_paged_append: %s must be a 16-byte aligned [1, >= %lld, %d, %d] bf16 view",
+              what, (long long)rows, H, D);
+  return OMM_OK;
+}
+}  // namespace
+}  // namespace omm
+
 extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
                                 const omm_view4* v_new, int32_t cid, int32_t chunk_tokens,
-                                const omm_view4* k_cmp, int32_t epoch, void* stream) {
+                                const omm_view4* k_cmp, const omm_view4* v_cmp, int32_t epoch,
+                                void* stream) {
   using namespace omm;
   OMM_REQUIRE(kv != nullptr && k_new != nullptr && v_new != nullptr, OMM_EINVAL,
               "omm_paged_append: null argument");
@@ -479,19 +508,22 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
   a.scale_k = kv->scale_k; a.scale_v = kv->scale_v;
   a.unit_table = kv->unit_table;
   a.stamp = kv->stamp;
+  const int64_t rows = static_cast<int64_t>(cid + 1) * ppc;
   if (k_cmp != nullptr && k_cmp->data != nullptr) {
-    OMM_REQUIRE(k_cmp->size[0] == 1 && k_cmp->size[1] >= static_cast<int64_t>(cid + 1) * ppc &&
-                    k_cmp->size[2] == H && k_cmp->size[3] == D && k_cmp->stride[3] == 1 &&
-                    k_cmp->stride[1] % 8 == 0 && k_cmp->stride[2] % 8 == 0 &&
-                    (reinterpret_cast<uintptr_t>(k_cmp->data) & 15u) == 0,
-                OMM_EINVAL,
-                "omm_paged_append: k_cmp must be a 16-byte aligned [1, >= %lld, %d, %d] bf16 view",
-                (long long)(cid + 1) * ppc, H, D);
+    const int rc = check_cmp(k_cmp, rows, H, D, "k_cmp");
+    if (rc) return rc;
     a.k_cmp = static_cast<bf16_t*>(const_cast<void*>(k_cmp->data));
     a.cs1 = k_cmp->stride[1]; a.cs2 = k_cmp->stride[2];
   }
+  if (v_cmp != nullptr && v_cmp->data != nullptr) {
+    const int rc = check_cmp(v_cmp, rows, H, D, "v_cmp");
+    if (rc) return rc;
+    a.v_cmp = static_cast<bf16_t*>(const_cast<void*>(v_cmp->data));
+    a.vcs1 = v_cmp->stride[1]; a.vcs2 = v_cmp->stride[2];
+  }
   a.H = H; a.D = D; a.P = P; a.ppc = ppc; a.max_chunks = kv->max_chunks; a.cid = cid;
   a.tokens = chunk_tokens;
+  a.n_slots = kv->n_slots;
   a.lph = D / 8;
   a.epoch = epoch;
   // lanes per head must divide the wave
@@ -508,7 +540,8 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
 extern "C" int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
                               const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
                               const int32_t* src_slot, const int32_t* dst_slot, int32_t n,
-                              int64_t unit_bytes, int64_t scale_bytes, void* stream) {
+                              int32_t n_src_slots, int32_t n_dst_slots, int64_t unit_bytes,
+                              int64_t scale_bytes, void* stream) {
   using namespace omm;
   OMM_REQUIRE(n >= 0 && unit_bytes > 0 && unit_bytes % 16 == 0 && scale_bytes >= 0, OMM_EINVAL,
               "omm_copy_units: n >= 0 and unit_bytes a positive multiple of 16 required");
@@ -524,7 +557,7 @@ extern "C" int omm_copy_units(const void* src_k, void* dst_k, const void* src_v,
              static_cast<const unsigned char*>(src_v), static_cast<unsigned char*>(dst_v),
              static_cast<const unsigned char*>(src_sk), static_cast<unsigned char*>(dst_sk),
              static_cast<const unsigned char*>(src_sv), static_cast<unsigned char*>(dst_sv),
-             src_slot, dst_slot, unit_bytes, scale_bytes};
+             src_slot, dst_slot, unit_bytes, scale_bytes, n_src_slots, n_dst_slots};
   const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>(cdiv64(unit_bytes, kCopyPart)));
   copy_units_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("omm_copy_units");

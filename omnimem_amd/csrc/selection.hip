@@ -84,6 +84,7 @@ struct DenseAcc {
     r.nvalid = static_cast<int>(n);
     return r;
   }
+  __device__ __forceinline__ void touch(int, int, int, int) const {}
 };
 
 struct PtrAcc {
@@ -104,6 +105,7 @@ struct PtrAcc {
     r.nvalid = bs;
     return r;
   }
+  __device__ __forceinline__ void touch(int, int, int, int) const {}
 };
 
 template <typename KVT>
@@ -119,8 +121,9 @@ struct PagedAcc {
   const float* hsc_v;
   const int32_t* unit;
   const int32_t* ids;
+  int32_t* stamp;
   int64_t is0, is1, is2, is3;
-  int max_chunks, n_chunks, chunk_len, P, ppc, D;
+  int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
   __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
     BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
     const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
@@ -128,7 +131,7 @@ struct PagedAcc {
     const int cid = bid / ppc, p = bid - cid * ppc;
     if (cid >= n_chunks || cid >= max_chunks) return r;
     const int32_t s = unit[static_cast<int64_t>(h) * max_chunks + cid];
-    if (s == -1) return r;
+    if (s == -1 || s >= n_slots || (s < 0 && -2 - s >= n_host)) return r;
     const int64_t page = (s >= 0 ? static_cast<int64_t>(s) : static_cast<int64_t>(-2 - s)) * ppc + p;
     const int64_t off = page * P * D;
     if (s >= 0) {
@@ -144,6 +147,19 @@ struct PagedAcc {
     const int rem = chunk_len - p * P;
     r.nvalid = rem < P ? rem : P;
     return r;
+  }
+  // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
+  // epoch, so the races are benign)
+  __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
+    if (stamp == nullptr || epoch <= 0) return;
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+      const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+      if (bid < 0) continue;
+      const int cid = bid / ppc;
+      if (cid >= n_chunks || cid >= max_chunks) continue;
+      const int64_t u = static_cast<int64_t>(h) * max_chunks + cid;
+      if (unit[u] != -1) stamp[u] = epoch;
+    }
   }
 };
 
@@ -298,6 +314,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   const int m0 = g * G + sub * 64;                       // first query of this workgroup
   const int m_end = min(min(g * G + G, M), m0 + 64);     // exclusive
   const int qc = (g * G) / chunk;
+  if (sub == 0) acc.touch(b, g, h, T);
   const int my_q = m0 + 16 * w + l16;
   const bool q_ok = my_q < m_end;
 
@@ -455,6 +472,7 @@ __global__ __launch_bounds__(256) void sel_fwd_valu_kernel(View4<const QT> q, Vi
   const int m0 = g * G + sub * 64;
   const int m_end = min(min(g * G + G, M), m0 + 64);
   const int qc = (g * G) / chunk;
+  if (sub == 0) acc.touch(b, g, h, T);
   const int qi = tid >> 2, part = tid & 3;
   const int my_q = m0 + qi;
   const bool q_ok = my_q < m_end;
@@ -691,7 +709,7 @@ extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const i
 
 extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                                  int32_t group_size, float scale, const omm_view4* out, float* lse,
-                                 void* stream) {
+                                 int32_t epoch, void* stream) {
   using namespace omm;
   int rc = check_q_out("omm_sel_fwd_paged", q, out);
   if (rc) return rc;
@@ -719,9 +737,10 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
                          nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
                          static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
-                         idp, ids->stride[0], ids->stride[1], ids->stride[2], ids->stride[3],
-                         kv->max_chunks, kv->n_chunks, kv->chunk_len, kv->page_tokens,
-                         kv->pages_per_chunk, kv->head_dim};
+                         idp, kv->stamp, ids->stride[0], ids->stride[1], ids->stride[2],
+                         ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
+                         kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
+                         kv->n_slots, kv->n_host_slots};
     return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
   }
   if (kv->dtype == OMM_FP8E4M3) {
@@ -730,9 +749,10 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<uint8_t> acc{static_cast<const uint8_t*>(kv->pool_k), static_cast<const uint8_t*>(kv->pool_v),
                           kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
                           static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
-                          kv->host_scale_v, kv->unit_table, idp, ids->stride[0], ids->stride[1],
-                          ids->stride[2], ids->stride[3], kv->max_chunks, kv->n_chunks,
-                          kv->chunk_len, kv->page_tokens, kv->pages_per_chunk, kv->head_dim};
+                          kv->host_scale_v, kv->unit_table, idp, kv->stamp, ids->stride[0],
+                          ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
+                          kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
+                          kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};
     return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
   }
   return set_error(OMM_EINVAL, "omm_sel_fwd_paged: unsupported cache dtype %d", kv->dtype);

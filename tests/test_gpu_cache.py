@@ -1,0 +1,355 @@
+"""GPU parity of the block KV cache path: reference pointer tables, the paged cache (append,
+fused block compression, fp8 pages, paged selection, evict / promote, LRU), and the reference's
+block-store kernels K1 / K2 / K3.
+
+Bit-exact: addresses, cache bytes (bf16 pages, fp8 codes and scales), pooled keys / values,
+residency moves, dedup keys.  Attention: float64 oracle within the bf16 tolerances
+(2e-2 max-abs, 1e-3 mean-abs), and bit-exact invariance under residency changes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import nsa_oracle as O
+from oracle.lru_model import ReferenceLRU
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check_attn(out, lse, want_o, want_l, mx=2e-2, mean=1e-3):
+    o = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(o - want_o)
+    assert err.max() <= mx, f"max-abs {err.max():.3e}"
+    assert err.mean() <= mean, f"mean-abs {err.mean():.3e}"
+    if lse is not None:
+        l = lse.cpu().numpy().astype(np.float64)
+        assert np.array_equal(np.isneginf(l), np.isneginf(want_l))
+        fin = ~np.isneginf(want_l)
+        if fin.any():
+            assert np.abs(l[fin] - want_l[fin]).max() <= 1e-3
+
+
+# ------------------------------------------------------------------ pointer tables (reference)
+def test_build_ptr_table_matches_address_rule():
+    from omnimem_amd.padded_ptr import build_ptr_table
+    rng = np.random.default_rng(0)
+    B, MG, H, T, MC, bpc = 2, 5, 3, 7, 6, 4
+    ids = rng.integers(-2, MC * bpc + 3, size=(B, MG, H, T)).astype(np.int32)
+    base_k = rng.integers(1, 2 ** 40, size=(H, MC)).astype(np.int64) * 256
+    base_v = rng.integers(1, 2 ** 40, size=(H, MC)).astype(np.int64) * 256
+    base_k[1, 2] = 0
+    base_v[2, 0] = 0
+    nblk = np.array([MC * bpc, 3 * bpc, MC * bpc - 1], np.int32)
+    bstride, icb = 1 << 20, 4096
+    pk, pv = build_ptr_table(torch.from_numpy(ids).to(DEV), torch.from_numpy(base_k).to(DEV),
+                             torch.from_numpy(base_v).to(DEV), torch.from_numpy(nblk).to(DEV),
+                             bstride, bpc, icb)
+    want_k = np.zeros_like(ids, dtype=np.int64)
+    want_v = np.zeros_like(ids, dtype=np.int64)
+    for b, g, h, t in np.ndindex(*ids.shape):
+        bid = int(ids[b, g, h, t])
+        if bid < 0 or bid >= nblk[h]:
+            continue
+        cid, loc = divmod(bid, bpc)
+        if cid >= MC:
+            continue
+        d = b * bstride + loc * icb
+        want_k[b, g, h, t] = base_k[h, cid] + d if base_k[h, cid] else 0
+        want_v[b, g, h, t] = base_v[h, cid] + d if base_v[h, cid] else 0
+    np.testing.assert_array_equal(pk.cpu().numpy(), want_k)
+    np.testing.assert_array_equal(pv.cpu().numpy(), want_v)
+
+
+def test_padded_ptr_fast_reference_geometry():
+    """The reference's AR shape (30-token blocks, groups of 15, 4680-token chunks) over
+    per-head chunk tensors addressed by base pointers; a non-resident chunk (base 0) is skipped."""
+    from omnimem_amd.padded_ptr import selection_attention_padded_ptr_fast
+    g = torch.Generator().manual_seed(1)
+    H, D, C, BS, G, T, n_chunks = 2, 128, 4680, 30, 15, 8, 3
+    chunks_k = [[(torch.randn((1, C, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+                 for _ in range(n_chunks)] for _ in range(H)]
+    chunks_v = [[torch.randn((1, C, D), generator=g).to(torch.bfloat16).to(DEV)
+                 for _ in range(n_chunks)] for _ in range(H)]
+    base_k = torch.tensor([[t.data_ptr() for t in row] for row in chunks_k], dtype=torch.int64)
+    base_v = torch.tensor([[t.data_ptr() for t in row] for row in chunks_v], dtype=torch.int64)
+    base_k[1, 0] = 0  # head 1, chunk 0 is "on the CPU"
+    M = 150
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    bpc = C // BS
+    ids = torch.stack([torch.randperm(n_chunks * bpc, generator=g)[:T] for _ in range(M // G * H)])
+    ids = ids.view(1, M // G, H, T).to(torch.int32)
+    strides = {"batch_stride_bytes": C * D * 2, "token_stride_bytes": D * 2, "stride_bn": D,
+               "stride_bd": 1, "chunk_len": C}
+    out, lse = selection_attention_padded_ptr_fast(
+        q.to(DEV), ids.to(DEV), BS, G, C, base_k.to(DEV), base_v.to(DEV),
+        torch.full((H,), n_chunks, dtype=torch.int32, device=DEV), strides, return_lse=True)
+    k = torch.stack([torch.cat([c[0] for c in row]) for row in chunks_k], 1)[None].float().cpu()
+    v = torch.stack([torch.cat([c[0] for c in row]) for row in chunks_v], 1)[None].float().cpu()
+    ids_np = ids.numpy().copy()
+    # the skipped chunk contributes nothing: drop its blocks from head 1 in the oracle
+    ids_np[:, :, 1][ids_np[:, :, 1] // bpc == 0] = -1
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.numpy(), v.numpy(), ids_np, G,
+                                           D ** -0.5, O.dense_block_tokens(n_chunks * C, BS, 1, False))
+    _check_attn(out, lse, want_o, want_l)
+
+
+# ------------------------------------------------------------------ paged cache
+def _chunk(g, S, H, D, scale=1.0, t_dist=False):
+    if t_dist:
+        x = torch.distributions.StudentT(4.0).sample((1, S, H, D))
+    else:
+        x = torch.randn((1, S, H, D), generator=g)
+    return (x * scale).to(torch.bfloat16)
+
+
+def _pages(x: np.ndarray, C: int, P: int):
+    """[S, D] chunk (S <= C) -> [ppc, P, D] pages with zero padding."""
+    ppc = -(-C // P)
+    out = np.zeros((ppc * P, x.shape[-1]), np.float32)
+    out[:x.shape[0]] = x
+    return out.reshape(ppc, P, -1)
+
+
+@pytest.mark.parametrize("S", [4680, 4000])
+def test_paged_append_bf16_bitexact_and_pooled(S):
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.index_topk import block_pool
+    g = torch.Generator().manual_seed(S)
+    H, D, C, P = 3, 128, 4680, 64
+    cache = PagedKVCache(1, H, D, max_chunks=4, chunk_len=C, page_tokens=P, hbm_slots=12,
+                         window_chunks=0)
+    k, v = _chunk(g, S, H, D), _chunk(g, S, H, D)
+    cache.append(0, k.to(DEV), v.to(DEV), 2)
+    for h in range(H):
+        kk, vv = cache.read_unit(0, h, 2)
+        np.testing.assert_array_equal(kk.float().numpy(), _pages(k[0, :, h].float().numpy(), C, P))
+        np.testing.assert_array_equal(vv.float().numpy(), _pages(v[0, :, h].float().numpy(), C, P))
+    kc, vc = cache.cmp_history(0)
+    ppc = cache.ppc
+    got_k = kc[:, 2 * ppc:3 * ppc].float().cpu().numpy()
+    got_v = vc[:, 2 * ppc:3 * ppc].float().cpu().numpy()
+    nfull = -(-S // P)
+    np.testing.assert_array_equal(got_k[:, :nfull], O.pool_mean(k.float().numpy(), P, "bf16"))
+    np.testing.assert_array_equal(got_v[:, :nfull], O.pool_mean(v.float().numpy(), P, "bf16"))
+    assert not got_k[:, nfull:].any()
+    # the fused pool equals the standalone block pool kernel
+    np.testing.assert_array_equal(got_k[:, :nfull], block_pool(k.to(DEV), P).float().cpu().numpy())
+
+
+def test_paged_append_fp8_codes_and_scales_bitexact():
+    from omnimem_amd.block_cache import PagedKVCache
+    torch.manual_seed(7)
+    H, D, C, P = 2, 128, 4680, 64
+    cache = PagedKVCache(1, H, D, max_chunks=2, chunk_len=C, page_tokens=P, dtype="fp8",
+                         hbm_slots=4, window_chunks=0)
+    k, v = _chunk(None, C, H, D, 3.0, True), _chunk(None, C, H, D, 2.0, True)
+    k[0, 128:192, 1] = 0  # page 2 of head 1 all zero: scale 1, codes 0
+    cache.append(0, k.to(DEV), v.to(DEV), 0)
+    for h in range(H):
+        kc, vc, sk, sv = cache.read_unit(0, h, 0)
+        for x, codes, sc in ((k, kc, sk), (v, vc, sv)):
+            pages = _pages(x[0, :, h].float().numpy(), C, P)
+            for p in range(cache.ppc):
+                valid = min(P, C - p * P)
+                want_c, want_s = O.quantize_pages(pages[p], valid)
+                np.testing.assert_array_equal(codes[p].numpy(), want_c, err_msg=f"h{h} p{p}")
+                assert np.float32(sc[p].item()) == want_s, (h, p)
+
+
+def _paged_oracle_inputs(chunks_k, chunks_v, fp8_cache=None, layer=0):
+    """Concatenate chunk tensors [1, C, H, D] into the oracle's [1, n*C, H, D]; for an fp8
+    cache, the dequantised values the kernel sees (code * scale rounded to bf16)."""
+    if fp8_cache is None:
+        return (torch.cat(chunks_k, 1).float().numpy(), torch.cat(chunks_v, 1).float().numpy())
+    c = fp8_cache
+    n = len(chunks_k)
+    H, D, C = c.H, c.D, c.chunk_len
+    out_k = np.zeros((1, n * C, H, D), np.float32)
+    out_v = np.zeros_like(out_k)
+    for cid in range(n):
+        for h in range(H):
+            kc, vc, sk, sv = c.read_unit(layer, h, cid)
+            for codes, sc, dst in ((kc, sk, out_k), (vc, sv, out_v)):
+                deq = O.dequantize_pages(codes.numpy(), sc.numpy()[:, None, None])
+                deq = O.round_to(deq, "bf16").reshape(-1, D)[:C]
+                dst[0, cid * C:(cid + 1) * C, h] = deq
+    return out_k, out_v
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype):
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.padded_ptr import selection_attention_paged
+    torch.manual_seed(11)
+    g = torch.Generator().manual_seed(11)
+    H, D, C, P, G, T, n = 3, 128, 4680, 64, 64, 16, 4
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         hbm_slots=H * n, window_chunks=0)
+    fp8 = dtype == "fp8"
+    ks = [_chunk(g, C, H, D, 0.3, fp8) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, fp8) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    M = C
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    MG = -(-M // G)
+    ppc = cache.ppc
+    ids = torch.stack([torch.randperm(n * ppc, generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32)
+    ids[0, 3, 1, :5] = -1
+    ids[0, 5, 0, 0] = n * ppc + 3  # a page of a chunk that does not exist yet: skipped
+    qd, idd = q.to(DEV), ids.to(DEV)
+    with torch.no_grad():
+        out, lse = selection_attention_paged(qd, idd, P, G, cache, 0, return_lse=True)
+    kk, vv = _paged_oracle_inputs(ks, vs, cache if fp8 else None)
+    want_o, want_l = O.selection_attention(q.float().numpy(), kk, vv, ids.numpy(), G, D ** -0.5,
+                                           O.paged_block_tokens(C, P, n))
+    _check_attn(out, lse, want_o, want_l)
+    # move every unit to the host pool: the kernel reads it there, bit for bit the same
+    cache.evict_all()
+    assert all(cache.where(0, h, c) == "host" for h in range(H) for c in range(n))
+    out2, lse2 = cache.select(qd, idd, 0, G, return_lse=True)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    # evicted bytes come back bit-exact after a promote
+    before = [cache.read_unit(0, h, c) for h in range(H) for c in range(n)]
+    cache.flush(reserve_next_chunk=False)
+    after = [cache.read_unit(0, h, c) for h in range(H) for c in range(n)]
+    assert all(cache.where(0, h, c) == "hbm" for h in range(H) for c in range(n))
+    for a, b in zip(before, after):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    out3 = cache.select(qd, idd, 0, G)
+    assert torch.equal(out, out3)
+
+
+def test_lru_residency_matches_reference_model():
+    """lru_max_size per (layer, head), no sink / window: after every flush the HBM-resident
+    chunks are exactly the reference LRU's (models/cache.py:673-699, :1032-1142)."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(5)
+    L, H, D, C, P, G, T, n, cap = 2, 3, 64, 640, 64, 64, 6, 7, 3
+    cache = PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P, hbm_slots=L * H * n,
+                         lru_max_size=cap, window_chunks=0, keep_window_kv=False)
+    model = ReferenceLRU(L, H, cap)
+    ppc = cache.ppc
+    rng = np.random.default_rng(5)
+    q = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    for cid in range(n):
+        for l in range(L):
+            k = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16).to(DEV)
+            cache.append(l, k, k, cid)
+            model.write(l, cid)
+            for _ in range(2):
+                ids = rng.integers(0, (cid + 1) * ppc, size=(1, C // G, H, T)).astype(np.int32)
+                cache.select(q, torch.from_numpy(ids).to(DEV), l, G)
+                model.select(l, ids, ppc, n)
+        cache.flush(reserve_next_chunk=False)
+        model.flush()
+        got = {(l, h, c) for l in range(L) for h in range(H) for c in range(cid + 1)
+               if cache.where(l, h, c) == "hbm"}
+        assert got == model.resident(), f"after chunk {cid}"
+
+
+def test_budget_flush_keeps_window_and_most_recent():
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(6)
+    L, H, D, C, P, n, slots = 1, 2, 64, 256, 64, 8, 10
+    cache = PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P, hbm_slots=slots,
+                         window_chunks=2, sink_chunks=1, keep_window_kv=False)
+    for cid in range(n):
+        k = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16).to(DEV)
+        cache.append(0, k, k, cid)
+        st = cache.flush()
+        resident = [(h, c) for h in range(H) for c in range(cid + 1) if cache.where(0, h, c) == "hbm"]
+        assert len(resident) + H <= slots  # the next chunk's slots are reserved
+        for h in range(H):
+            assert cache.where(0, h, 0) == "hbm"                   # sink
+            for c in range(max(0, cid - 1), cid + 1):
+                assert cache.where(0, h, c) == "hbm"               # window
+        assert st["evicted_units"] >= 0
+    assert cache.stats["evicted_units"] > 0
+
+
+# ------------------------------------------------------------------ K1 / K2 / K3
+def test_block_kv_warmup_known_answers():
+    from omnimem_amd import block_kv_ops
+    assert block_kv_ops.warmup(DEV) > 0
+
+
+def test_dedup_matches_numpy_unique():
+    from omnimem_amd.block_kv_ops import DeviceBlockDedup
+    rng = np.random.default_rng(8)
+    H, T, bpc, n_chunks = 12, 16, 74, 80
+    mb = bpc * n_chunks
+    ids = rng.integers(-1, mb + 5, size=(1, 74, H, T)).astype(np.int32)
+    dd = DeviceBlockDedup(H, mb, T, cap=20000, device=DEV, blocks_per_chunk=bpc)
+    for rep in range(2):
+        keys, n, overflow = dd.unique_keys(torch.from_numpy(ids).to(DEV))
+        want = set()
+        for (b, g, h, t), bid in np.ndenumerate(ids):
+            if 0 <= bid < mb:
+                cid, loc = divmod(int(bid), bpc)
+                want.add((cid * H + h) * bpc + loc)
+        assert n == len(want) and not overflow
+        np.testing.assert_array_equal(np.asarray(keys), np.array(sorted(want), np.int32))
+        ids = rng.integers(-1, mb, size=ids.shape).astype(np.int32)
+    small = DeviceBlockDedup(H, mb, T, cap=10, device=DEV, blocks_per_chunk=bpc)
+    keys, n, overflow = small.unique_keys(torch.from_numpy(ids).to(DEV))
+    assert overflow and n > 10 and len(keys) == 10
+
+
+def test_gather_publish_clear_and_block_range():
+    from omnimem_amd.block_kv_ops import (clear_block_range, gather_publish_clear,
+                                          register_block_range, table_entry_addresses)
+    g = torch.Generator().manual_seed(9)
+    BT, D = 64, 128
+    src = torch.randn((3, BT, D), generator=g).to(torch.bfloat16).pin_memory()  # host sources
+    src_v = torch.randn((3, BT, D), generator=g).to(torch.bfloat16).pin_memory()
+    dst = torch.zeros((3, BT, D), dtype=torch.bfloat16, device=DEV)
+    dst_v = torch.zeros_like(dst)
+    table = torch.full((2, 1, 8), 7, dtype=torch.int64, device=DEV)
+    pub_k = table_entry_addresses(table, 0, [0, 1, 2])
+    pub_v = table_entry_addresses(table, 1, [0, 1, 2])
+    clear = table_entry_addresses(table, 0, [5, 6])
+    desc = torch.tensor([src[i].data_ptr() for i in range(3)] + [src_v[i].data_ptr() for i in range(3)]
+                        + [dst[i].data_ptr() for i in range(3)] + [dst_v[i].data_ptr() for i in range(3)]
+                        + list(pub_k) + list(pub_v) + list(clear), dtype=torch.int64, device=DEV)
+    assert gather_publish_clear(desc, 3, 2, BT, D, dst) == 4
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), src) and torch.equal(dst_v.cpu(), src_v)
+    t = table.cpu()
+    assert t[0, 0, :3].tolist() == [dst[i].data_ptr() for i in range(3)]
+    assert t[1, 0, :3].tolist() == [dst_v[i].data_ptr() for i in range(3)]
+    assert t[0, 0, 5:7].tolist() == [0, 0] and t[0, 0, 7].item() == 7
+    tab = torch.zeros((2, 3, 10), dtype=torch.int64, device=DEV)
+    nv = torch.zeros(3, dtype=torch.int32, device=DEV)
+    register_block_range(tab, nv, 2, 5, 1 << 30, 1 << 31, 4096, 64, 7)
+    t = tab.cpu()
+    for h in range(3):
+        assert t[0, h, 2:7].tolist() == [(1 << 30) + h * 4096 + j * 64 for j in range(5)]
+        assert t[1, h, 2:7].tolist() == [(1 << 31) + h * 4096 + j * 64 for j in range(5)]
+        assert t[:, h, :2].abs().sum() == 0 and t[:, h, 7:].abs().sum() == 0
+    assert nv.tolist() == [7, 7, 7]
+    clear_block_range(tab, nv, 3, 2, -1, which="k")
+    t = tab.cpu()
+    assert t[0, :, 3:5].abs().sum() == 0 and t[1, :, 3:5].abs().sum() > 0 and nv.tolist() == [7] * 3
+
+
+def test_block_store_entry_uses_paged_cache():
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.padded_ptr import selection_attention_block_store, selection_attention_paged
+    g = torch.Generator().manual_seed(12)
+    H, D, C, P = 2, 128, 1024, 64
+    cache = PagedKVCache(1, H, D, max_chunks=2, chunk_len=C, page_tokens=P, window_chunks=0)
+    for cid in range(2):
+        k = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16).to(DEV)
+        cache.append(0, k, k, cid)
+    q = torch.randn((1, 128, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    ids = torch.randint(0, 32, (1, 2, H, 4), generator=g).to(torch.int32).to(DEV)
+    with torch.no_grad():
+        a = selection_attention_block_store(q, ids, P, 64, cache, 0)
+        b = selection_attention_paged(q, ids, P, 64, cache, 0)
+    assert torch.equal(a, b)
+    with pytest.raises(RuntimeError):
+        selection_attention_block_store(q, ids, P, 64, cache, 0)  # grad enabled

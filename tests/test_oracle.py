@@ -316,3 +316,30 @@ def test_cpu_baseline_topk_matches_oracle_without_ties():
     want = O.topk(q, k, 8, 64 ** -0.5, O.Mask(block_size=64, group_size=64, chunk_q=256,
                                               chunk_k=256, causal=1))
     np.testing.assert_array_equal(got, want)
+
+
+# ---------------------------------------------------------------- reference LRU model
+def test_reference_lru_model_matches_closed_form():
+    """An LRU of capacity C holds the C most recently touched distinct keys; the model's
+    per-(layer, head) OrderedDict must agree with that closed form on random touch streams."""
+    from oracle.lru_model import ReferenceLRU, lru_contents_bruteforce
+    rng = np.random.default_rng(40)
+    for cap in (1, 3, 7):
+        m = ReferenceLRU(1, 2, cap)
+        streams = {0: [], 1: []}
+        for _ in range(300):
+            h, c = int(rng.integers(0, 2)), int(rng.integers(0, 12))
+            m.touch(0, h, c)
+            streams[h].append(c)
+        for h in (0, 1):
+            assert list(m.lru[(0, h)].keys()) == lru_contents_bruteforce(streams[h], cap)
+
+
+def test_reference_lru_flush_offloads_marked_outside_lru_and_window():
+    from oracle.lru_model import ReferenceLRU
+    m = ReferenceLRU(1, 1, 2, window=1, sink=1)
+    for c in range(5):
+        m.write(0, c)
+    m.flush()
+    # LRU = {3, 4}; sink chunk 0 and window chunk 4 protected; 1, 2 offloaded
+    assert m.resident() == {(0, 0, 0), (0, 0, 3), (0, 0, 4)}
