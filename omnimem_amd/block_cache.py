@@ -75,8 +75,8 @@ class PagedKVCache:
 
     dtype: ``torch.bfloat16`` or ``"fp8"`` (OCP e4m3fn codes with one fp32 scale per
     (page, head) for K and for V).  Capacity: ``hbm_slots`` units per pool, or derived from
-    ``hbm_budget_bytes`` (K + V + scales).  ``host_slots`` defaults to every unit that can exist
-    minus the HBM slots.
+    ``hbm_budget_bytes`` (K + V + scales).  ``host_slots`` defaults to the units the HBM pool
+    cannot hold plus one chunk of every layer and head (the slack a flush reserves).
     """
 
     def __init__(self, num_layers: int, num_heads: int, head_dim: int, max_chunks: int,
@@ -112,7 +112,8 @@ class PagedKVCache:
                 f"HBM pool of {self.n_slots} units cannot hold one chunk of every layer and head "
                 f"({self.L * self.H} units)")
         if host_slots is None:
-            host_slots = total_units - self.n_slots
+            # every unit the HBM pool cannot hold, plus the chunk reserved at a flush
+            host_slots = min(total_units, total_units - self.n_slots + self.L * self.H)
         self.n_host = int(host_slots)
         self.hbm_budget_bytes = self.n_slots * per_slot
         self.lru_max_size = int(lru_max_size)

@@ -185,7 +185,7 @@ def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype):
     g = torch.Generator().manual_seed(11)
     H, D, C, P, G, T, n = 3, 128, 4680, 64, 64, 16, 4
     cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
-                         hbm_slots=H * n, window_chunks=0)
+                         hbm_slots=H * n, host_slots=H * n, window_chunks=0)
     fp8 = dtype == "fp8"
     ks = [_chunk(g, C, H, D, 0.3, fp8) for _ in range(n)]
     vs = [_chunk(g, C, H, D, 1.0, fp8) for _ in range(n)]
@@ -230,7 +230,8 @@ def test_lru_residency_matches_reference_model():
     g = torch.Generator().manual_seed(5)
     L, H, D, C, P, G, T, n, cap = 2, 3, 64, 640, 64, 64, 6, 7, 3
     cache = PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P, hbm_slots=L * H * n,
-                         lru_max_size=cap, window_chunks=0, keep_window_kv=False)
+                         host_slots=L * H * n, lru_max_size=cap, window_chunks=0,
+                         keep_window_kv=False)
     model = ReferenceLRU(L, H, cap)
     ppc = cache.ppc
     rng = np.random.default_rng(5)
