@@ -50,6 +50,10 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target duration of the CPU baseline sample")
+    p.add_argument("--ar-history", type=int, default=80,
+                   help="cached chunks before the timed AR steps (80 chunks = 240 latent frames)")
+    p.add_argument("--ar-steps", type=int, default=3, help="timed AR chunks per cache dtype")
+    p.add_argument("--no-ar", action="store_true", help="skip the AR (configs 4 and 5) leg")
     return p.parse_args()
 
 
@@ -123,6 +127,82 @@ def cpu_baseline(q, k, v, ids, seconds: float):
                   f"({100.0 * done / (MG * Hh):.1f}% of the step), {t_total:.1f} s of CPU time; "
                   f"cpu={platform.processor() or platform.machine()}, nproc={os.cpu_count()}",
     }
+
+
+def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
+    """Configs 4 / 5: ms per AR chunk with ``history`` chunks cached, 48 GB HBM budget."""
+    import torch
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.wan_ar import WanARConfig, WanNSAAR
+    cfg = WanARConfig()
+    warm = 1
+    max_chunks = history + warm + steps + 2
+    t0 = time.perf_counter()
+    cache = PagedKVCache(cfg.layers, cfg.heads, cfg.head_dim, max_chunks=max_chunks,
+                         chunk_len=cfg.chunk_tokens, page_tokens=cfg.page_tokens, dtype=dtype,
+                         hbm_budget_bytes=int(budget_bytes), window_chunks=cfg.window_chunks)
+    model = WanNSAAR(cfg, cache, seed=4)
+    t_alloc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    model.prefill(history, seed=5, student_t=(dtype == "fp8"))
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    noise = lambda: torch.randn((1, cfg.chunk_tokens, cfg.in_dim * cfg.patch), generator=gen,
+                                device="cuda").to(torch.bfloat16)
+    cid = history
+    for _ in range(warm):
+        model.step(cid, noise())
+        cid += 1
+    torch.cuda.synchronize()
+    s0 = dict(cache.stats)
+    times = []
+    for _ in range(steps):
+        x = noise()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.step(cid, x)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        cid += 1
+    s1 = dict(cache.stats)
+    # one more chunk with per-category event timers (not part of the timed mean)
+    model.timers = {}
+    model.step(cid, noise())
+    torch.cuda.synchronize()
+    breakdown = {k: round(sum(a.elapsed_time(b) for a, b in v), 3) for k, v in model.timers.items()}
+    model.timers = None
+    moved = (s1["evicted_bytes"] - s0["evicted_bytes"]) + (s1["promoted_bytes"] - s0["promoted_bytes"])
+    res = {
+        "dtype": "fp8e4m3" if dtype == "fp8" else "bf16",
+        "ms_per_ar_chunk": round(1e3 * sum(times) / len(times), 2),
+        "steps": steps,
+        "cached_chunks_at_start": history,
+        "cached_tokens_per_layer": history * cfg.chunk_tokens,
+        "cache_bytes_total": history * cfg.layers * cfg.heads * 2 * cache.unit_bytes,
+        "hbm_budget_bytes": cache.hbm_budget_bytes,
+        "hbm_unit_slots": cache.n_slots,
+        "host_unit_slots": cache.n_host,
+        "per_chunk": {
+            "evicted_bytes": (s1["evicted_bytes"] - s0["evicted_bytes"]) // steps,
+            "promoted_bytes": (s1["promoted_bytes"] - s0["promoted_bytes"]) // steps,
+            "host_units_touched": (s1["misses"] - s0["misses"]) // steps,
+            "hbm_units_touched": (s1["hits"] - s0["hits"]) // steps,
+        },
+        "host_link_bytes_per_chunk": moved // steps,
+        "lru_hit_rate": round((s1["hits"] - s0["hits"]) /
+                              max(1, (s1["hits"] - s0["hits"]) + (s1["misses"] - s0["misses"])), 4),
+        "breakdown_ms_one_chunk": breakdown,
+        "setup_s": {"alloc": round(t_alloc, 1), "prefill": round(t_prefill, 1)},
+        "selection_useful_tflop_per_chunk": round(
+            (cfg.denoise_steps + 1) * cfg.layers * 4 * cfg.chunk_tokens * cfg.heads * cfg.head_dim *
+            cfg.topk * cfg.page_tokens / 1e12, 3),
+    }
+    del model
+    cache.close()
+    del cache
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -230,6 +310,13 @@ def main():
         "ms_per_ar_chunk": None,
         "cpu_baseline": None,
     }
+    if not args.no_ar:
+        del q2, k2
+        torch.cuda.empty_cache()
+        res["ms_per_ar_chunk"] = {
+            "bf16": run_ar(torch.bfloat16, args.ar_history, args.ar_steps),
+            "fp8": run_ar("fp8", args.ar_history, args.ar_steps),
+        }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(q, k, v, ids, args.cpu_seconds)
     print(json.dumps(res), flush=True)
