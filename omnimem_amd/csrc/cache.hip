@@ -73,13 +73,10 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& r, float (&f)[8]) {
 }
 
 __device__ __forceinline__ uint2 quant8(const float (&x)[8], float inv) {
-  uint32_t w[2] = {0u, 0u};
+  float y[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float y = fminf(fmaxf(x[i] * inv, -448.0f), 448.0f);
-    w[i / 4] |= static_cast<uint32_t>(f32_to_e4m3(y)) << (8 * (i & 3));
-  }
-  return make_uint2(w[0], w[1]);
+  for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(x[i] * inv, -448.0f), 448.0f);
+  return make_uint2(f32x4_to_e4m3(y[0], y[1], y[2], y[3]), f32x4_to_e4m3(y[4], y[5], y[6], y[7]));
 }
 
 // 8 pooled sums / count, rounded to bf16 and packed (zeros for an empty page)

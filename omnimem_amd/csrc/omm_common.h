@@ -80,6 +80,29 @@ __host__ __device__ inline float e4m3_to_f32(uint8_t c) {
   return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | sign);
 }
 
+// ---- hardware conversions (gfx950) ------------------------------------------------------------
+typedef float omm_f32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 omm_bf16x2;
+
+// Two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const omm_bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// Four OCP e4m3fn codes (one word, byte 0 first) -> four floats, exact (v_cvt_pk_f32_fp8).
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* f) {
+  const omm_f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const omm_f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
+}
+// Four floats already within [-448, 448] -> four e4m3fn codes, round to nearest even
+// (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return static_cast<uint32_t>(w);
+}
+
 // Element traits: T is the storage type of q/k/v tensors.
 struct bf16_t { uint16_t bits; };
 struct f16_t { _Float16 v; };

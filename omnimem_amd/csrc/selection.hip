@@ -29,8 +29,7 @@ template <> struct Mfma<bf16_t> {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
-           (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    return pack_bf16x2(lo, hi);
   }
 };
 template <> struct Mfma<f16_t> {
@@ -252,16 +251,11 @@ template <> struct Stage<uint8_t> {
   }
   template <typename QT>
   __device__ __forceinline__ static uint4 dequant8(uint2 c, float s) {
-    const uint32_t w[2] = {c.x, c.y};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t word = w[i / 2] >> (16 * (i & 1));
-      const float lo = e4m3_to_f32(static_cast<uint8_t>(word & 0xffu)) * s;
-      const float hi = e4m3_to_f32(static_cast<uint8_t>((word >> 8) & 0xffu)) * s;
-      o[i] = Mfma<QT>::pack2(lo, hi);
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    float f[8];
+    e4m3x4_to_f32(c.x, f);
+    e4m3x4_to_f32(c.y, f + 4);
+    return make_uint4(Mfma<QT>::pack2(f[0] * s, f[1] * s), Mfma<QT>::pack2(f[2] * s, f[3] * s),
+                      Mfma<QT>::pack2(f[4] * s, f[5] * s), Mfma<QT>::pack2(f[6] * s, f[7] * s));
   }
 };
 

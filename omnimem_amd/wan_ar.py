@@ -143,6 +143,7 @@ class WanNSAAR:
         half = hd // 2
         self.inv_freq = 1.0 / (10000 ** (torch.arange(half, device=self.device, dtype=torch.float64) / half))
         self.timers: Optional[Dict[str, List]] = None
+        self._rope_tab: Dict = {}
 
     # ------------------------------------------------------------------ pieces
     def _tic(self, name):
@@ -160,15 +161,18 @@ class WanNSAAR:
         self.timers.setdefault(tok[0], []).append((tok[1], e))
 
     def _rope(self, x: torch.Tensor, start: int) -> torch.Tensor:
-        """x [1, S, H, D]: rotate interleaved pairs by angle pos * inv_freq (fp64 angles)."""
+        """x [1, S, H, D]: rotate interleaved pairs by angle pos * inv_freq (complex multiply in
+        fp32; the angle table of a chunk is built once, in fp64)."""
         S = x.shape[1]
-        pos = torch.arange(start, start + S, device=x.device, dtype=torch.float64)
-        ang = torch.outer(pos, self.inv_freq)
-        cos, sin = ang.cos().float()[None, :, None, :], ang.sin().float()[None, :, None, :]
-        xf = x.float().unflatten(-1, (-1, 2))
-        a, b = xf[..., 0], xf[..., 1]
-        out = torch.stack((a * cos - b * sin, a * sin + b * cos), -1).flatten(-2)
-        return out.to(x.dtype)
+        key = (start, S)
+        rot = self._rope_tab.get(key)
+        if rot is None:
+            pos = torch.arange(start, start + S, device=x.device, dtype=torch.float64)
+            ang = torch.outer(pos, self.inv_freq)
+            rot = torch.polar(torch.ones_like(ang), ang).to(torch.complex64)[None, :, None, :]
+            self._rope_tab = {key: rot}  # one chunk at a time
+        xc = torch.view_as_complex(x.float().unflatten(-1, (-1, 2)).contiguous())
+        return torch.view_as_real(xc * rot).flatten(-2).to(x.dtype)
 
     def _time_embed(self, t: float) -> torch.Tensor:
         cfg = self.cfg
