@@ -16,8 +16,9 @@ Recency.  Every append and every selection call stamps the units it touches with
 device (no host synchronisation, unlike the reference's ``unique().cpu()`` per call).  At a chunk
 boundary ``flush()`` reads the stamps once, ranks units by (epoch, chunk id) -- the order in which
 the reference's OrderedDict LRU sees them -- and moves units between the pools in one batched
-copy: the most recent units stay in HBM up to ``lru_max_size`` units per (layer, head) (the
-reference's count) or up to the HBM budget (bytes); sink and window chunks always stay.
+copy: per (layer, head), the most recent units stay in HBM up to ``lru_max_size`` units (the
+reference's count) or up to an equal share of the HBM byte budget; sink and window chunks always
+stay.
 
 Streams.  Every method enqueues on the current stream of ``device``; use one stream per cache.
 """
@@ -319,38 +320,35 @@ class PagedKVCache:
             mask[l, :, :] = prot[None, :]
         return mask
 
+    def head_capacity(self) -> int:
+        """HBM units each (layer, head) may keep: ``lru_max_size`` (the reference's count), or an
+        equal share of the budget minus the slot reserved for the next chunk."""
+        if self.lru_max_size > 0:
+            return self.lru_max_size
+        return max(1, self.n_slots // (self.L * self.H) - 1)
+
     def _plan(self, st: np.ndarray, reserve: int):
-        """Desired HBM set: protected units, then the most recent (epoch, chunk) units."""
+        """Desired HBM set: per (layer, head), its sink / window units, then its most recent
+        (epoch, chunk) units up to ``head_capacity()``.  A per-head share, not one LRU over all
+        layers: the layers are touched in a fixed cycle, and a single LRU would evict whole layers
+        every chunk."""
         written = self._table_h != -1
         prot = self._protected() & written
-        # rank key: epoch * 2^20 + chunk (later epoch, then larger chunk = more recent)
+        # rank key: later epoch first, then larger chunk id (the reference's touch order)
         key = st * (1 << 20) + np.arange(self.max_chunks)[None, None, :]
-        desired = prot.copy()
-        if self.lru_max_size > 0:
-            for l in range(self.L):
-                for h in range(self.H):
-                    cand = np.nonzero(written[l, h] & ~prot[l, h])[0]
-                    if cand.size == 0:
-                        continue
-                    room = max(0, self.lru_max_size - int(prot[l, h].sum()))
-                    order = cand[np.argsort(-key[l, h, cand], kind="stable")]
-                    desired[l, h, order[:room]] = True
-        cap = self.n_slots - reserve
-        n_prot = int(desired.sum())
-        if n_prot > cap:
+        key = np.where(written & ~prot, key, -1)
+        cap = self.head_capacity()
+        room = np.maximum(0, cap - prot.sum(-1))                          # [L, H]
+        order = np.argsort(-key, axis=-1, kind="stable")                  # most recent first
+        rank = np.empty_like(order)
+        np.put_along_axis(rank, order, np.arange(self.max_chunks)[None, None, :].repeat(
+            self.L, 0).repeat(self.H, 1), axis=-1)
+        desired = prot | ((key >= 0) & (rank < room[..., None]))
+        total = int(desired.sum())
+        if total > self.n_slots - reserve:
             raise BlockKVBackendError(
-                f"{n_prot} protected / LRU units exceed the {cap} HBM slots left after reserving "
-                f"{reserve} for the next chunk")
-        cand = written & ~desired
-        if self.lru_max_size > 0:
-            # the per-head LRU decides; the budget only caps it
-            cand_idx = np.zeros(0, dtype=np.int64)
-        else:
-            cand_idx = np.flatnonzero(cand)
-        if cand_idx.size:
-            order = cand_idx[np.argsort(-key.reshape(-1)[cand_idx], kind="stable")]
-            flat = desired.reshape(-1)
-            flat[order[:cap - n_prot]] = True
+                f"{total} units wanted in HBM exceed the {self.n_slots - reserve} slots left after "
+                f"reserving {reserve} for the next chunk (lower lru_max_size or raise the budget)")
         return desired
 
     def _move(self, layer_units, to_host: bool):
