@@ -320,12 +320,12 @@ class PagedKVCache:
             mask[l, :, :] = prot[None, :]
         return mask
 
-    def head_capacity(self) -> int:
+    def head_capacity(self, reserve: int = 0) -> int:
         """HBM units each (layer, head) may keep: ``lru_max_size`` (the reference's count), or an
-        equal share of the budget minus the slot reserved for the next chunk."""
+        equal share of the budget left after ``reserve`` slots (the next chunk's)."""
         if self.lru_max_size > 0:
             return self.lru_max_size
-        return max(1, self.n_slots // (self.L * self.H) - 1)
+        return max(1, (self.n_slots - reserve) // (self.L * self.H))
 
     def _plan(self, st: np.ndarray, reserve: int):
         """Desired HBM set: per (layer, head), its sink / window units, then its most recent
@@ -337,7 +337,7 @@ class PagedKVCache:
         # rank key: later epoch first, then larger chunk id (the reference's touch order)
         key = st * (1 << 20) + np.arange(self.max_chunks)[None, None, :]
         key = np.where(written & ~prot, key, -1)
-        cap = self.head_capacity()
+        cap = self.head_capacity(reserve)
         room = np.maximum(0, cap - prot.sum(-1))                          # [L, H]
         order = np.argsort(-key, axis=-1, kind="stable")                  # most recent first
         rank = np.empty_like(order)
