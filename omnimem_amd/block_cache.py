@@ -394,24 +394,48 @@ class PagedKVCache:
         return len(src) * 2 * (self.unit_bytes + self.scale_bytes)
 
     def _apply(self, desired: np.ndarray):
+        """Move units so that HBM holds exactly the desired written units.  Evictions and
+        promotions alternate in batches bounded by the free slots of the receiving pool (a
+        promotion frees a host slot, an eviction an HBM slot), so a full host pool never
+        blocks a swap; the least recent units leave first, the most recent arrive first."""
         resident = self._table_h >= 0
         on_host = self._table_h <= -2
-        evict = list(zip(*np.nonzero(resident & ~desired)))
-        promote = list(zip(*np.nonzero(on_host & desired)))
-        if len(evict) > len(self._free_host):
-            raise BlockKVBackendError(
-                f"host pool full: {len(evict)} units to evict, {len(self._free_host)} host slots free")
-        eb = self._move(evict, to_host=True)
-        room = len(self._free_hbm)
-        promote = promote[:room]
-        pb = self._move(promote, to_host=False)
-        for l in sorted({u[0] for u in evict} | {u[0] for u in promote}):
-            self._upload_table(l)
-        self.stats["evicted_units"] += len(evict)
-        self.stats["promoted_units"] += len(promote)
+        st = None
+        evict = np.argwhere(resident & ~desired)
+        promote = np.argwhere(on_host & desired)
+        if len(evict) > 1 or len(promote) > 1:
+            st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
+            key = lambda u: st[u[:, 0], u[:, 1], u[:, 2]] * (1 << 20) + u[:, 2]
+            if len(evict) > 1:
+                evict = evict[np.argsort(key(evict), kind="stable")]
+            if len(promote) > 1:
+                promote = promote[np.argsort(-key(promote), kind="stable")]
+        evict = [tuple(u) for u in evict]
+        promote = [tuple(u) for u in promote]
+        n_ev = n_pr = eb = pb = 0
+        touched = set()
+        while evict or promote:
+            ne = min(len(evict), len(self._free_host))
+            if ne:
+                eb += self._move(evict[:ne], to_host=True)
+                touched.update(u[0] for u in evict[:ne])
+                evict, n_ev = evict[ne:], n_ev + ne
+            npr = min(len(promote), len(self._free_hbm))
+            if npr:
+                pb += self._move(promote[:npr], to_host=False)
+                touched.update(u[0] for u in promote[:npr])
+                promote, n_pr = promote[npr:], n_pr + npr
+            if ne == 0 and npr == 0:
+                raise BlockKVBackendError(
+                    f"no free slot to swap through ({len(evict)} evictions, {len(promote)} "
+                    f"promotions pending)")
+        for l in sorted(touched):
+            self._upload_table(int(l))
+        self.stats["evicted_units"] += n_ev
+        self.stats["promoted_units"] += n_pr
         self.stats["evicted_bytes"] += eb
         self.stats["promoted_bytes"] += pb
-        return len(evict), len(promote)
+        return n_ev, n_pr
 
     def _make_room(self, need: int):
         st = self._recency()
