@@ -173,6 +173,7 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
     breakdown = {k: round(sum(a.elapsed_time(b) for a, b in v), 3) for k, v in model.timers.items()}
     model.timers = None
     moved = (s1["evicted_bytes"] - s0["evicted_bytes"]) + (s1["promoted_bytes"] - s0["promoted_bytes"])
+    page_bytes = 2 * cfg.page_tokens * cfg.head_dim * cache.elem  # one K page + one V page
     res = {
         "dtype": "fp8e4m3" if dtype == "fp8" else "bf16",
         "ms_per_ar_chunk": round(1e3 * sum(times) / len(times), 2),
@@ -188,8 +189,11 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
             "promoted_bytes": (s1["promoted_bytes"] - s0["promoted_bytes"]) // steps,
             "host_units_touched": (s1["misses"] - s0["misses"]) // steps,
             "hbm_units_touched": (s1["hits"] - s0["hits"]) // steps,
+            "host_page_reads": (s1["host_page_reads"] - s0["host_page_reads"]) // steps,
+            "hbm_page_reads": (s1["hbm_page_reads"] - s0["hbm_page_reads"]) // steps,
         },
-        "host_link_bytes_per_chunk": moved // steps,
+        "host_link_bytes_per_chunk": moved // steps + page_bytes *
+        (s1["host_page_reads"] - s0["host_page_reads"]) // steps,
         "lru_hit_rate": round((s1["hits"] - s0["hits"]) /
                               max(1, (s1["hits"] - s0["hits"]) + (s1["misses"] - s0["misses"])), 4),
         "breakdown_ms_one_chunk": breakdown,

@@ -108,6 +108,8 @@ typedef struct omm_paged_kv {
   const int32_t* unit_table;  /* [num_heads][max_chunks]: s >= 0 HBM slot; s <= -2 host slot
                                  (-2 - s); -1 never written */
   int32_t* stamp;             /* [num_heads][max_chunks] epoch of the last touch, or NULL */
+  int32_t* reads;             /* [num_heads][max_chunks] pages read since the caller last
+                                 cleared it (residency policy input), or NULL */
   int32_t num_heads;
   int32_t max_chunks;
   int32_t n_chunks;           /* chunks 0 .. n_chunks-1 are readable */
@@ -210,7 +212,8 @@ int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_v
  * with min(page_tokens, chunk_len - p*page_tokens) valid tokens); ids outside the readable
  * chunks or of units never written are skipped.  With kv->stamp and epoch > 0 every unit read
  * gets stamp = epoch (the LRU touch of the reference's _touch_lru_and_detect_missing,
- * nsa/ops/selection/padded_ptr/wrapper.py:253-291, without its host synchronisation). */
+ * nsa/ops/selection/padded_ptr/wrapper.py:253-291, without its host synchronisation); with
+ * kv->reads, reads[h][cid] += 1 for every listed page of the unit. */
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
                       int32_t epoch, void* stream);

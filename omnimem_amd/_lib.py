@@ -41,7 +41,7 @@ class PagedKV(ctypes.Structure):
         ("scale_k", ctypes.c_void_p), ("scale_v", ctypes.c_void_p),
         ("host_k", ctypes.c_void_p), ("host_v", ctypes.c_void_p),
         ("host_scale_k", ctypes.c_void_p), ("host_scale_v", ctypes.c_void_p),
-        ("unit_table", ctypes.c_void_p), ("stamp", ctypes.c_void_p),
+        ("unit_table", ctypes.c_void_p), ("stamp", ctypes.c_void_p), ("reads", ctypes.c_void_p),
         ("num_heads", ctypes.c_int32), ("max_chunks", ctypes.c_int32),
         ("n_chunks", ctypes.c_int32), ("chunk_len", ctypes.c_int32),
         ("page_tokens", ctypes.c_int32), ("pages_per_chunk", ctypes.c_int32),

@@ -12,13 +12,16 @@ kernel reads directly, so a unit that is not in HBM is never a miss that stalls 
 read over the host link page by page.  ``unit_table[layer]`` (int32 [H, max_chunks], on the
 device) maps a unit to its slot: s >= 0 HBM, s <= -2 host slot -2-s, -1 never written.
 
-Recency.  Every append and every selection call stamps the units it touches with an epoch on the
-device (no host synchronisation, unlike the reference's ``unique().cpu()`` per call).  At a chunk
-boundary ``flush()`` reads the stamps once, ranks units by (epoch, chunk id) -- the order in which
-the reference's OrderedDict LRU sees them -- and moves units between the pools in one batched
-copy: per (layer, head), the most recent units stay in HBM up to ``lru_max_size`` units (the
-reference's count) or up to an equal share of the HBM byte budget; sink and window chunks always
-stay.
+Residency.  Every append and every selection call stamps the units it touches with an epoch,
+and the selection kernel counts the pages it reads per unit, on the device (no host
+synchronisation, unlike the reference's ``unique().cpu()`` per call).  At a chunk boundary
+``flush()`` reads stamps and counts once and moves units between the pools in batched copies.
+With ``lru_max_size`` (the reference's count, models/cache.py:673-699) each (layer, head) keeps its
+most recent units by (epoch, chunk id), the order in which the reference's OrderedDict sees
+them.  With a byte budget the policy is cost-based, because a host unit is read in place page by
+page: units are evicted only to make room (coldest first: fewest pages read, then least recent),
+and a host unit is promoted only when its page reads over the last interval exceed the bytes a
+swap would move.  Sink and window chunks always stay in HBM.
 
 Streams.  Every method enqueues on the current stream of ``device``; use one stream per cache.
 """
@@ -139,6 +142,8 @@ class PagedKVCache:
                            for _ in range(self.L)]
         self.stamp = [torch.zeros((H, MC), dtype=torch.int32, device=self.device)
                       for _ in range(self.L)]
+        self.reads = [torch.zeros((H, MC), dtype=torch.int32, device=self.device)
+                      for _ in range(self.L)]
         ncb = MC * self.ppc
         self.k_cmp = [torch.zeros((1, ncb, H, self.D), dtype=torch.bfloat16, device=self.device)
                       for _ in range(self.L)]
@@ -166,12 +171,14 @@ class PagedKVCache:
         for l in range(self.L):
             self.unit_table[l].fill_(-1)
             self.stamp[l].zero_()
+            self.reads[l].zero_()
         self.n_chunks = [0] * self.L
         self._staged_k.clear()
         self._epoch = 0
         self._flush_epoch = 0
         self.stats = {"hits": 0, "misses": 0, "evicted_units": 0, "promoted_units": 0,
-                      "evicted_bytes": 0, "promoted_bytes": 0, "flushes": 0}
+                      "evicted_bytes": 0, "promoted_bytes": 0, "flushes": 0,
+                      "hbm_page_reads": 0, "host_page_reads": 0}
 
     def next_epoch(self) -> int:
         self._epoch += 1
@@ -194,6 +201,7 @@ class PagedKVCache:
         kv.host_k, kv.host_v = self._host_k.dev_ptr, self._host_v.dev_ptr
         kv.unit_table = self.unit_table[layer].data_ptr()
         kv.stamp = self.stamp[layer].data_ptr()
+        kv.reads = self.reads[layer].data_ptr()
         kv.num_heads, kv.max_chunks, kv.n_chunks = self.H, self.max_chunks, self.n_chunks[layer]
         kv.chunk_len, kv.page_tokens, kv.pages_per_chunk = self.chunk_len, self.P, self.ppc
         kv.head_dim = self.D
@@ -306,11 +314,6 @@ class PagedKVCache:
         return (out, lse) if return_lse else out
 
     # ---------------------------------------------------------------- residency
-    def _recency(self):
-        """Host copy of every layer's stamps: int64 [L, H, MC] (one synchronisation)."""
-        st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
-        return st
-
     def _protected(self) -> np.ndarray:
         mask = np.zeros((self.L, self.H, self.max_chunks), dtype=bool)
         c = np.arange(self.max_chunks)
@@ -327,11 +330,14 @@ class PagedKVCache:
             return self.lru_max_size
         return max(1, (self.n_slots - reserve) // (self.L * self.H))
 
-    def _plan(self, st: np.ndarray, reserve: int):
+    def _plan(self, st: np.ndarray, reserve: int, rd: Optional[np.ndarray] = None):
+        if self.lru_max_size > 0 or rd is None:
+            return self._plan_lru(st, reserve)
+        return self._plan_cost(st, rd, reserve)
+
+    def _plan_lru(self, st: np.ndarray, reserve: int):
         """Desired HBM set: per (layer, head), its sink / window units, then its most recent
-        (epoch, chunk) units up to ``head_capacity()``.  A per-head share, not one LRU over all
-        layers: the layers are touched in a fixed cycle, and a single LRU would evict whole layers
-        every chunk."""
+        (epoch, chunk) units up to ``head_capacity()``."""
         written = self._table_h != -1
         prot = self._protected() & written
         # rank key: later epoch first, then larger chunk id (the reference's touch order)
@@ -350,6 +356,47 @@ class PagedKVCache:
                 f"{total} units wanted in HBM exceed the {self.n_slots - reserve} slots left after "
                 f"reserving {reserve} for the next chunk (lower lru_max_size or raise the budget)")
         return desired
+
+    def _plan_cost(self, st: np.ndarray, rd: np.ndarray, reserve: int):
+        """Budget policy: keep what is resident, evict the coldest units only to make room, and
+        swap a host unit in when its page reads beat a resident unit's by more than the pages a
+        swap moves (two units each way)."""
+        written = self._table_h != -1
+        prot = (self._protected() & written).reshape(-1)
+        res = (self._table_h >= 0).reshape(-1)
+        host = (self._table_h <= -2).reshape(-1)
+        reads = rd.reshape(-1).astype(np.int64)
+        stamp = st.reshape(-1)
+        chunk = np.broadcast_to(np.arange(self.max_chunks), st.shape).reshape(-1)
+        desired = res | prot
+        cap = self.n_slots - reserve
+        # coldest first: fewest pages read, then oldest touch, then oldest chunk
+        cold = lambda idx: idx[np.lexsort((chunk[idx], stamp[idx], reads[idx]))]
+        movable = cold(np.flatnonzero(desired & ~prot))
+        over = int(desired.sum()) - cap
+        if over > 0:
+            if over > movable.size:
+                raise BlockKVBackendError(
+                    f"{int(prot.sum())} sink / window units exceed the {cap} HBM slots left after "
+                    f"reserving {reserve}")
+            desired[movable[:over]] = False
+            movable = movable[over:]
+        hot = np.flatnonzero(host & ~desired & (reads > 0))
+        hot = hot[np.argsort(-reads[hot], kind="stable")]
+        unit_pages = self.ppc
+        free = cap - int(desired.sum())
+        i = 0
+        while i < hot.size and free > 0 and reads[hot[i]] > unit_pages:
+            desired[hot[i]] = True
+            free -= 1
+            i += 1
+        j = 0
+        while i < hot.size and j < movable.size and reads[hot[i]] > reads[movable[j]] + 2 * unit_pages:
+            desired[hot[i]] = True
+            desired[movable[j]] = False
+            i += 1
+            j += 1
+        return desired.reshape(self._table_h.shape)
 
     def _move(self, layer_units, to_host: bool):
         """Copy units (list of (l, h, c)) between the pools; returns bytes moved."""
@@ -437,27 +484,38 @@ class PagedKVCache:
         self.stats["promoted_bytes"] += pb
         return n_ev, n_pr
 
+    def _counts(self):
+        """Host copies of every layer's stamps and page-read counts (one synchronisation)."""
+        st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
+        rd = torch.stack(self.reads).cpu().numpy()
+        return st, rd
+
     def _make_room(self, need: int):
-        st = self._recency()
-        desired = self._plan(st, reserve=need)
+        st, rd = self._counts()
+        desired = self._plan(st, reserve=need, rd=rd)
         self._apply(desired)
         if len(self._free_hbm) < need:
             raise BlockKVBackendError(f"cannot free {need} HBM slots")
 
     def flush(self, reserve_next_chunk: bool = True) -> dict:
         """Chunk-boundary residency update (MMCache.flush_offload, models/cache.py:1032): one
-        stamp read, then batched evict / promote copies.  With ``reserve_next_chunk`` the HBM
-        slots of the next chunk of every layer and head are assigned here, so the appends of the
-        next AR step never touch the host.  Returns this flush's counts."""
-        st = self._recency()
+        read of the stamps and page counts, then batched evict / promote copies.  With
+        ``reserve_next_chunk`` the HBM slots of the next chunk of every layer and head are
+        assigned here, so the appends of the next AR step never touch the host.  Returns this
+        flush's counts."""
+        st, rd = self._counts()
         touched = st > self._flush_epoch
         written = self._table_h != -1
-        hits = int((touched & (self._table_h >= 0)).sum())
-        misses = int((touched & (self._table_h <= -2)).sum())
+        res, host = self._table_h >= 0, self._table_h <= -2
+        hits = int((touched & res).sum())
+        misses = int((touched & host).sum())
+        hbm_reads, host_reads = int(rd[res].sum()), int(rd[host].sum())
         self.stats["hits"] += hits
         self.stats["misses"] += misses
+        self.stats["hbm_page_reads"] += hbm_reads
+        self.stats["host_page_reads"] += host_reads
         reserve = self.L * self.H if reserve_next_chunk else 0
-        desired = self._plan(st, reserve=reserve) & written
+        desired = self._plan(st, reserve=reserve, rd=rd) & written
         ev, pr = self._apply(desired)
         if reserve_next_chunk:
             for l in range(self.L):
@@ -471,9 +529,12 @@ class PagedKVCache:
                 for h in free:
                     row[h] = self._free_hbm.pop()
                 self._upload_table(l)
+        for r in self.reads:
+            r.zero_()
         self._flush_epoch = self._epoch
         self.stats["flushes"] += 1
-        return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr}
+        return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr,
+                "hbm_page_reads": hbm_reads, "host_page_reads": host_reads}
 
     def lru_hit_rate_overall(self) -> float:
         """Fraction of touched units found in HBM (models/cache.py:713)."""

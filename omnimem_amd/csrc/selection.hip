@@ -121,6 +121,7 @@ struct PagedAcc {
   const int32_t* unit;
   const int32_t* ids;
   int32_t* stamp;
+  int32_t* reads;
   int64_t is0, is1, is2, is3;
   int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
   __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
@@ -148,16 +149,19 @@ struct PagedAcc {
     return r;
   }
   // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
-  // epoch, so the races are benign)
+  // epoch, so the races are benign) and count its pages read (vector atomics)
   __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
-    if (stamp == nullptr || epoch <= 0) return;
+    const bool st = stamp != nullptr && epoch > 0;
+    if (!st && reads == nullptr) return;
     for (int t = threadIdx.x; t < T; t += blockDim.x) {
       const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
       if (bid < 0) continue;
       const int cid = bid / ppc;
       if (cid >= n_chunks || cid >= max_chunks) continue;
       const int64_t u = static_cast<int64_t>(h) * max_chunks + cid;
-      if (unit[u] != -1) stamp[u] = epoch;
+      if (unit[u] == -1) continue;
+      if (st) stamp[u] = epoch;
+      if (reads != nullptr) atomicAdd(reads + u, 1);
     }
   }
 };
@@ -731,7 +735,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
                          nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
                          static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
-                         idp, kv->stamp, ids->stride[0], ids->stride[1], ids->stride[2],
+                         idp, kv->stamp, kv->reads, ids->stride[0], ids->stride[1], ids->stride[2],
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
                          kv->n_slots, kv->n_host_slots};
@@ -743,7 +747,8 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<uint8_t> acc{static_cast<const uint8_t*>(kv->pool_k), static_cast<const uint8_t*>(kv->pool_v),
                           kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
                           static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
-                          kv->host_scale_v, kv->unit_table, idp, kv->stamp, ids->stride[0],
+                          kv->host_scale_v, kv->unit_table, idp, kv->stamp, kv->reads,
+                          ids->stride[0],
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
                           kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};
