@@ -210,98 +210,143 @@ __device__ __forceinline__ TileIt next_tile(const Acc& acc, const TileIt& c, int
 }
 
 // ---- staging: global -> registers -> LDS -----------------------------------------------------
-// A staging unit is 4 consecutive keys x 8 consecutive dims.
-template <typename KVT> struct Stage;
+// K tile in LDS: Ks[key][KP], KP = D + 8 (row pitch 272 B for D = 128: the 16-byte A-operand
+// reads of 16 consecutive rows and the 16-byte row stores are both bank-conflict free).
+// V tile in LDS, transposed: Vt[d][VP], VP = 72; the 4-key chunk c of row d is stored at chunk
+// c ^ ((d >> 3) & 15), which makes both the transposing 8-byte stores (16 lanes: one key chunk,
+// 16 row groups) and the 8-byte PV-operand reads (16 consecutive rows) conflict free.
+constexpr int kVP = 72;
 
-// 16-bit storage (bf16 / f16): 16-byte loads, stored as is.
-template <typename KVT> struct Stage16 {
-  uint4 k[4], v[4];
-  template <typename QT>
-  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int kq, int dc) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int key = kq * 4 + kk;
-      if (key < n) {
-        const int64_t row = tok0 + key;
-        k[kk] = *reinterpret_cast<const uint4*>(static_cast<const KVT*>(br.k) + row * br.sk + dc * 8);
-        v[kk] = *reinterpret_cast<const uint4*>(static_cast<const KVT*>(br.v) + row * br.sv + dc * 8);
-      } else {
-        k[kk] = make_uint4(0, 0, 0, 0);
-        v[kk] = make_uint4(0, 0, 0, 0);
-      }
-    }
+__device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
+
+// 8 consecutive elements of a K/V row at byte address p as 8 MFMA-type elements: 16-bit storage
+// loads 16 bytes as is; fp8 pages load 8 bytes and dequantise (code * page scale, rounded).
+template <typename KVT> struct Row8;
+template <> struct Row8<bf16_t> {
+  __device__ __forceinline__ static uint4 load(const char* p, int, float) {
+    return *reinterpret_cast<const uint4*>(p);
   }
 };
-template <> struct Stage<bf16_t> : Stage16<bf16_t> {};
-template <> struct Stage<f16_t> : Stage16<f16_t> {};
-
-// fp8 e4m3fn pages: 8-byte loads, dequantised (code * page scale) and rounded to the MFMA type.
-template <> struct Stage<uint8_t> {
-  uint4 k[4], v[4];
-  template <typename QT>
-  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int kq, int dc) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int key = kq * 4 + kk;
-      uint2 ck = make_uint2(0, 0), cv = make_uint2(0, 0);
-      if (key < n) {
-        const int64_t row = tok0 + key;
-        ck = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(br.k) + row * br.sk + dc * 8);
-        cv = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(br.v) + row * br.sv + dc * 8);
-      }
-      k[kk] = dequant8<QT>(ck, br.scale_k);
-      v[kk] = dequant8<QT>(cv, br.scale_v);
-    }
+template <> struct Row8<f16_t> {
+  __device__ __forceinline__ static uint4 load(const char* p, int, float) {
+    return *reinterpret_cast<const uint4*>(p);
   }
-  template <typename QT>
-  __device__ __forceinline__ static uint4 dequant8(uint2 c, float s) {
+};
+template <> struct Row8<uint8_t> {
+  __device__ __forceinline__ static uint4 load(const char* p, int, float s) {
+    const uint2 c = *reinterpret_cast<const uint2*>(p);
     float f[8];
     e4m3x4_to_f32(c.x, f);
     e4m3x4_to_f32(c.y, f + 4);
-    return make_uint4(Mfma<QT>::pack2(f[0] * s, f[1] * s), Mfma<QT>::pack2(f[2] * s, f[3] * s),
-                      Mfma<QT>::pack2(f[4] * s, f[5] * s), Mfma<QT>::pack2(f[6] * s, f[7] * s));
+    return make_uint4(pack_bf16x2(f[0] * s, f[1] * s), pack_bf16x2(f[2] * s, f[3] * s),
+                      pack_bf16x2(f[4] * s, f[5] * s), pack_bf16x2(f[6] * s, f[7] * s));
   }
 };
 
-// 16-bit element i (0..7) of a 16-byte register group.
-__device__ __forceinline__ uint32_t half_of(const uint4& r, int i) {
-  const uint32_t w = (i < 2) ? r.x : (i < 4) ? r.y : (i < 6) ? r.z : r.w;
-  return (i & 1) ? (w >> 16) : (w & 0xffffu);
-}
+// Register staging of one 64-key tile by 128 threads.
+//   K: unit u = tid + 128 j -> key tid / DC + (128 / DC) j, 8-dim slice tid % DC (DC lanes per row)
+//   V: quad q = tid + 128 j -> dims slice tid % DC, keys 4 (tid / DC + (128 / DC) j) + r, r < 4
+// Each thread's byte offset inside a tile is computed once; a tile adds a wave-uniform base, so
+// the loads take the scalar-base + 32-bit-offset form with no per-load address arithmetic.
+template <typename KVT, int D>
+struct Stager {
+  static constexpr int DC = D / 8;                 // 16-byte slices per row
+  static constexpr int KU = 64 * DC / 128;         // K units per thread
+  static constexpr int VQ = 16 * DC / 128;         // V quads per thread
+  static constexpr int RS = 128 / DC;              // rows between a thread's units
+  static constexpr int ES = static_cast<int>(sizeof(KVT));
+  uint4 k[KU];
+  uint4 v[VQ][4];
+  uint32_t koff, voff;                             // bytes, within a tile
 
-template <int D>
-__device__ __forceinline__ void store_tile(const uint4 (&k)[4], const uint4 (&v)[4], uint16_t* Ks,
-                                           uint16_t* Vt, int kq, int dc) {
-  constexpr int KP = D + 8, VP = 64 + 8;
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-    *reinterpret_cast<uint4*>(Ks + (kq * 4 + kk) * KP + dc * 8) = k[kk];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint2 w;
-    w.x = half_of(v[0], i) | (half_of(v[1], i) << 16);
-    w.y = half_of(v[2], i) | (half_of(v[3], i) << 16);
-    *reinterpret_cast<uint2*>(Vt + (dc * 8 + i) * VP + kq * 4) = w;
+  __device__ __forceinline__ void init(int tid, int64_t sk, int64_t sv) {
+    koff = static_cast<uint32_t>(((tid / DC) * sk + (tid % DC) * 8) * ES);
+    voff = static_cast<uint32_t>((4 * (tid / DC) * sv + (tid % DC) * 8) * ES);
   }
-}
+
+  template <bool FULL>
+  __device__ __forceinline__ void load_impl(const BlockRef& br, int tok0, int n, int tid) {
+    const char* kb = static_cast<const char*>(br.k) + static_cast<int64_t>(tok0) * br.sk * ES;
+    const char* vb = static_cast<const char*>(br.v) + static_cast<int64_t>(tok0) * br.sv * ES;
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
+      if (FULL || tid / DC + RS * j < n)
+        k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
+      else
+        k[j] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < VQ; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const char* p = vb + static_cast<int64_t>(4 * RS * j + r) * br.sv * ES;
+        if (FULL || 4 * (tid / DC + RS * j) + r < n)
+          v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
+        else
+          v[j][r] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int tid) {
+    if (n >= 64)
+      load_impl<true>(br, tok0, n, tid);
+    else
+      load_impl<false>(br, tok0, n, tid);
+  }
+
+  __device__ __forceinline__ void store(uint16_t* Ks, uint16_t* Vt, int tid) const {
+    constexpr int KP = D + 8;
+    const int dc = tid % DC;
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const int key = tid / DC + RS * j;
+      *reinterpret_cast<uint4*>(Ks + key * KP + dc * 8) = k[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VQ; ++j) {
+      const int kq = tid / DC + RS * j;
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[j][0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[j][1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[j][2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[j][3]);
+      // rows 8 dc .. 8 dc + 7 share the swizzle (8 dc) >> 3 = dc
+      uint16_t* vrow = Vt + (8 * dc) * kVP + ((kq ^ (dc & 15)) << 2);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // dims 8dc + 2e (low halves) and 8dc + 2e + 1 (high halves) of the 4 keys
+        const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u),
+                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100u));
+        const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u),
+                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302u));
+        *reinterpret_cast<uint2*>(vrow + (2 * e) * kVP) = lo;
+        *reinterpret_cast<uint2*>(vrow + (2 * e + 1) * kVP) = hi;
+      }
+    }
+  }
+};
 
 // ---- MFMA kernel ------------------------------------------------------------------------------
-constexpr int kMfmaThreads = 256;
+// One workgroup = (b, head, 64 queries of one query group), 2 waves x 32 queries.  Each wave owns
+// two 16-query MFMA row blocks that share every K and V^T operand read from LDS, so the LDS
+// bytes per MFMA FLOP are half those of 16 queries per wave.
+constexpr int kMfmaThreads = 128;
 
 template <typename QT, typename Acc, int D>
 __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
     int MG, int T, int chunk, float scale, int nsub) {
-  constexpr int KP = D + 8, VP = 64 + 8;
-  constexpr int KS = 64 * KP, VS = D * VP;
+  constexpr int KP = D + 8;
+  constexpr int KS = 64 * KP, VS = D * kVP;
   constexpr int SD = D / 32;   // k-steps of QK^T
   constexpr int ND = D / 16;   // d-tiles of PV
-  constexpr int UNITS = 16 * (D / 8);
-  __shared__ __align__(16) uint16_t lds[2 * (KS + VS)];
+  __shared__ __align__(16) uint16_t lds[KS + VS];
+  uint16_t* Ks = lds;
+  uint16_t* Vt = lds + KS;
 
   const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
-  // work item: (b, h, g, sub), XCD-major so one XCD walks consecutive groups of one head
   const int total = static_cast<int>(gridDim.x);
   int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
   const int sub = wi % nsub; wi /= nsub;
@@ -309,126 +354,155 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   const int h = wi % H;
   const int b = wi / H;
 
-  const int m0 = g * G + sub * 64;                       // first query of this workgroup
-  const int m_end = min(min(g * G + G, M), m0 + 64);     // exclusive
+  const int m0 = g * G + sub * 64;
+  const int m_end = min(min(g * G + G, M), m0 + 64);
   const int qc = (g * G) / chunk;
   if (sub == 0) acc.touch(b, g, h, T);
-  const int my_q = m0 + 16 * w + l16;
-  const bool q_ok = my_q < m_end;
 
-  // Q^T operand: row my_q, dims 32s + 8 j4 .. +7
-  uint4 qb[SD];
+  // Q^T operands of this wave's two 16-query blocks: row my_q[qb], dims 32 s + 8 j4 .. +7
+  int my_q[2];
+  bool q_ok[2];
+  uint4 qb[2][SD];
 #pragma unroll
-  for (int s = 0; s < SD; ++s)
-    qb[s] = q_ok ? *reinterpret_cast<const uint4*>(q.at(b, my_q, h, 32 * s + 8 * j4))
-                 : make_uint4(0, 0, 0, 0);
-
-  f32x4 o[ND];
+  for (int x = 0; x < 2; ++x) {
+    my_q[x] = m0 + 32 * w + 16 * x + l16;
+    q_ok[x] = my_q[x] < m_end;
 #pragma unroll
-  for (int i = 0; i < ND; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m2 = kNegInf, lsum = 0.0f;
-  const float c2 = scale * kLog2e;
-  const bool wave_active = (m0 + 16 * w) < m_end;
-
-  TileIt it = first_tile(acc, b, g, h, T, qc, 0);
-  using KVT = typename Acc::KV;
-  Stage<KVT> st;
-  const int unit = tid;  // one unit per thread when UNITS == 256
-  const int kq = unit / (D / 8), dc = unit % (D / 8);
-  const bool stager = unit < UNITS;
-  int cur = 0;
-  if (it.valid) {
-    if (stager) {
-      st.template load<QT>(it.br, it.tok0, it.n, kq, dc);
-      store_tile<D>(st.k, st.v, lds, lds + KS, kq, dc);
-    }
+    for (int s = 0; s < SD; ++s)
+      qb[x][s] = q_ok[x] ? *reinterpret_cast<const uint4*>(q.at(b, my_q[x], h, 32 * s + 8 * j4))
+                         : make_uint4(0, 0, 0, 0);
   }
+  const bool wave_active = (m0 + 32 * w) < m_end;
+  // PV operand row bases (see the V^T swizzle): bit 0 of the chunk is j4_0 ^ (l16 >> 3), bit 1
+  // is j4_1 ^ (i & 1)
+  const int sw0 = (j4 & 1) ^ (l16 >> 3);
+  const uint16_t* vb[2] = {Vt + l16 * kVP + 4 * sw0 + 8 * (j4 >> 1),
+                           Vt + l16 * kVP + 4 * sw0 + 8 * (1 - (j4 >> 1))};
+
+  f32x4 o[2][ND];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m2[2] = {kNegInf, kNegInf}, lsum[2] = {0.0f, 0.0f};
+  const float c2 = scale * kLog2e;
+
+  using KVT = typename Acc::KV;
+  Stager<KVT, D> st;
+  TileIt it = first_tile(acc, b, g, h, T, qc, 0);
+  st.init(tid, it.br.sk, it.br.sv);  // row strides are the same for every block of a call
+  if (it.valid) st.load(it.br, it.tok0, it.n, tid);
   while (it.valid) {
-    const TileIt nx = next_tile(acc, it, b, g, h, T, qc);
-    if (nx.valid && stager) st.template load<QT>(nx.br, nx.tok0, nx.n, kq, dc);
+    __syncthreads();  // every wave is done reading the previous tile
+    st.store(Ks, Vt, tid);
     __syncthreads();
+    const TileIt nx = next_tile(acc, it, b, g, h, T, qc);
+    if (nx.valid) st.load(nx.br, nx.tok0, nx.n, tid);  // in flight during this tile's MFMAs
     if (wave_active) {
-      const uint16_t* Ks = lds + cur * (KS + VS);
-      const uint16_t* Vt = Ks + KS;
-      f32x4 s4[4];
+      // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks
+      f32x4 s4[2][4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        s4[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        s4[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < SD; ++s) {
           const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
-          s4[t] = Mfma<QT>::run(a, qb[s], s4[t]);
+          s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+          s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
         }
+        __builtin_amdgcn_sched_barrier(0);  // bound the operand reads in flight (registers)
       }
-      // mask + online softmax (log2 domain); this lane holds keys 16t + 4 j4 + r of query l16
-      float mt = kNegInf;
+      if (it.n < 64) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = 16 * t + 4 * j4 + r;
-          const float x = key < it.n ? s4[t][r] * c2 : kNegInf;
-          s4[t][r] = x;
-          mt = fmaxf(mt, x);
+          for (int r = 0; r < 4; ++r)
+            if (16 * t + 4 * j4 + r >= it.n) s4[0][t][r] = s4[1][t][r] = kNegInf;
+      }
+      // online softmax in the log2 domain: p = 2^(s * c2 - m), m the running max of s * c2
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        float mt = kNegInf;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          mt = fmaxf(mt, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
+        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        // lazy rescale: keep the running max while no lane's max grows by more than 2^8
+        // (p stays <= 256, exact enough in fp32 and in the bf16 P operand)
+        const float mcand = fmaxf(m2[x], mt * c2);
+        if (__ballot(mcand > m2[x] + 8.0f) != 0ull) {
+          const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
+          const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
+          lsum[x] *= alpha;
+#pragma unroll
+          for (int i = 0; i < ND; ++i) o[x][i] *= alpha;
+          m2[x] = mcand;
         }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-      const float mnew = fmaxf(m2, mt);
-      const float alpha = (m2 == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m2 - mnew);
-      float ps = 0.0f;
+        const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+        float ps = 0.0f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = (s4[t][r] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s4[t][r] - mnew);
-          s4[t][r] = p;
-          ps += p;
-        }
-      lsum = lsum * alpha + ps;
-      m2 = mnew;
-#pragma unroll
-      for (int i = 0; i < ND; ++i) o[i] *= alpha;
-      // O^T += V^T P^T; k-slot s of lane group j4 is key 32u + 4 j4 + s (s < 4) or
-      // 32u + 16 + 4 j4 + (s - 4), for both operands
+          for (int r = 0; r < 4; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, -msafe));
+            s4[x][t][r] = pv;
+            ps += pv;
+          }
+        lsum[x] += ps;
+      }
+      // O^T += V^T P^T; k-slot e of lane group j4 is key 32u + 4 j4 + e (e < 4) or
+      // 32u + 16 + 4 j4 + (e - 4), for both operands
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        uint4 pb;
-        pb.x = Mfma<QT>::pack2(s4[2 * u][0], s4[2 * u][1]);
-        pb.y = Mfma<QT>::pack2(s4[2 * u][2], s4[2 * u][3]);
-        pb.z = Mfma<QT>::pack2(s4[2 * u + 1][0], s4[2 * u + 1][1]);
-        pb.w = Mfma<QT>::pack2(s4[2 * u + 1][2], s4[2 * u + 1][3]);
+        uint4 pb[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          pb[x].x = Mfma<QT>::pack2(s4[x][2 * u][0], s4[x][2 * u][1]);
+          pb[x].y = Mfma<QT>::pack2(s4[x][2 * u][2], s4[x][2 * u][3]);
+          pb[x].z = Mfma<QT>::pack2(s4[x][2 * u + 1][0], s4[x][2 * u + 1][1]);
+          pb[x].w = Mfma<QT>::pack2(s4[x][2 * u + 1][2], s4[x][2 * u + 1][3]);
+        }
 #pragma unroll
         for (int i = 0; i < ND; ++i) {
-          const uint16_t* vr = Vt + (16 * i + l16) * VP + 32 * u + 4 * j4;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-          o[i] = Mfma<QT>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[i]);
+          // row d = 16i + l16, chunk c = 8u + 4h + j4 stored at c ^ (2i + (l16 >> 3)): the
+          // lane-dependent bits are in vb[i & 1], the rest is a compile-time offset
+          const int i1 = (i >> 1) & 1, i2 = (i >> 2) & 1;
+          const uint16_t* vr = vb[i & 1] + (16 * i) * kVP + 32 * (u ^ i2);
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + 16 * i1);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16 * (1 - i1));
+          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          o[0][i] = Mfma<QT>::run(a, pb[0], o[0][i]);
+          o[1][i] = Mfma<QT>::run(a, pb[1], o[1][i]);
+          if ((i & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
-    if (!nx.valid) break;
-    cur ^= 1;
-    if (stager) store_tile<D>(st.k, st.v, lds + cur * (KS + VS), lds + cur * (KS + VS) + KS, kq, dc);
     it = nx;
   }
 
   // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
-  lsum += __shfl_xor(lsum, 16, kWave);
-  lsum += __shfl_xor(lsum, 32, kWave);
-  if (q_ok) {
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    QT* op = out.at(b, my_q, h, 0);
 #pragma unroll
-    for (int i = 0; i < ND; ++i) {
-      const int d0 = 16 * i + 4 * j4;
-      uint2 w2;
-      w2.x = Mfma<QT>::pack2(o[i][0] * inv, o[i][1] * inv);
-      w2.y = Mfma<QT>::pack2(o[i][2] * inv, o[i][3] * inv);
-      *reinterpret_cast<uint2*>(op + d0) = w2;
+  for (int x = 0; x < 2; ++x) {
+    float ls = lsum[x];
+    ls += __shfl_xor(ls, 16, kWave);
+    ls += __shfl_xor(ls, 32, kWave);
+    if (q_ok[x]) {
+      const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
+      QT* op = out.at(b, my_q[x], h, 0);
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        const int d0 = 16 * i + 4 * j4;
+        uint2 w2;
+        w2.x = Mfma<QT>::pack2(o[x][i][0] * inv, o[x][i][1] * inv);
+        w2.y = Mfma<QT>::pack2(o[x][i][2] * inv, o[x][i][3] * inv);
+        *reinterpret_cast<uint2*>(op + d0) = w2;
+      }
+      if (lse != nullptr && j4 == 0)
+        lse[(static_cast<int64_t>(b) * H + h) * M + my_q[x]] =
+            ls > 0.0f ? (m2[x] + __builtin_log2f(ls)) * kLn2 : kNegInf;
     }
-    if (lse != nullptr && j4 == 0)
-      lse[(static_cast<int64_t>(b) * H + h) * M + my_q] =
-          lsum > 0.0f ? (m2 + __builtin_log2f(lsum)) * kLn2 : kNegInf;
   }
 }
 
