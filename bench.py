@@ -293,13 +293,13 @@ def main():
                    "topk": TOPK, "chunk": CHUNK, "causal": True, "layers_per_forward": 30},
         "useful_gflop_per_step": round(flops / 1e9, 3),
         "roofline": {
-            "kernel": "sel_fwd_mfma_kernel",
+            "kernel": "sel_fwd_dma_kernel",
             "bound": "mfma",
             "achieved": round(sel_tflops, 3),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("sel_fwd_mfma_kernel<bf16_t, DenseAcc<bf16_t>, 128>"),
+            "traffic": measured_traffic("sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128>"),
             "kernel_ms": round(sel_ms, 4),
         },
         "topk": {

@@ -55,61 +55,90 @@ struct BlockRef {
   float scale_k, scale_v;
 };
 
+// Each accessor resolves slot t of a row in two steps: resolve() -> a compact entry (Ent: a few
+// 32-bit words, n = visible tokens, n <= 0 when skipped), evaluated by the MFMA kernels for 64
+// slots at once, one per lane; ref() -> the block's addresses from a wave-uniform entry.
+// order_key() orders the blocks of a row by position in memory (the walk visits them in that
+// order, so concurrent rows that share blocks tend to read them at the same time).
 template <typename T>
 struct DenseAcc {
   using KV = T;
+  struct Ent {
+    int t0, n;  // first token, visible tokens
+  };
   View4<const T> k, v;
   const int32_t* ids;
   int64_t is0, is1, is2, is3;
   int N, bs, chunk;
   bool causal;
-  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int q_chunk) const {
-    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int q_chunk) const {
+    Ent e{0, 0};
     const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
-    if (bid < 0) return r;
+    if (bid < 0) return e;
     const int64_t t0 = static_cast<int64_t>(bid) * bs;
-    if (t0 >= N) return r;
-    if (causal && t0 / chunk > q_chunk) return r;
+    if (t0 >= N) return e;
     int64_t n = N - t0 < bs ? N - t0 : bs;
     if (causal) {
+      // visible prefix ends at the query chunk's end: t0 / chunk > q_chunk  <=>  lim <= 0
       const int64_t lim = static_cast<int64_t>(q_chunk + 1) * chunk - t0;
       n = n < lim ? n : lim;
     }
-    if (n <= 0) return r;
-    r.k = k.at(b, t0, h, 0);
-    r.v = v.at(b, t0, h, 0);
-    r.sk = k.s1;
-    r.sv = v.s1;
-    r.nvalid = static_cast<int>(n);
-    return r;
+    if (n <= 0) return e;
+    e.t0 = static_cast<int>(t0);
+    e.n = static_cast<int>(n);
+    return e;
   }
+  __device__ __forceinline__ BlockRef ref(int b, int h, const Ent& e) const {
+    return BlockRef{k.at(b, e.t0, h, 0), v.at(b, e.t0, h, 0), k.s1, v.s1, e.n, 1.0f, 1.0f};
+  }
+  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.t0; }
   __device__ __forceinline__ void touch(int, int, int, int) const {}
 };
 
 struct PtrAcc {
   using KV = bf16_t;
+  struct Ent {
+    int64_t k, v;  // raw addresses (0 = skip)
+    int n;
+    int pad;
+  };
   const int64_t* pk;
   const int64_t* pv;
   int64_t s0, s1, s2, s3;
   int64_t stride_n;
   int bs;
-  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
-    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
     const int64_t off = b * s0 + g * s1 + h * s2 + t * s3;
-    const int64_t ak = pk[off], av = pv[off];
-    if (ak == 0 || av == 0) return r;
-    r.k = reinterpret_cast<const void*>(static_cast<uintptr_t>(ak));
-    r.v = reinterpret_cast<const void*>(static_cast<uintptr_t>(av));
-    r.sk = r.sv = stride_n;
-    r.nvalid = bs;
-    return r;
+    Ent e{pk[off], pv[off], 0, 0};
+    e.n = (e.k == 0 || e.v == 0) ? 0 : bs;
+    return e;
   }
+  __device__ __forceinline__ BlockRef ref(int, int, const Ent& e) const {
+    return BlockRef{reinterpret_cast<const void*>(static_cast<uintptr_t>(e.k)),
+                    reinterpret_cast<const void*>(static_cast<uintptr_t>(e.v)), stride_n,
+                    stride_n, e.n, 1.0f, 1.0f};
+  }
+  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.k; }
   __device__ __forceinline__ void touch(int, int, int, int) const {}
 };
+
+// Paged entries: page >= 0 is an HBM pool page, page < 0 the host pool page -1 - page; bid is
+// the block id (the walk order must not depend on residency); fp8 pages carry their
+// dequantisation scales.
+struct PagedEnt16 {
+  int page, n, bid;
+};
+struct PagedEnt8 {
+  int page, n, bid;
+  float sk, sv;
+};
+template <typename KVT> struct PagedEntOf { using type = PagedEnt16; };
+template <> struct PagedEntOf<uint8_t> { using type = PagedEnt8; };
 
 template <typename KVT>
 struct PagedAcc {
   using KV = KVT;
+  using Ent = typename PagedEntOf<KVT>::type;
   const KVT* pool_k;
   const KVT* pool_v;
   const float* sc_k;
@@ -124,30 +153,38 @@ struct PagedAcc {
   int32_t* reads;
   int64_t is0, is1, is2, is3;
   int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
-  __device__ __forceinline__ BlockRef block(int b, int g, int h, int t, int) const {
-    BlockRef r{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
+    Ent e{};
     const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
-    if (bid < 0) return r;
+    if (bid < 0) return e;
     const int cid = bid / ppc, p = bid - cid * ppc;
-    if (cid >= n_chunks || cid >= max_chunks) return r;
+    if (cid >= n_chunks || cid >= max_chunks) return e;
     const int32_t s = unit[static_cast<int64_t>(h) * max_chunks + cid];
-    if (s == -1 || s >= n_slots || (s < 0 && -2 - s >= n_host)) return r;
-    const int64_t page = (s >= 0 ? static_cast<int64_t>(s) : static_cast<int64_t>(-2 - s)) * ppc + p;
-    const int64_t off = page * P * D;
-    if (s >= 0) {
-      r.k = pool_k + off;
-      r.v = pool_v + off;
-      if (sc_k != nullptr) { r.scale_k = sc_k[page]; r.scale_v = sc_v[page]; }
-    } else {
-      r.k = host_k + off;
-      r.v = host_v + off;
-      if (hsc_k != nullptr) { r.scale_k = hsc_k[page]; r.scale_v = hsc_v[page]; }
-    }
-    r.sk = r.sv = D;
+    if (s == -1 || s >= n_slots || (s < 0 && -2 - s >= n_host)) return e;
+    const int page = (s >= 0 ? s : -2 - s) * ppc + p;
     const int rem = chunk_len - p * P;
-    r.nvalid = rem < P ? rem : P;
+    e.page = s >= 0 ? page : -1 - page;
+    e.n = rem < P ? rem : P;
+    e.bid = bid;
+    if constexpr (sizeof(KVT) == 1) {
+      const float* ck = s >= 0 ? sc_k : hsc_k;
+      const float* cv = s >= 0 ? sc_v : hsc_v;
+      e.sk = ck != nullptr ? ck[page] : 1.0f;
+      e.sv = cv != nullptr ? cv[page] : 1.0f;
+    }
+    return e;
+  }
+  __device__ __forceinline__ BlockRef ref(int, int, const Ent& e) const {
+    const bool hbm = e.page >= 0;
+    const int64_t off = static_cast<int64_t>(hbm ? e.page : -1 - e.page) * P * D;
+    BlockRef r{(hbm ? pool_k : host_k) + off, (hbm ? pool_v : host_v) + off, D, D, e.n, 1.0f, 1.0f};
+    if constexpr (sizeof(KVT) == 1) {
+      r.scale_k = e.sk;
+      r.scale_v = e.sv;
+    }
     return r;
   }
+  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.bid; }
   // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
   // epoch, so the races are benign) and count its pages read (vector atomics)
   __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
@@ -166,7 +203,15 @@ struct PagedAcc {
   }
 };
 
-// Key tiles of up to 64 tokens over the listed blocks (wave-uniform).
+template <typename Acc>
+__device__ __forceinline__ BlockRef resolve_block(const Acc& acc, int b, int g, int h, int t,
+                                                  int qc) {
+  const typename Acc::Ent e = acc.resolve(b, g, h, t, qc);
+  if (e.n <= 0) return BlockRef{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
+  return acc.ref(b, h, e);
+}
+
+// Key tiles of up to 64 tokens over the listed blocks (wave-uniform), one slot at a time.
 struct TileIt {
   int t, tok0, n;  // block slot, first token of the tile within the block, tokens in tile
   BlockRef br;
@@ -178,7 +223,7 @@ __device__ __forceinline__ TileIt first_tile(const Acc& acc, int b, int g, int h
                                              int t) {
   TileIt it;
   for (; t < T; ++t) {
-    const BlockRef br = acc.block(b, g, h, t, qc);
+    const BlockRef br = resolve_block(acc, b, g, h, t, qc);
     if (br.k != nullptr && br.nvalid > 0) {
       it.t = t;
       it.tok0 = 0;
@@ -208,6 +253,100 @@ __device__ __forceinline__ TileIt next_tile(const Acc& acc, const TileIt& c, int
   }
   return first_tile(acc, b, g, h, T, qc, c.t + 1);
 }
+
+// The same walk for a wave that resolved 64 slots at once: lane i holds the entry of slot
+// base + i.  Live slots are visited in ascending order_key (ties by slot): every workgroup then
+// sweeps its blocks from low to high addresses, so the workgroups running together on an XCD
+// read overlapping blocks at about the same time and share them in L2.  A slot's rank among the
+// live slots is counted once per 64 slots (one readlane and compare per live slot); the next
+// block is then a compare, a ballot and a find-first-set, with no memory access.  Within a row
+// the order only changes the fp32 summation order of the softmax.
+template <typename E>
+__device__ __forceinline__ E lane_entry(const E& e, int lane) {
+  static_assert(sizeof(E) % 4 == 0, "entries are 32-bit words");
+  constexpr int W = sizeof(E) / 4;
+  int w[W];
+  __builtin_memcpy(w, &e, sizeof(E));
+#pragma unroll
+  for (int i = 0; i < W; ++i) w[i] = __builtin_amdgcn_readlane(w[i], lane);
+  E r;
+  __builtin_memcpy(&r, w, sizeof(E));
+  return r;
+}
+
+template <typename Acc, int TK = 64>
+struct WaveWalk {
+  typename Acc::Ent e;
+  int rank;        // this lane's rank among the live slots of the batch (-1: not live)
+  int nlive, pos;  // live slots in the batch; rank of the current block (-1 before the first)
+  int base;        // first slot of the batch
+  int tok0, n;     // current tile: first token within the block, tokens (<= TK)
+  BlockRef br;
+  bool valid;
+
+  __device__ __forceinline__ void fill(const Acc& acc, int b, int g, int h, int T, int qc) {
+    const int lane = lane_id();
+    const int t = base + lane;
+    if (t < T) {
+      e = acc.resolve(b, g, h, t, qc);
+    } else {
+      e = typename Acc::Ent{};
+    }
+    const bool live = e.n > 0;
+    uint64_t m = __ballot(live);
+    nlive = __builtin_popcountll(m);
+    const int64_t key = Acc::order_key(e);
+    int r = 0;
+    while (m != 0ull) {
+      const int l = __builtin_ctzll(m);
+      m &= m - 1ull;
+      const int64_t ko = static_cast<int64_t>(
+          (static_cast<uint64_t>(static_cast<uint32_t>(
+               __builtin_amdgcn_readlane(static_cast<int>(key >> 32), l))) << 32) |
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), l)));
+      r += (ko < key || (ko == key && l < lane)) ? 1 : 0;
+    }
+    rank = live ? r : -1;
+    pos = -1;
+  }
+  // advance to the first tile of the next live slot
+  __device__ __forceinline__ void next_block(const Acc& acc, int b, int g, int h, int T, int qc) {
+    for (;;) {
+      if (pos + 1 < nlive) {
+        ++pos;
+        const int slot = __builtin_ctzll(__ballot(rank == pos));
+        br = acc.ref(b, h, lane_entry(e, slot));
+        tok0 = 0;
+        n = br.nvalid < TK ? br.nvalid : TK;
+        valid = true;
+        return;
+      }
+      base += 64;
+      if (base >= T) {
+        valid = false;
+        n = 0;
+        return;
+      }
+      fill(acc, b, g, h, T, qc);
+    }
+  }
+  __device__ __forceinline__ void start(const Acc& acc, int b, int g, int h, int T, int qc) {
+    base = 0;
+    valid = false;
+    if (T <= 0) return;
+    fill(acc, b, g, h, T, qc);
+    next_block(acc, b, g, h, T, qc);
+  }
+  __device__ __forceinline__ void advance(const Acc& acc, int b, int g, int h, int T, int qc) {
+    if (tok0 + TK < br.nvalid) {
+      tok0 += TK;
+      const int rem = br.nvalid - tok0;
+      n = rem < TK ? rem : TK;
+      return;
+    }
+    next_block(acc, b, g, h, T, qc);
+  }
+};
 
 // ---- staging: global -> registers -> LDS -----------------------------------------------------
 // K tile in LDS: Ks[key][KP], KP = D + 8 (row pitch 272 B for D = 128: the 16-byte A-operand
@@ -264,36 +403,42 @@ struct Stager {
     voff = static_cast<uint32_t>((4 * (tid / DC) * sv + (tid % DC) * 8) * ES);
   }
 
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int j = 0; j < KU; ++j) k[j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < VQ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[j][r] = make_uint4(0, 0, 0, 0);
+  }
+
+  // Rows at or past n are not loaded: their registers keep finite values from an earlier tile
+  // (or the initial zeros).  Their scores are masked to -inf, so their V rows get weight 0.
+  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int tid) {
+    if (n >= 64)
+      load_impl<true>(br, tok0, n, tid);
+    else
+      load_impl<false>(br, tok0, n, tid);
+  }
+
   template <bool FULL>
   __device__ __forceinline__ void load_impl(const BlockRef& br, int tok0, int n, int tid) {
     const char* kb = static_cast<const char*>(br.k) + static_cast<int64_t>(tok0) * br.sk * ES;
     const char* vb = static_cast<const char*>(br.v) + static_cast<int64_t>(tok0) * br.sv * ES;
+    const int row0 = tid / DC;
 #pragma unroll
     for (int j = 0; j < KU; ++j) {
       const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
-      if (FULL || tid / DC + RS * j < n)
-        k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
-      else
-        k[j] = make_uint4(0, 0, 0, 0);
+      if (FULL || row0 + RS * j < n) k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
     }
 #pragma unroll
     for (int j = 0; j < VQ; ++j) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const char* p = vb + static_cast<int64_t>(4 * RS * j + r) * br.sv * ES;
-        if (FULL || 4 * (tid / DC + RS * j) + r < n)
-          v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
-        else
-          v[j][r] = make_uint4(0, 0, 0, 0);
+        if (FULL || 4 * (row0 + RS * j) + r < n) v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
       }
     }
-  }
-
-  __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int tid) {
-    if (n >= 64)
-      load_impl<true>(br, tok0, n, tid);
-    else
-      load_impl<false>(br, tok0, n, tid);
   }
 
   __device__ __forceinline__ void store(uint16_t* Ks, uint16_t* Vt, int tid) const {
@@ -385,54 +530,84 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m2[2] = {kNegInf, kNegInf}, lsum[2] = {0.0f, 0.0f};
-  const float c2 = scale * kLog2e;
+  // the softmax works on s * c2 with c2 > 0; a negative scale negates Q instead, which is exact
+  // (the host routes a zero or non-finite scale to the VALU kernel)
+  float c2 = scale * kLog2e;
+  if (c2 < 0.0f) {
+    c2 = -c2;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        qb[x][s].x ^= 0x80008000u;
+        qb[x][s].y ^= 0x80008000u;
+        qb[x][s].z ^= 0x80008000u;
+        qb[x][s].w ^= 0x80008000u;
+      }
+  }
 
   using KVT = typename Acc::KV;
   Stager<KVT, D> st;
-  TileIt it = first_tile(acc, b, g, h, T, qc, 0);
-  st.init(tid, it.br.sk, it.br.sv);  // row strides are the same for every block of a call
-  if (it.valid) st.load(it.br, it.tok0, it.n, tid);
-  while (it.valid) {
+  WaveWalk<Acc> wk;
+  wk.start(acc, b, g, h, T, qc);
+  st.init(tid, wk.br.sk, wk.br.sv);  // row strides are the same for every block of a call
+  st.zero();
+  if (wk.valid) st.load(wk.br, wk.tok0, wk.n, tid);
+  while (wk.valid) {
     __syncthreads();  // every wave is done reading the previous tile
     st.store(Ks, Vt, tid);
     __syncthreads();
-    const TileIt nx = next_tile(acc, it, b, g, h, T, qc);
-    if (nx.valid) st.load(nx.br, nx.tok0, nx.n, tid);  // in flight during this tile's MFMAs
+    const int tile_n = wk.n;
+    wk.advance(acc, b, g, h, T, qc);
+    if (wk.valid) st.load(wk.br, wk.tok0, wk.n, tid);  // in flight during this tile's MFMAs
     if (wave_active) {
-      // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks
+      // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks.  A
+      // partial tile seeds the accumulators with 0 / -inf per key, so masked keys come out -inf.
       f32x4 s4[2][4];
+      if (tile_n >= 64) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s4[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; ++t) {
+          s4[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < SD; ++s) {
-          const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
-          s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
-          s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+          for (int s = 0; s < SD; ++s) {
+            const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
+            s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+            s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // bound the operand reads in flight (registers)
         }
-        __builtin_amdgcn_sched_barrier(0);  // bound the operand reads in flight (registers)
-      }
-      if (it.n < 64) {
+      } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
+          const int lim = tile_n - 16 * t - 4 * j4;
+          const f32x4 bias{lim > 0 ? 0.f : kNegInf, lim > 1 ? 0.f : kNegInf,
+                           lim > 2 ? 0.f : kNegInf, lim > 3 ? 0.f : kNegInf};
+          s4[0][t] = bias;
+          s4[1][t] = bias;
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (16 * t + 4 * j4 + r >= it.n) s4[0][t][r] = s4[1][t][r] = kNegInf;
+          for (int s = 0; s < SD; ++s) {
+            const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
+            s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+            s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-      // online softmax in the log2 domain: p = 2^(s * c2 - m), m the running max of s * c2
+      // online softmax in the log2 domain: p = 2^(s * c2 - m), m a running max of s * c2 shared
+      // by the 4 lane groups of a query.  m is raised only when some lane's tile max exceeds it
+      // by more than 2^8 (p then stays <= 256, exact enough in fp32 and in the bf16 P operand),
+      // so after the first tiles the cross-lane max reduction is rarely needed.
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         float mt = kNegInf;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           mt = fmaxf(mt, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
-        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-        // lazy rescale: keep the running max while no lane's max grows by more than 2^8
-        // (p stays <= 256, exact enough in fp32 and in the bf16 P operand)
-        const float mcand = fmaxf(m2[x], mt * c2);
-        if (__ballot(mcand > m2[x] + 8.0f) != 0ull) {
+        if (__ballot(mt * c2 > m2[x] + 8.0f) != 0ull) {
+          mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+          mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+          const float mcand = fmaxf(m2[x], mt * c2);
           const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
           const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
           lsum[x] *= alpha;
@@ -479,7 +654,6 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
         }
       }
     }
-    it = nx;
   }
 
   // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
@@ -501,6 +675,290 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
       }
       if (lse != nullptr && j4 == 0)
         lse[(static_cast<int64_t>(b) * H + h) * M + my_q[x]] =
+            ls > 0.0f ? (m2[x] + __builtin_log2f(ls)) * kLn2 : kNegInf;
+    }
+  }
+}
+
+// ---- DMA kernel (16-bit K / V) ----------------------------------------------------------------
+// One workgroup = up to 64 queries of one query group; 2 waves x 32 queries (2 MFMA row blocks
+// of 16 each, sharing every K and V^T operand read), 2 waves per SIMD so that one wave's softmax
+// VALU work overlaps another's MFMAs.  K and V tiles of TK keys (8 KiB each) go global -> LDS by
+// buffer_load ... lds with no register staging; rows past the block's visible tokens read as 0
+// through the buffer bound, so a partial tile holds finite values.  Two LDS buffers each for K
+// and V: the copy of tile i + 1 is issued right after the barrier that opens tile i (each wave
+// issues half of a tile's copy instructions and waits for its own before that barrier).
+//   LDS K rows:  16-byte chunk c of row r at slot c ^ (r % CPR), so the 16-row b128 operand reads
+//                of one chunk column hit 16 distinct slots;
+//   LDS V rows:  chunk c of row r at slot c ^ (2 (r % 8) % CPR); the V^T operand comes from
+//                ds_read_b64_tr_b16, which gives lane L of a 16-lane group element L of the 4
+//                rows its group addresses: 4 consecutive keys of one head dim.
+template <int D>
+struct DmaGeom {
+  static constexpr int ROWB = 2 * D;       // bytes per K / V row
+  static constexpr int CPR = D / 8;        // 16-byte chunks per row
+  static constexpr int TK = 8192 / ROWB;   // keys per tile
+  static constexpr int RPI = 1024 / ROWB;  // rows per copy instruction (64 lanes x 16 bytes)
+  static constexpr int NT = TK / 16;       // 16-key score blocks per tile
+  static constexpr int NU = TK / 32;       // 32-key PV steps per tile
+  static constexpr int SD = D / 32;        // QK k-steps
+  static constexpr int ND = D / 16;        // PV d-tiles
+  __device__ static int swz_k(int r) { return r & (CPR - 1); }
+  __device__ static int swz_v(int r) { return ((r & 7) << 1) & (CPR - 1); }
+};
+
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+#define OMM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) bf16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// This wave's 4 of the 8 copy instructions of one K or V tile: rows [0, nrows) of `base` (row
+// stride rsb bytes) into the 8 KiB LDS buffer dst; instruction j (= 4 w + jj) fills dst bytes
+// [1024 j, 1024 j + 1024) and off[jj] is this lane's source offset for it.
+__device__ __forceinline__ void dma_part(const void* base, int rsb, int nrows, char* dst, int w,
+                                         const int (&off)[4]) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrows * rsb, 0x00020000);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, OMM_LDS(dst + 1024 * (4 * w + jj)), 16, off[jj],
+                                             0, 0, 0);
+}
+
+constexpr int kDmaThreads = 128;
+
+template <typename QT, typename Acc, int D>
+__global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
+    View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale, int nsub) {
+  using DG = DmaGeom<D>;
+  constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
+  constexpr int NT = DG::NT, NU = DG::NU, SD = DG::SD, ND = DG::ND;
+  __shared__ __align__(16) char lds[4][8192];  // K buffers 0, 1; V buffers 2, 3
+
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int sub = wi % nsub; wi /= nsub;
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+
+  const int m0 = g * G + sub * 64;
+  const int m_end = min(min(g * G + G, M), m0 + 64);
+  const int qc = (g * G) / chunk;
+  if (sub == 0) acc.touch(b, g, h, T);
+
+  // Q^T operands of this wave's 2 query blocks: row m0 + 32 w + 16 x + l16, dims 32 s + 8 j4 ..
+  bool q_ok[2];
+  uint4 qb[2][SD];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int mq = m0 + 32 * w + 16 * x + l16;
+    q_ok[x] = mq < m_end;
+#pragma unroll
+    for (int s = 0; s < SD; ++s)
+      qb[x][s] = q_ok[x] ? *reinterpret_cast<const uint4*>(q.at(b, mq, h, 32 * s + 8 * j4))
+                         : make_uint4(0, 0, 0, 0);
+  }
+  // the softmax works on s * c2 with c2 > 0; a negative scale negates Q instead, which is exact
+  float c2 = scale * kLog2e;
+  if (c2 < 0.0f) {
+    c2 = -c2;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        qb[x][s].x ^= 0x80008000u;
+        qb[x][s].y ^= 0x80008000u;
+        qb[x][s].z ^= 0x80008000u;
+        qb[x][s].w ^= 0x80008000u;
+      }
+  }
+
+  // LDS read offsets inside a tile buffer.  K operand (t, s): row 16 t + l16, chunk 4 s + j4
+  // (16 t rows are a compile-time offset).  V^T operand (u, half, i): row 32 u + 16 half + 4 j4
+  // + (l16 >> 2), dims 16 i + 4 (l16 & 3) .. +3.
+  int koff[SD], voff[ND];
+#pragma unroll
+  for (int s = 0; s < SD; ++s) koff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_k(l16)) << 4);
+  {
+    const int vr = 4 * j4 + (l16 >> 2), vm = l16 & 3;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      voff[i] = vr * ROWB + (((2 * i + (vm >> 1)) ^ DG::swz_v(vr)) << 4) + ((vm & 1) << 3);
+  }
+
+  f32x4 o[2][ND];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m2[2] = {kNegInf, kNegInf};
+  float lsum[2] = {0.0f, 0.0f};  // fp32 row sums of the unrounded p (lane partials)
+
+  WaveWalk<Acc, TK> wk;
+  wk.start(acc, b, g, h, T, qc);
+  int n_cur = 0;        // visible keys of the current tile (0: done)
+  int kdo[4], vdo[4];   // this lane's source offsets of this wave's copy instructions
+  int rsk = 0, rsv = 0;
+  if (wk.valid) {
+    // row strides are the same for every block of a call
+    rsk = static_cast<int>(wk.br.sk) * 2;
+    rsv = static_cast<int>(wk.br.sv) * 2;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
+      kdo[jj] = row * rsk + ((c ^ DG::swz_k(row)) << 4);
+      vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
+    }
+    dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
+             lds[0], w, kdo);
+    dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
+             lds[2], w, vdo);
+    n_cur = wk.n;
+    wk.advance(acc, b, g, h, T, qc);
+  }
+
+  // One key tile in LDS buffers BI (0 or 1; unrolling the two costs registers for no gain).
+  auto step = [&](int BI) -> bool {
+    // this wave's copies of the tile are in LDS; after the barrier every wave's are, and every
+    // wave is done reading buffers BI ^ 1 (the previous tile)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int n_nx = 0;
+    if (wk.valid) {
+      dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+               wk.n, lds[BI ^ 1], w, kdo);
+      dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
+               wk.n, lds[2 + (BI ^ 1)], w, vdo);
+      n_nx = wk.n;
+      wk.advance(acc, b, g, h, T, qc);
+    }
+    const char* Kt = lds[BI];
+    const char* Vt = lds[2 + BI];
+
+    // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks
+    f32x4 s4[2][NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      s4[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        const uint4 a = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
+        s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+        s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+      }
+    }
+    if (n_cur < TK) {  // partial tile: keys past n_cur are not visible
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * t + 4 * j4 + r >= n_cur) s4[0][t][r] = s4[1][t][r] = kNegInf;
+    }
+
+    // online softmax in the log2 domain: e = s c2 - m with m a running max of s c2 per query
+    // (0 while none is finite), p = 2^e.  m is raised only when some e exceeds 8 (p stays
+    // <= 256, exact enough in fp32 and in the 16-bit P operand), so the common path needs no
+    // cross-lane max.
+    bool raise = false;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+      const float thr = m2[x] == kNegInf ? kNegInf : 8.0f;
+      float mx = kNegInf;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = __builtin_fmaf(s4[x][t][r], c2, -msafe);
+          s4[x][t][r] = e;
+          mx = fmaxf(mx, e);
+        }
+      raise = raise || (mx > thr);
+    }
+    if (__ballot(raise) != 0ull) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+        float v = kNegInf;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          v = fmaxf(v, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
+        v = fmaxf(v, __shfl_xor(v, 16, kWave));
+        v = fmaxf(v, __shfl_xor(v, 32, kWave));
+        // v: the query's largest e of this tile, relative to msafe
+        const float mcand = fmaxf(m2[x], v + msafe);
+        const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
+        const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
+        lsum[x] *= alpha;
+#pragma unroll
+        for (int i2 = 0; i2 < ND; ++i2) o[x][i2] *= alpha;
+        m2[x] = mcand;
+        const float shift = msafe - msafe_new;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s4[x][t][r] += shift;
+      }
+    }
+
+    // O^T += V^T P^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
+    // 32 u + 16 + 4 j4 + (e - 4), for both operands
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      uint4 pb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(s4[x][2 * u + (e >> 2)][e & 3]);
+        lsum[x] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        pb[x] = make_uint4(Mfma<QT>::pack2(pv[0], pv[1]), Mfma<QT>::pack2(pv[2], pv[3]),
+                           Mfma<QT>::pack2(pv[4], pv[5]), Mfma<QT>::pack2(pv[6], pv[7]));
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < ND; ++i2) {
+        const uint2 lo = lds_read_tr16(Vt + voff[i2] + (32 * u) * ROWB);
+        const uint2 hi = lds_read_tr16(Vt + voff[i2] + (32 * u + 16) * ROWB);
+        const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        o[0][i2] = Mfma<QT>::run(va, pb[0], o[0][i2]);
+        o[1][i2] = Mfma<QT>::run(va, pb[1], o[1][i2]);
+      }
+    }
+    n_cur = n_nx;
+    return n_cur > 0;
+  };
+  if (n_cur > 0)
+    for (int it = 0; step(it & 1); ++it) {
+    }
+
+  // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    float ls = lsum[x];
+    ls += __shfl_xor(ls, 16, kWave);
+    ls += __shfl_xor(ls, 32, kWave);
+    if (q_ok[x]) {
+      const int mq = m0 + 32 * w + 16 * x + l16;
+      const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
+      QT* op = out.at(b, mq, h, 0);
+#pragma unroll
+      for (int i2 = 0; i2 < ND; ++i2) {
+        uint2 w2;
+        w2.x = Mfma<QT>::pack2(o[x][i2][0] * inv, o[x][i2][1] * inv);
+        w2.y = Mfma<QT>::pack2(o[x][i2][2] * inv, o[x][i2][3] * inv);
+        *reinterpret_cast<uint2*>(op + 16 * i2 + 4 * j4) = w2;
+      }
+      if (lse != nullptr && j4 == 0)
+        lse[(static_cast<int64_t>(b) * H + h) * M + mq] =
             ls > 0.0f ? (m2[x] + __builtin_log2f(ls)) * kLn2 : kNegInf;
     }
   }
@@ -645,6 +1103,15 @@ int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float*
   return check_launch("selection attention (mfma)");
 }
 
+template <typename QT, typename Acc, int D>
+int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
+               const Acc& acc, int chunk, float scale, hipStream_t s) {
+  sel_fwd_dma_kernel<QT, Acc, D><<<static_cast<unsigned>(gm.items), kDmaThreads, 0, s>>>(
+      make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T, chunk,
+      scale, gm.nsub);
+  return check_launch("selection attention (dma)");
+}
+
 template <typename QT, typename Acc>
 int launch_valu(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
                 const Acc& acc, int chunk, float scale, int64_t kv_sd, hipStream_t s) {
@@ -674,12 +1141,24 @@ inline bool qo_mfma_ok(const omm_view4& q, const omm_view4& out) {
          out.stride[0] % 4 == 0 && out.stride[1] % 4 == 0 && out.stride[2] % 4 == 0;
 }
 
+// kv_row_bytes: the larger K / V row stride in bytes (the DMA kernel's 32-bit tile offsets and
+// its zero-fill bound need TK rows to fit in 2^31 bytes and rows no shorter than D elements).
 template <typename QT, typename Acc>
 int dispatch(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse, const Acc& acc,
-             int chunk, float scale, bool mfma_ok, int64_t kv_sd, hipStream_t s) {
+             int chunk, float scale, bool mfma_ok, int64_t kv_sd, int64_t kv_row_bytes,
+             hipStream_t s) {
   if constexpr (sizeof(QT) == 2) {
-    if (mfma_ok && gm.D == 128) return launch_mfma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
-    if (mfma_ok && gm.D == 64) return launch_mfma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
+    // the MFMA softmax needs a finite non-zero scale (its masking uses -inf scores)
+    const bool ok = mfma_ok && scale != 0.0f && __builtin_isfinite(scale);
+    if constexpr (sizeof(typename Acc::KV) == 2) {
+      const bool rows_ok = kv_row_bytes >= 2 * gm.D && kv_row_bytes * 64 < (int64_t{1} << 31);
+      if (ok && rows_ok && gm.D == 128)
+        return launch_dma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
+      if (ok && rows_ok && gm.D == 64)
+        return launch_dma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
+    }
+    if (ok && gm.D == 128) return launch_mfma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
+    if (ok && gm.D == 64) return launch_mfma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
   }
   return launch_valu<QT, Acc>(gm, q, out, lse, acc, chunk, scale, kv_sd, s);
 }
@@ -712,7 +1191,9 @@ int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, co
   // the VALU kernel reads K and V with K's dim stride
   OMM_REQUIRE(mfma || k.stride[3] == v.stride[3], OMM_EUNSUPPORTED,
               "selection attention: k and v need the same dim stride");
-  return dispatch<QT>(gm, q, out, lse, acc, causal ? chunk : 1, scale, mfma, k.stride[3], s);
+  const int64_t row_bytes = 2 * (k.stride[1] > v.stride[1] ? k.stride[1] : v.stride[1]);
+  return dispatch<QT>(gm, q, out, lse, acc, causal ? chunk : 1, scale, mfma, k.stride[3],
+                      row_bytes, s);
 }
 
 }  // namespace
@@ -775,7 +1256,7 @@ extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const i
   // pointer rows must be 16-byte aligned for the MFMA staging loads (checked per call on the
   // host only for the strides; addresses of cache chunks are allocator-aligned)
   const bool mfma = stride_bd == 1 && stride_bn % 8 == 0 && qo_mfma_ok(*q, *out);
-  return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, stride_bd,
+  return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, stride_bd, 2 * stride_bn,
                           static_cast<hipStream_t>(stream));
 }
 
@@ -813,7 +1294,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
                          kv->n_slots, kv->n_host_slots};
-    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s);
   }
   if (kv->dtype == OMM_FP8E4M3) {
     OMM_REQUIRE(kv->scale_k != nullptr && kv->scale_v != nullptr, OMM_EINVAL,
@@ -826,7 +1307,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
                           kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};
-    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, s);
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s);
   }
   return set_error(OMM_EINVAL, "omm_sel_fwd_paged: unsupported cache dtype %d", kv->dtype);
 }
