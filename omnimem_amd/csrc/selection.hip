@@ -716,18 +716,44 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (gfx9 layout): base address, stride 0, num_records = nbytes (loads at or
+// past it read 0), dword 3 = the gfx9 data-format bits of an untyped buffer.
+__device__ __forceinline__ i32x4 buffer_desc(const void* base, int nbytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));  // address bits 32-47
+  r.z = __builtin_amdgcn_readfirstlane(nbytes);
+  r.w = 0x00020000;
+  return r;
+}
+
 // This wave's 4 of the 8 copy instructions of one K or V tile: rows [0, nrows) of `base` (row
 // stride rsb bytes) into the 8 KiB LDS buffer dst; instruction j (= 4 w + jj) fills dst bytes
-// [1024 j, 1024 j + 1024) and off[jj] is this lane's source offset for it.
+// [1024 j, 1024 j + 1024) and off[jj] is this lane's source offset for it.  Issued as inline asm
+// (M0 = LDS destination): the compiler then does not treat it as an LDS store, so it does not
+// make the next LDS read wait for this copy; the kernel orders copies and reads itself
+// (s_waitcnt vmcnt(0) and a barrier before a buffer is read, a barrier before it is refilled).
+// M0 is set here and used by nothing else in the kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_part(const void* base, int rsb, int nrows, char* dst, int w,
                                          const int (&off)[4]) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrows * rsb, 0x00020000);
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, OMM_LDS(dst + 1024 * (4 * w + jj)), 16, off[jj],
-                                             0, 0, 0);
+  const i32x4 r = buffer_desc(base, nrows * rsb);
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + 4096u * w)));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %4, %5, 0 offen lds"
+      :
+      : "s"(m0), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(r)
+      : "memory", "m0", "scc");
 }
+#pragma clang diagnostic pop
 
 constexpr int kDmaThreads = 128;
 
@@ -824,6 +850,11 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
     n_cur = wk.n;
     wk.advance(acc, b, g, h, T, qc);
   }
+
+  // Q and the block walk's loads are complete before the loop: without this compiler-visible
+  // wait the loop would re-wait vmcnt(0) every tile (for loads it cannot tell are done), which
+  // would also wait for the next tile's copy.
+  __builtin_amdgcn_s_waitcnt(0);
 
   // One key tile in LDS buffers BI (0 or 1; unrolling the two costs registers for no gain).
   auto step = [&](int BI) -> bool {
