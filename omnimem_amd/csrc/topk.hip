@@ -12,8 +12,8 @@
 //      tile's loads in flight during the current tile's arithmetic); lane = column, each wave
 //      owns 4 rows, and every score is fmaf over d ascending from 0, then * scale, so the fp32
 //      score is a fixed function of its inputs (reproduced bit for bit by the C oracle).
-//   3. selection, one wave per row: theta = topk-th largest of the 64 per-lane maxima (one
-//      wave-wide bitonic sort); only keys >= theta survive (at most topk lanes contribute);
+//   3. selection, one wave per row: keys in registers; theta = topk-th largest score word of the
+//      64 per-lane maxima (ranked across lanes); only keys at or above it survive;
 //      each survivor's exact rank among survivors is counted from LDS; rank < topk is written.
 //      Column chunk ids are precomputed once per workgroup in LDS.
 //   Rows whose columns are split over several workgroups (long key histories) write packed
@@ -109,32 +109,162 @@ __device__ __forceinline__ int row_ub(const MaskDev& m, const RowInfo& r, int NC
 }
 
 // ---- selection over n candidates of one row, one wave -------------------------------------
-// key(i) gives the packed key of candidate i < n (0 = not a candidate).  emit(rank, key) for
-// rank < topk; pad(p) for output positions p >= number of candidates.  All lanes of the wave
-// must call this; sv is the wave's LDS survivor buffer.
+// key(i) gives the packed key of candidate i < n (0 = not a candidate).
+// emit(rank, key) for rank < topk; pad(p) for output positions p >= number of candidates.  All
+// lanes of the wave must call this; sv is the wave's LDS survivor buffer.
+//   1. every lane loads its keys (candidates lane, lane + 64, ...) into registers once;
+//   2. theta = the topk-th largest high word (score half) of the 64 per-lane maxima, from each
+//      lane's rank among them (readlane compares, no LDS and no scalar round trips);
+//   3. survivors = keys whose high word is >= theta (at least topk of them whenever that many
+//      candidates exist, and every key of the top topk), compacted into sv;
+//   4. each survivor's exact rank among the survivors (keys are distinct) -> emit if < topk.
+constexpr int kMaxPer = kSpanCap / kWave;
+
+// Wave-wide max of an unsigned value (DPP row shifts and row broadcasts; every lane gets it).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_max(uint32_t v) {
+  const uint32_t t = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+  return v > t ? v : t;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = dpp_max<0x111, 0xf>(v);  // row_shr:1
+  v = dpp_max<0x112, 0xf>(v);  // row_shr:2
+  v = dpp_max<0x114, 0xf>(v);  // row_shr:4
+  v = dpp_max<0x118, 0xf>(v);  // row_shr:8 -> lane 15 of each row holds the row max
+  v = dpp_max<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_max<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3 -> lane 63 holds the wave max
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), kWave - 1));
+}
+
+// The topk-th largest of the 64 lane values v (0 if topk > 64): every lane counts the values
+// >= its own (64 LDS broadcast values in the wave-private scratch), and the answer is the
+// largest value whose count reaches topk.  scratch: 64 words of wave-private LDS.
+__device__ __forceinline__ uint32_t lane_max_threshold(uint32_t v, int topk, uint32_t* scratch) {
+  if (topk > kWave) return 0u;
+  const int lane = lane_id();
+  scratch[lane] = v;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kWave / 4; ++j) {
+    const uint4 w = reinterpret_cast<const uint4*>(scratch)[j];
+    cnt += (w.x >= v ? 1 : 0) + (w.y >= v ? 1 : 0) + (w.z >= v ? 1 : 0) + (w.w >= v ? 1 : 0);
+  }
+  const uint32_t theta = wave_max_u32(cnt >= topk ? v : 0u);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // scratch is reused after this
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return theta;
+}
+
+template <int PER, typename KeyF, typename EmitF, typename PadF>
+__device__ __forceinline__ void wave_select_impl(int n, int topk, KeyF key, EmitF emit, PadF pad,
+                                                 uint64_t* sv) {
+  const int lane = lane_id();
+  // keys of slots j * 64 + lane; slots past n read candidate n - 1 (in bounds) and count as 0
+  uint64_t kv[PER];
+  uint32_t lmax = 0;  // high word of the lane's largest key
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = j * kWave + lane;
+    const uint64_t k = key(i < n ? i : n - 1);
+    kv[j] = i < n ? k : 0ull;
+    const uint32_t hi = static_cast<uint32_t>(kv[j] >> 32);
+    lmax = hi > lmax ? hi : lmax;
+  }
+  // theta: the topk-th largest lane maximum (0 if fewer than topk lanes hold candidates)
+  const uint32_t theta = lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv));
+
+  int ns = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint64_t k = kv[j];
+    const bool surv = k != 0ull && static_cast<uint32_t>(k >> 32) >= theta;
+    const uint64_t m = ballot64(surv);
+    const int pos = ns + lanes_below(m);
+    if (surv && pos < kSurvCap) sv[pos] = k;
+    ns += popc64(m);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (ns <= kWave) {
+    // one survivor per lane; survivors past ns read as 0 (below every key), so groups of 8
+    // broadcast reads need no bound checks
+    const uint64_t mine = lane < ns ? sv[lane] : 0ull;
+    if (lane >= ns && lane < ((ns + 7) & ~7)) sv[lane] = 0ull;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank = 0;
+    for (int j = 0; j < ns; j += 8) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const ulonglong2 w = reinterpret_cast<const ulonglong2*>(sv + j)[e];
+        rank += (w.x > mine ? 1 : 0) + (w.y > mine ? 1 : 0);
+      }
+    }
+    if (lane < ns && rank < topk) emit(rank, mine);
+  } else if (ns <= kSurvCap) {
+    for (int i = lane; i < ns; i += kWave) {
+      const uint64_t k = sv[i];
+      int rank = 0;
+      for (int j = 0; j < ns; ++j) rank += (sv[j] > k) ? 1 : 0;
+      if (rank < topk) emit(rank, k);
+    }
+  } else {
+    // too many survivors for the buffer (massive score ties): extract the maxima one at a
+    // time, each a wave-wide max over the keys below the previous one
+    uint64_t prev = ~0ull;
+    int r = 0;
+    for (; r < topk; ++r) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const uint64_t k = kv[j];
+        if (k < prev && k > best) best = k;
+      }
+#pragma unroll
+      for (int mm = 1; mm < kWave; mm <<= 1) {
+        const uint64_t o = shfl_xor_u64(best, mm);
+        best = o > best ? o : best;
+      }
+      if (best == 0ull) break;
+      if (lane == 0) emit(r, best);
+      prev = best;
+    }
+    ns = r;
+  }
+  for (int p = lane; p < topk; p += kWave)
+    if (p >= ns) pad(p);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Any n (the merge of many column spans): keys are re-read per pass instead of held.
 template <typename KeyF, typename EmitF, typename PadF>
-__device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emit, PadF pad,
-                                            uint64_t* sv) {
+__device__ __forceinline__ void wave_select_stream(int n, int topk, KeyF key, EmitF emit,
+                                                   PadF pad, uint64_t* sv) {
   const int lane = lane_id();
   const int per = (n + kWave - 1) / kWave;
-  uint64_t lmax = 0;
+  uint32_t lmax = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
     if (i < n) {
-      const uint64_t k = key(i);
-      lmax = k > lmax ? k : lmax;
+      const uint32_t hi = static_cast<uint32_t>(key(i) >> 32);
+      lmax = hi > lmax ? hi : lmax;
     }
   }
-  const uint64_t sorted = wave_sort_desc(lmax);
-  const uint32_t t_lo = __shfl(static_cast<uint32_t>(sorted), topk - 1, kWave);
-  const uint32_t t_hi = __shfl(static_cast<uint32_t>(sorted >> 32), topk - 1, kWave);
-  const uint64_t theta = (static_cast<uint64_t>(t_hi) << 32) | t_lo;
-
+  const uint32_t theta = lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv));
   int ns = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
     const uint64_t k = (i < n) ? key(i) : 0ull;
-    const bool surv = k != 0ull && k >= theta;
+    const bool surv = k != 0ull && static_cast<uint32_t>(k >> 32) >= theta;
     const uint64_t m = ballot64(surv);
     const int pos = ns + lanes_below(m);
     if (surv && pos < kSurvCap) sv[pos] = k;
@@ -144,7 +274,6 @@ __device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emi
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (ns <= kSurvCap) {
-    // exact rank of each survivor among the survivors (keys are distinct)
     for (int i = lane; i < ns; i += kWave) {
       const uint64_t k = sv[i];
       int rank = 0;
@@ -152,8 +281,6 @@ __device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emi
       if (rank < topk) emit(rank, k);
     }
   } else {
-    // too many survivors for the buffer: extract the maxima one at a time, each a wave-wide
-    // max over the keys below the previous one
     uint64_t prev = ~0ull;
     int r = 0;
     for (; r < topk; ++r) {
@@ -179,6 +306,25 @@ __device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emi
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename KeyF, typename EmitF, typename PadF>
+__device__ __forceinline__ void wave_select(int n, int topk, KeyF key, EmitF emit, PadF pad,
+                                            uint64_t* sv) {
+  if (n <= 0) {  // no candidates (wave-uniform): all padding
+    for (int p = lane_id(); p < topk; p += kWave) pad(p);
+    return;
+  }
+  if (n > kMaxPer * kWave) {
+    wave_select_stream(n, topk, key, emit, pad, sv);
+    return;
+  }
+  if (n <= 4 * kWave)
+    wave_select_impl<4>(n, topk, key, emit, pad, sv);
+  else if (n <= 8 * kWave)
+    wave_select_impl<8>(n, topk, key, emit, pad, sv);
+  else
+    wave_select_impl<kMaxPer>(n, topk, key, emit, pad, sv);
 }
 
 // ---- element helpers ------------------------------------------------------------------------
@@ -451,8 +597,13 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
     const float* srow = sc + r * span;
     const int64_t orow = (static_cast<int64_t>(b) * a.MG + g) * a.H + h;
     const int NC = a.NC;
+    // plain causal / non-causal masks (no tf, no exclusions): the visible columns are exactly
+    // those below the row bound, because chunk ids do not decrease with the column
+    const bool simple = !mk.tf && mk.ex_sink <= 0 && mk.ex_win <= 0;
+    const int rub = row_ub(mk, ri, NC) - c_begin;
     auto key = [&](int i) -> uint64_t {
-      return visible(mk, ri, kc[i]) ? make_key(srow[i], c_begin + i, NC) : 0ull;
+      const bool vis = simple ? (i < rub) : visible(mk, ri, kc[i]);
+      return vis ? make_key(srow[i], c_begin + i, NC) : 0ull;
     };
     if (a.nsplit == 1) {
       int32_t* o = a.out + orow * a.topk;
