@@ -54,7 +54,24 @@ def parse():
                    help="cached chunks before the timed AR steps (80 chunks = 240 latent frames)")
     p.add_argument("--ar-steps", type=int, default=3, help="timed AR chunks per cache dtype")
     p.add_argument("--no-ar", action="store_true", help="skip the AR (configs 4 and 5) leg")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run 5 device copies of 256 MiB (the reference kernel for scaling "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
     return p.parse_args()
+
+
+def copy_calibration():
+    """5 copies of a 256 MiB device buffer: a kernel of known traffic (256 MiB read + 256 MiB
+    written per dispatch) for calibrating the HBM byte counters."""
+    import torch
+    n = 256 * 1024 * 1024
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 5}))
 
 
 def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
@@ -211,6 +228,9 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the selection path has no "
               "multi-GPU mode in this build", file=sys.stderr)

@@ -5,14 +5,15 @@
 // resolution, partial blocks, pointer 0 = skip), :327-332 (chunk-causal visible prefix),
 // selection_fwd.cu:218 (a query group's chunk is that of its first query).
 //
-// gfx950 design (bf16 / f16): one workgroup = (b, query group, head), 4 waves x 16 queries.
+// gfx950 design (bf16 / f16 queries): one workgroup = (b, query group of 64, head).
 //   S^T = K Q^T on v_mfma_f32_16x16x32 (A = K rows from LDS, B = Q^T held in registers), so the
 //   S^T accumulator already has the layout of the B operand of O^T = V^T P^T: P goes from the
-//   softmax straight into the PV MFMA with no LDS round trip.  V is staged transposed in LDS
-//   (Vt[d][key]) so the A operand of PV is two 8-byte LDS reads.  Key tiles of 64 tokens are
-//   double-buffered: the next tile's global loads are in flight during the current tile's MFMAs.
-//   fp8 pages are dequantised (x * page scale -> bf16) while staging.
-// fp32 (and any shape the MFMA kernel does not cover) runs a VALU kernel in full fp32.
+//   softmax straight into the PV MFMA with no LDS round trip.
+//   sel_fwd_dma_kernel (16-bit K / V): K / V tiles copied global -> LDS by buffer_load ... lds,
+//   V read as V^T with ds_read_b64_tr_b16 (details at the kernel).
+//   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (dequantised while staging,
+//   x * page scale -> bf16) and for row strides the DMA kernel cannot address.
+// fp32 (and any shape the MFMA kernels do not cover) runs a VALU kernel in full fp32.
 #include "omm_common.h"
 
 namespace omm {
