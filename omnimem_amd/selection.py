@@ -16,7 +16,7 @@ import torch
 from . import _lib
 from .backend import NSABackendError, get_backend
 
-__all__ = ["selection_attention", "sel_fwd"]
+__all__ = ["selection_attention", "sel_fwd", "dense_attention"]
 
 
 def _debug_checks_enabled() -> bool:
@@ -122,3 +122,37 @@ def selection_attention(
     out, lse = sel_fwd(q, k, v, block_indices, block_size, chunk_size, sc, causal, group_size,
                        allow_tf32)
     return (out, lse) if return_lse else out
+
+
+_ALL_BLOCKS = {}
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    scale: Optional[float] = None, return_lse: bool = False,
+                    out: Optional[torch.Tensor] = None):
+    """Full (non-causal) softmax attention of q [B, M, H, D] over k, v [B, N, H, D], computed by
+    the selection kernel with every 64-token block listed for every 64-query group.
+
+    This is the AR driver's compressed-history branch (o_cmp over the pooled keys,
+    models/transformers/causal_wan_nsa_model.py:506) and window branch (o_swa,
+    :508), which the reference runs through flash attention.  The block list is one
+    ``arange`` broadcast with stride 0 over groups and heads, so a call allocates nothing but
+    the output.  Returns out (q's layout) or (out, lse [B, H, M] fp32)."""
+    _lib.require_cuda((q, "q"), (k, "k"), (v, "v"))
+    B, M, H, D = q.shape
+    N = k.shape[1]
+    if k.shape != (B, N, H, D) or v.shape != (B, N, H, D):
+        raise NSABackendError(f"dense_attention: expected k, v {(B, N, H, D)}, got "
+                              f"{tuple(k.shape)} / {tuple(v.shape)}")
+    G = BS = 64
+    T = max(1, -(-N // BS))
+    key = (q.device, T)
+    ar = _ALL_BLOCKS.get(key)
+    if ar is None:
+        ar = torch.arange(T, dtype=torch.int32, device=q.device)
+        _ALL_BLOCKS[key] = ar
+    ids = ar.view(1, 1, 1, T).expand(B, -(-M // G), H, T)
+    o, lse = sel_fwd(q, k, v, ids, BS, 1, D ** -0.5 if scale is None else scale, False, G,
+                     out=out,
+                     lse=None if return_lse else torch.empty(0, device=q.device))
+    return (o, lse) if return_lse else o

@@ -16,7 +16,8 @@ of the reference's AR inference branch, and the AR loop of its pipeline:
   and 1 context forward (t = 0) that rewrite the chunk's cache entries, then the offload flush.
 
 What stays PyTorch-ROCm (dense, off the selection path): the linear layers (hipBLASLt), the
-norms, the window and compressed attentions (``scaled_dot_product_attention``), cross-attention.
+norms and the cross-attention.  The window and compressed attentions run on the selection kernel
+(``dense_attention``: every block of the window / pooled history listed for every query group).
 Rotary embedding is a plain interleaved rotation over the head dim with per-position angles (the
 reference's 3-axis frequency split and token reorder only permute which angles a token gets).
 The scheduler arithmetic between denoise steps is one axpy: timing does not depend on it.
@@ -33,6 +34,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .block_cache import PagedKVCache
 from .index_topk import parallel_nsa_topk
+from .selection import dense_attention
 
 __all__ = ["WanARConfig", "WanNSAAR"]
 
@@ -203,12 +205,11 @@ class WanNSAAR:
         self._toc(tk)
         tk = self._tic("attn_cmp")
         k_cmp, v_cmp = cache.cmp_history(layer)
-        qh = q.transpose(1, 2)
-        o_cmp = F.scaled_dot_product_attention(qh, k_cmp.transpose(1, 2), v_cmp.transpose(1, 2))
+        o_cmp = dense_attention(q, k_cmp, v_cmp)       # over the pooled history
         self._toc(tk)
         tk = self._tic("attn_swa")
         wk, wv = cache.window_kv(layer)
-        o_swa = F.scaled_dot_product_attention(qh, wk.transpose(1, 2), wv.transpose(1, 2))
+        o_swa = dense_attention(q, wk, wv)             # over the window chunks
         self._toc(tk)
         tk = self._tic("topk")
         ids = parallel_nsa_topk(q, k_cmp, cfg.topk, block_size=cfg.page_tokens,
@@ -223,8 +224,7 @@ class WanNSAAR:
         o_slc = cache.select(q, ids, layer, cfg.group_size)
         self._toc(tk)
         tk = self._tic("linear")
-        o = (g[..., 0:1] * o_cmp.transpose(1, 2) + g[..., 1:2] * o_slc
-             + g[..., 2:3] * o_swa.transpose(1, 2))
+        o = g[..., 0:1] * o_cmp + g[..., 1:2] * o_slc + g[..., 2:3] * o_swa
         out = F.linear(o.flatten(2), *blk.o)
         self._toc(tk)
         return out

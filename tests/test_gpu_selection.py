@@ -156,3 +156,40 @@ def test_selection_attention_facade_validation():
         selection_attention(q, q, q, ids, 2, 64, group_size=64)  # id 5 >= 1 block
     with pytest.raises(NotImplementedError):
         selection_attention(q.requires_grad_(), q, q, ids.clamp(max=0), 2, 64, group_size=64)
+
+
+@pytest.mark.parametrize("M,N,H", [(130, 300, 2), (64, 64, 1), (300, 1500, 3), (1, 70, 1)])
+def test_dense_attention_matches_oracle(M, N, H):
+    """dense_attention (every block listed; the AR driver's window and compressed-history
+    branches) against plain softmax attention in float64, ragged M and N included."""
+    from omnimem_amd.selection import dense_attention
+    D = 128
+    gen = torch.Generator().manual_seed(M * 7 + N)
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
+    v = torch.randn((1, N, H, D), generator=gen).to(torch.bfloat16)
+    out, lse = dense_attention(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True)
+    T = -(-N // 64)
+    ids = np.broadcast_to(np.arange(T, dtype=np.int32), (1, -(-M // 64), H, T))
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                           ids, 64, D ** -0.5, O.dense_block_tokens(N, 64, 1, False))
+    _check(out, lse, want_o, want_l, torch.bfloat16)
+
+
+def test_dense_attention_window_shape_sampled():
+    """AR window shape (one chunk of 4680 queries over 3 chunks of keys), sampled query groups."""
+    from omnimem_amd.selection import dense_attention
+    M, N, H, D = 4680, 3 * 4680, 2, 128
+    gen = torch.Generator().manual_seed(5)
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
+    v = torch.randn((1, N, H, D), generator=gen).to(torch.bfloat16)
+    out, lse = dense_attention(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True)
+    T = -(-N // 64)
+    groups = [0, 37, 73]
+    ids = np.broadcast_to(np.arange(T, dtype=np.int32), (1, -(-M // 64), H, T))
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                           ids, 64, D ** -0.5, O.dense_block_tokens(N, 64, 1, False),
+                                           groups=groups)
+    rows = np.concatenate([np.arange(g * 64, min(M, g * 64 + 64)) for g in groups])
+    _check(out, lse, want_o, want_l, torch.bfloat16, rows=rows)
