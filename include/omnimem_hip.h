@@ -20,6 +20,9 @@
  *                              in, indices out, so bit-exactness is testable on identical scores
  *   omm_sel_fwd             <- torch.ops.omnimem_nsa.sel_fwd (bindings.cpp:16-19, ops.h:25-29,
  *                              selection_fwd.cu:934-966)
+ *   omm_sel_bwd             <- torch.ops.omnimem_nsa.sel_bwd (bindings.cpp:25-28, ops.h:38-43,
+ *                              selection_bwd.cu:1329-1407) with its inverted index
+ *                              (inverted_index.cu:103-177)
  *   omm_sel_fwd_ptr         <- torch.ops.omnimem_nsa.sel_fwd_ptr (bindings.cpp:20-23,
  *                              selection_fwd.cu:968-992)
  *   omm_build_ptr_table     <- torch.ops.omnimem_nsa.build_ptr_table (bindings.cpp:12-15,
@@ -174,6 +177,25 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 const omm_view4* ids, int32_t dtype, int32_t block_size, int32_t chunk_size,
                 int32_t causal, int32_t group_size, float scale, const omm_view4* out,
                 float* lse, void* stream);
+/* ---- selection attention backward, dense K/V -------------------------------------------- */
+/* Reference: torch.ops.omnimem_nsa.sel_bwd (bindings.cpp:25-28, ops.h:38-43,
+ * selection_bwd.cu:1329-1407) and the inverted index it builds (inverted_index.cu:103-177).
+ * Same arguments as omm_sel_fwd plus the forward's out and lse (fp32 contiguous [B, H, M]) and
+ * d_out ([B, M, H, D], q dtype).  With delta_m = sum_d out[m,d] d_out[m,d] (fp32),
+ * P = exp(q.k * scale - lse) (0 for rows with lse = -inf) and dS = P (d_out.v - delta) scale:
+ * dq = dS K (q dtype), dk = dS^T Q and dv = P^T d_out over every (query, token) pair the forward
+ * attends to (k dtype, fp32 accumulation, one rounding).  Every element of dq, dk and dv is
+ * written (0 for tokens no query sees).  Duplicated ids in a row count twice, as in the
+ * forward.  bf16 / f16, head dim 64 or 128, unit dim strides and 16-byte aligned rows; the
+ * workspace (256-byte aligned) holds delta, the per-block CSR offsets and the bucket lists. */
+size_t omm_sel_bwd_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t N,
+                                   int32_t block_size, int32_t group_size, int64_t T);
+int omm_sel_bwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                const omm_view4* ids, const omm_view4* out, const float* lse,
+                const omm_view4* d_out, int32_t dtype, int32_t block_size, int32_t chunk_size,
+                int32_t causal, int32_t group_size, float scale, const omm_view4* dq,
+                const omm_view4* dk, const omm_view4* dv, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /* ---- pointer-table selection (a6, reference address contract) ------------------------ */
 /* ptr_x[b,g,h,t] = base_x[h, cid] + b*batch_stride + (bid % bpc)*in_chunk_block_bytes with

@@ -14,195 +14,10 @@
 //   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (dequantised while staging,
 //   x * page scale -> bf16) and for row strides the DMA kernel cannot address.
 // fp32 (and any shape the MFMA kernels do not cover) runs a VALU kernel in full fp32.
-#include "omm_common.h"
+#include "sel_common.h"
 
 namespace omm {
 namespace {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
-
-template <typename T> struct Mfma;
-template <> struct Mfma<bf16_t> {
-  __device__ __forceinline__ static f32x4 run(uint4 a, uint4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return pack_bf16x2(lo, hi);
-  }
-};
-template <> struct Mfma<f16_t> {
-  __device__ __forceinline__ static f32x4 run(uint4 a, uint4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-  }
-};
-
-// ---- block accessors ---------------------------------------------------------------------
-// A resolved block: nvalid tokens visible from row 0, rows at k + r*sk (elements of its storage
-// type), k == nullptr when the block is skipped.
-struct BlockRef {
-  const void* k;
-  const void* v;
-  int64_t sk, sv;
-  int nvalid;
-  float scale_k, scale_v;
-};
-
-// Each accessor resolves slot t of a row in two steps: resolve() -> a compact entry (Ent: a few
-// 32-bit words, n = visible tokens, n <= 0 when skipped), evaluated by the MFMA kernels for 64
-// slots at once, one per lane; ref() -> the block's addresses from a wave-uniform entry.
-// order_key() orders the blocks of a row by position in memory (the walk visits them in that
-// order, so concurrent rows that share blocks tend to read them at the same time).
-template <typename T>
-struct DenseAcc {
-  using KV = T;
-  struct Ent {
-    int t0, n;  // first token, visible tokens
-  };
-  View4<const T> k, v;
-  const int32_t* ids;
-  int64_t is0, is1, is2, is3;
-  int N, bs, chunk;
-  bool causal;
-  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int q_chunk) const {
-    Ent e{0, 0};
-    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
-    if (bid < 0) return e;
-    const int64_t t0 = static_cast<int64_t>(bid) * bs;
-    if (t0 >= N) return e;
-    int64_t n = N - t0 < bs ? N - t0 : bs;
-    if (causal) {
-      // visible prefix ends at the query chunk's end: t0 / chunk > q_chunk  <=>  lim <= 0
-      const int64_t lim = static_cast<int64_t>(q_chunk + 1) * chunk - t0;
-      n = n < lim ? n : lim;
-    }
-    if (n <= 0) return e;
-    e.t0 = static_cast<int>(t0);
-    e.n = static_cast<int>(n);
-    return e;
-  }
-  __device__ __forceinline__ BlockRef ref(int b, int h, const Ent& e) const {
-    return BlockRef{k.at(b, e.t0, h, 0), v.at(b, e.t0, h, 0), k.s1, v.s1, e.n, 1.0f, 1.0f};
-  }
-  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.t0; }
-  __device__ __forceinline__ void touch(int, int, int, int) const {}
-};
-
-struct PtrAcc {
-  using KV = bf16_t;
-  struct Ent {
-    int64_t k, v;  // raw addresses (0 = skip)
-    int n;
-    int pad;
-  };
-  const int64_t* pk;
-  const int64_t* pv;
-  int64_t s0, s1, s2, s3;
-  int64_t stride_n;
-  int bs;
-  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
-    const int64_t off = b * s0 + g * s1 + h * s2 + t * s3;
-    Ent e{pk[off], pv[off], 0, 0};
-    e.n = (e.k == 0 || e.v == 0) ? 0 : bs;
-    return e;
-  }
-  __device__ __forceinline__ BlockRef ref(int, int, const Ent& e) const {
-    return BlockRef{reinterpret_cast<const void*>(static_cast<uintptr_t>(e.k)),
-                    reinterpret_cast<const void*>(static_cast<uintptr_t>(e.v)), stride_n,
-                    stride_n, e.n, 1.0f, 1.0f};
-  }
-  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.k; }
-  __device__ __forceinline__ void touch(int, int, int, int) const {}
-};
-
-// Paged entries: page >= 0 is an HBM pool page, page < 0 the host pool page -1 - page; bid is
-// the block id (the walk order must not depend on residency); fp8 pages carry their
-// dequantisation scales.
-struct PagedEnt16 {
-  int page, n, bid;
-};
-struct PagedEnt8 {
-  int page, n, bid;
-  float sk, sv;
-};
-template <typename KVT> struct PagedEntOf { using type = PagedEnt16; };
-template <> struct PagedEntOf<uint8_t> { using type = PagedEnt8; };
-
-template <typename KVT>
-struct PagedAcc {
-  using KV = KVT;
-  using Ent = typename PagedEntOf<KVT>::type;
-  const KVT* pool_k;
-  const KVT* pool_v;
-  const float* sc_k;
-  const float* sc_v;
-  const KVT* host_k;
-  const KVT* host_v;
-  const float* hsc_k;
-  const float* hsc_v;
-  const int32_t* unit;
-  const int32_t* ids;
-  int32_t* stamp;
-  int32_t* reads;
-  int64_t is0, is1, is2, is3;
-  int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
-  __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
-    Ent e{};
-    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
-    if (bid < 0) return e;
-    const int cid = bid / ppc, p = bid - cid * ppc;
-    if (cid >= n_chunks || cid >= max_chunks) return e;
-    const int32_t s = unit[static_cast<int64_t>(h) * max_chunks + cid];
-    if (s == -1 || s >= n_slots || (s < 0 && -2 - s >= n_host)) return e;
-    const int page = (s >= 0 ? s : -2 - s) * ppc + p;
-    const int rem = chunk_len - p * P;
-    e.page = s >= 0 ? page : -1 - page;
-    e.n = rem < P ? rem : P;
-    e.bid = bid;
-    if constexpr (sizeof(KVT) == 1) {
-      const float* ck = s >= 0 ? sc_k : hsc_k;
-      const float* cv = s >= 0 ? sc_v : hsc_v;
-      e.sk = ck != nullptr ? ck[page] : 1.0f;
-      e.sv = cv != nullptr ? cv[page] : 1.0f;
-    }
-    return e;
-  }
-  __device__ __forceinline__ BlockRef ref(int, int, const Ent& e) const {
-    const bool hbm = e.page >= 0;
-    const int64_t off = static_cast<int64_t>(hbm ? e.page : -1 - e.page) * P * D;
-    BlockRef r{(hbm ? pool_k : host_k) + off, (hbm ? pool_v : host_v) + off, D, D, e.n, 1.0f, 1.0f};
-    if constexpr (sizeof(KVT) == 1) {
-      r.scale_k = e.sk;
-      r.scale_v = e.sv;
-    }
-    return r;
-  }
-  __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.bid; }
-  // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
-  // epoch, so the races are benign) and count its pages read (vector atomics)
-  __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
-    const bool st = stamp != nullptr && epoch > 0;
-    if (!st && reads == nullptr) return;
-    for (int t = threadIdx.x; t < T; t += blockDim.x) {
-      const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
-      if (bid < 0) continue;
-      const int cid = bid / ppc;
-      if (cid >= n_chunks || cid >= max_chunks) continue;
-      const int64_t u = static_cast<int64_t>(h) * max_chunks + cid;
-      if (unit[u] == -1) continue;
-      if (st) stamp[u] = epoch;
-      if (reads != nullptr) atomicAdd(reads + u, 1);
-    }
-  }
-};
 
 template <typename Acc>
 __device__ __forceinline__ BlockRef resolve_block(const Acc& acc, int b, int g, int h, int t,
@@ -255,99 +70,6 @@ __device__ __forceinline__ TileIt next_tile(const Acc& acc, const TileIt& c, int
   return first_tile(acc, b, g, h, T, qc, c.t + 1);
 }
 
-// The same walk for a wave that resolved 64 slots at once: lane i holds the entry of slot
-// base + i.  Live slots are visited in ascending order_key (ties by slot): every workgroup then
-// sweeps its blocks from low to high addresses, so the workgroups running together on an XCD
-// read overlapping blocks at about the same time and share them in L2.  A slot's rank among the
-// live slots is counted once per 64 slots (one readlane and compare per live slot); the next
-// block is then a compare, a ballot and a find-first-set, with no memory access.  Within a row
-// the order only changes the fp32 summation order of the softmax.
-template <typename E>
-__device__ __forceinline__ E lane_entry(const E& e, int lane) {
-  static_assert(sizeof(E) % 4 == 0, "entries are 32-bit words");
-  constexpr int W = sizeof(E) / 4;
-  int w[W];
-  __builtin_memcpy(w, &e, sizeof(E));
-#pragma unroll
-  for (int i = 0; i < W; ++i) w[i] = __builtin_amdgcn_readlane(w[i], lane);
-  E r;
-  __builtin_memcpy(&r, w, sizeof(E));
-  return r;
-}
-
-template <typename Acc, int TK = 64>
-struct WaveWalk {
-  typename Acc::Ent e;
-  int rank;        // this lane's rank among the live slots of the batch (-1: not live)
-  int nlive, pos;  // live slots in the batch; rank of the current block (-1 before the first)
-  int base;        // first slot of the batch
-  int tok0, n;     // current tile: first token within the block, tokens (<= TK)
-  BlockRef br;
-  bool valid;
-
-  __device__ __forceinline__ void fill(const Acc& acc, int b, int g, int h, int T, int qc) {
-    const int lane = lane_id();
-    const int t = base + lane;
-    if (t < T) {
-      e = acc.resolve(b, g, h, t, qc);
-    } else {
-      e = typename Acc::Ent{};
-    }
-    const bool live = e.n > 0;
-    uint64_t m = __ballot(live);
-    nlive = __builtin_popcountll(m);
-    const int64_t key = Acc::order_key(e);
-    int r = 0;
-    while (m != 0ull) {
-      const int l = __builtin_ctzll(m);
-      m &= m - 1ull;
-      const int64_t ko = static_cast<int64_t>(
-          (static_cast<uint64_t>(static_cast<uint32_t>(
-               __builtin_amdgcn_readlane(static_cast<int>(key >> 32), l))) << 32) |
-          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), l)));
-      r += (ko < key || (ko == key && l < lane)) ? 1 : 0;
-    }
-    rank = live ? r : -1;
-    pos = -1;
-  }
-  // advance to the first tile of the next live slot
-  __device__ __forceinline__ void next_block(const Acc& acc, int b, int g, int h, int T, int qc) {
-    for (;;) {
-      if (pos + 1 < nlive) {
-        ++pos;
-        const int slot = __builtin_ctzll(__ballot(rank == pos));
-        br = acc.ref(b, h, lane_entry(e, slot));
-        tok0 = 0;
-        n = br.nvalid < TK ? br.nvalid : TK;
-        valid = true;
-        return;
-      }
-      base += 64;
-      if (base >= T) {
-        valid = false;
-        n = 0;
-        return;
-      }
-      fill(acc, b, g, h, T, qc);
-    }
-  }
-  __device__ __forceinline__ void start(const Acc& acc, int b, int g, int h, int T, int qc) {
-    base = 0;
-    valid = false;
-    if (T <= 0) return;
-    fill(acc, b, g, h, T, qc);
-    next_block(acc, b, g, h, T, qc);
-  }
-  __device__ __forceinline__ void advance(const Acc& acc, int b, int g, int h, int T, int qc) {
-    if (tok0 + TK < br.nvalid) {
-      tok0 += TK;
-      const int rem = br.nvalid - tok0;
-      n = rem < TK ? rem : TK;
-      return;
-    }
-    next_block(acc, b, g, h, T, qc);
-  }
-};
 
 // ---- staging: global -> registers -> LDS -----------------------------------------------------
 // K tile in LDS: Ks[key][KP], KP = D + 8 (row pitch 272 B for D = 128: the 16-byte A-operand
@@ -694,67 +416,6 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 //   LDS V rows:  chunk c of row r at slot c ^ (2 (r % 8) % CPR); the V^T operand comes from
 //                ds_read_b64_tr_b16, which gives lane L of a 16-lane group element L of the 4
 //                rows its group addresses: 4 consecutive keys of one head dim.
-template <int D>
-struct DmaGeom {
-  static constexpr int ROWB = 2 * D;       // bytes per K / V row
-  static constexpr int CPR = D / 8;        // 16-byte chunks per row
-  static constexpr int TK = 8192 / ROWB;   // keys per tile
-  static constexpr int RPI = 1024 / ROWB;  // rows per copy instruction (64 lanes x 16 bytes)
-  static constexpr int NT = TK / 16;       // 16-key score blocks per tile
-  static constexpr int NU = TK / 32;       // 32-key PV steps per tile
-  static constexpr int SD = D / 32;        // QK k-steps
-  static constexpr int ND = D / 16;        // PV d-tiles
-  __device__ static int swz_k(int r) { return r & (CPR - 1); }
-  __device__ static int swz_v(int r) { return ((r & 7) << 1) & (CPR - 1); }
-};
-
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
-#define OMM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
-  const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (__attribute__((address_space(3))) bf16x4*)(p));
-  return __builtin_bit_cast(uint2, v);
-}
-
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor (gfx9 layout): base address, stride 0, num_records = nbytes (loads at or
-// past it read 0), dword 3 = the gfx9 data-format bits of an untyped buffer.
-__device__ __forceinline__ i32x4 buffer_desc(const void* base, int nbytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));  // address bits 32-47
-  r.z = __builtin_amdgcn_readfirstlane(nbytes);
-  r.w = 0x00020000;
-  return r;
-}
-
-// This wave's 4 of the 8 copy instructions of one K or V tile: rows [0, nrows) of `base` (row
-// stride rsb bytes) into the 8 KiB LDS buffer dst; instruction j (= 4 w + jj) fills dst bytes
-// [1024 j, 1024 j + 1024) and off[jj] is this lane's source offset for it.  Issued as inline asm
-// (M0 = LDS destination): the compiler then does not treat it as an LDS store, so it does not
-// make the next LDS read wait for this copy; the kernel orders copies and reads itself
-// (s_waitcnt vmcnt(0) and a barrier before a buffer is read, a barrier before it is refilled).
-// M0 is set here and used by nothing else in the kernel.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_part(const void* base, int rsb, int nrows, char* dst, int w,
-                                         const int (&off)[4]) {
-  const i32x4 r = buffer_desc(base, nrows * rsb);
-  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-      static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + 4096u * w)));
-  asm volatile(
-      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %4, %5, 0 offen lds"
-      :
-      : "s"(m0), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(r)
-      : "memory", "m0", "scc");
-}
-#pragma clang diagnostic pop
 
 constexpr int kDmaThreads = 128;
 

@@ -1,0 +1,735 @@
+// Selection attention backward over dense K / V: delta, dQ, the block -> query-group index, and
+// dK / dV.
+//
+// Reference semantics: cuda_backend/csrc/selection_bwd.cu:18-163 (dQ: delta = rowsum(out * dO)
+// in fp32, P recomputed as exp(s * scale - lse), dS = P (dP - delta) scale, dQ = dS K),
+// :164-306 (dK / dV: one owner per key block walks the query groups that selected it, no
+// atomics), inverted_index.cu:13-34 (which (group, slot) pairs a block receives: id in range,
+// block not after the group's chunk when causal), bwd_common.cuh:33-60 (partial tail blocks,
+// per-token chunk-causal prefix), :1329-1407 (dK / dV of never-selected tokens are 0, results
+// in the K / V dtype).
+//
+// gfx950 design (bf16 / f16), three launches:
+//   sel_bwd_dq_kernel    one workgroup = 64 queries of one group, 2 waves x 32 queries, the same
+//                        block walk and LDS-DMA K / V tiles as the forward kernel.  Per key tile:
+//                        S^T = K Q^T and dP^T = V dO^T (K and V rows from LDS, Q^T and dO^T held
+//                        in registers), P = 2^(s c2 - lse log2 e), dS = P (dP - delta) scale,
+//                        then dQ^T += K^T dS^T with dS^T straight from the accumulator layout and
+//                        K^T from ds_read_b64_tr_b16.  Writes dQ and delta.
+//   sel_bwd_index_kernel one workgroup per (b, h): counts, scans and scatters every valid
+//                        (group, slot) pair into per-block buckets (CSR), in (group, slot) order,
+//                        so the dK / dV sums have a fixed order (the reference's buckets are in
+//                        atomic arrival order).
+//   sel_bwd_dkv_kernel   one workgroup per (b, h, block, 64-key tile), 2 waves x 32 keys.  K and V
+//                        of its keys stay in registers as MFMA operands; the queries of each
+//                        bucket group stream through LDS (64-row Q / dO tiles by LDS DMA, double
+//                        buffered, with their lse and delta).  S = Q K^T, dP = dO V^T, then
+//                        dV += P^T dO and dK += dS^T Q with P^T / dS^T from the accumulator
+//                        layout and dO / Q from transposed LDS reads.  Every token of every block
+//                        is written (0 when no group selected it).
+#include "sel_common.h"
+
+namespace omm {
+namespace {
+
+// 8 packed 16-bit values of two rows -> fp32 dot product (fixed order, fp32 products).
+template <typename QT> __device__ __forceinline__ float dot8(uint4 a, uint4 b);
+template <> __device__ __forceinline__ float dot8<bf16_t>(uint4 a, uint4 b) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += __builtin_bit_cast(float, x[i] << 16) * __builtin_bit_cast(float, y[i] << 16);
+    s += __builtin_bit_cast(float, x[i] & 0xffff0000u) * __builtin_bit_cast(float, y[i] & 0xffff0000u);
+  }
+  return s;
+}
+template <> __device__ __forceinline__ float dot8<f16_t>(uint4 a, uint4 b) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const _Float16 x0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i]));
+    const _Float16 x1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] >> 16));
+    const _Float16 y0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(y[i]));
+    const _Float16 y1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(y[i] >> 16));
+    s += static_cast<float>(x0) * static_cast<float>(y0);
+    s += static_cast<float>(x1) * static_cast<float>(y1);
+  }
+  return s;
+}
+
+// -lse in the log2 domain; -inf for a row with no visible token (its P is then 0).
+__device__ __forceinline__ float neg_lse2(float l) { return l == kNegInf ? kNegInf : -l * kLog2e; }
+
+// ---- dQ -------------------------------------------------------------------------------------
+constexpr int kDqThreads = 128;
+
+template <typename QT, typename Acc, int D>
+__global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
+    View4<const QT> q, View4<const QT> o, View4<const QT> dout, View4<QT> dq,
+    const float* __restrict__ lse, float* __restrict__ delta, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale, int nsub) {
+  using DG = DmaGeom<D>;
+  constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
+  constexpr int NT = DG::NT, NU = DG::NU, SD = DG::SD, ND = DG::ND;
+  __shared__ __align__(16) char lds[4][8192];  // K buffers 0, 1; V buffers 2, 3
+
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int sub = wi % nsub; wi /= nsub;
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+
+  const int m0 = g * G + sub * 64;
+  const int m_end = min(min(g * G + G, M), m0 + 64);
+  const int qc = (g * G) / chunk;
+
+  // Q^T and dO^T operands of this wave's 2 query blocks (row m0 + 32 w + 16 x + l16, dims
+  // 32 s + 8 j4 ..), each query's delta (a 4-lane-group reduction) and -lse log2 e
+  bool q_ok[2];
+  uint4 qb[2][SD], db[2][SD];
+  float nl2[2], dl[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int mq = m0 + 32 * w + 16 * x + l16;
+    q_ok[x] = mq < m_end;
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SD; ++s) {
+      if (q_ok[x]) {
+        qb[x][s] = *reinterpret_cast<const uint4*>(q.at(b, mq, h, 32 * s + 8 * j4));
+        db[x][s] = *reinterpret_cast<const uint4*>(dout.at(b, mq, h, 32 * s + 8 * j4));
+        part += dot8<QT>(*reinterpret_cast<const uint4*>(o.at(b, mq, h, 32 * s + 8 * j4)),
+                         db[x][s]);
+      } else {
+        qb[x][s] = make_uint4(0, 0, 0, 0);
+        db[x][s] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    part += __shfl_xor(part, 16, kWave);
+    part += __shfl_xor(part, 32, kWave);
+    dl[x] = part;
+    const int64_t li = (static_cast<int64_t>(b) * H + h) * M + mq;
+    nl2[x] = q_ok[x] ? neg_lse2(lse[li]) : kNegInf;
+    if (q_ok[x] && j4 == 0) delta[li] = part;
+  }
+  const float c2 = scale * kLog2e;
+
+  // LDS read offsets inside a tile buffer.  K / V row operand (t, s): row 16 t + l16, chunk
+  // 4 s + j4.  K^T operand (u, half, i): row 32 u + 16 half + 4 j4 + (l16 >> 2), dims
+  // 16 i + 4 (l16 & 3) .. +3 (ds_read_b64_tr_b16 hands lane l16 dim 16 i + l16 of 4 keys).
+  int koff[SD], vroff[SD], ktoff[ND];
+#pragma unroll
+  for (int s = 0; s < SD; ++s) {
+    koff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_k(l16)) << 4);
+    vroff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_v(l16)) << 4);
+  }
+  {
+    const int kr = 4 * j4 + (l16 >> 2), km = l16 & 3;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      ktoff[i] = kr * ROWB + (((2 * i + (km >> 1)) ^ DG::swz_k(kr)) << 4) + ((km & 1) << 3);
+  }
+
+  f32x4 acc_dq[2][ND];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc_dq[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  WaveWalk<Acc, TK> wk;
+  wk.start(acc, b, g, h, T, qc);
+  int n_cur = 0;
+  int kdo[4], vdo[4];
+  int rsk = 0, rsv = 0;
+  if (wk.valid) {
+    rsk = static_cast<int>(wk.br.sk) * 2;
+    rsv = static_cast<int>(wk.br.sv) * 2;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
+      kdo[jj] = row * rsk + ((c ^ DG::swz_k(row)) << 4);
+      vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
+    }
+    dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
+             lds[0], w, kdo);
+    dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
+             lds[2], w, vdo);
+    n_cur = wk.n;
+    wk.advance(acc, b, g, h, T, qc);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+
+  auto step = [&](int BI) -> bool {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int n_nx = 0;
+    if (wk.valid) {
+      dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+               wk.n, lds[BI ^ 1], w, kdo);
+      dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
+               wk.n, lds[2 + (BI ^ 1)], w, vdo);
+      n_nx = wk.n;
+      wk.advance(acc, b, g, h, T, qc);
+    }
+    const char* Kt = lds[BI];
+    const char* Vt = lds[2 + BI];
+
+    // S^T = K Q^T and dP^T = V dO^T: lane holds keys 16 t + 4 j4 + r of query l16
+    f32x4 s4[2][NT], p4[2][NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      s4[0][t] = s4[1][t] = p4[0][t] = p4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        const uint4 a = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
+        s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+        s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+        const uint4 av = *reinterpret_cast<const uint4*>(Vt + vroff[s] + 16 * t * ROWB);
+        p4[0][t] = Mfma<QT>::run(av, db[0][s], p4[0][t]);
+        p4[1][t] = Mfma<QT>::run(av, db[1][s], p4[1][t]);
+      }
+    }
+    // dS = P (dP - delta) scale, P = 2^(s c2 - lse log2 e); keys past n_cur are not visible
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
+          if (n_cur < TK && 16 * t + 4 * j4 + r >= n_cur) p = 0.0f;
+          s4[x][t][r] = p * (p4[x][t][r] - dl[x]) * scale;
+        }
+    // dQ^T += K^T dS^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
+    // 32 u + 16 + 4 j4 + (e - 4), for both operands
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      uint4 sb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        sb[x] = make_uint4(Mfma<QT>::pack2(s4[x][2 * u][0], s4[x][2 * u][1]),
+                           Mfma<QT>::pack2(s4[x][2 * u][2], s4[x][2 * u][3]),
+                           Mfma<QT>::pack2(s4[x][2 * u + 1][0], s4[x][2 * u + 1][1]),
+                           Mfma<QT>::pack2(s4[x][2 * u + 1][2], s4[x][2 * u + 1][3]));
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        const uint2 lo = lds_read_tr16(Kt + ktoff[i] + (32 * u) * ROWB);
+        const uint2 hi = lds_read_tr16(Kt + ktoff[i] + (32 * u + 16) * ROWB);
+        const uint4 ka = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        acc_dq[0][i] = Mfma<QT>::run(ka, sb[0], acc_dq[0][i]);
+        acc_dq[1][i] = Mfma<QT>::run(ka, sb[1], acc_dq[1][i]);
+      }
+    }
+    n_cur = n_nx;
+    return n_cur > 0;
+  };
+  if (n_cur > 0)
+    for (int it = 0; step(it & 1); ++it) {
+    }
+
+  // lane holds dQ[query l16][dims 16 i + 4 j4 + r]
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    if (!q_ok[x]) continue;
+    const int mq = m0 + 32 * w + 16 * x + l16;
+    QT* op = dq.at(b, mq, h, 0);
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      uint2 w2;
+      w2.x = Mfma<QT>::pack2(acc_dq[x][i][0], acc_dq[x][i][1]);
+      w2.y = Mfma<QT>::pack2(acc_dq[x][i][2], acc_dq[x][i][3]);
+      *reinterpret_cast<uint2*>(op + 16 * i + 4 * j4) = w2;
+    }
+  }
+}
+
+// ---- block -> query-group index --------------------------------------------------------------
+constexpr int kIdxThreads = 256;
+constexpr int kIdxRange = 2048;  // buckets per pass over the pairs (LDS: 2048 x 36 bytes)
+
+// Bucket of (group g, slot t) of row (b, h), or -1 when the pair reaches no key.
+struct PairBucket {
+  const int32_t* ids;
+  int64_t is0, is1, is2, is3;
+  int T, NS, bs, chunk, G;
+  bool causal;
+  __device__ __forceinline__ int operator()(int b, int h, int p) const {
+    const int g = p / T, t = p - g * T;
+    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    if (bid < 0 || bid >= NS) return -1;
+    if (causal && (static_cast<int64_t>(bid) * bs) / chunk > (static_cast<int64_t>(g) * G) / chunk)
+      return -1;
+    return bid;
+  }
+};
+
+// offsets: [B*H][NS+1]; groups: [B*H][MG*T] (bucket j of row r is groups[r][offsets[r][j] ..
+// offsets[r][j+1]), ascending (group, slot)).  Pairs are taken 256 at a time; a pair's place in
+// its bucket is the bucket cursor plus the number of earlier pairs of the batch in the same
+// bucket, read from a 256-bit per-bucket mask (one 64-bit word per wave) in LDS.
+__global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
+    PairBucket pb, int H, int P, int32_t* __restrict__ offsets, int32_t* __restrict__ groups) {
+  __shared__ unsigned long long mask[kIdxRange][kIdxThreads / kWave];
+  __shared__ int cur[kIdxRange];
+  __shared__ int wsum[kIdxThreads / kWave];
+  constexpr int NW = kIdxThreads / kWave, PER = kIdxRange / kIdxThreads;
+  const int row = static_cast<int>(blockIdx.x);
+  const int b = row / H, h = row - (row / H) * H;
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int NS = pb.NS;
+  int32_t* off = offsets + static_cast<int64_t>(row) * (NS + 1);
+  int32_t* grp = groups + static_cast<int64_t>(row) * P;
+
+  for (int i = tid; i < kIdxRange; i += kIdxThreads)
+#pragma unroll
+    for (int j = 0; j < NW; ++j) mask[i][j] = 0ull;
+
+  int base = 0;
+  for (int lo = 0; lo < NS; lo += kIdxRange) {
+    const int nb = min(kIdxRange, NS - lo);
+    for (int i = tid; i < kIdxRange; i += kIdxThreads) cur[i] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += kIdxThreads) {
+      const int k = pb(b, h, p) - lo;
+      if (k >= 0 && k < nb) atomicAdd(&cur[k], 1);
+    }
+    __syncthreads();
+    // exclusive scan of the counts: PER consecutive buckets per thread
+    int v[PER], sum = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      v[j] = cur[PER * tid + j];
+      sum += v[j];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int y = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += y;
+    }
+    if (lane == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      before += j < w ? wsum[j] : 0;
+      tot += wsum[j];
+    }
+    int run = base + before + incl - sum;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = PER * tid + j;
+      if (i < nb) off[lo + i] = run;
+      cur[i] = run;
+      run += v[j];
+    }
+    base += tot;
+    __syncthreads();
+    for (int p0 = 0; p0 < P; p0 += kIdxThreads) {
+      const int p = p0 + tid;
+      const int k = p < P ? pb(b, h, p) - lo : -1;
+      const bool in = k >= 0 && k < nb;
+      if (in) atomicOr(&mask[k][w], 1ull << lane);
+      __syncthreads();
+      bool lead = false;
+      int cnt = 0;
+      if (in) {
+        int r = __builtin_popcountll(mask[k][w] & ((1ull << lane) - 1ull));
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+          const int c = __builtin_popcountll(mask[k][j]);
+          r += j < w ? c : 0;
+          cnt += c;
+        }
+        grp[cur[k] + r] = p / pb.T;
+        lead = r == 0;
+      }
+      __syncthreads();
+      if (lead) {
+        cur[k] += cnt;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) mask[k][j] = 0ull;
+      }
+      __syncthreads();
+    }
+  }
+  if (tid == 0) off[NS] = base;
+}
+
+// ---- dK / dV ----------------------------------------------------------------------------------
+constexpr int kKvThreads = 128;
+
+// One 64-bit-per-lane dword copy: lane L's float at base + 4 L (rows past nvalid read 0) into
+// LDS dst + 4 L, issued like dma_part (inline asm, ordered by the kernel's own waits).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_f32x64(const float* base, int nvalid, float* dst) {
+  const i32x4 r = buffer_desc(base, 4 * nvalid);
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)))));
+  const int off = 4 * lane_id();
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(off), "s"(r)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <typename QT, int D>
+__global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
+    View4<const QT> q, View4<const QT> dout, View4<const QT> k, View4<const QT> v, View4<QT> dk,
+    View4<QT> dv, const float* __restrict__ lse, const float* __restrict__ delta,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ groups, int M, int N, int H,
+    int G, int MG, int T, int NS, int bs, int nkt, int chunk, bool causal, float scale,
+    int nsub) {
+  using DG = DmaGeom<D>;
+  constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
+  constexpr int SD = DG::SD, ND = DG::ND;
+  constexpr int QH = 64 / TK;        // 8 KiB copy units per 64-row tile
+  constexpr int QB = 64 * ROWB;      // bytes of one 64-row tile
+  __shared__ __align__(16) char qlds[2][QB];
+  __shared__ __align__(16) char dlds[2][QB];
+  __shared__ __align__(16) float slds[2][2][64];  // [buffer][lse, delta][query]
+
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int kt = wi % nkt; wi /= nkt;
+  const int bid = wi % NS; wi /= NS;
+  const int h = wi % H;
+  const int b = wi / H;
+
+  const int t0 = bid * bs + 64 * kt;                         // first token of the tile
+  const int nk = min(min(bs - 64 * kt, 64), N - t0);         // tokens of the tile
+  if (nk <= 0) return;
+
+  // K^T and V^T operands of this wave's keys 32 w + 16 nt + l16, dims 32 s + 8 j4 ..
+  uint4 kb[2][SD], vb[2][SD];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int key = 32 * w + 16 * nt + l16;
+#pragma unroll
+    for (int s = 0; s < SD; ++s) {
+      const bool ok = key < nk;
+      kb[nt][s] = ok ? *reinterpret_cast<const uint4*>(k.at(b, t0 + key, h, 32 * s + 8 * j4))
+                     : make_uint4(0, 0, 0, 0);
+      vb[nt][s] = ok ? *reinterpret_cast<const uint4*>(v.at(b, t0 + key, h, 32 * s + 8 * j4))
+                     : make_uint4(0, 0, 0, 0);
+    }
+  }
+  const float c2 = scale * kLog2e;
+
+  // LDS offsets (Q and dO tiles share one layout, rows swizzled by swz_v).  Row operand
+  // (x, s): row 16 x + l16, chunk 4 s + j4.  Transposed operand (half, i): row 16 half + 4 j4 +
+  // (l16 >> 2), dims 16 i + 4 (l16 & 3) .. +3.
+  int roff[SD], troff[ND];
+#pragma unroll
+  for (int s = 0; s < SD; ++s) roff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_v(l16)) << 4);
+  {
+    const int tr = 4 * j4 + (l16 >> 2), tm = l16 & 3;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      troff[i] = tr * ROWB + (((2 * i + (tm >> 1)) ^ DG::swz_v(tr)) << 4) + ((tm & 1) << 3);
+  }
+  // this lane's source offsets of its wave's copy instructions (same rows for Q and dO)
+  const int rsq = static_cast<int>(q.s1) * 2, rsd = static_cast<int>(dout.s1) * 2;
+  int qdo[4], ddo[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
+    qdo[jj] = row * rsq + ((c ^ DG::swz_v(row)) << 4);
+    ddo[jj] = row * rsd + ((c ^ DG::swz_v(row)) << 4);
+  }
+
+  f32x4 acc_dk[2][ND], acc_dv[2][ND];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc_dk[nt][i] = acc_dv[nt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t orow = (static_cast<int64_t>(b) * H + h) * (NS + 1);
+  const int e0 = offsets[orow + bid], e1 = offsets[orow + bid + 1];
+  const int32_t* grp = groups + (static_cast<int64_t>(b) * H + h) * (static_cast<int64_t>(MG) * T);
+  const int nitems = (e1 - e0) * nsub;
+  const int64_t lrow = (static_cast<int64_t>(b) * H + h) * M;
+
+  // item i = (bucket entry i / nsub, 64-query part i % nsub): its first query, queries and
+  // visible keys of this tile; the next item with work at or after i
+  struct Item {
+    int i, q0, nq, nv;
+  };
+  auto find = [&](int i) -> Item {
+    for (; i < nitems; ++i) {
+      const int e = i / nsub, part = i - (i / nsub) * nsub;
+      const int g = grp[e0 + e];
+      const int q0 = g * G + 64 * part;
+      const int nq = min(min(g * G + G, M) - q0, 64);
+      int nv = nk;
+      if (causal) {
+        const int64_t lim = static_cast<int64_t>((g * G) / chunk + 1) * chunk - t0;
+        nv = lim < nv ? static_cast<int>(lim > 0 ? lim : 0) : nv;
+      }
+      if (nq > 0 && nv > 0) return Item{i, q0, nq, nv};
+    }
+    return Item{nitems, 0, 0, 0};
+  };
+  auto issue = [&](const Item& it, int buf) {
+    const char* qbase = reinterpret_cast<const char*>(q.at(b, it.q0, h, 0));
+    const char* dbase = reinterpret_cast<const char*>(dout.at(b, it.q0, h, 0));
+#pragma unroll
+    for (int c = 0; c < QH; ++c) {
+      const int nr = min(max(it.nq - c * TK, 0), TK);
+      dma_part(qbase + static_cast<int64_t>(c) * TK * rsq, rsq, nr, qlds[buf] + c * 8192, w, qdo);
+      dma_part(dbase + static_cast<int64_t>(c) * TK * rsd, rsd, nr, dlds[buf] + c * 8192, w, ddo);
+    }
+    dma_f32x64((w == 0 ? lse : delta) + lrow + it.q0, it.nq, slds[buf][w]);
+  };
+
+  Item cur = find(0);
+  if (cur.i < nitems) issue(cur, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+
+  int BI = 0;
+  while (cur.i < nitems) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const Item nx = find(cur.i + 1);
+    if (nx.i < nitems) issue(nx, BI ^ 1);
+    const char* Qt = qlds[BI];
+    const char* Dt = dlds[BI];
+    const float* Ls = slds[BI][0];
+    const float* Ds = slds[BI][1];
+
+#pragma unroll
+    for (int hq = 0; hq < 2; ++hq) {  // queries 32 hq + 16 x + ...
+      // S = Q K^T and dP = dO V^T: lane holds queries 32 hq + 16 x + 4 j4 + r of key
+      // 32 w + 16 nt + l16
+      f32x4 s4[2][2], p4[2][2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        s4[x][0] = s4[x][1] = p4[x][0] = p4[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SD; ++s) {
+          const int ro = roff[s] + (32 * hq + 16 * x) * ROWB;
+          const uint4 aq = *reinterpret_cast<const uint4*>(Qt + ro);
+          const uint4 ad = *reinterpret_cast<const uint4*>(Dt + ro);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            s4[x][nt] = Mfma<QT>::run(aq, kb[nt][s], s4[x][nt]);
+            p4[x][nt] = Mfma<QT>::run(ad, vb[nt][s], p4[x][nt]);
+          }
+        }
+      }
+      // P and dS; padded query rows have zero Q / dO and lse = delta = 0, so they add nothing
+      uint4 pa[2], sa[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const bool kv = 32 * w + 16 * nt + l16 < cur.nv;
+        float pv[2][4], dsv[2][4];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const float4 L4 = *reinterpret_cast<const float4*>(Ls + 32 * hq + 16 * x + 4 * j4);
+          const float4 D4 = *reinterpret_cast<const float4*>(Ds + 32 * hq + 16 * x + 4 * j4);
+          const float Lr[4] = {L4.x, L4.y, L4.z, L4.w}, Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][nt][r], c2, neg_lse2(Lr[r])));
+            p = kv ? p : 0.0f;
+            pv[x][r] = p;
+            dsv[x][r] = p * (p4[x][nt][r] - Dr[r]) * scale;
+          }
+        }
+        // k-slot e of lane group j4 is query 32 hq + 4 j4 + e (e < 4) or 32 hq + 16 + 4 j4 +
+        // (e - 4): x = 0 rows then x = 1 rows
+        pa[nt] = make_uint4(Mfma<QT>::pack2(pv[0][0], pv[0][1]), Mfma<QT>::pack2(pv[0][2], pv[0][3]),
+                            Mfma<QT>::pack2(pv[1][0], pv[1][1]), Mfma<QT>::pack2(pv[1][2], pv[1][3]));
+        sa[nt] = make_uint4(Mfma<QT>::pack2(dsv[0][0], dsv[0][1]),
+                            Mfma<QT>::pack2(dsv[0][2], dsv[0][3]),
+                            Mfma<QT>::pack2(dsv[1][0], dsv[1][1]),
+                            Mfma<QT>::pack2(dsv[1][2], dsv[1][3]));
+      }
+      // dV += P^T dO and dK += dS^T Q: B operands dO / Q rows 32 hq + 4 j4 + y (+16), dim
+      // 16 i + l16, from transposed reads
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        const int to = troff[i] + (32 * hq) * ROWB;
+        const uint2 dlo = lds_read_tr16(Dt + to), dhi = lds_read_tr16(Dt + to + 16 * ROWB);
+        const uint2 qlo = lds_read_tr16(Qt + to), qhi = lds_read_tr16(Qt + to + 16 * ROWB);
+        const uint4 bd = make_uint4(dlo.x, dlo.y, dhi.x, dhi.y);
+        const uint4 bq = make_uint4(qlo.x, qlo.y, qhi.x, qhi.y);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc_dv[nt][i] = Mfma<QT>::run(pa[nt], bd, acc_dv[nt][i]);
+          acc_dk[nt][i] = Mfma<QT>::run(sa[nt], bq, acc_dk[nt][i]);
+        }
+      }
+    }
+    cur = nx;
+    BI ^= 1;
+  }
+
+  // lane holds dK / dV[key 32 w + 16 nt + 4 j4 + r][dim 16 i + l16]
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = 32 * w + 16 * nt + 4 * j4 + r;
+      if (key >= nk) continue;
+      QT* kp = dk.at(b, t0 + key, h, 0);
+      QT* vp = dv.at(b, t0 + key, h, 0);
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        kp[16 * i + l16] = from_f32<QT>(acc_dk[nt][i][r]);
+        vp[16 * i + l16] = from_f32<QT>(acc_dv[nt][i][r]);
+      }
+    }
+}
+
+// ---- host side ----------------------------------------------------------------------------------
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct BwdWs {
+  size_t delta, offsets, groups, total;
+};
+inline BwdWs bwd_ws(int64_t B, int64_t M, int64_t H, int64_t MG, int64_t T, int64_t NS) {
+  BwdWs w;
+  w.delta = 0;
+  w.offsets = align256(static_cast<size_t>(B * H * M) * 4);
+  w.groups = w.offsets + align256(static_cast<size_t>(B * H * (NS + 1)) * 4);
+  w.total = w.groups + align256(static_cast<size_t>(B * H * MG * T) * 4);
+  return w;
+}
+
+inline bool aligned16b(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte rows with unit dim stride, element strides in multiples of 8, rows of at least D
+// elements and 64 rows within the 32-bit tile offsets of the LDS copies.
+inline bool rows16(const omm_view4& x, int64_t D) {
+  return x.stride[3] == 1 && aligned16b(x.data) && x.stride[0] % 8 == 0 && x.stride[1] % 8 == 0 &&
+         x.stride[2] % 8 == 0 && x.stride[1] >= D && 2 * x.stride[1] * 64 < (int64_t{1} << 31);
+}
+
+template <typename QT, int D>
+int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
+                   const omm_view4& ids, const omm_view4& out, const float* lse,
+                   const omm_view4& dout, int bs, int chunk, bool causal, int G, float scale,
+                   const omm_view4& dq, const omm_view4& dk, const omm_view4& dv, float* delta,
+                   char* ws, const BwdWs& L, hipStream_t s) {
+  const int B = static_cast<int>(q.size[0]), M = static_cast<int>(q.size[1]);
+  const int H = static_cast<int>(q.size[2]), N = static_cast<int>(k.size[1]);
+  const int MG = static_cast<int>(ids.size[1]), T = static_cast<int>(ids.size[3]);
+  const int NS = static_cast<int>(cdiv64(N, bs));
+  const int nsub = (G + 63) / 64;
+  const int ch = causal ? chunk : 1;
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* groups = reinterpret_cast<int32_t*>(ws + L.groups);
+
+  DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
+                   static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
+                   ids.stride[2], ids.stride[3], N, bs, ch, causal};
+  const int64_t dq_items = static_cast<int64_t>(B) * H * MG * nsub;
+  const int nkt = (bs + 63) / 64;
+  const int64_t kv_items = static_cast<int64_t>(B) * H * NS * nkt;
+  OMM_REQUIRE(dq_items <= 2147483647ll && kv_items <= 2147483647ll, OMM_EUNSUPPORTED,
+              "omm_sel_bwd: grid too large");
+  sel_bwd_dq_kernel<QT, DenseAcc<QT>, D><<<static_cast<unsigned>(dq_items), kDqThreads, 0, s>>>(
+      make_view<const QT>(q), make_view<const QT>(out), make_view<const QT>(dout),
+      make_view<QT>(dq), lse, delta, acc, M, H, G, MG, T, ch, scale, nsub);
+  int rc = check_launch("selection backward (dq)");
+  if (rc) return rc;
+
+  PairBucket pb{static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
+                ids.stride[2], ids.stride[3], T, NS, bs, ch, G, causal};
+  sel_bwd_index_kernel<<<static_cast<unsigned>(B * H), kIdxThreads, 0, s>>>(pb, H, MG * T, offsets,
+                                                                           groups);
+  rc = check_launch("selection backward (index)");
+  if (rc) return rc;
+
+  if (kv_items == 0) return OMM_OK;
+  sel_bwd_dkv_kernel<QT, D><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
+      make_view<const QT>(q), make_view<const QT>(dout), make_view<const QT>(k),
+      make_view<const QT>(v), make_view<QT>(dk), make_view<QT>(dv), lse, delta, offsets, groups, M,
+      N, H, G, MG, T, NS, bs, nkt, ch, causal, scale, nsub);
+  return check_launch("selection backward (dk/dv)");
+}
+
+}  // namespace
+}  // namespace omm
+
+extern "C" size_t omm_sel_bwd_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t N,
+                                              int32_t block_size, int32_t group_size, int64_t T) {
+  if (B <= 0 || M <= 0 || H <= 0 || N < 0 || block_size < 1 || group_size < 1 || T < 1) return 0;
+  const int64_t MG = omm::cdiv64(M, group_size), NS = omm::cdiv64(N, block_size);
+  return omm::bwd_ws(B, M, H, MG, T, NS).total;
+}
+
+extern "C" int omm_sel_bwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                           const omm_view4* ids, const omm_view4* out, const float* lse,
+                           const omm_view4* dout, int32_t dtype, int32_t block_size,
+                           int32_t chunk_size, int32_t causal, int32_t group_size, float scale,
+                           const omm_view4* dq, const omm_view4* dk, const omm_view4* dv,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(q && k && v && ids && out && lse && dout && dq && dk && dv, OMM_EINVAL,
+              "omm_sel_bwd: null argument");
+  const int64_t B = q->size[0], M = q->size[1], H = q->size[2], D = q->size[3];
+  const int64_t N = k->size[1];
+  for (int i = 0; i < 4; ++i) {
+    OMM_REQUIRE(out->size[i] == q->size[i] && dout->size[i] == q->size[i] &&
+                    dq->size[i] == q->size[i],
+                OMM_EINVAL, "omm_sel_bwd: out, d_out and dq must have q's shape");
+    OMM_REQUIRE(v->size[i] == k->size[i] && dk->size[i] == k->size[i] && dv->size[i] == k->size[i],
+                OMM_EINVAL, "omm_sel_bwd: v, dk and dv must have k's shape");
+  }
+  OMM_REQUIRE(k->size[0] == B && k->size[2] == H && k->size[3] == D, OMM_EINVAL,
+              "omm_sel_bwd: expected k/v [B,N,H,D] compatible with q");
+  OMM_REQUIRE(group_size >= 1 && block_size >= 1 && chunk_size >= 1, OMM_EINVAL,
+              "omm_sel_bwd: group_size, block_size and chunk_size must be >= 1");
+  const int64_t MG = cdiv64(M, group_size);
+  OMM_REQUIRE(ids->size[0] == B && ids->size[1] == MG && ids->size[2] == H && ids->size[3] >= 1,
+              OMM_EINVAL, "omm_sel_bwd: block_indices must be [%lld,%lld,%lld,T>=1]", (long long)B,
+              (long long)MG, (long long)H);
+  OMM_REQUIRE(N <= 2147483647ll && M <= 2147483647ll && MG * ids->size[3] <= 2147483647ll &&
+                  B * H * MG * ids->size[3] <= 2147483647ll,
+              OMM_EUNSUPPORTED, "omm_sel_bwd: sizes exceed the int32 index range");
+  if (B == 0 || M == 0 || H == 0) return OMM_OK;
+  const int64_t T = ids->size[3];
+  const BwdWs L = bwd_ws(B, M, H, MG, T, cdiv64(N, block_size));
+  OMM_REQUIRE(workspace != nullptr && workspace_bytes >= L.total &&
+                  (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+              OMM_EWORKSPACE, "omm_sel_bwd: workspace of %zu bytes (256-byte aligned) required",
+              L.total);
+  OMM_REQUIRE(dtype == OMM_BF16 || dtype == OMM_F16, OMM_EUNSUPPORTED,
+              "omm_sel_bwd: bf16 and f16 only (dtype %d)", dtype);
+  OMM_REQUIRE(D == 64 || D == 128, OMM_EUNSUPPORTED, "omm_sel_bwd: head dim 64 or 128 (got %lld)",
+              (long long)D);
+  OMM_REQUIRE(scale != 0.0f && __builtin_isfinite(scale), OMM_EINVAL,
+              "omm_sel_bwd: scale must be finite and non-zero");
+  bool ok = true;
+  for (const omm_view4* x : {q, k, v, out, dout, dq, dk, dv}) ok = ok && rows16(*x, D);
+  OMM_REQUIRE(ok, OMM_EUNSUPPORTED,
+              "omm_sel_bwd: q/k/v/out/d_out/dq/dk/dv need unit dim stride, 16-byte aligned rows "
+              "and row strides that are multiples of 8 elements");
+  char* ws = static_cast<char*>(workspace);
+  float* delta = reinterpret_cast<float*>(ws + L.delta);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool c = causal != 0;
+  if (dtype == OMM_BF16) {
+    if (D == 128)
+      return sel_bwd_launch<bf16_t, 128>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size,
+                                         c, group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
+    return sel_bwd_launch<bf16_t, 64>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
+                                      group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
+  }
+  if (D == 128)
+    return sel_bwd_launch<f16_t, 128>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
+                                      group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
+  return sel_bwd_launch<f16_t, 64>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
+                                   group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
+}

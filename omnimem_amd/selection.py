@@ -1,8 +1,10 @@
 """Dense selection attention with the reference's Python signature.
 
-Reference: src/omnimem/nsa/ops/selection/__init__.py:12-100 (facade and validation) and
-cuda_backend/ops.py:90-101 (op adapter).  Forward only: this build serves inference, so a call
-that would need gradients raises instead of returning a tensor without a backward.
+Reference: src/omnimem/nsa/ops/selection/__init__.py:12-100 (facade and validation),
+cuda_backend/ops.py:90-117 (op adapters) and cuda_backend/autograd.py:9-45 (autograd wiring:
+the forward saves q, k, v, ids, out and lse; the backward returns dq, dk, dv).  The backward
+runs on gfx950 for bf16 / f16 with head dim 64 or 128; a call that needs gradients outside that
+raises at the forward instead of returning a tensor without a backward.
 Extension: ``M % group_size`` need not be 0 (the last query group may be ragged).
 """
 from __future__ import annotations
@@ -16,7 +18,7 @@ import torch
 from . import _lib
 from .backend import NSABackendError, get_backend
 
-__all__ = ["selection_attention", "sel_fwd", "dense_attention"]
+__all__ = ["selection_attention", "sel_fwd", "sel_bwd", "dense_attention"]
 
 
 def _debug_checks_enabled() -> bool:
@@ -56,11 +58,16 @@ def _debug_check_unique(block_indices):
         raise ValueError("duplicate valid block ids within a row are not allowed (OMNIMEM_NSA_DEBUG)")
 
 
-def _no_grad_needed(*ts):
-    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts):
+def _grad_needed(*ts) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad
+                                           for t in ts)
+
+
+def _check_bwd_supported(q):
+    if q.dtype not in (torch.bfloat16, torch.float16) or q.shape[-1] not in (64, 128):
         raise NotImplementedError(
-            "selection attention backward is not part of this build (inference only); "
-            "call under torch.no_grad() or detach the inputs")
+            f"selection attention backward runs for bf16 / f16 with head dim 64 or 128 "
+            f"(got {q.dtype}, D={q.shape[-1]}); call under torch.no_grad() or detach the inputs")
 
 
 def sel_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
@@ -85,6 +92,67 @@ def sel_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: to
               int(group_size), float(scale), _lib.view4(out), lse.data_ptr() if lse.numel() else None,
               _lib.stream_of(q))
     return out, lse
+
+
+def sel_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+            out: torch.Tensor, lse: torch.Tensor, d_out: torch.Tensor, block_size: int,
+            chunk_size: int, scale: float, causal: bool, group_size: int,
+            allow_tf32: bool = True) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Op-level adapter (counterpart of ``omnimem_nsa::sel_bwd``): returns (dq, dk, dv) in the
+    q / k / v dtypes.  No host synchronisation.  ``allow_tf32`` is accepted for signature
+    compatibility: the MFMA operands are always 16-bit with fp32 accumulation."""
+    _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"),
+                      (out, "out"), (lse, "lse"), (d_out, "d_out"))
+    if not (q.dtype == k.dtype == v.dtype == out.dtype == d_out.dtype):
+        raise NSABackendError("sel_bwd: q/k/v/out/d_out must share one dtype")
+    if lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise NSABackendError("sel_bwd: lse must be contiguous fp32 [B, H, M]")
+    if block_indices.dtype != torch.int32:
+        block_indices = block_indices.to(torch.int32)
+    d_out = d_out if d_out.stride(-1) == 1 else d_out.contiguous()
+    B, M, H, D = q.shape
+    N = k.shape[1]
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or M == 0 or H == 0:
+        return dq, dk.zero_(), dv.zero_()
+    T = block_indices.shape[-1]
+    ws = _lib.workspace(_lib.lib().omm_sel_bwd_workspace_bytes(B, M, H, N, int(block_size),
+                                                               int(group_size), T), q.device)
+    _lib.call("omm_sel_bwd", _lib.view4(q), _lib.view4(k), _lib.view4(v),
+              _lib.view4(block_indices), _lib.view4(out), lse.data_ptr(), _lib.view4(d_out),
+              _lib.dtype_code(q), int(block_size), int(chunk_size), int(bool(causal)),
+              int(group_size), float(scale), _lib.view4(dq), _lib.view4(dk), _lib.view4(dv),
+              ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+    return dq, dk, dv
+
+
+class SelectionAttentionFn(torch.autograd.Function):
+    """Autograd wiring of the reference's SelectionAttentionCUDA (cuda_backend/autograd.py:9-45)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, block_indices, block_size, chunk_size=1, softmax_scale=None,
+                causal=False, return_lse=False, allow_tf32=True, bwd_method='auto',
+                group_size=1):
+        if softmax_scale is None:
+            softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+        out, lse = sel_fwd(q, k, v, block_indices, block_size, chunk_size, softmax_scale, causal,
+                           group_size, allow_tf32)
+        ctx.save_for_backward(q, k, v, block_indices, out, lse)
+        ctx.args = (block_size, chunk_size, softmax_scale, causal, group_size, allow_tf32)
+        if return_lse:
+            ctx.mark_non_differentiable(lse)
+            return out, lse
+        return out
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        q, k, v, block_indices, out, lse = ctx.saved_tensors
+        block_size, chunk_size, scale, causal, group_size, allow_tf32 = ctx.args
+        dq, dk, dv = sel_bwd(q, k, v, block_indices, out, lse, grad_outputs[0], block_size,
+                             chunk_size, scale, causal, group_size, allow_tf32)
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None
 
 
 def selection_attention(
@@ -117,8 +185,13 @@ def selection_attention(
     _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size, causal)
     if _debug_checks_enabled():
         _debug_check_unique(block_indices)
-    _no_grad_needed(q, k, v)
+    if block_indices.dtype != torch.int32:
+        block_indices = block_indices.to(torch.int32)
     sc = scale if scale is not None else q.shape[-1] ** -0.5
+    if _grad_needed(q, k, v):
+        _check_bwd_supported(q)
+        return SelectionAttentionFn.apply(q, k, v, block_indices, block_size, chunk_size, sc,
+                                          causal, return_lse, allow_tf32, bwd_method, group_size)
     out, lse = sel_fwd(q, k, v, block_indices, block_size, chunk_size, sc, causal, group_size,
                        allow_tf32)
     return (out, lse) if return_lse else out

@@ -18,6 +18,8 @@ wuyushuwys/OmniMem):
 * ``selection_attention``  -- dense selection attention (cuda_backend/csrc/common.cuh:158-190,
                               :327-332; selection_fwd.cu:1-3,218) as a float64 softmax over the
                               gathered token set; duplicated ids count twice, as in the kernel.
+* ``selection_attention_bwd`` -- its backward from (out, lse, d_out): delta, P recomputed from
+                              LSE, dS, dQ, dK, dV (cuda_backend/csrc/selection_bwd.cu:18-306).
 * ``e4m3_encode/decode``   -- OCP fp8 e4m3fn with round-to-nearest-even and saturation (new: the
                               reference has no fp8 cache).
 * ``quantize_pages``       -- per (page, head) amax/448 scaling of the fp8 cache.
@@ -273,6 +275,60 @@ def selection_attention(q, k, v, ids, group_size: int, scale: float, block_token
                 out[b, m0:m1, h] = (p @ vv) / den
                 lse[b, h, m0:m1] = (mx + np.log(den))[:, 0]
     return out, lse
+
+
+def selection_attention_bwd(q, k, v, ids, out, lse, d_out, group_size: int, scale: float,
+                            block_tokens, chunk_size: int = 1, causal: bool = False,
+                            groups=None):
+    """float64 backward of ``selection_attention`` from the forward's (out, lse), as the
+    reference's dQ and dK/dV kernels define it (cuda_backend/csrc/selection_bwd.cu:18-163,
+    :164-306; bwd_common.cuh:33-60):
+
+        delta_m = sum_d out[m, d] * d_out[m, d]
+        P_mj    = exp(q_m . k_j * scale - lse_m)        (0 when lse_m = -inf)
+        dS_mj   = P_mj * (d_out_m . v_j - delta_m) * scale
+        dq_m    = sum_j dS_mj k_j,   dk_j += sum_m dS_mj q_m,   dv_j += sum_m P_mj d_out_m
+
+    over the tokens each query group selects (a duplicated id contributes twice, as in the
+    forward).  Returns (dq, dk, dv, delta [B, H, M]); tokens no group selects get 0."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    out = np.asarray(out, dtype=np.float64)
+    d_out = np.asarray(d_out, dtype=np.float64)
+    lse = np.asarray(lse, dtype=np.float64)
+    B, M, H, D = q.shape
+    G = group_size
+    MG = ids.shape[1]
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    delta = np.einsum("bmhd,bmhd->bhm", out, d_out)
+    for b in range(B):
+        for g in (range(MG) if groups is None else groups):
+            m0, m1 = g * G, min((g + 1) * G, M)
+            if m0 >= M:
+                continue
+            q_chunk = (g * G) // chunk_size if causal else 0
+            for h in range(H):
+                toks = []
+                for bid in ids[b, g, h]:
+                    r = block_tokens(int(bid), q_chunk)
+                    if r is not None:
+                        toks.extend(range(r[0], r[0] + r[1]))
+                if not toks:
+                    continue
+                idx = np.asarray(toks, dtype=np.int64)
+                kk, vv = k[b, idx, h], v[b, idx, h]
+                qq, do = q[b, m0:m1, h], d_out[b, m0:m1, h]
+                l = lse[b, h, m0:m1][:, None]
+                fin = np.isfinite(l)
+                p = np.where(fin, np.exp((qq @ kk.T) * scale - np.where(fin, l, 0.0)), 0.0)
+                ds = p * ((do @ vv.T) - delta[b, h, m0:m1][:, None]) * scale
+                dq[b, m0:m1, h] = ds @ kk
+                np.add.at(dk[b, :, h], idx, ds.T @ qq)
+                np.add.at(dv[b, :, h], idx, p.T @ do)
+    return dq, dk, dv, delta
 
 
 # ---------------------------------------------------------------------------------------------

@@ -263,6 +263,96 @@ def test_selection_no_visible_token_gives_zero_and_neg_inf():
     assert np.all(out == 0) and np.all(np.isneginf(lse))
 
 
+def _bwd_case(seed):
+    """Tiny causal case with a ragged last group, a partial tail block, -1 and out-of-range ids,
+    a duplicated id and a group whose blocks are all invisible."""
+    rng = np.random.default_rng(seed)
+    B, M, N, H, D, BS, C, G = 1, 11, 22, 2, 4, 4, 8, 3
+    q, k, v = (rng.standard_normal((B, L, H, D)) for L in (M, N, N))
+    MG = -(-M // G)
+    ids = rng.integers(0, 6, size=(B, MG, H, 3)).astype(np.int32)
+    ids[0, 1, 0] = [0, 0, 1]        # duplicate: counted twice
+    ids[0, 2, 1, 2] = -1
+    ids[0, 3, 0, 1] = 9             # out of range: skipped
+    ids[0, 0, 1] = [5, 4, 3]        # group 0 (chunk 0) sees none of these
+    return q, k, v, ids, dict(group_size=G, scale=-0.7,
+                              block_tokens=O.dense_block_tokens(N, BS, C, True), chunk_size=C,
+                              causal=True)
+
+
+def test_selection_bwd_matches_finite_differences():
+    q, k, v, ids, kw = _bwd_case(30)
+    w = np.random.default_rng(31).standard_normal(q.shape)
+
+    def loss(q_, k_, v_):
+        return float((O.selection_attention(q_, k_, v_, ids, **kw)[0] * w).sum())
+
+    out, lse = O.selection_attention(q, k, v, ids, **kw)
+    assert np.isneginf(lse[0, 1, 0:3]).all()   # the invisible group really is empty
+    dq, dk, dv, _ = O.selection_attention_bwd(q, k, v, ids, out, lse, w, **kw)
+    eps = 1e-6
+    for x, g in ((q, dq), (k, dk), (v, dv)):
+        num = np.zeros_like(x)
+        for i in np.ndindex(x.shape):
+            x0 = x[i]
+            x[i] = x0 + eps
+            lp = loss(q, k, v)
+            x[i] = x0 - eps
+            lm = loss(q, k, v)
+            x[i] = x0
+            num[i] = (lp - lm) / (2 * eps)
+        np.testing.assert_allclose(g, num, atol=1e-7, rtol=1e-6)
+    assert np.abs(dk).sum() > 0 and np.abs(dq).sum() > 0
+
+
+def test_selection_bwd_matches_torch_autograd_of_masked_softmax():
+    """Same gradients from torch autograd (float64) of a per-group masked softmax attention."""
+    rng = np.random.default_rng(32)
+    B, M, N, H, D, BS, C, G = 1, 40, 50, 2, 8, 8, 20, 5
+    q, k, v = (rng.standard_normal((B, L, H, D)) for L in (M, N, N))
+    MG = M // G
+    ids = np.stack([np.stack([rng.permutation(7)[:3] for _ in range(H)]) for _ in range(MG)])
+    ids = ids.astype(np.int32)[None]
+    scale = 0.3
+    kw = dict(group_size=G, scale=scale, block_tokens=O.dense_block_tokens(N, BS, C, True),
+              chunk_size=C, causal=True)
+    out, lse = O.selection_attention(q, k, v, ids, **kw)
+    w = rng.standard_normal(q.shape)
+    dq, dk, dv, _ = O.selection_attention_bwd(q, k, v, ids, out, lse, w, **kw)
+
+    qt, kt, vt = (torch.tensor(a, requires_grad=True) for a in (q, k, v))
+    total = 0.0
+    for g in range(MG):
+        for h in range(H):
+            allowed = np.zeros(N, bool)
+            for bid in ids[0, g, h]:
+                t = np.arange(bid * BS, min(N, bid * BS + BS))
+                allowed[t[(t // C) <= (g * G) // C]] = True
+            if not allowed.any():
+                continue
+            rows = slice(g * G, (g + 1) * G)
+            s = (qt[0, rows, h] @ kt[0, :, h].T) * scale
+            s = s.masked_fill(~torch.from_numpy(allowed)[None], float("-inf"))
+            o = torch.softmax(s, dim=-1) @ vt[0, :, h]
+            total = total + (o * torch.from_numpy(w[0, rows, h])).sum()
+    total.backward()
+    for mine, t in ((dq, qt), (dk, kt), (dv, vt)):
+        np.testing.assert_allclose(mine, t.grad.numpy(), atol=1e-12)
+
+
+def test_selection_bwd_column_sums():
+    """sum_j dS_mj = 0 for every query (delta is the P-weighted mean of dP), so dk sums to 0
+    over keys; P rows sum to 1, so dv sums to the d_out of the queries that see a token."""
+    q, k, v, ids, kw = _bwd_case(33)
+    out, lse = O.selection_attention(q, k, v, ids, **kw)
+    w = np.random.default_rng(34).standard_normal(q.shape)
+    _, dk, dv, delta = O.selection_attention_bwd(q, k, v, ids, out, lse, w, **kw)
+    np.testing.assert_allclose(dk.sum(axis=1), 0.0, atol=1e-12)
+    seen = np.isfinite(lse).transpose(0, 2, 1)[..., None]           # [B, M, H, 1]
+    np.testing.assert_allclose(dv.sum(axis=1), (w * seen).sum(axis=1), atol=1e-12)
+    np.testing.assert_allclose(delta, np.einsum("bmhd,bmhd->bhm", out, w), atol=0)
+
+
 def test_quantize_pages_error_bound_and_amax():
     rng = np.random.default_rng(22)
     x = (rng.standard_t(4, size=(64, 128)) * 3).astype(np.float32)
