@@ -12,8 +12,10 @@ All 30 layers of a forward have this shape, so a forward is 30 steps.  ``value``
 selection-attention TFLOP/s of the whole step (4 * D * visible selected tokens per query, summed,
 divided by the step time); ``roofline`` is the selection-attention kernel alone, timed with HIP
 events on the stream it runs on.  Config 2 (top-k alone) is timed beside it and reported as
-``topk`` (GB/s of algorithmic bytes).  ``cpu_baseline`` times the reference's PyTorch CPU
-formulation (oracle/cpu_baseline.py) on a bounded sample of the same workload.
+``topk`` (GB/s of algorithmic bytes), and the selection backward of the same layer as ``sel_bwd``
+(useful work 2.5x the forward's).  ``ms_per_ar_chunk`` runs the AR driver (configs 4 and 5).
+``cpu_baseline`` times the reference's PyTorch CPU formulation (oracle/cpu_baseline.py) on a
+bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -295,6 +297,24 @@ def main():
     topk_ms = e0.elapsed_time(e1) / args.steps
 
     sel_tflops = flops / (sel_ms * 1e-3) / 1e12
+
+    # selection backward on the same layer (dq, dk, dv from the step's out / lse): useful work is
+    # 2.5x the forward's (S recomputed, dP, dQ, dK, dV: 5 products of the forward's 2)
+    from omnimem_amd.selection import sel_bwd
+    d_out = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
+    for _ in range(2):
+        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    b0.record()
+    for _ in range(args.steps):
+        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
+    b1.record()
+    torch.cuda.synchronize()
+    bwd_ms = b0.elapsed_time(b1) / args.steps
+    bwd_tflops = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
+    del d_out
+
     res = {
         "metric": METRIC,
         "value": round(flops / dt / 1e12, 3),
@@ -330,6 +350,12 @@ def main():
             "GB/s": round(C2_BYTES / (topk_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(C2_BYTES / (topk_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic("topk_kernel<bf16_t, 1>"),
+        },
+        "sel_bwd": {
+            "workload": "config 3 layer backward (dq, dk, dv; dQ, block index and dK/dV kernels)",
+            "ms": round(bwd_ms, 4),
+            "useful_tflops": round(bwd_tflops, 3),
+            "frac_bf16_peak": round(bwd_tflops / PEAK_BF16_TFLOPS, 4),
         },
         "ms_per_ar_chunk": None,
         "cpu_baseline": None,

@@ -68,8 +68,8 @@ constexpr int kDqThreads = 128;
 template <typename QT, typename Acc, int D>
 __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     View4<const QT> q, View4<const QT> o, View4<const QT> dout, View4<QT> dq,
-    const float* __restrict__ lse, float* __restrict__ delta, Acc acc, int M, int H, int G,
-    int MG, int T, int chunk, float scale, int nsub) {
+    const float* __restrict__ lse, float* __restrict__ delta, float* __restrict__ nl2out, Acc acc,
+    int M, int H, int G, int MG, int T, int chunk, float scale, int nsub) {
   using DG = DmaGeom<D>;
   constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
   constexpr int NT = DG::NT, NU = DG::NU, SD = DG::SD, ND = DG::ND;
@@ -115,24 +115,26 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     dl[x] = part;
     const int64_t li = (static_cast<int64_t>(b) * H + h) * M + mq;
     nl2[x] = q_ok[x] ? neg_lse2(lse[li]) : kNegInf;
-    if (q_ok[x] && j4 == 0) delta[li] = part;
+    if (q_ok[x] && j4 == 0) {
+      delta[li] = part;
+      nl2out[li] = nl2[x];
+    }
   }
   const float c2 = scale * kLog2e;
 
-  // LDS read offsets inside a tile buffer.  K / V row operand (t, s): row 16 t + l16, chunk
-  // 4 s + j4.  K^T operand (u, half, i): row 32 u + 16 half + 4 j4 + (l16 >> 2), dims
-  // 16 i + 4 (l16 & 3) .. +3 (ds_read_b64_tr_b16 hands lane l16 dim 16 i + l16 of 4 keys).
-  int koff[SD], vroff[SD], ktoff[ND];
+  // LDS read offsets inside a tile buffer; K and V rows are swizzled by swz_v (K is read both as
+  // rows and transposed; measured on gfx950 swz_v serves both read kinds best).  K / V row
+  // operand (t, s): row 16 t + l16, chunk 4 s + j4.  K^T operand (u, half, i): row 32 u +
+  // 16 half + 4 j4 + (l16 >> 2), dims 16 i + 4 (l16 & 3) .. +3 (ds_read_b64_tr_b16 hands lane
+  // l16 dim 16 i + l16 of 4 keys).
+  int koff[SD], ktoff[ND];
 #pragma unroll
-  for (int s = 0; s < SD; ++s) {
-    koff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_k(l16)) << 4);
-    vroff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_v(l16)) << 4);
-  }
+  for (int s = 0; s < SD; ++s) koff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_v(l16)) << 4);
   {
     const int kr = 4 * j4 + (l16 >> 2), km = l16 & 3;
 #pragma unroll
     for (int i = 0; i < ND; ++i)
-      ktoff[i] = kr * ROWB + (((2 * i + (km >> 1)) ^ DG::swz_k(kr)) << 4) + ((km & 1) << 3);
+      ktoff[i] = kr * ROWB + (((2 * i + (km >> 1)) ^ DG::swz_v(kr)) << 4) + ((km & 1) << 3);
   }
 
   f32x4 acc_dq[2][ND];
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
-      kdo[jj] = row * rsk + ((c ^ DG::swz_k(row)) << 4);
+      kdo[jj] = row * rsk + ((c ^ DG::swz_v(row)) << 4);
       vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
     }
     dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
@@ -189,12 +191,13 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
         const uint4 a = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
         s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
         s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
-        const uint4 av = *reinterpret_cast<const uint4*>(Vt + vroff[s] + 16 * t * ROWB);
+        const uint4 av = *reinterpret_cast<const uint4*>(Vt + koff[s] + 16 * t * ROWB);
         p4[0][t] = Mfma<QT>::run(av, db[0][s], p4[0][t]);
         p4[1][t] = Mfma<QT>::run(av, db[1][s], p4[1][t]);
       }
     }
-    // dS = P (dP - delta) scale, P = 2^(s c2 - lse log2 e); keys past n_cur are not visible
+    // dS / scale = P (dP - delta), P = 2^(s c2 - lse log2 e); keys past n_cur are not visible
+    // (the scale multiplies the dQ sums once at the end)
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -203,7 +206,7 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
         for (int r = 0; r < 4; ++r) {
           float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
           if (n_cur < TK && 16 * t + 4 * j4 + r >= n_cur) p = 0.0f;
-          s4[x][t][r] = p * (p4[x][t][r] - dl[x]) * scale;
+          s4[x][t][r] = p * (p4[x][t][r] - dl[x]);
         }
     // dQ^T += K^T dS^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
     // 32 u + 16 + 4 j4 + (e - 4), for both operands
@@ -241,8 +244,8 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
       uint2 w2;
-      w2.x = Mfma<QT>::pack2(acc_dq[x][i][0], acc_dq[x][i][1]);
-      w2.y = Mfma<QT>::pack2(acc_dq[x][i][2], acc_dq[x][i][3]);
+      w2.x = Mfma<QT>::pack2(acc_dq[x][i][0] * scale, acc_dq[x][i][1] * scale);
+      w2.y = Mfma<QT>::pack2(acc_dq[x][i][2] * scale, acc_dq[x][i][3] * scale);
       *reinterpret_cast<uint2*>(op + 16 * i + 4 * j4) = w2;
     }
   }
@@ -251,6 +254,7 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 // ---- block -> query-group index --------------------------------------------------------------
 constexpr int kIdxThreads = 256;
 constexpr int kIdxRange = 2048;  // buckets per pass over the pairs (LDS: 2048 x 36 bytes)
+constexpr int kIdxCache = 8192;  // pairs whose bucket is kept in LDS (32 KiB)
 
 // Bucket of (group g, slot t) of row (b, h), or -1 when the pair reaches no key.
 struct PairBucket {
@@ -276,6 +280,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
     PairBucket pb, int H, int P, int32_t* __restrict__ offsets, int32_t* __restrict__ groups) {
   __shared__ unsigned long long mask[kIdxRange][kIdxThreads / kWave];
   __shared__ int cur[kIdxRange];
+  __shared__ int bkt[kIdxCache];  // buckets of pairs 0 .. kIdxCache-1 (the rest are recomputed)
   __shared__ int wsum[kIdxThreads / kWave];
   constexpr int NW = kIdxThreads / kWave, PER = kIdxRange / kIdxThreads;
   const int row = static_cast<int>(blockIdx.x);
@@ -284,7 +289,9 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
   const int NS = pb.NS;
   int32_t* off = offsets + static_cast<int64_t>(row) * (NS + 1);
   int32_t* grp = groups + static_cast<int64_t>(row) * P;
+  auto bucket = [&](int p) { return p < kIdxCache ? bkt[p] : pb(b, h, p); };
 
+  for (int p = tid; p < min(P, kIdxCache); p += kIdxThreads) bkt[p] = pb(b, h, p);
   for (int i = tid; i < kIdxRange; i += kIdxThreads)
 #pragma unroll
     for (int j = 0; j < NW; ++j) mask[i][j] = 0ull;
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
     for (int i = tid; i < kIdxRange; i += kIdxThreads) cur[i] = 0;
     __syncthreads();
     for (int p = tid; p < P; p += kIdxThreads) {
-      const int k = pb(b, h, p) - lo;
+      const int k = bucket(p) - lo;
       if (k >= 0 && k < nb) atomicAdd(&cur[k], 1);
     }
     __syncthreads();
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
     __syncthreads();
     for (int p0 = 0; p0 < P; p0 += kIdxThreads) {
       const int p = p0 + tid;
-      const int k = p < P ? pb(b, h, p) - lo : -1;
+      const int k = p < P ? bucket(p) - lo : -1;
       const bool in = k >= 0 && k < nb;
       if (in) atomicOr(&mask[k][w], 1ull << lane);
       __syncthreads();
@@ -362,10 +369,16 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
 }
 
 // ---- dK / dV ----------------------------------------------------------------------------------
-constexpr int kKvThreads = 128;
+// Workgroup = 4 waves over one 64-key tile: wave w owns keys 16 w .. 16 w + 15 (one MFMA column
+// block) for every query of every item.  Its K / V operands and fp32 dK / dV sums take ~100
+// registers, so two waves share each SIMD (the workgroup's 66 KiB of LDS allows two workgroups
+// per CU): one wave's exp / dS VALU work overlaps the other's MFMAs.  The item's lse arrives
+// already as -lse log2 e (written by the dQ kernel), and the softmax scale of dK is applied once
+// to the sums.
+constexpr int kKvThreads = 256;
 
-// One 64-bit-per-lane dword copy: lane L's float at base + 4 L (rows past nvalid read 0) into
-// LDS dst + 4 L, issued like dma_part (inline asm, ordered by the kernel's own waits).
+// One dword per lane: lane L's float at base + 4 L (lanes at or past nvalid read 0) into LDS
+// dst + 4 L, issued like dma_part (inline asm, ordered by the kernel's own waits).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_f32x64(const float* base, int nvalid, float* dst) {
@@ -381,20 +394,20 @@ __device__ __forceinline__ void dma_f32x64(const float* base, int nvalid, float*
 #pragma clang diagnostic pop
 
 template <typename QT, int D>
-__global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
+__global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
     View4<const QT> q, View4<const QT> dout, View4<const QT> k, View4<const QT> v, View4<QT> dk,
-    View4<QT> dv, const float* __restrict__ lse, const float* __restrict__ delta,
+    View4<QT> dv, const float* __restrict__ nl2, const float* __restrict__ delta,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ groups, int M, int N, int H,
     int G, int MG, int T, int NS, int bs, int nkt, int chunk, bool causal, float scale,
     int nsub) {
   using DG = DmaGeom<D>;
-  constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
+  constexpr int ROWB = DG::ROWB, CPR = DG::CPR, RPI = DG::RPI;
   constexpr int SD = DG::SD, ND = DG::ND;
-  constexpr int QH = 64 / TK;        // 8 KiB copy units per 64-row tile
-  constexpr int QB = 64 * ROWB;      // bytes of one 64-row tile
-  __shared__ __align__(16) char qlds[2][QB];
-  __shared__ __align__(16) char dlds[2][QB];
-  __shared__ __align__(16) float slds[2][2][64];  // [buffer][lse, delta][query]
+  constexpr int QB = 64 * ROWB;           // bytes of one 64-row Q or dO tile
+  constexpr int NPC = QB / 4096;          // 4 KiB copy pieces per tile (4 copy instructions)
+  constexpr int PPW = 2 * NPC / 4;        // pieces per wave (Q and dO pieces of both tiles)
+  // [Q buffer 0, Q buffer 1, dO buffer 0, dO buffer 1][QB] then [buffer][lse, delta][64]
+  __shared__ __align__(16) char smem[4 * QB + 2 * 2 * 64 * 4];
 
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
@@ -409,49 +422,48 @@ __global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
   const int nk = min(min(bs - 64 * kt, 64), N - t0);         // tokens of the tile
   if (nk <= 0) return;
 
-  // K^T and V^T operands of this wave's keys 32 w + 16 nt + l16, dims 32 s + 8 j4 ..
-  uint4 kb[2][SD], vb[2][SD];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int key = 32 * w + 16 * nt + l16;
+  // K^T and V^T operands of this wave's key 16 w + l16, dims 32 s + 8 j4 ..
+  uint4 kb[SD], vb[SD];
+  {
+    const int key = 16 * w + l16;
+    const bool ok = key < nk;
 #pragma unroll
     for (int s = 0; s < SD; ++s) {
-      const bool ok = key < nk;
-      kb[nt][s] = ok ? *reinterpret_cast<const uint4*>(k.at(b, t0 + key, h, 32 * s + 8 * j4))
-                     : make_uint4(0, 0, 0, 0);
-      vb[nt][s] = ok ? *reinterpret_cast<const uint4*>(v.at(b, t0 + key, h, 32 * s + 8 * j4))
-                     : make_uint4(0, 0, 0, 0);
+      kb[s] = ok ? *reinterpret_cast<const uint4*>(k.at(b, t0 + key, h, 32 * s + 8 * j4))
+                 : make_uint4(0, 0, 0, 0);
+      vb[s] = ok ? *reinterpret_cast<const uint4*>(v.at(b, t0 + key, h, 32 * s + 8 * j4))
+                 : make_uint4(0, 0, 0, 0);
     }
   }
   const float c2 = scale * kLog2e;
 
-  // LDS offsets (Q and dO tiles share one layout, rows swizzled by swz_v).  Row operand
-  // (x, s): row 16 x + l16, chunk 4 s + j4.  Transposed operand (half, i): row 16 half + 4 j4 +
-  // (l16 >> 2), dims 16 i + 4 (l16 & 3) .. +3.
-  int roff[SD], troff[ND];
-#pragma unroll
-  for (int s = 0; s < SD; ++s) roff[s] = l16 * ROWB + (((4 * s + j4) ^ DG::swz_v(l16)) << 4);
-  {
-    const int tr = 4 * j4 + (l16 >> 2), tm = l16 & 3;
-#pragma unroll
-    for (int i = 0; i < ND; ++i)
-      troff[i] = tr * ROWB + (((2 * i + (tm >> 1)) ^ DG::swz_v(tr)) << 4) + ((tm & 1) << 3);
-  }
-  // this lane's source offsets of its wave's copy instructions (same rows for Q and dO)
+  // LDS offsets (Q and dO tiles share one layout, rows swizzled by swz_v, which depends on the
+  // row modulo 8 only; measured on gfx950 it serves the b128 row reads as well as swz_k and the
+  // transposed reads best).  Row operand (hq, x, s): row 32 hq + 16 x + l16, 16-byte chunk
+  // (4 s + j4) ^ swz_v(l16) = rx ^ 4 s.  Transposed operand (hq, half, i): row 32 hq +
+  // 16 half + tr, tr = 4 j4 + (l16 >> 2), chunk (2 i + (tm >> 1)) ^ swz_v(tr) =
+  // 2 (i ^ tx) + (tm >> 1) (swz_v is even), plus 8 bytes for odd tm = l16 & 3.  Offsets are
+  // formed at each use from these few registers.
+  const int rbase = l16 * ROWB;
+  const int rx = j4 ^ DG::swz_v(l16);
+  const int tr = 4 * j4 + (l16 >> 2), tm = l16 & 3;
+  const int tbase = tr * ROWB + ((tm >> 1) << 4) + ((tm & 1) << 3);
+  const int tx = DG::swz_v(tr) >> 1;
+  auto roff = [&](int s) { return rbase + ((rx ^ (4 * s)) << 4); };
+  auto troff = [&](int i) { return tbase + ((i ^ tx) << 5); };
+  // copy pieces of this wave: piece p = w + 4 pp of [Q pieces 0 .. NPC-1, dO pieces 0 .. NPC-1];
+  // instruction jj of piece pc copies rows (4 pc + jj) RPI + lane / CPR, whose row modulo 8
+  // (and so swizzle) does not depend on pc
   const int rsq = static_cast<int>(q.s1) * 2, rsd = static_cast<int>(dout.s1) * 2;
-  int qdo[4], ddo[4];
+  const int crow = lane / CPR;
+  int csw[4];
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
-    qdo[jj] = row * rsq + ((c ^ DG::swz_v(row)) << 4);
-    ddo[jj] = row * rsd + ((c ^ DG::swz_v(row)) << 4);
-  }
+  for (int jj = 0; jj < 4; ++jj) csw[jj] = ((lane % CPR) ^ DG::swz_v(jj * RPI + crow)) << 4;
 
-  f32x4 acc_dk[2][ND], acc_dv[2][ND];
+  // dK / scale and dV of keys 16 w + 4 j4 + r, dims 16 i + l16
+  f32x4 acc_dk[ND], acc_dv[ND];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int i = 0; i < ND; ++i) acc_dk[nt][i] = acc_dv[nt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < ND; ++i) acc_dk[i] = acc_dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t orow = (static_cast<int64_t>(b) * H + h) * (NS + 1);
   const int e0 = offsets[orow + bid], e1 = offsets[orow + bid + 1];
@@ -460,14 +472,23 @@ __global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
   const int64_t lrow = (static_cast<int64_t>(b) * H + h) * M;
 
   // item i = (bucket entry i / nsub, 64-query part i % nsub): its first query, queries and
-  // visible keys of this tile; the next item with work at or after i
+  // visible keys of this tile; find() returns the next item with work at or after i
   struct Item {
     int i, q0, nq, nv;
+  };
+  // bucket entries held in a VGPR, 64 at a time (lane j: entry gwin + j), read with readlane
+  int gwin = -64, gv = 0;
+  auto group_of = [&](int e) -> int {
+    if ((e & ~63) != gwin) {
+      gwin = e & ~63;
+      gv = gwin + lane < e1 - e0 ? grp[e0 + gwin + lane] : 0;
+    }
+    return __builtin_amdgcn_readlane(gv, e & 63);
   };
   auto find = [&](int i) -> Item {
     for (; i < nitems; ++i) {
       const int e = i / nsub, part = i - (i / nsub) * nsub;
-      const int g = grp[e0 + e];
+      const int g = group_of(e);
       const int q0 = g * G + 64 * part;
       const int nq = min(min(g * G + G, M) - q0, 64);
       int nv = nk;
@@ -483,12 +504,18 @@ __global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
     const char* qbase = reinterpret_cast<const char*>(q.at(b, it.q0, h, 0));
     const char* dbase = reinterpret_cast<const char*>(dout.at(b, it.q0, h, 0));
 #pragma unroll
-    for (int c = 0; c < QH; ++c) {
-      const int nr = min(max(it.nq - c * TK, 0), TK);
-      dma_part(qbase + static_cast<int64_t>(c) * TK * rsq, rsq, nr, qlds[buf] + c * 8192, w, qdo);
-      dma_part(dbase + static_cast<int64_t>(c) * TK * rsd, rsd, nr, dlds[buf] + c * 8192, w, ddo);
+    for (int pp = 0; pp < PPW; ++pp) {
+      const int piece = w + 4 * pp, pc = piece % NPC;
+      const bool isq = piece < NPC;
+      const int rs = isq ? rsq : rsd;
+      int off[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) off[jj] = ((4 * pc + jj) * RPI + crow) * rs + csw[jj];
+      dma_part(isq ? qbase : dbase, rs, it.nq, smem + (isq ? buf : 2 + buf) * QB, pc, off);
     }
-    dma_f32x64((w == 0 ? lse : delta) + lrow + it.q0, it.nq, slds[buf][w]);
+    if (w < 2)
+      dma_f32x64((w == 0 ? nl2 : delta) + lrow + it.q0, it.nq,
+                 reinterpret_cast<float*>(smem + 4 * QB) + (buf * 2 + w) * 64);
   };
 
   Item cur = find(0);
@@ -501,106 +528,107 @@ __global__ __launch_bounds__(kKvThreads, 1) void sel_bwd_dkv_kernel(
     __syncthreads();
     const Item nx = find(cur.i + 1);
     if (nx.i < nitems) issue(nx, BI ^ 1);
-    const char* Qt = qlds[BI];
-    const char* Dt = dlds[BI];
-    const float* Ls = slds[BI][0];
-    const float* Ds = slds[BI][1];
+    const char* Qt = smem + BI * QB;
+    const char* Dt = smem + (2 + BI) * QB;
+    const float* Ls = reinterpret_cast<const float*>(smem + 4 * QB) + BI * 128;
+    const float* Ds = Ls + 64;
+    const bool kv = 16 * w + l16 < cur.nv;
 
 #pragma unroll
-    for (int hq = 0; hq < 2; ++hq) {  // queries 32 hq + 16 x + ...
-      // S = Q K^T and dP = dO V^T: lane holds queries 32 hq + 16 x + 4 j4 + r of key
-      // 32 w + 16 nt + l16
-      f32x4 s4[2][2], p4[2][2];
+    for (int hq = 0; hq < 2; ++hq) {  // queries 32 hq .. 32 hq + 31
+      // S = Q K^T and dP = dO V^T: lane holds queries 32 hq + 16 x + 4 j4 + r of key 16 w + l16
+      f32x4 s4[2], p4[2];
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        s4[x][0] = s4[x][1] = p4[x][0] = p4[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        s4[x] = p4[x] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < SD; ++s) {
-          const int ro = roff[s] + (32 * hq + 16 * x) * ROWB;
-          const uint4 aq = *reinterpret_cast<const uint4*>(Qt + ro);
-          const uint4 ad = *reinterpret_cast<const uint4*>(Dt + ro);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            s4[x][nt] = Mfma<QT>::run(aq, kb[nt][s], s4[x][nt]);
-            p4[x][nt] = Mfma<QT>::run(ad, vb[nt][s], p4[x][nt]);
-          }
+          const int ro = roff(s) + (32 * hq + 16 * x) * ROWB;
+          s4[x] = Mfma<QT>::run(*reinterpret_cast<const uint4*>(Qt + ro), kb[s], s4[x]);
+          p4[x] = Mfma<QT>::run(*reinterpret_cast<const uint4*>(Dt + ro), vb[s], p4[x]);
         }
       }
-      // P and dS; padded query rows have zero Q / dO and lse = delta = 0, so they add nothing
-      uint4 pa[2], sa[2];
+      // P and dS / scale; padded query rows have zero Q / dO and lse = delta = 0, so they add
+      // nothing
+      float pv[2][4], dsv[2][4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const bool kv = 32 * w + 16 * nt + l16 < cur.nv;
-        float pv[2][4], dsv[2][4];
+      for (int x = 0; x < 2; ++x) {
+        const float4 L4 = *reinterpret_cast<const float4*>(Ls + 32 * hq + 16 * x + 4 * j4);
+        const float4 D4 = *reinterpret_cast<const float4*>(Ds + 32 * hq + 16 * x + 4 * j4);
+        const float Lr[4] = {L4.x, L4.y, L4.z, L4.w}, Dr[4] = {D4.x, D4.y, D4.z, D4.w};
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const float4 L4 = *reinterpret_cast<const float4*>(Ls + 32 * hq + 16 * x + 4 * j4);
-          const float4 D4 = *reinterpret_cast<const float4*>(Ds + 32 * hq + 16 * x + 4 * j4);
-          const float Lr[4] = {L4.x, L4.y, L4.z, L4.w}, Dr[4] = {D4.x, D4.y, D4.z, D4.w};
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][nt][r], c2, neg_lse2(Lr[r])));
-            p = kv ? p : 0.0f;
-            pv[x][r] = p;
-            dsv[x][r] = p * (p4[x][nt][r] - Dr[r]) * scale;
-          }
+        for (int r = 0; r < 4; ++r) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][r], c2, Lr[r]));
+          p = kv ? p : 0.0f;
+          pv[x][r] = p;
+          dsv[x][r] = p * (p4[x][r] - Dr[r]);
         }
-        // k-slot e of lane group j4 is query 32 hq + 4 j4 + e (e < 4) or 32 hq + 16 + 4 j4 +
-        // (e - 4): x = 0 rows then x = 1 rows
-        pa[nt] = make_uint4(Mfma<QT>::pack2(pv[0][0], pv[0][1]), Mfma<QT>::pack2(pv[0][2], pv[0][3]),
-                            Mfma<QT>::pack2(pv[1][0], pv[1][1]), Mfma<QT>::pack2(pv[1][2], pv[1][3]));
-        sa[nt] = make_uint4(Mfma<QT>::pack2(dsv[0][0], dsv[0][1]),
-                            Mfma<QT>::pack2(dsv[0][2], dsv[0][3]),
-                            Mfma<QT>::pack2(dsv[1][0], dsv[1][1]),
-                            Mfma<QT>::pack2(dsv[1][2], dsv[1][3]));
       }
+      // k-slot e of lane group j4 is query 32 hq + 4 j4 + e (e < 4) or 32 hq + 16 + 4 j4 +
+      // (e - 4): x = 0 rows then x = 1 rows
+      const uint4 pa = make_uint4(Mfma<QT>::pack2(pv[0][0], pv[0][1]),
+                                  Mfma<QT>::pack2(pv[0][2], pv[0][3]),
+                                  Mfma<QT>::pack2(pv[1][0], pv[1][1]),
+                                  Mfma<QT>::pack2(pv[1][2], pv[1][3]));
+      const uint4 sa = make_uint4(Mfma<QT>::pack2(dsv[0][0], dsv[0][1]),
+                                  Mfma<QT>::pack2(dsv[0][2], dsv[0][3]),
+                                  Mfma<QT>::pack2(dsv[1][0], dsv[1][1]),
+                                  Mfma<QT>::pack2(dsv[1][2], dsv[1][3]));
       // dV += P^T dO and dK += dS^T Q: B operands dO / Q rows 32 hq + 4 j4 + y (+16), dim
       // 16 i + l16, from transposed reads
 #pragma unroll
       for (int i = 0; i < ND; ++i) {
-        const int to = troff[i] + (32 * hq) * ROWB;
+        const int to = troff(i) + 32 * hq * ROWB;
         const uint2 dlo = lds_read_tr16(Dt + to), dhi = lds_read_tr16(Dt + to + 16 * ROWB);
         const uint2 qlo = lds_read_tr16(Qt + to), qhi = lds_read_tr16(Qt + to + 16 * ROWB);
-        const uint4 bd = make_uint4(dlo.x, dlo.y, dhi.x, dhi.y);
-        const uint4 bq = make_uint4(qlo.x, qlo.y, qhi.x, qhi.y);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          acc_dv[nt][i] = Mfma<QT>::run(pa[nt], bd, acc_dv[nt][i]);
-          acc_dk[nt][i] = Mfma<QT>::run(sa[nt], bq, acc_dk[nt][i]);
-        }
+        acc_dv[i] = Mfma<QT>::run(pa, make_uint4(dlo.x, dlo.y, dhi.x, dhi.y), acc_dv[i]);
+        acc_dk[i] = Mfma<QT>::run(sa, make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), acc_dk[i]);
       }
     }
     cur = nx;
     BI ^= 1;
   }
 
-  // lane holds dK / dV[key 32 w + 16 nt + 4 j4 + r][dim 16 i + l16]
+  // stage the fp32 key rows ([dK, dV][64 keys][D], 64 KiB: the Q / dO buffers) so that the
+  // whole workgroup converts 8 values at a time (packed conversions) and stores 16 bytes per
+  // lane; no copy is in flight here (the last item issued none)
+  float* stage = reinterpret_cast<float*>(smem);
+  static_assert(4 * QB >= 2 * 64 * D * 4, "staging area");
+  __syncthreads();
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int r = 0; r < 4; ++r) {
+    const int key = 16 * w + 4 * j4 + r;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = 32 * w + 16 * nt + 4 * j4 + r;
-      if (key >= nk) continue;
-      QT* kp = dk.at(b, t0 + key, h, 0);
-      QT* vp = dv.at(b, t0 + key, h, 0);
-#pragma unroll
-      for (int i = 0; i < ND; ++i) {
-        kp[16 * i + l16] = from_f32<QT>(acc_dk[nt][i][r]);
-        vp[16 * i + l16] = from_f32<QT>(acc_dv[nt][i][r]);
-      }
+    for (int i = 0; i < ND; ++i) {
+      stage[key * D + 16 * i + l16] = acc_dk[i][r] * scale;
+      stage[(64 + key) * D + 16 * i + l16] = acc_dv[i][r];
     }
+  }
+  __syncthreads();
+  constexpr int CH = D / 8;  // 8-element chunks per row
+  for (int c = tid; c < 2 * 64 * CH; c += kKvThreads) {
+    const int row = c / CH, ch = c - (c / CH) * CH;
+    const int key = row & 63;
+    if (key >= nk) continue;
+    const float4 x0 = *reinterpret_cast<const float4*>(stage + row * D + 8 * ch);
+    const float4 x1 = *reinterpret_cast<const float4*>(stage + row * D + 8 * ch + 4);
+    *reinterpret_cast<uint4*>((row < 64 ? dk : dv).at(b, t0 + key, h, 8 * ch)) =
+        make_uint4(Mfma<QT>::pack2(x0.x, x0.y), Mfma<QT>::pack2(x0.z, x0.w),
+                   Mfma<QT>::pack2(x1.x, x1.y), Mfma<QT>::pack2(x1.z, x1.w));
+  }
 }
 
 // ---- host side ----------------------------------------------------------------------------------
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 struct BwdWs {
-  size_t delta, offsets, groups, total;
+  size_t delta, nl2, offsets, groups, total;
 };
 inline BwdWs bwd_ws(int64_t B, int64_t M, int64_t H, int64_t MG, int64_t T, int64_t NS) {
   BwdWs w;
   w.delta = 0;
-  w.offsets = align256(static_cast<size_t>(B * H * M) * 4);
+  w.nl2 = align256(static_cast<size_t>(B * H * M) * 4);
+  w.offsets = w.nl2 + align256(static_cast<size_t>(B * H * M) * 4);
   w.groups = w.offsets + align256(static_cast<size_t>(B * H * (NS + 1)) * 4);
   w.total = w.groups + align256(static_cast<size_t>(B * H * MG * T) * 4);
   return w;
@@ -628,6 +656,7 @@ int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
   const int nsub = (G + 63) / 64;
   const int ch = causal ? chunk : 1;
   int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  float* nl2 = reinterpret_cast<float*>(ws + L.nl2);
   int32_t* groups = reinterpret_cast<int32_t*>(ws + L.groups);
 
   DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
@@ -640,7 +669,7 @@ int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
               "omm_sel_bwd: grid too large");
   sel_bwd_dq_kernel<QT, DenseAcc<QT>, D><<<static_cast<unsigned>(dq_items), kDqThreads, 0, s>>>(
       make_view<const QT>(q), make_view<const QT>(out), make_view<const QT>(dout),
-      make_view<QT>(dq), lse, delta, acc, M, H, G, MG, T, ch, scale, nsub);
+      make_view<QT>(dq), lse, delta, nl2, acc, M, H, G, MG, T, ch, scale, nsub);
   int rc = check_launch("selection backward (dq)");
   if (rc) return rc;
 
@@ -654,7 +683,7 @@ int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
   if (kv_items == 0) return OMM_OK;
   sel_bwd_dkv_kernel<QT, D><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
       make_view<const QT>(q), make_view<const QT>(dout), make_view<const QT>(k),
-      make_view<const QT>(v), make_view<QT>(dk), make_view<QT>(dv), lse, delta, offsets, groups, M,
+      make_view<const QT>(v), make_view<QT>(dk), make_view<QT>(dv), nl2, delta, offsets, groups, M,
       N, H, G, MG, T, NS, bs, nkt, ch, causal, scale, nsub);
   return check_launch("selection backward (dk/dv)");
 }
