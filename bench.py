@@ -27,6 +27,7 @@ import os
 import platform
 import sys
 import time
+from typing import Optional
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -148,8 +149,11 @@ def cpu_baseline(q, k, v, ids, seconds: float):
     }
 
 
-def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
-    """Configs 4 / 5: ms per AR chunk with ``history`` chunks cached, 48 GB HBM budget."""
+def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
+           keep_window_kv: Optional[bool] = None):
+    """Configs 4 / 5: ms per AR chunk with ``history`` chunks cached, 48 GB HBM budget.  The
+    sliding window of a bf16 cache is read from the cache's pages; an fp8 cache keeps a dense
+    bf16 ring of the window (``keep_window_kv`` overrides either choice)."""
     import torch
     from omnimem_amd.block_cache import PagedKVCache
     from omnimem_amd.wan_ar import WanARConfig, WanNSAAR
@@ -159,7 +163,9 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9):
     t0 = time.perf_counter()
     cache = PagedKVCache(cfg.layers, cfg.heads, cfg.head_dim, max_chunks=max_chunks,
                          chunk_len=cfg.chunk_tokens, page_tokens=cfg.page_tokens, dtype=dtype,
-                         hbm_budget_bytes=int(budget_bytes), window_chunks=cfg.window_chunks)
+                         hbm_budget_bytes=int(budget_bytes), window_chunks=cfg.window_chunks,
+                         keep_window_kv=(dtype == "fp8") if keep_window_kv is None
+                         else keep_window_kv)
     model = WanNSAAR(cfg, cache, seed=4)
     t_alloc = time.perf_counter() - t0
     t0 = time.perf_counter()

@@ -154,6 +154,7 @@ class PagedKVCache:
             self.win_k = [torch.zeros(wshape, dtype=torch.bfloat16, device=self.device)
                           for _ in range(self.L)]
             self.win_v = [torch.zeros_like(self.win_k[0]) for _ in range(self.L)]
+        self._win_ids: Dict[tuple, torch.Tensor] = {}
         self._table_h = np.full((self.L, H, MC), -1, dtype=np.int32)
         self._stage = torch.empty((H, MC), dtype=torch.int32).pin_memory()
         self.n_chunks = [0] * self.L
@@ -284,6 +285,47 @@ class PagedKVCache:
         L = self.chunk_len
         return (self.win_k[layer][:w].reshape(1, w * L, self.H, self.D),
                 self.win_v[layer][:w].reshape(1, w * L, self.H, self.D))
+
+    def window_attention(self, q: torch.Tensor, layer: int, softmax_scale: Optional[float] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Sliding-window attention (the reference's SWA branch, causal_wan_nsa_model.py:508, whose
+        window K/V come from the cache, models/cache.py:576-588): softmax attention of q (bf16
+        [1, M, H, D]) over every token of the last ``window_chunks`` chunks written.
+
+        With ``keep_window_kv`` the dense ring is read (``window_kv``); otherwise the pages of the
+        window chunks are read in place by the paged selection kernel, every page listed for
+        every query group (the window is protected from eviction, and a host-resident page would
+        still be read).  The paged read neither stamps the LRU nor counts page reads."""
+        from .selection import dense_attention
+        if self.keep_window_kv:
+            wk, wv = self.window_kv(layer)
+            return dense_attention(q, wk, wv, scale=softmax_scale, out=out)
+        _lib.require_cuda((q, "q"))
+        if q.dtype != torch.bfloat16:
+            raise BlockKVBackendError(f"window attention needs bf16 queries, got {q.dtype}")
+        B, M, H, D = q.shape
+        n = self.n_chunks[layer]
+        w = min(n, self.window)
+        if out is None:
+            out = torch.empty_like(q)
+        if w == 0:
+            return out.zero_()
+        G = 64
+        T = w * self.ppc
+        key = (q.device, n - w, T)
+        ids = self._win_ids.get(key)
+        if ids is None:
+            ids = torch.arange((n - w) * self.ppc, n * self.ppc, dtype=torch.int32, device=q.device)
+            self._win_ids = {key: ids}
+        ids4 = ids.view(1, 1, 1, T).expand(B, -(-M // G), H, T)
+        kv = self.layer_view(layer)
+        kv.stamp = None
+        kv.reads = None
+        scale = softmax_scale if softmax_scale is not None else D ** -0.5
+        _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(ids4), ctypes.byref(kv), G,
+                  float(scale), _lib.view4(out), None, 0, _lib.stream_of(q),
+                  error=BlockKVBackendError)
+        return out
 
     def cmp_history(self, layer: int):
         """Pooled keys / values of every page written so far: [1, n_chunks*ppc, H, D] each."""

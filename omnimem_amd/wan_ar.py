@@ -16,8 +16,10 @@ of the reference's AR inference branch, and the AR loop of its pipeline:
   and 1 context forward (t = 0) that rewrite the chunk's cache entries, then the offload flush.
 
 What stays PyTorch-ROCm (dense, off the selection path): the linear layers (hipBLASLt), the
-norms and the cross-attention.  The window and compressed attentions run on the selection kernel
-(``dense_attention``: every block of the window / pooled history listed for every query group).
+norms and the cross-attention.  The compressed attention runs on the selection kernel
+(``dense_attention``: every pooled block listed for every query group), and so does the window
+attention (``PagedKVCache.window_attention``: the window's pages read in place, or a dense ring
+for an fp8 cache).
 Rotary embedding is a plain interleaved rotation over the head dim with per-position angles (the
 reference's 3-axis frequency split and token reorder only permute which angles a token gets).
 The scheduler arithmetic between denoise steps is one axpy: timing does not depend on it.
@@ -208,8 +210,7 @@ class WanNSAAR:
         o_cmp = dense_attention(q, k_cmp, v_cmp)       # over the pooled history
         self._toc(tk)
         tk = self._tic("attn_swa")
-        wk, wv = cache.window_kv(layer)
-        o_swa = dense_attention(q, wk, wv)             # over the window chunks
+        o_swa = cache.window_attention(q, layer)        # over the window chunks
         self._toc(tk)
         tk = self._tic("topk")
         ids = parallel_nsa_topk(q, k_cmp, cfg.topk, block_size=cfg.page_tokens,

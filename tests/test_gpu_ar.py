@@ -26,7 +26,8 @@ def _run(hbm_slots, dtype=torch.bfloat16, history=5, steps=2):
     n = history + steps + 1
     cache = PagedKVCache(cfg.layers, cfg.heads, cfg.head_dim, max_chunks=n,
                          chunk_len=cfg.chunk_tokens, page_tokens=cfg.page_tokens, dtype=dtype,
-                         hbm_slots=hbm_slots, window_chunks=cfg.window_chunks)
+                         hbm_slots=hbm_slots, window_chunks=cfg.window_chunks,
+                         keep_window_kv=(dtype == "fp8"))
     model = WanNSAAR(cfg, cache, seed=3)
     model.prefill(history, seed=4, student_t=(dtype == "fp8"))
     g = torch.Generator(device="cuda").manual_seed(5)

@@ -223,6 +223,39 @@ def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype):
     assert torch.equal(out, out3)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_window_attention_reads_pages_in_place(dtype):
+    """SWA over the paged cache (window_attention without the dense ring) against float64
+    softmax attention over every token of the last 3 chunks: ragged chunks (300 tokens = 4 full
+    pages + 44), a window that covers part of the history, and for bf16 the dense-ring path on
+    the same data, which must agree with it."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(13)
+    H, D, C, P, n, W, M = 2, 128, 300, 64, 5, 3, 200
+    fp8 = dtype == "fp8"
+    caches = [PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                           window_chunks=W, keep_window_kv=keep)
+              for keep in ((False, True) if not fp8 else (False,))]
+    ks = [_chunk(g, C, H, D, 0.3, fp8) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, fp8) for _ in range(n)]
+    for cache in caches:
+        for cid in range(n):
+            cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    with torch.no_grad():
+        outs = [c.window_attention(q.to(DEV), 0) for c in caches]
+    torch.cuda.synchronize()
+    kk, vv = _paged_oracle_inputs(ks, vs, caches[0] if fp8 else None)
+    kk, vv = kk[:, (n - W) * C:], vv[:, (n - W) * C:]
+    ids = np.broadcast_to(np.arange(W * caches[0].ppc, dtype=np.int32), (1, -(-M // 64), H, W * caches[0].ppc))
+    want_o, _ = O.selection_attention(q.float().numpy(), kk, vv, ids, 64, D ** -0.5,
+                                      O.paged_block_tokens(C, P, W))
+    for out in outs:
+        _check_attn(out, None, want_o, None)
+    if len(outs) == 2:
+        assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-2
+
+
 def test_lru_residency_matches_reference_model():
     """lru_max_size per (layer, head), no sink / window: after every flush the HBM-resident
     chunks are exactly the reference LRU's (models/cache.py:673-699, :1032-1142)."""
