@@ -19,58 +19,6 @@
 namespace omm {
 namespace {
 
-template <typename Acc>
-__device__ __forceinline__ BlockRef resolve_block(const Acc& acc, int b, int g, int h, int t,
-                                                  int qc) {
-  const typename Acc::Ent e = acc.resolve(b, g, h, t, qc);
-  if (e.n <= 0) return BlockRef{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
-  return acc.ref(b, h, e);
-}
-
-// Key tiles of up to 64 tokens over the listed blocks (wave-uniform), one slot at a time.
-struct TileIt {
-  int t, tok0, n;  // block slot, first token of the tile within the block, tokens in tile
-  BlockRef br;
-  bool valid;
-};
-
-template <typename Acc>
-__device__ __forceinline__ TileIt first_tile(const Acc& acc, int b, int g, int h, int T, int qc,
-                                             int t) {
-  TileIt it;
-  for (; t < T; ++t) {
-    const BlockRef br = resolve_block(acc, b, g, h, t, qc);
-    if (br.k != nullptr && br.nvalid > 0) {
-      it.t = t;
-      it.tok0 = 0;
-      it.br = br;
-      it.n = br.nvalid < 64 ? br.nvalid : 64;
-      it.valid = true;
-      return it;
-    }
-  }
-  it.valid = false;
-  it.t = T;
-  it.tok0 = 0;
-  it.n = 0;
-  it.br = BlockRef{nullptr, nullptr, 0, 0, 0, 1.0f, 1.0f};
-  return it;
-}
-
-template <typename Acc>
-__device__ __forceinline__ TileIt next_tile(const Acc& acc, const TileIt& c, int b, int g, int h,
-                                            int T, int qc) {
-  if (c.tok0 + 64 < c.br.nvalid) {
-    TileIt it = c;
-    it.tok0 += 64;
-    const int rem = c.br.nvalid - it.tok0;
-    it.n = rem < 64 ? rem : 64;
-    return it;
-  }
-  return first_tile(acc, b, g, h, T, qc, c.t + 1);
-}
-
-
 // ---- staging: global -> registers -> LDS -----------------------------------------------------
 // K tile in LDS: Ks[key][KP], KP = D + 8 (row pitch 272 B for D = 128: the 16-byte A-operand
 // reads of 16 consecutive rows and the 16-byte row stores are both bank-conflict free).
@@ -659,21 +607,6 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
 
 // ---- VALU kernel (fp32 arithmetic, any head dim <= 256, any strides) -------------------------
 constexpr int kValuKeys = 32;
-
-template <typename KVT> __device__ __forceinline__ float kv_elem(const void* p, int64_t i, float s);
-template <> __device__ __forceinline__ float kv_elem<float>(const void* p, int64_t i, float) {
-  return static_cast<const float*>(p)[i];
-}
-template <> __device__ __forceinline__ float kv_elem<bf16_t>(const void* p, int64_t i, float) {
-  return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
-template <> __device__ __forceinline__ float kv_elem<f16_t>(const void* p, int64_t i, float) {
-  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
-}
-template <> __device__ __forceinline__ float kv_elem<uint8_t>(const void* p, int64_t i, float s) {
-  // dequantised value as the MFMA path sees it: code * scale rounded to bf16
-  return bf16_bits_to_f32(f32_to_bf16_bits(e4m3_to_f32(static_cast<const uint8_t*>(p)[i]) * s));
-}
 
 template <typename QT, typename Acc, int DQ>
 __global__ __launch_bounds__(256) void sel_fwd_valu_kernel(View4<const QT> q, View4<QT> out,

@@ -618,6 +618,195 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
   }
 }
 
+// ---- VALU kernels (fp32 arithmetic; any element type, head dim <= 256 and strides) ------------
+// The reference's FP32 SIMT kernels (selection_bwd.cu:18-306) in the same roles: dQ walks a
+// group's blocks with 4 lanes per query (DQ dims each, dot products reduced over the 4 lanes),
+// dK / dV owns a 64-key tile with 4 lanes per key and walks the bucket groups' queries through
+// LDS.  P = exp(s scale - lse) in the natural-log domain, as the reference computes it.
+constexpr int kVKeys = 32;   // keys per LDS tile (dQ)
+constexpr int kVQ = 16;      // queries per LDS tile (dK / dV)
+
+template <typename QT, typename Acc, int DQ>
+__global__ __launch_bounds__(256) void sel_bwd_dq_valu_kernel(
+    View4<const QT> q, View4<const QT> o, View4<const QT> dout, View4<QT> dq,
+    const float* __restrict__ lse, float* __restrict__ delta, float* __restrict__ nl2out, Acc acc,
+    int M, int H, int D, int G, int MG, int T, int chunk, float scale, int nsub, int64_t kv_sd) {
+  constexpr int DP = 4 * DQ;
+  __shared__ float Ks[kVKeys * DP];
+  __shared__ float Vs[kVKeys * DP];
+  using KVT = typename Acc::KV;
+  const int tid = threadIdx.x;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int sub = wi % nsub; wi /= nsub;
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+  const int m0 = g * G + sub * 64;
+  const int m_end = min(min(g * G + G, M), m0 + 64);
+  const int qc = (g * G) / chunk;
+  const int qi = tid >> 2, part = tid & 3;
+  const int my_q = m0 + qi;
+  const bool q_ok = my_q < m_end;
+  const int d0 = part * DQ;
+
+  float qr[DQ], dr[DQ], acc_q[DQ];
+  float dl = 0.0f;
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) {
+    const int d = d0 + i;
+    const bool ok = q_ok && d < D;
+    qr[i] = ok ? to_f32<QT>(*q.at(b, my_q, h, d)) : 0.0f;
+    dr[i] = ok ? to_f32<QT>(*dout.at(b, my_q, h, d)) : 0.0f;
+    dl += ok ? to_f32<QT>(*o.at(b, my_q, h, d)) * dr[i] : 0.0f;
+    acc_q[i] = 0.0f;
+  }
+  dl += __shfl_xor(dl, 1, kWave);
+  dl += __shfl_xor(dl, 2, kWave);
+  const int64_t li = (static_cast<int64_t>(b) * H + h) * M + my_q;
+  const float L = q_ok ? lse[li] : kNegInf;
+  if (q_ok && part == 0) {
+    delta[li] = dl;
+    nl2out[li] = neg_lse2(L);
+  }
+  for (TileIt it = first_tile(acc, b, g, h, T, qc, 0); it.valid;) {
+    for (int k0 = 0; k0 < it.n; k0 += kVKeys) {
+      const int nk = min(kVKeys, it.n - k0);
+      __syncthreads();
+      for (int i = tid; i < kVKeys * DP; i += 256) {
+        const int kk = i / DP, d = i - kk * DP;
+        float kvv = 0.0f, vvv = 0.0f;
+        if (kk < nk && d < D) {
+          const int64_t row = it.tok0 + k0 + kk;
+          kvv = kv_elem<KVT>(it.br.k, row * it.br.sk + d * kv_sd, it.br.scale_k);
+          vvv = kv_elem<KVT>(it.br.v, row * it.br.sv + d * kv_sd, it.br.scale_v);
+        }
+        Ks[i] = kvv;
+        Vs[i] = vvv;
+      }
+      __syncthreads();
+      for (int kk = 0; kk < nk; ++kk) {
+        float s = 0.0f, dp = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) {
+          s = __builtin_fmaf(qr[i], Ks[kk * DP + d0 + i], s);
+          dp = __builtin_fmaf(dr[i], Vs[kk * DP + d0 + i], dp);
+        }
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        dp += __shfl_xor(dp, 1, kWave);
+        dp += __shfl_xor(dp, 2, kWave);
+        const float p = L == kNegInf ? 0.0f : expf(s * scale - L);
+        const float ds = p * (dp - dl) * scale;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) acc_q[i] = __builtin_fmaf(ds, Ks[kk * DP + d0 + i], acc_q[i]);
+      }
+    }
+    it = next_tile(acc, it, b, g, h, T, qc);
+  }
+  if (q_ok) {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int d = d0 + i;
+      if (d < D) *dq.at(b, my_q, h, d) = from_f32<QT>(acc_q[i]);
+    }
+  }
+}
+
+template <typename QT, int DQ>
+__global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
+    View4<const QT> q, View4<const QT> dout, View4<const QT> k, View4<const QT> v, View4<QT> dk,
+    View4<QT> dv, const float* __restrict__ lse, const float* __restrict__ delta,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ groups, int M, int N, int H,
+    int D, int G, int MG, int T, int NS, int bs, int nkt, int chunk, bool causal, float scale) {
+  constexpr int DP = 4 * DQ;
+  __shared__ float Qs[kVQ * DP];
+  __shared__ float Ds[kVQ * DP];
+  __shared__ float Ls[kVQ], Dl[kVQ];
+  const int tid = threadIdx.x;
+  const int total = static_cast<int>(gridDim.x);
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  const int kt = wi % nkt; wi /= nkt;
+  const int bid = wi % NS; wi /= NS;
+  const int h = wi % H;
+  const int b = wi / H;
+  const int t0 = bid * bs + 64 * kt;
+  const int nk = min(min(bs - 64 * kt, 64), N - t0);
+  if (nk <= 0) return;
+  const int key = tid >> 2, part = tid & 3, d0 = part * DQ;
+  const bool k_ok = key < nk;
+
+  float kr[DQ], vr[DQ], acc_k[DQ], acc_v[DQ];
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) {
+    const int d = d0 + i;
+    const bool ok = k_ok && d < D;
+    kr[i] = ok ? to_f32<QT>(*k.at(b, t0 + key, h, d)) : 0.0f;
+    vr[i] = ok ? to_f32<QT>(*v.at(b, t0 + key, h, d)) : 0.0f;
+    acc_k[i] = acc_v[i] = 0.0f;
+  }
+  const int64_t orow = (static_cast<int64_t>(b) * H + h) * (NS + 1);
+  const int e0 = offsets[orow + bid], e1 = offsets[orow + bid + 1];
+  const int32_t* grp = groups + (static_cast<int64_t>(b) * H + h) * (static_cast<int64_t>(MG) * T);
+  const int64_t lrow = (static_cast<int64_t>(b) * H + h) * M;
+  for (int e = e0; e < e1; ++e) {
+    const int g = grp[e];
+    const int q_begin = g * G, q_end = min(g * G + G, M);
+    int nv = nk;
+    if (causal) {
+      const int64_t lim = static_cast<int64_t>((g * G) / chunk + 1) * chunk - t0;
+      nv = lim < nv ? static_cast<int>(lim > 0 ? lim : 0) : nv;
+    }
+    if (nv <= 0) continue;  // workgroup-uniform
+    const bool kv = key < nv;
+    for (int q0 = q_begin; q0 < q_end; q0 += kVQ) {
+      const int nq = min(kVQ, q_end - q0);
+      __syncthreads();
+      for (int i = tid; i < kVQ * DP; i += 256) {
+        const int qq = i / DP, d = i - qq * DP;
+        const bool ok = qq < nq && d < D;
+        Qs[i] = ok ? to_f32<QT>(*q.at(b, q0 + qq, h, d)) : 0.0f;
+        Ds[i] = ok ? to_f32<QT>(*dout.at(b, q0 + qq, h, d)) : 0.0f;
+      }
+      if (tid < kVQ) {
+        Ls[tid] = tid < nq ? lse[lrow + q0 + tid] : kNegInf;
+        Dl[tid] = tid < nq ? delta[lrow + q0 + tid] : 0.0f;
+      }
+      __syncthreads();
+      for (int qq = 0; qq < nq; ++qq) {
+        float s = 0.0f, dp = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) {
+          s = __builtin_fmaf(Qs[qq * DP + d0 + i], kr[i], s);
+          dp = __builtin_fmaf(Ds[qq * DP + d0 + i], vr[i], dp);
+        }
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        dp += __shfl_xor(dp, 1, kWave);
+        dp += __shfl_xor(dp, 2, kWave);
+        const float L = Ls[qq];
+        const float p = (kv && L != kNegInf) ? expf(s * scale - L) : 0.0f;
+        const float ds = p * (dp - Dl[qq]) * scale;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) {
+          acc_k[i] = __builtin_fmaf(ds, Qs[qq * DP + d0 + i], acc_k[i]);
+          acc_v[i] = __builtin_fmaf(p, Ds[qq * DP + d0 + i], acc_v[i]);
+        }
+      }
+    }
+  }
+  if (k_ok) {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int d = d0 + i;
+      if (d < D) {
+        *dk.at(b, t0 + key, h, d) = from_f32<QT>(acc_k[i]);
+        *dv.at(b, t0 + key, h, d) = from_f32<QT>(acc_v[i]);
+      }
+    }
+  }
+}
+
 // ---- host side ----------------------------------------------------------------------------------
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -643,20 +832,31 @@ inline bool rows16(const omm_view4& x, int64_t D) {
          x.stride[2] % 8 == 0 && x.stride[1] >= D && 2 * x.stride[1] * 64 < (int64_t{1} << 31);
 }
 
-template <typename QT, int D>
-int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
-                   const omm_view4& ids, const omm_view4& out, const float* lse,
-                   const omm_view4& dout, int bs, int chunk, bool causal, int G, float scale,
-                   const omm_view4& dq, const omm_view4& dk, const omm_view4& dv, float* delta,
-                   char* ws, const BwdWs& L, hipStream_t s) {
+struct BwdArgs {
+  const omm_view4 *q, *k, *v, *ids, *out, *dout, *dq, *dk, *dv;
+  const float* lse;
+  int bs, chunk, G;
+  bool causal;
+  float scale;
+};
+
+// Launches: dQ (and delta, -lse log2 e), the block -> group index, dK / dV.  MFMA kernels when
+// D is 64 or 128 with 16-bit rows (DM = D), else the VALU kernels with DQ dims per lane.
+template <typename QT, int DM, int DQ>
+int sel_bwd_launch(const BwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
+  const omm_view4 &q = *a.q, &k = *a.k, &v = *a.v, &ids = *a.ids;
   const int B = static_cast<int>(q.size[0]), M = static_cast<int>(q.size[1]);
-  const int H = static_cast<int>(q.size[2]), N = static_cast<int>(k.size[1]);
+  const int H = static_cast<int>(q.size[2]), D = static_cast<int>(q.size[3]);
+  const int N = static_cast<int>(k.size[1]);
   const int MG = static_cast<int>(ids.size[1]), T = static_cast<int>(ids.size[3]);
+  const int bs = a.bs, G = a.G;
   const int NS = static_cast<int>(cdiv64(N, bs));
   const int nsub = (G + 63) / 64;
-  const int ch = causal ? chunk : 1;
-  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  const bool causal = a.causal;
+  const int ch = causal ? a.chunk : 1;
+  float* delta = reinterpret_cast<float*>(ws + L.delta);
   float* nl2 = reinterpret_cast<float*>(ws + L.nl2);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
   int32_t* groups = reinterpret_cast<int32_t*>(ws + L.groups);
 
   DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
@@ -667,9 +867,16 @@ int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
   const int64_t kv_items = static_cast<int64_t>(B) * H * NS * nkt;
   OMM_REQUIRE(dq_items <= 2147483647ll && kv_items <= 2147483647ll, OMM_EUNSUPPORTED,
               "omm_sel_bwd: grid too large");
-  sel_bwd_dq_kernel<QT, DenseAcc<QT>, D><<<static_cast<unsigned>(dq_items), kDqThreads, 0, s>>>(
-      make_view<const QT>(q), make_view<const QT>(out), make_view<const QT>(dout),
-      make_view<QT>(dq), lse, delta, nl2, acc, M, H, G, MG, T, ch, scale, nsub);
+  if constexpr (DM > 0) {
+    sel_bwd_dq_kernel<QT, DenseAcc<QT>, DM><<<static_cast<unsigned>(dq_items), kDqThreads, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.out), make_view<const QT>(*a.dout),
+        make_view<QT>(*a.dq), a.lse, delta, nl2, acc, M, H, G, MG, T, ch, a.scale, nsub);
+  } else {
+    sel_bwd_dq_valu_kernel<QT, DenseAcc<QT>, DQ><<<static_cast<unsigned>(dq_items), 256, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.out), make_view<const QT>(*a.dout),
+        make_view<QT>(*a.dq), a.lse, delta, nl2, acc, M, H, D, G, MG, T, ch, a.scale, nsub,
+        k.stride[3]);
+  }
   int rc = check_launch("selection backward (dq)");
   if (rc) return rc;
 
@@ -681,11 +888,30 @@ int sel_bwd_launch(const omm_view4& q, const omm_view4& k, const omm_view4& v,
   if (rc) return rc;
 
   if (kv_items == 0) return OMM_OK;
-  sel_bwd_dkv_kernel<QT, D><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
-      make_view<const QT>(q), make_view<const QT>(dout), make_view<const QT>(k),
-      make_view<const QT>(v), make_view<QT>(dk), make_view<QT>(dv), nl2, delta, offsets, groups, M,
-      N, H, G, MG, T, NS, bs, nkt, ch, causal, scale, nsub);
+  if constexpr (DM > 0) {
+    sel_bwd_dkv_kernel<QT, DM><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), make_view<const QT>(k),
+        make_view<const QT>(v), make_view<QT>(*a.dk), make_view<QT>(*a.dv), nl2, delta, offsets,
+        groups, M, N, H, G, MG, T, NS, bs, nkt, ch, causal, a.scale, nsub);
+  } else {
+    sel_bwd_dkv_valu_kernel<QT, DQ><<<static_cast<unsigned>(kv_items), 256, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), make_view<const QT>(k),
+        make_view<const QT>(v), make_view<QT>(*a.dk), make_view<QT>(*a.dv), a.lse, delta, offsets,
+        groups, M, N, H, D, G, MG, T, NS, bs, nkt, ch, causal, a.scale);
+  }
   return check_launch("selection backward (dk/dv)");
+}
+
+template <typename QT>
+int sel_bwd_typed(const BwdArgs& a, bool mfma, char* ws, const BwdWs& L, hipStream_t s) {
+  const int64_t D = a.q->size[3];
+  if constexpr (sizeof(QT) == 2) {
+    if (mfma && D == 128) return sel_bwd_launch<QT, 128, 0>(a, ws, L, s);
+    if (mfma && D == 64) return sel_bwd_launch<QT, 64, 0>(a, ws, L, s);
+  }
+  if (D <= 64) return sel_bwd_launch<QT, 0, 16>(a, ws, L, s);
+  if (D <= 128) return sel_bwd_launch<QT, 0, 32>(a, ws, L, s);
+  return sel_bwd_launch<QT, 0, 64>(a, ws, L, s);
 }
 
 }  // namespace
@@ -734,31 +960,25 @@ extern "C" int omm_sel_bwd(const omm_view4* q, const omm_view4* k, const omm_vie
                   (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
               OMM_EWORKSPACE, "omm_sel_bwd: workspace of %zu bytes (256-byte aligned) required",
               L.total);
-  OMM_REQUIRE(dtype == OMM_BF16 || dtype == OMM_F16, OMM_EUNSUPPORTED,
-              "omm_sel_bwd: bf16 and f16 only (dtype %d)", dtype);
-  OMM_REQUIRE(D == 64 || D == 128, OMM_EUNSUPPORTED, "omm_sel_bwd: head dim 64 or 128 (got %lld)",
-              (long long)D);
-  OMM_REQUIRE(scale != 0.0f && __builtin_isfinite(scale), OMM_EINVAL,
-              "omm_sel_bwd: scale must be finite and non-zero");
-  bool ok = true;
-  for (const omm_view4* x : {q, k, v, out, dout, dq, dk, dv}) ok = ok && rows16(*x, D);
-  OMM_REQUIRE(ok, OMM_EUNSUPPORTED,
-              "omm_sel_bwd: q/k/v/out/d_out/dq/dk/dv need unit dim stride, 16-byte aligned rows "
-              "and row strides that are multiples of 8 elements");
+  OMM_REQUIRE(D >= 1 && D <= 256, OMM_EUNSUPPORTED, "omm_sel_bwd: head dim must be in [1, 256] "
+              "(got %lld)", (long long)D);
+  OMM_REQUIRE(__builtin_isfinite(scale), OMM_EINVAL, "omm_sel_bwd: scale must be finite");
+  // MFMA kernels: 16-bit rows of head dim 64 / 128, 16-byte aligned, and a non-zero scale;
+  // everything else runs the VALU kernels (k and v then need one dim stride)
+  bool rows_ok = true;
+  for (const omm_view4* x : {q, k, v, out, dout, dq, dk, dv}) rows_ok = rows_ok && rows16(*x, D);
+  const bool mfma = (dtype == OMM_BF16 || dtype == OMM_F16) && (D == 64 || D == 128) && rows_ok &&
+                    scale != 0.0f;
+  OMM_REQUIRE(mfma || k->stride[3] == v->stride[3], OMM_EUNSUPPORTED,
+              "omm_sel_bwd: k and v need the same dim stride");
   char* ws = static_cast<char*>(workspace);
-  float* delta = reinterpret_cast<float*>(ws + L.delta);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool c = causal != 0;
-  if (dtype == OMM_BF16) {
-    if (D == 128)
-      return sel_bwd_launch<bf16_t, 128>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size,
-                                         c, group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
-    return sel_bwd_launch<bf16_t, 64>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
-                                      group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
+  const BwdArgs a{q, k, v, ids, out, dout, dq, dk, dv, lse, block_size, chunk_size, group_size,
+                  causal != 0, scale};
+  switch (dtype) {
+    case OMM_BF16: return sel_bwd_typed<bf16_t>(a, mfma, ws, L, s);
+    case OMM_F16: return sel_bwd_typed<f16_t>(a, mfma, ws, L, s);
+    case OMM_F32: return sel_bwd_typed<float>(a, false, ws, L, s);
+    default: return set_error(OMM_EINVAL, "omm_sel_bwd: unsupported dtype %d", dtype);
   }
-  if (D == 128)
-    return sel_bwd_launch<f16_t, 128>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
-                                      group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
-  return sel_bwd_launch<f16_t, 64>(*q, *k, *v, *ids, *out, lse, *dout, block_size, chunk_size, c,
-                                   group_size, scale, *dq, *dk, *dv, delta, ws, L, s);
 }

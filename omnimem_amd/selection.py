@@ -3,8 +3,8 @@
 Reference: src/omnimem/nsa/ops/selection/__init__.py:12-100 (facade and validation),
 cuda_backend/ops.py:90-117 (op adapters) and cuda_backend/autograd.py:9-45 (autograd wiring:
 the forward saves q, k, v, ids, out and lse; the backward returns dq, dk, dv).  The backward
-runs on gfx950 for bf16 / f16 with head dim 64 or 128; a call that needs gradients outside that
-raises at the forward instead of returning a tensor without a backward.
+runs on gfx950 MFMA for bf16 / f16 with head dim 64 or 128, and on fp32 VALU kernels for fp32
+and every other head dim up to 256.
 Extension: ``M % group_size`` need not be 0 (the last query group may be ragged).
 """
 from __future__ import annotations
@@ -64,10 +64,10 @@ def _grad_needed(*ts) -> bool:
 
 
 def _check_bwd_supported(q):
-    if q.dtype not in (torch.bfloat16, torch.float16) or q.shape[-1] not in (64, 128):
+    if q.shape[-1] > 256:
         raise NotImplementedError(
-            f"selection attention backward runs for bf16 / f16 with head dim 64 or 128 "
-            f"(got {q.dtype}, D={q.shape[-1]}); call under torch.no_grad() or detach the inputs")
+            f"selection attention backward supports head dims up to 256 (got {q.shape[-1]}); "
+            "call under torch.no_grad() or detach the inputs")
 
 
 def sel_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
@@ -100,7 +100,8 @@ def sel_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: to
             allow_tf32: bool = True) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Op-level adapter (counterpart of ``omnimem_nsa::sel_bwd``): returns (dq, dk, dv) in the
     q / k / v dtypes.  No host synchronisation.  ``allow_tf32`` is accepted for signature
-    compatibility: the MFMA operands are always 16-bit with fp32 accumulation."""
+    compatibility: 16-bit inputs use 16-bit MFMA operands with fp32 accumulation, fp32 inputs
+    full fp32 arithmetic."""
     _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"),
                       (out, "out"), (lse, "lse"), (d_out, "d_out"))
     if not (q.dtype == k.dtype == v.dtype == out.dtype == d_out.dtype):
@@ -109,7 +110,6 @@ def sel_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: to
         raise NSABackendError("sel_bwd: lse must be contiguous fp32 [B, H, M]")
     if block_indices.dtype != torch.int32:
         block_indices = block_indices.to(torch.int32)
-    d_out = d_out if d_out.stride(-1) == 1 else d_out.contiguous()
     B, M, H, D = q.shape
     N = k.shape[1]
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)

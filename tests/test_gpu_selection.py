@@ -154,8 +154,8 @@ def test_selection_attention_facade_validation():
     ids = torch.full((1, 1, 1, 2), 5, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError):
         selection_attention(q, q, q, ids, 2, 64, group_size=64)  # id 5 >= 1 block
-    with pytest.raises(NotImplementedError):
-        selection_attention(q.requires_grad_(), q, q, ids.clamp(max=0), 2, 64, group_size=64)
+    o = selection_attention(q.requires_grad_(), q, q, ids.clamp(max=0), 2, 64, group_size=64)
+    assert o.grad_fn is not None  # the backward is wired (head dim 16 runs the VALU kernels)
 
 
 @pytest.mark.parametrize("M,N,H", [(130, 300, 2), (64, 64, 1), (300, 1500, 3), (1, 70, 1)])

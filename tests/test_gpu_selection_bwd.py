@@ -4,7 +4,9 @@ The oracle's backward (oracle.nsa_oracle.selection_attention_bwd, pinned in test
 finite differences and by torch autograd) is fed the same bf16/f16 inputs and the GPU forward's
 own (out, lse), so the comparison isolates the backward kernels.  Tolerance, per gradient tensor
 g with oracle value r: max|g - r| <= 2e-2 * max|r| and mean|g - r| <= 5e-3 * mean|r| (16-bit
-MFMA operands for P and dS, fp32 accumulation, one rounding of the result to the input dtype).
+MFMA operands for P and dS, fp32 accumulation, one rounding of the result to the input dtype);
+fp32 inputs (full fp32 VALU arithmetic, BASELINE's fp32 bar): 1e-4 * max|r| and 1e-5 * mean|r|.
+Head dims other than 64 / 128, fp32 and non-unit dim strides run the VALU kernels.
 
 Cases follow the forward's (reference rules: cuda_backend/csrc/selection_bwd.cu:18-306,
 inverted_index.cu:13-34, bwd_common.cuh:33-60): partial tail blocks, chunk-causal prefixes, -1
@@ -33,6 +35,9 @@ def _ids(gen, B, MG, H, T, nblocks, minus=0.0, dup=False):
     if dup:
         ids[..., 1] = ids[..., 0]
     return ids
+
+
+TOL = {torch.bfloat16: (2e-2, 5e-3), torch.float16: (2e-2, 5e-3), torch.float32: (1e-4, 1e-5)}
 
 
 def _close(name, got, want, mx=2e-2, mean=5e-3):
@@ -70,6 +75,15 @@ CASES = [
 ]
 
 
+CASES_VALU = [
+    # M, N, H, D, G, BS, T, causal, chunk, minus, dup
+    (256, 512, 2, 128, 64, 64, 4, False, 1, 0.0, False),
+    (300, 700, 3, 128, 15, 30, 8, True, 600, 0.1, False),
+    (200, 333, 2, 96, 100, 100, 3, True, 150, 0.0, True),
+    (90, 180, 1, 200, 30, 16, 6, True, 60, 0.2, False),
+]
+
+
 @pytest.mark.parametrize("case", CASES, ids=[f"case{i}" for i in range(len(CASES))])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_sel_bwd_matches_oracle(case, dtype):
@@ -90,6 +104,75 @@ def test_sel_bwd_matches_oracle(case, dtype):
         return
     for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
         _close(name, got, w)
+
+
+@pytest.mark.parametrize("case", CASES_VALU, ids=[f"valu{i}" for i in range(len(CASES_VALU))])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sel_bwd_valu_matches_oracle(case, dtype):
+    """fp32 everywhere, and bf16 at head dims the MFMA kernels do not take (96, 200)."""
+    M, N, H, D, G, BS, T, causal, chunk, minus, dup = case
+    if dtype == torch.bfloat16 and D in (64, 128):
+        pytest.skip("bf16 at D = 64 / 128 runs the MFMA kernels (test_sel_bwd_matches_oracle)")
+    gen = torch.Generator().manual_seed(hash(case) % 997)
+    q, k, v = (torch.randn((1, L, H, D), generator=gen).to(dtype) for L in (M, N, N))
+    ids = _ids(gen, 1, -(-M // G), H, T, -(-N // BS), minus, dup)
+    out, lse, do, dq, dk, dv, scale = _run(q, k, v, ids, G, BS, causal, chunk, dtype)
+    want = O.selection_attention_bwd(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                                     ids.numpy(), out.double().cpu().numpy(),
+                                     lse.double().cpu().numpy(), do.double().numpy(), G, scale,
+                                     O.dense_block_tokens(N, BS, chunk, causal), chunk_size=chunk,
+                                     causal=causal)
+    mx, mean = TOL[dtype]
+    for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
+        _close(name, got, w, mx, mean)
+
+
+def test_sel_bwd_strided_views():
+    """q / k / v / d_out as non-contiguous views: dim stride 2 (VALU kernels) and head-major
+    layouts with unit dim stride (MFMA kernels)."""
+    from omnimem_amd.selection import sel_fwd, sel_bwd
+    dtype = torch.bfloat16
+    M, N, H, D, G, BS, T = 128, 320, 2, 128, 64, 64, 3
+    gen = torch.Generator().manual_seed(21)
+    ids = _ids(gen, 1, M // G, H, T, N // BS)
+    for mode in ("dim_stride_2", "head_major"):
+        if mode == "dim_stride_2":
+            src = [torch.randn((1, L, H, 2 * D), generator=gen).to(dtype) for L in (M, N, N, M)]
+            host = [x[..., ::2] for x in src]
+            dev = [x.to(DEV)[..., ::2] for x in src]
+        else:
+            src = [torch.randn((1, H, L, D), generator=gen).to(dtype) for L in (M, N, N, M)]
+            host = [x.transpose(1, 2) for x in src]
+            dev = [x.to(DEV).transpose(1, 2) for x in src]
+        assert dev[0].stride(-1) == (2 if mode == "dim_stride_2" else 1)
+        q, k, v, do = host
+        qd, kd, vd, dod = dev
+        out, lse = sel_fwd(qd, kd, vd, ids.to(DEV), BS, 1, D ** -0.5, False, G)
+        dq, dk, dv = sel_bwd(qd, kd, vd, ids.to(DEV), out, lse, dod, BS, 1, D ** -0.5, False, G)
+        want = O.selection_attention_bwd(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                                         ids.numpy(), out.double().cpu().numpy(),
+                                         lse.double().cpu().numpy(), do.double().numpy(), G,
+                                         D ** -0.5, O.dense_block_tokens(N, BS, 1, False))
+        for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
+            _close(f"{name} ({mode})", got, w)
+
+
+def test_sel_bwd_config1_fp32_full_size():
+    """BASELINE config 1 (fp32, q [1,1560,12,128], k/v [1,4680,12,128] ~ N(0,1)/sqrt(128),
+    64-token blocks, groups of 64, top-16 from our top-k): every gradient of every head."""
+    from omnimem_amd.index_topk import parallel_nsa_topk, block_pool
+    gen = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn((1, L, 12, 128), generator=gen) / 128 ** 0.5 for L in (1560, 4680, 4680))
+    kd = k.to(DEV)
+    ids = parallel_nsa_topk(q.to(DEV), block_pool(kd, 64), 16, block_size=64, chunk_size=1560,
+                            causal=False, group_size=64).cpu()
+    out, lse, do, dq, dk, dv, scale = _run(q, k, v, ids, 64, 64, False, 1560, torch.float32)
+    want = O.selection_attention_bwd(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                                     ids.numpy(), out.double().cpu().numpy(),
+                                     lse.double().cpu().numpy(), do.double().numpy(), 64, scale,
+                                     O.dense_block_tokens(4680, 64, 1560, False))
+    for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
+        _close(name, got, w, *TOL[torch.float32])
 
 
 def test_sel_bwd_negative_scale_and_determinism():
@@ -175,7 +258,7 @@ def test_sel_bwd_config3_full_size():
 def test_sel_bwd_rejects_unsupported():
     from omnimem_amd.backend import NSABackendError
     from omnimem_amd.selection import sel_bwd
-    q = torch.zeros((1, 64, 1, 96), device=DEV, dtype=torch.bfloat16)
+    q = torch.zeros((1, 64, 1, 300), device=DEV, dtype=torch.bfloat16)
     ids = torch.zeros((1, 1, 1, 1), device=DEV, dtype=torch.int32)
     lse = torch.zeros((1, 1, 64), device=DEV)
     with pytest.raises(NSABackendError, match="head dim"):
