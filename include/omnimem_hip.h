@@ -186,8 +186,10 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
  * dq = dS K (q dtype), dk = dS^T Q and dv = P^T d_out over every (query, token) pair the forward
  * attends to (k dtype, fp32 accumulation, one rounding).  Every element of dq, dk and dv is
  * written (0 for tokens no query sees).  Duplicated ids in a row count twice, as in the
- * forward.  bf16 / f16, head dim 64 or 128, unit dim strides and 16-byte aligned rows; the
- * workspace (256-byte aligned) holds delta, the per-block CSR offsets and the bucket lists. */
+ * forward.  bf16 / f16 with head dim 64 or 128, unit dim strides and 16-byte aligned rows run on
+ * MFMA (16-bit P and dS operands); f32 and every other head dim <= 256 or stride run full fp32
+ * arithmetic.  The workspace (256-byte aligned) holds delta, -lse log2 e, the per-block CSR
+ * offsets and the bucket lists. */
 size_t omm_sel_bwd_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t N,
                                    int32_t block_size, int32_t group_size, int64_t T);
 int omm_sel_bwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
