@@ -578,6 +578,48 @@ class PagedKVCache:
         return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr,
                 "hbm_page_reads": hbm_reads, "host_page_reads": host_reads}
 
+    def flush_offload(self, layer_idx: Optional[int] = None) -> dict:
+        """MMCache-compatible name of ``flush`` (models/cache.py:1032).  Residency is planned for
+        all layers at once, so ``layer_idx`` is accepted and ignored."""
+        return self.flush()
+
+    def preallocate_offload_buffer(self, sample: torch.Tensor, max_entries_per_call: int,
+                                   segment_cids: int = 10):
+        """MMCache-compatible no-op (models/cache.py:970): the pinned host pool is sized when
+        the cache is built."""
+        return None
+
+    def lru_touch_per_head(self, layer_idx: int, name: str, head: int, cid: int):
+        """MMCache-compatible LRU touch (models/cache.py:673): stamps unit (head, cid) with a
+        new epoch, as the selection kernel does for every unit it reads."""
+        if name not in ("k_cache", "v_cache"):
+            raise BlockKVBackendError(f"unknown cache name {name!r}")
+        self.stamp[layer_idx][int(head), int(cid)] = self.next_epoch()
+
+    def get_chunk_metadata(self, layer_idx: int, name: str):
+        """MMCache-compatible chunk table (models/cache.py:340-347): (int64 [H, max_chunks] byte
+        address of each (head, chunk) unit or 0 when unwritten, int32 [H] chunks per head, the
+        strides dict of ``selection_attention_padded_ptr_fast``).  Host-resident units get their
+        device-mapped host address, which the pointer kernels read in place.  A unit is
+        ``pages_per_chunk * page_tokens`` rows of ``head_dim`` bf16; when ``page_tokens`` divides
+        ``chunk_len`` (the reference's 30-token blocks of 4680-token chunks) this is the
+        reference's per-head chunk layout.  The addresses are valid until the next ``flush``."""
+        if name not in ("k_cache", "v_cache"):
+            raise BlockKVBackendError(f"unknown cache name {name!r}")
+        if self.fp8:
+            raise BlockKVBackendError("pointer-table metadata is bf16-only (the reference's "
+                                      "pointer kernels read bf16 blocks)")
+        pool = self.pool_k if name == "k_cache" else self.pool_v
+        host = (self._host_k if name == "k_cache" else self._host_v).dev_ptr
+        s = self.unit_table[layer_idx].to(torch.int64)
+        ub = self.unit_bytes
+        ptrs = torch.where(s >= 0, pool.data_ptr() + s * ub,
+                           torch.where(s <= -2, host + (-2 - s) * ub, torch.zeros_like(s)))
+        n = torch.full((self.H,), self.n_chunks[layer_idx], dtype=torch.int32, device=self.device)
+        strides = {"batch_stride_bytes": ub, "token_stride_bytes": self.D * 2,
+                   "stride_bn": self.D, "stride_bd": 1, "chunk_len": self.chunk_len}
+        return ptrs, n, strides
+
     def lru_hit_rate_overall(self) -> float:
         """Fraction of touched units found in HBM (models/cache.py:713)."""
         tot = self.stats["hits"] + self.stats["misses"]

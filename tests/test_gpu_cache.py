@@ -256,6 +256,47 @@ def test_window_attention_reads_pages_in_place(dtype):
         assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-2
 
 
+def test_mmcache_adapters_and_chunk_metadata_feed_the_pointer_path():
+    """Reference call sites unchanged: get_chunk_metadata -> selection_attention_padded_ptr_fast
+    without a cache (the pointer kernels; reference geometry, 30-token blocks dividing the chunk)
+    agrees with the paged kernel and the float64 oracle, including after units move to the host
+    pool (mapped addresses); flush_offload / preallocate_offload_buffer / lru_touch_per_head
+    exist with the reference's signatures."""
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.padded_ptr import selection_attention_padded_ptr_fast
+    g = torch.Generator().manual_seed(17)
+    H, D, C, P, G, T, n = 2, 128, 120, 30, 15, 6, 4
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, window_chunks=0,
+                         hbm_slots=H * n, host_slots=H * n)
+    assert cache.preallocate_offload_buffer(torch.empty(1, C, D), 4) is None
+    ks = [_chunk(g, C, H, D, 0.3) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0) for _ in range(n)]
+    for cid in range(n):
+        cache.update_cache("k_cache", ks[cid].to(DEV), 0, cid * C)
+        cache.update_cache("v_cache", vs[cid].to(DEV), 0, cid * C)
+    cache.lru_touch_per_head(0, "k_cache", 1, 2)
+    M = 90
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(M // G * H)])
+    ids = ids.view(1, M // G, H, T).to(torch.int32)
+    want_o, want_l = O.selection_attention(q.float().numpy(), *_paged_oracle_inputs(ks, vs),
+                                           ids.numpy(), G, D ** -0.5, O.paged_block_tokens(C, P, n))
+    qd, idd = q.to(DEV), ids.to(DEV)
+    for step in ("hbm", "host"):
+        if step == "host":
+            cache.evict_all()
+        pk, nk, st = cache.get_chunk_metadata(0, "k_cache")
+        pv, _, _ = cache.get_chunk_metadata(0, "v_cache")
+        assert st["chunk_len"] == C and st["stride_bn"] == D
+        with torch.no_grad():
+            out, lse = selection_attention_padded_ptr_fast(qd, idd, P, G, C, pk, pv, nk, st,
+                                                           return_lse=True)
+            ref = cache.select(qd, idd, 0, G)
+        _check_attn(out, lse, want_o, want_l)
+        assert (out.float() - ref.float()).abs().max().item() <= 1e-2
+    cache.flush_offload()
+
+
 def test_lru_residency_matches_reference_model():
     """lru_max_size per (layer, head), no sink / window: after every flush the HBM-resident
     chunks are exactly the reference LRU's (models/cache.py:673-699, :1032-1142)."""
