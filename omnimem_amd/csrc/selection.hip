@@ -14,6 +14,8 @@
 //   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (dequantised while staging,
 //   x * page scale -> bf16) and for row strides the DMA kernel cannot address.
 // fp32 (and any shape the MFMA kernels do not cover) runs a VALU kernel in full fp32.
+#include <type_traits>
+
 #include "sel_common.h"
 
 namespace omm {
@@ -436,6 +438,8 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
 #pragma unroll
     for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m2[2] = {kNegInf, kNegInf};
+  // -max(m2, 0 if none finite) and the raise threshold (8, or -inf while m2 = -inf)
+  float nms[2] = {0.0f, 0.0f}, thr[2] = {kNegInf, kNegInf};
   float lsum[2] = {0.0f, 0.0f};  // fp32 row sums of the unrounded p (lane partials)
 
   WaveWalk<Acc, TK> wk;
@@ -466,8 +470,10 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
   // would also wait for the next tile's copy.
   __builtin_amdgcn_s_waitcnt(0);
 
-  // One key tile in LDS buffers BI (0 or 1; unrolling the two costs registers for no gain).
-  auto step = [&](int BI) -> bool {
+  // One key tile in LDS buffers BI (0 or 1), a compile-time constant so that every LDS address
+  // is a lane offset plus an immediate.
+  auto step = [&](auto BIc) -> bool {
+    constexpr int BI = decltype(BIc)::value;
     // this wave's copies of the tile are in LDS; after the barrier every wave's are, and every
     // wave is done reading buffers BI ^ 1 (the previous tile)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -484,7 +490,17 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
     const char* Kt = lds[BI];
     const char* Vt = lds[2 + BI];
 
-    // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks
+    // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks.  All K
+    // operand reads are issued before the first MFMA, and all V^T operand reads right after the
+    // last one, so that their LDS latency overlaps the MFMAs and the softmax instead of
+    // stalling each MFMA pair on its own read.
+    uint4 ka[NT][SD];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int s = 0; s < SD; ++s)
+        ka[t][s] = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 s4[2][NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -492,11 +508,20 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
       s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < SD; ++s) {
-        const uint4 a = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
-        s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
-        s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+        s4[0][t] = Mfma<QT>::run(ka[t][s], qb[0][s], s4[0][t]);
+        s4[1][t] = Mfma<QT>::run(ka[t][s], qb[1][s], s4[1][t]);
       }
     }
+    uint4 va[NU][ND];
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int i2 = 0; i2 < ND; ++i2) {
+        const uint2 lo = lds_read_tr16(Vt + voff[i2] + (32 * u) * ROWB);
+        const uint2 hi = lds_read_tr16(Vt + voff[i2] + (32 * u + 16) * ROWB);
+        va[u][i2] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+    __builtin_amdgcn_sched_barrier(0);
     if (n_cur < TK) {  // partial tile: keys past n_cur are not visible
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -512,8 +537,7 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
     bool raise = false;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
-      const float thr = m2[x] == kNegInf ? kNegInf : 8.0f;
+      const float msafe = -nms[x];
       float mx = kNegInf;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -523,7 +547,7 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
           s4[x][t][r] = e;
           mx = fmaxf(mx, e);
         }
-      raise = raise || (mx > thr);
+      raise = raise || (mx > thr[x]);
     }
     if (__ballot(raise) != 0ull) {
 #pragma unroll
@@ -543,6 +567,8 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
 #pragma unroll
         for (int i2 = 0; i2 < ND; ++i2) o[x][i2] *= alpha;
         m2[x] = mcand;
+        nms[x] = -msafe_new;
+        thr[x] = mcand == kNegInf ? kNegInf : 8.0f;
         const float shift = msafe - msafe_new;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -567,18 +593,15 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
       }
 #pragma unroll
       for (int i2 = 0; i2 < ND; ++i2) {
-        const uint2 lo = lds_read_tr16(Vt + voff[i2] + (32 * u) * ROWB);
-        const uint2 hi = lds_read_tr16(Vt + voff[i2] + (32 * u + 16) * ROWB);
-        const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        o[0][i2] = Mfma<QT>::run(va, pb[0], o[0][i2]);
-        o[1][i2] = Mfma<QT>::run(va, pb[1], o[1][i2]);
+        o[0][i2] = Mfma<QT>::run(va[u][i2], pb[0], o[0][i2]);
+        o[1][i2] = Mfma<QT>::run(va[u][i2], pb[1], o[1][i2]);
       }
     }
     n_cur = n_nx;
     return n_cur > 0;
   };
   if (n_cur > 0)
-    for (int it = 0; step(it & 1); ++it) {
+    while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
     }
 
   // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
