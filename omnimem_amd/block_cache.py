@@ -310,7 +310,7 @@ class PagedKVCache:
             out = torch.empty_like(q)
         if w == 0:
             return out.zero_()
-        G = 64
+        G = 128  # every group lists the same pages: 128-query groups share each K/V tile
         T = w * self.ppc
         key = (q.device, n - w, T)
         ids = self._win_ids.get(key)

@@ -395,28 +395,39 @@ __device__ __forceinline__ i32x4 buffer_desc(const void* base, int nbytes) {
   return r;
 }
 
-// This wave's 4 of the 8 copy instructions of one K or V tile: rows [0, nrows) of `base` (row
-// stride rsb bytes) into the 8 KiB LDS buffer dst; instruction j (= 4 w + jj) fills dst bytes
-// [1024 j, 1024 j + 1024) and off[jj] is this lane's source offset for it.  Issued as inline asm
-// (M0 = LDS destination): the compiler then does not treat it as an LDS store, so it does not
-// make the next LDS read wait for this copy; the kernel orders copies and reads itself
-// (s_waitcnt vmcnt(0) and a barrier before a buffer is read, a barrier before it is refilled).
-// M0 is set here and used by nothing else in the kernel.
+// This wave's NI of the 8 copy instructions of one K or V tile (NI = 8 / waves per workgroup):
+// rows [0, nrows) of `base` (row stride rsb bytes) into the 8 KiB LDS buffer dst; instruction
+// j (= NI w + jj) fills dst bytes [1024 j, 1024 j + 1024) and off[jj] is this lane's source
+// offset for it.  Issued as inline asm (M0 = LDS destination): the compiler then does not treat
+// it as an LDS store, so it does not make the next LDS read wait for this copy; the kernel
+// orders copies and reads itself (s_waitcnt vmcnt(0) and a barrier before a buffer is read, a
+// barrier before it is refilled).  M0 is set here and used by nothing else in the kernel.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+template <int NI>
 __device__ __forceinline__ void dma_part(const void* base, int rsb, int nrows, char* dst, int w,
-                                         const int (&off)[4]) {
+                                         const int (&off)[NI]) {
+  static_assert(NI == 2 || NI == 4, "2 or 4 copy instructions per wave");
   const i32x4 r = buffer_desc(base, nrows * rsb);
-  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-      static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + 4096u * w)));
-  asm volatile(
-      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %4, %5, 0 offen lds"
-      :
-      : "s"(m0), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(r)
-      : "memory", "m0", "scc");
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + 1024u * NI * w)));
+  if constexpr (NI == 4) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %4, %5, 0 offen lds"
+        :
+        : "s"(m0), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(r)
+        : "memory", "m0", "scc");
+  } else {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds"
+        :
+        : "s"(m0), "v"(off[0]), "v"(off[1]), "s"(r)
+        : "memory", "m0", "scc");
+  }
 }
 #pragma clang diagnostic pop
 

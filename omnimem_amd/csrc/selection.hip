@@ -354,25 +354,29 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 }
 
 // ---- DMA kernel (16-bit K / V) ----------------------------------------------------------------
-// One workgroup = up to 64 queries of one query group; 2 waves x 32 queries (2 MFMA row blocks
-// of 16 each, sharing every K and V^T operand read), 2 waves per SIMD so that one wave's softmax
-// VALU work overlaps another's MFMAs.  K and V tiles of TK keys (8 KiB each) go global -> LDS by
-// buffer_load ... lds with no register staging; rows past the block's visible tokens read as 0
-// through the buffer bound, so a partial tile holds finite values.  Two LDS buffers each for K
-// and V: the copy of tile i + 1 is issued right after the barrier that opens tile i (each wave
-// issues half of a tile's copy instructions and waits for its own before that barrier).
+// One workgroup = up to 64 queries of one query group (NW = 2 waves) or two 64-query subgroups
+// of one group (NW = 4); each wave owns 32 queries (2 MFMA row blocks of 16 each, sharing every
+// K and V^T operand read), 2 waves per SIMD.  K and V tiles of TK keys (8 KiB each) go
+// global -> LDS by buffer_load ... lds with no register staging; rows past the block's visible
+// tokens read as 0 through the buffer bound, so a partial tile holds finite values.  Two LDS
+// buffers each for K and V: the copy of tile i + 1 is issued right after the barrier that opens
+// tile i (each wave issues 8 / NW of a tile's copy instructions and waits for its own before
+// that barrier).
 //   LDS K rows:  16-byte chunk c of row r at slot c ^ (r % CPR), so the 16-row b128 operand reads
 //                of one chunk column hit 16 distinct slots;
 //   LDS V rows:  chunk c of row r at slot c ^ (2 (r % 8) % CPR); the V^T operand comes from
 //                ds_read_b64_tr_b16, which gives lane L of a 16-lane group element L of the 4
 //                rows its group addresses: 4 consecutive keys of one head dim.
 
-constexpr int kDmaThreads = 128;
-
-template <typename QT, typename Acc, int D>
-__global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
+// NW = 4 serves query groups of more than 64 queries: the 4 waves share every K / V tile, which
+// halves the copies per query.
+template <typename QT, typename Acc, int D, int NW>
+__global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
     int MG, int T, int chunk, float scale, int nsub) {
+  static_assert(NW == 2 || NW == 4, "2 or 4 waves");
+  constexpr int SPW = NW / 2;  // 64-query subgroups per workgroup
+  constexpr int NI = 8 / NW;   // copy instructions per wave per K or V tile
   using DG = DmaGeom<D>;
   constexpr int ROWB = DG::ROWB, CPR = DG::CPR, TK = DG::TK, RPI = DG::RPI;
   constexpr int NT = DG::NT, NU = DG::NU, SD = DG::SD, ND = DG::ND;
@@ -381,23 +385,26 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
   const int total = static_cast<int>(gridDim.x);
+  const int nsw = (nsub + SPW - 1) / SPW;  // workgroups per query group
   int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
-  const int sub = wi % nsub; wi /= nsub;
+  const int sw = wi % nsw; wi /= nsw;
   const int g = wi % MG; wi /= MG;
   const int h = wi % H;
   const int b = wi / H;
 
+  // this wave's 32 queries: subgroup sub, half ws (a subgroup past the group has none)
+  const int sub = sw * SPW + w / 2, ws = w & 1;
   const int m0 = g * G + sub * 64;
   const int m_end = min(min(g * G + G, M), m0 + 64);
   const int qc = (g * G) / chunk;
-  if (sub == 0) acc.touch(b, g, h, T);
+  if (sw == 0) acc.touch(b, g, h, T);
 
-  // Q^T operands of this wave's 2 query blocks: row m0 + 32 w + 16 x + l16, dims 32 s + 8 j4 ..
+  // Q^T operands of this wave's 2 query blocks: row m0 + 32 ws + 16 x + l16, dims 32 s + 8 j4 ..
   bool q_ok[2];
   uint4 qb[2][SD];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    const int mq = m0 + 32 * w + 16 * x + l16;
+    const int mq = m0 + 32 * ws + 16 * x + l16;
     q_ok[x] = mq < m_end;
 #pragma unroll
     for (int s = 0; s < SD; ++s)
@@ -445,15 +452,15 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
   WaveWalk<Acc, TK> wk;
   wk.start(acc, b, g, h, T, qc);
   int n_cur = 0;        // visible keys of the current tile (0: done)
-  int kdo[4], vdo[4];   // this lane's source offsets of this wave's copy instructions
+  int kdo[NI], vdo[NI];  // this lane's source offsets of this wave's copy instructions
   int rsk = 0, rsv = 0;
   if (wk.valid) {
     // row strides are the same for every block of a call
     rsk = static_cast<int>(wk.br.sk) * 2;
     rsv = static_cast<int>(wk.br.sv) * 2;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int row = (4 * w + jj) * RPI + lane / CPR, c = lane % CPR;
+    for (int jj = 0; jj < NI; ++jj) {
+      const int row = (NI * w + jj) * RPI + lane / CPR, c = lane % CPR;
       kdo[jj] = row * rsk + ((c ^ DG::swz_k(row)) << 4);
       vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
     }
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(kDmaThreads, 2) void sel_fwd_dma_kernel(
     ls += __shfl_xor(ls, 16, kWave);
     ls += __shfl_xor(ls, 32, kWave);
     if (q_ok[x]) {
-      const int mq = m0 + 32 * w + 16 * x + l16;
+      const int mq = m0 + 32 * ws + 16 * x + l16;
       const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
       QT* op = out.at(b, mq, h, 0);
 #pragma unroll
@@ -755,9 +762,16 @@ int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float*
 template <typename QT, typename Acc, int D>
 int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
                const Acc& acc, int chunk, float scale, hipStream_t s) {
-  sel_fwd_dma_kernel<QT, Acc, D><<<static_cast<unsigned>(gm.items), kDmaThreads, 0, s>>>(
-      make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T, chunk,
-      scale, gm.nsub);
+  if (gm.nsub >= 2) {  // two 64-query subgroups per workgroup
+    const int64_t grid = gm.items / gm.nsub * ((gm.nsub + 1) / 2);
+    sel_fwd_dma_kernel<QT, Acc, D, 4><<<static_cast<unsigned>(grid), 4 * kWave, 0, s>>>(
+        make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
+        chunk, scale, gm.nsub);
+  } else {
+    sel_fwd_dma_kernel<QT, Acc, D, 2><<<static_cast<unsigned>(gm.items), 2 * kWave, 0, s>>>(
+        make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
+        chunk, scale, gm.nsub);
+  }
   return check_launch("selection attention (dma)");
 }
 

@@ -204,7 +204,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     scale: Optional[float] = None, return_lse: bool = False,
                     out: Optional[torch.Tensor] = None):
     """Full (non-causal) softmax attention of q [B, M, H, D] over k, v [B, N, H, D], computed by
-    the selection kernel with every 64-token block listed for every 64-query group.
+    the selection kernel with every 64-token block listed for every 128-query group.
 
     This is the AR driver's compressed-history branch (o_cmp over the pooled keys,
     models/transformers/causal_wan_nsa_model.py:506) and window branch (o_swa,
@@ -217,7 +217,10 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if k.shape != (B, N, H, D) or v.shape != (B, N, H, D):
         raise NSABackendError(f"dense_attention: expected k, v {(B, N, H, D)}, got "
                               f"{tuple(k.shape)} / {tuple(v.shape)}")
-    G = BS = 64
+    # 128-query groups: the kernel then runs 4-wave workgroups that share each K/V tile between
+    # two 64-query halves (the same blocks are listed for every group, so the result does not
+    # depend on the grouping)
+    G, BS = 128, 64
     T = max(1, -(-N // BS))
     key = (q.device, T)
     ar = _ALL_BLOCKS.get(key)

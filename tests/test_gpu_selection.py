@@ -55,6 +55,10 @@ CASES = [
     (130, 256, 2, 64, 64, 32, 5, False, 1, 0.2, True),
     (90, 180, 1, 96, 30, 16, 6, True, 60, 0.0, False),
     (128, 64, 1, 128, 64, 64, 3, False, 1, 1.0, False),  # every id -1: O = 0, lse = -inf
+    # groups of more than 64 queries: 4-wave workgroups covering two 64-query subgroups (the
+    # second workgroup of a 192-query group has one empty subgroup)
+    (400, 512, 2, 128, 192, 64, 5, True, 256, 0.1, False),
+    (300, 384, 2, 64, 128, 64, 4, False, 1, 0.0, True),
 ]
 
 
