@@ -16,8 +16,8 @@
 //                        in registers), P = 2^(s c2 - lse log2 e), dS = P (dP - delta) scale,
 //                        then dQ^T += K^T dS^T with dS^T straight from the accumulator layout and
 //                        K^T from ds_read_b64_tr_b16.  Writes dQ and delta.
-//   sel_bwd_index_kernel one workgroup per (b, h): counts, scans and scatters every valid
-//                        (group, slot) pair into per-block buckets (CSR), in (group, slot) order,
+//   sel_bwd_index_kernel one workgroup per (b, h, 64 blocks): counts, scans and scatters every
+//                        valid (group, slot) pair into per-block buckets (CSR), in (group, slot) order,
 //                        so the dK / dV sums have a fixed order (the reference's buckets are in
 //                        atomic arrival order).
 //   sel_bwd_dkv_kernel   one workgroup per (b, h, block, 64-key tile), 2 waves x 32 keys.  K and V
@@ -252,9 +252,9 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 }
 
 // ---- block -> query-group index --------------------------------------------------------------
-constexpr int kIdxThreads = 256;
-constexpr int kIdxRange = 2048;  // buckets per pass over the pairs (LDS: 2048 x 36 bytes)
-constexpr int kIdxCache = 8192;  // pairs whose bucket is kept in LDS (32 KiB)
+constexpr int kIdxThreads = 512;
+constexpr int kIdxWaves = kIdxThreads / kWave;
+constexpr int kIdxBuckets = 64;  // buckets per workgroup
 
 // Bucket of (group g, slot t) of row (b, h), or -1 when the pair reaches no key.
 struct PairBucket {
@@ -262,110 +262,137 @@ struct PairBucket {
   int64_t is0, is1, is2, is3;
   int T, NS, bs, chunk, G;
   bool causal;
-  __device__ __forceinline__ int operator()(int b, int h, int p) const {
+  __device__ __forceinline__ int32_t id(int b, int h, int p) const {
     const int g = p / T, t = p - g * T;
-    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    return ids[b * is0 + g * is1 + h * is2 + t * is3];
+  }
+  __device__ __forceinline__ int operator()(int b, int h, int p) const { return bucket(id(b, h, p), p); }
+  __device__ __forceinline__ int bucket(int32_t bid, int p) const {
+    const int g = p / T;
     if (bid < 0 || bid >= NS) return -1;
-    if (causal && (static_cast<int64_t>(bid) * bs) / chunk > (static_cast<int64_t>(g) * G) / chunk)
+    // 32-bit unsigned: bid * bs < N + bs and g * G < M + G, with M, N < 2^31
+    if (causal && (static_cast<uint32_t>(bid) * static_cast<uint32_t>(bs)) / static_cast<uint32_t>(chunk) >
+                      (static_cast<uint32_t>(g) * static_cast<uint32_t>(G)) / static_cast<uint32_t>(chunk))
       return -1;
     return bid;
   }
 };
 
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // offsets: [B*H][NS+1]; groups: [B*H][MG*T] (bucket j of row r is groups[r][offsets[r][j] ..
-// offsets[r][j+1]), ascending (group, slot)).  Pairs are taken 256 at a time; a pair's place in
-// its bucket is the bucket cursor plus the number of earlier pairs of the batch in the same
-// bucket, read from a 256-bit per-bucket mask (one 64-bit word per wave) in LDS.
+// offsets[r][j+1]), ascending (group, slot)).  One workgroup per (row, 64 buckets lo .. lo+63):
+// wave w of 8 takes the w-th eighth of the row's pairs in order.  Pass 1 counts, per wave, the pairs
+// of each of the workgroup's buckets and those below lo; the scan then gives every bucket its
+// offset and every (wave, bucket) its first place.  Pass 2 walks each wave's pairs 64 at a time;
+// a pair's place is its (wave, bucket) cursor plus the number of lower lanes of the batch in the
+// same bucket, read from a 64-bit per-(wave, bucket) mask.  Waves touch only their own counters
+// and masks, so the passes need no workgroup barrier inside.
 __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
-    PairBucket pb, int H, int P, int32_t* __restrict__ offsets, int32_t* __restrict__ groups) {
-  __shared__ unsigned long long mask[kIdxRange][kIdxThreads / kWave];
-  __shared__ int cur[kIdxRange];
-  __shared__ int bkt[kIdxCache];  // buckets of pairs 0 .. kIdxCache-1 (the rest are recomputed)
-  __shared__ int wsum[kIdxThreads / kWave];
-  constexpr int NW = kIdxThreads / kWave, PER = kIdxRange / kIdxThreads;
-  const int row = static_cast<int>(blockIdx.x);
+    PairBucket pb, int H, int P, int nrange, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ groups) {
+  constexpr int NW = kIdxWaves, R = kIdxBuckets;
+  static_assert(R == kWave, "one bucket per lane in the scan");
+  __shared__ int cur[NW][R];                   // counts, then cursors
+  __shared__ unsigned long long msk[NW][R];
+  __shared__ int below[NW];
+  const int row = static_cast<int>(blockIdx.x) / nrange;
+  const int rg = static_cast<int>(blockIdx.x) - row * nrange;
   const int b = row / H, h = row - (row / H) * H;
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
-  const int NS = pb.NS;
+  const int NS = pb.NS, lo = rg * R, nb = min(R, NS - lo);
   int32_t* off = offsets + static_cast<int64_t>(row) * (NS + 1);
   int32_t* grp = groups + static_cast<int64_t>(row) * P;
-  auto bucket = [&](int p) { return p < kIdxCache ? bkt[p] : pb(b, h, p); };
+  const int per = (P + NW - 1) / NW;
+  const int p0 = min(P, w * per), p1 = min(P, p0 + per);
 
-  for (int p = tid; p < min(P, kIdxCache); p += kIdxThreads) bkt[p] = pb(b, h, p);
-  for (int i = tid; i < kIdxRange; i += kIdxThreads)
+  // a wave's pairs are read PL per lane at a time, all loads in flight together
+  constexpr int PL = 16;
+  auto load = [&](int c0, int (&kk)[PL]) {
+    int32_t raw[PL];
 #pragma unroll
-    for (int j = 0; j < NW; ++j) mask[i][j] = 0ull;
+    for (int j = 0; j < PL; ++j) raw[j] = pb.id(b, h, min(c0 + j * kWave + lane, p1 - 1));
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int p = c0 + j * kWave + lane;
+      kk[j] = p < p1 ? pb.bucket(raw[j], p) : -1;
+    }
+  };
 
-  int base = 0;
-  for (int lo = 0; lo < NS; lo += kIdxRange) {
-    const int nb = min(kIdxRange, NS - lo);
-    for (int i = tid; i < kIdxRange; i += kIdxThreads) cur[i] = 0;
-    __syncthreads();
-    for (int p = tid; p < P; p += kIdxThreads) {
-      const int k = bucket(p) - lo;
-      if (k >= 0 && k < nb) atomicAdd(&cur[k], 1);
-    }
-    __syncthreads();
-    // exclusive scan of the counts: PER consecutive buckets per thread
-    int v[PER], sum = 0;
+  cur[w][lane] = 0;
+  msk[w][lane] = 0ull;
+  wave_sync_lds();
+  int nbelow = 0;
+  for (int c0 = p0; c0 < p1; c0 += PL * kWave) {
+    int kk[PL];
+    load(c0, kk);
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      v[j] = cur[PER * tid + j];
-      sum += v[j];
+    for (int j = 0; j < PL; ++j) {
+      const int k = kk[j];
+      if (k >= 0 && k < lo) ++nbelow;
+      else if (k >= lo && k < lo + nb) atomicAdd(&cur[w][k - lo], 1);
     }
-    int incl = sum;
+  }
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) nbelow += __shfl_xor(nbelow, d, kWave);
+  if (lane == 0) below[w] = nbelow;
+  __syncthreads();
+
+  if (w == 0) {  // lane = bucket lo + lane
+    int c[NW], tot = 0, base = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      c[j] = cur[j][lane];
+      tot += c[j];
+      base += below[j];
+    }
+    int incl = tot;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
       const int y = __shfl_up(incl, d, kWave);
       if (lane >= d) incl += y;
     }
-    if (lane == kWave - 1) wsum[w] = incl;
-    __syncthreads();
-    int before = 0, tot = 0;
+    int run = base + incl - tot;
+    if (lane < nb) off[lo + lane] = run;
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
-      before += j < w ? wsum[j] : 0;
-      tot += wsum[j];
+      cur[j][lane] = run;
+      run += c[j];
     }
-    int run = base + before + incl - sum;
+    if (lo + R >= NS && lane == kWave - 1) off[NS] = base + incl;
+  }
+  __syncthreads();
+
+  for (int c0 = p0; c0 < p1; c0 += PL * kWave) {
+    int kk[PL];
+    load(c0, kk);
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = PER * tid + j;
-      if (i < nb) off[lo + i] = run;
-      cur[i] = run;
-      run += v[j];
-    }
-    base += tot;
-    __syncthreads();
-    for (int p0 = 0; p0 < P; p0 += kIdxThreads) {
-      const int p = p0 + tid;
-      const int k = p < P ? bucket(p) - lo : -1;
+    for (int j = 0; j < PL; ++j) {
+      if (c0 + j * kWave >= p1) break;  // wave-uniform
+      const int p = c0 + j * kWave + lane;
+      const int k = kk[j] >= 0 ? kk[j] - lo : -1;
       const bool in = k >= 0 && k < nb;
-      if (in) atomicOr(&mask[k][w], 1ull << lane);
-      __syncthreads();
-      bool lead = false;
-      int cnt = 0;
+      if (in) atomicOr(&msk[w][k], 1ull << lane);
+      wave_sync_lds();
+      unsigned long long m = 0ull;
+      int r = 0;
       if (in) {
-        int r = __builtin_popcountll(mask[k][w] & ((1ull << lane) - 1ull));
-#pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          const int c = __builtin_popcountll(mask[k][j]);
-          r += j < w ? c : 0;
-          cnt += c;
-        }
-        grp[cur[k] + r] = p / pb.T;
-        lead = r == 0;
+        m = msk[w][k];
+        r = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        grp[cur[w][k] + r] = p / pb.T;
       }
-      __syncthreads();
-      if (lead) {
-        cur[k] += cnt;
-#pragma unroll
-        for (int j = 0; j < NW; ++j) mask[k][j] = 0ull;
+      wave_sync_lds();
+      if (in && r == 0) {
+        cur[w][k] += __builtin_popcountll(m);
+        msk[w][k] = 0ull;
       }
-      __syncthreads();
+      wave_sync_lds();
     }
   }
-  if (tid == 0) off[NS] = base;
 }
 
 // ---- dK / dV ----------------------------------------------------------------------------------
@@ -882,8 +909,9 @@ int sel_bwd_launch(const BwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
 
   PairBucket pb{static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
                 ids.stride[2], ids.stride[3], T, NS, bs, ch, G, causal};
-  sel_bwd_index_kernel<<<static_cast<unsigned>(B * H), kIdxThreads, 0, s>>>(pb, H, MG * T, offsets,
-                                                                           groups);
+  const int nrange = std::max(1, (NS + kIdxBuckets - 1) / kIdxBuckets);  // NS = 0: offsets[0] = 0
+  sel_bwd_index_kernel<<<static_cast<unsigned>(B * H * nrange), kIdxThreads, 0, s>>>(
+      pb, H, MG * T, nrange, offsets, groups);
   rc = check_launch("selection backward (index)");
   if (rc) return rc;
 
