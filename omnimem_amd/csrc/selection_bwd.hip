@@ -399,7 +399,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
 // Workgroup = 4 waves over one 64-key tile: wave w owns keys 16 w .. 16 w + 15 (one MFMA column
 // block) for every query of every item.  Its K / V operands and fp32 dK / dV sums take ~100
 // registers, so two waves share each SIMD (the workgroup's 66 KiB of LDS allows two workgroups
-// per CU): one wave's exp / dS VALU work overlaps the other's MFMAs.  The item's lse arrives
+// per CU) and one wave's LDS and memory waits are covered by the other's work.  The item's lse arrives
 // already as -lse log2 e (written by the dQ kernel), and the softmax scale of dK is applied once
 // to the sums.
 constexpr int kKvThreads = 256;
