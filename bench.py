@@ -345,7 +345,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128>"),
+            "traffic": measured_traffic("sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128, 2>"),
             "kernel_ms": round(sel_ms, 4),
         },
         "topk": {
