@@ -98,6 +98,11 @@ def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
 PMC_FILE = os.path.join(ROOT, "profiles", "bench_config3_layer_pmc.json")
 
 
+# rocprofv3 names of the kernels whose traffic the line reports (config 3 forward, config 2 top-k)
+ROOFLINE_KERNEL = "sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128, 2>"
+TOPK_KERNEL = "topk_kernel<bf16_t, 1>"
+
+
 def measured_traffic(kernel_prefix: str):
     """HBM bytes per launch of a kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary of this benchmark (calibrated against a plain copy), or None."""
@@ -345,7 +350,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128, 2>"),
+            "traffic": measured_traffic(ROOFLINE_KERNEL),
             "kernel_ms": round(sel_ms, 4),
         },
         "topk": {
@@ -355,7 +360,7 @@ def main():
             "algorithmic_bytes": C2_BYTES,
             "GB/s": round(C2_BYTES / (topk_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(C2_BYTES / (topk_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic("topk_kernel<bf16_t, 1>"),
+            "traffic": measured_traffic(TOPK_KERNEL),
         },
         "sel_bwd": {
             "workload": "config 3 layer backward (dq, dk, dv; dQ, block index and dK/dV kernels)",
