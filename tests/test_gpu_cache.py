@@ -61,12 +61,13 @@ def test_build_ptr_table_matches_address_rule():
     np.testing.assert_array_equal(pv.cpu().numpy(), want_v)
 
 
-def test_padded_ptr_fast_reference_geometry():
+@pytest.mark.parametrize("G", [15, 150])  # 150: 4-wave workgroups (3 subgroups of a group)
+def test_padded_ptr_fast_reference_geometry(G):
     """The reference's AR shape (30-token blocks, groups of 15, 4680-token chunks) over
     per-head chunk tensors addressed by base pointers; a non-resident chunk (base 0) is skipped."""
     from omnimem_amd.padded_ptr import selection_attention_padded_ptr_fast
     g = torch.Generator().manual_seed(1)
-    H, D, C, BS, G, T, n_chunks = 2, 128, 4680, 30, 15, 8, 3
+    H, D, C, BS, T, n_chunks = 2, 128, 4680, 30, 8, 3
     chunks_k = [[(torch.randn((1, C, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
                  for _ in range(n_chunks)] for _ in range(H)]
     chunks_v = [[torch.randn((1, C, D), generator=g).to(torch.bfloat16).to(DEV)
@@ -178,12 +179,13 @@ def _paged_oracle_inputs(chunks_k, chunks_v, fp8_cache=None, layer=0):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
-def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype):
+@pytest.mark.parametrize("G", [64, 128])  # 128: 4-wave workgroups over two 64-query halves
+def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype, G):
     from omnimem_amd.block_cache import PagedKVCache
     from omnimem_amd.padded_ptr import selection_attention_paged
     torch.manual_seed(11)
     g = torch.Generator().manual_seed(11)
-    H, D, C, P, G, T, n = 3, 128, 4680, 64, 64, 16, 4
+    H, D, C, P, T, n = 3, 128, 4680, 64, 16, 4
     cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
                          hbm_slots=H * n, host_slots=H * n, window_chunks=0)
     fp8 = dtype == "fp8"
