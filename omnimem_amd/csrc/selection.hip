@@ -29,8 +29,6 @@ namespace {
 // 16 row groups) and the 8-byte PV-operand reads (16 consecutive rows) conflict free.
 constexpr int kVP = 72;
 
-__device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
-
 // 8 consecutive elements of a K/V row at byte address p as 8 MFMA-type elements: 16-bit storage
 // loads 16 bytes as is; fp8 pages load 8 bytes and dequantise (code * page scale, rounded).
 template <typename KVT> struct Row8;
