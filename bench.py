@@ -326,6 +326,7 @@ def main():
     bwd_tflops = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
     del d_out
 
+    traffic = measured_traffic(ROOFLINE_KERNEL)
     res = {
         "metric": METRIC,
         "value": round(flops / dt / 1e12, 3),
@@ -350,8 +351,11 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(sel_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(ROOFLINE_KERNEL),
+            "traffic": traffic,
             "kernel_ms": round(sel_ms, 4),
+            # the same launch seen from HBM: measured traffic over its time, against 8 TB/s
+            "traffic_frac_hbm": (round(traffic / (sel_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+                                 if traffic else None),
         },
         "topk": {
             "workload": "config 2: q [1,32768,12,128] bf16 pooled by 64, k_cmp [1,512,12,128], "
