@@ -3,7 +3,9 @@
 // Reference semantics: cuda_backend/csrc/topk.cu -- visibility rule (:36-97), ordering
 // (score desc, id asc; :3, :100-102), -1 padding and output contract (ops.h:11-12).
 //
-// gfx950 design: one workgroup = 16 query rows x one column span of one (b, h), 4 waves.
+// gfx950 design: one workgroup = 12 query rows x one column span of one (b, h), 4 waves.  Two
+// workgroups fit a CU, and 12 rows rather than 16 put config 2's 6144 rows on 516 workgroups,
+// about two per CU, instead of 384 (one CU in two holding two).
 //   1. rows: pooled query rows are staged in LDS as fp32.  In the fused mode the workgroup
 //      pools them itself from the full-resolution queries (16-byte loads, fp32 sum in ascending
 //      token order, one division, one rounding to the element type -- the omm_block_pool
@@ -23,7 +25,7 @@
 namespace omm {
 namespace {
 
-constexpr int kRG = 16;                 // query rows per workgroup
+constexpr int kRG = 12;                 // query rows per workgroup (3 per wave)
 constexpr int kThreads = 256;           // 4 waves
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsPerWave = kRG / kWaves;
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
     const T* kp = static_cast<const T*>(a.k);
 
     // ---- 1. query rows -> LDS (fp32) ----
-    {
+    if (tid / 16 < kRG) {  // 16 threads per row
       const int r = tid / 16, p = tid % 16, g = row0 + r;
       float* qrow = qs + r * DP;
       if (a.vec) {
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   }
   __syncthreads();
 
-  // ---- 3. selection: wave w owns rows w, w + 4, w + 8, w + 12 ----
+  // ---- 3. selection: wave w owns rows w, w + 4, w + 8 ----
   uint64_t* wsv = sv + wave * kSurvCap;
   for (int rr = 0; rr < kRowsPerWave; ++rr) {
     const int r = wave + kWaves * rr, g = row0 + r;
