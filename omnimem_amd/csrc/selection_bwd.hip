@@ -438,12 +438,16 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
 
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
-  const int total = static_cast<int>(gridDim.x);
-  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  // Work order: heads fastest, then blocks ascending, dispatched round-robin over the XCDs.  A
+  // key block's work is the number of query groups that selected it, and under a causal chunk
+  // mask the early blocks are visible to (and picked by) many more groups than the late ones, so
+  // this order launches the heavy items first and spreads them evenly over the XCDs.  Contiguous
+  // per-XCD ranges of (head, block) items left some XCDs a head and a half of early blocks.
+  int wi = static_cast<int>(blockIdx.x);
   const int kt = wi % nkt; wi /= nkt;
-  const int bid = wi % NS; wi /= NS;
-  const int h = wi % H;
-  const int b = wi / H;
+  const int h = wi % H; wi /= H;
+  const int bid = wi % NS;
+  const int b = wi / NS;
 
   const int t0 = bid * bs + 64 * kt;                         // first token of the tile
   const int nk = min(min(bs - 64 * kt, 64), N - t0);         // tokens of the tile
@@ -751,12 +755,16 @@ __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
   __shared__ float Ds[kVQ * DP];
   __shared__ float Ls[kVQ], Dl[kVQ];
   const int tid = threadIdx.x;
-  const int total = static_cast<int>(gridDim.x);
-  int wi = xcd_remap(static_cast<int>(blockIdx.x), total);
+  // Work order: heads fastest, then blocks ascending, dispatched round-robin over the XCDs.  A
+  // key block's work is the number of query groups that selected it, and under a causal chunk
+  // mask the early blocks are visible to (and picked by) many more groups than the late ones, so
+  // this order launches the heavy items first and spreads them evenly over the XCDs.  Contiguous
+  // per-XCD ranges of (head, block) items left some XCDs a head and a half of early blocks.
+  int wi = static_cast<int>(blockIdx.x);
   const int kt = wi % nkt; wi /= nkt;
-  const int bid = wi % NS; wi /= NS;
-  const int h = wi % H;
-  const int b = wi / H;
+  const int h = wi % H; wi /= H;
+  const int bid = wi % NS;
+  const int b = wi / NS;
   const int t0 = bid * bs + 64 * kt;
   const int nk = min(min(bs - 64 * kt, 64), N - t0);
   if (nk <= 0) return;
