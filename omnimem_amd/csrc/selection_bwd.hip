@@ -438,16 +438,29 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
 
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
-  // Work order: heads fastest, then blocks ascending, dispatched round-robin over the XCDs.  A
-  // key block's work is the number of query groups that selected it, and under a causal chunk
-  // mask the early blocks are visible to (and picked by) many more groups than the late ones, so
-  // this order launches the heavy items first and spreads them evenly over the XCDs.  Contiguous
-  // per-XCD ranges of (head, block) items left some XCDs a head and a half of early blocks.
-  int wi = static_cast<int>(blockIdx.x);
-  const int kt = wi % nkt; wi /= nkt;
-  const int h = wi % H; wi /= H;
-  const int bid = wi % NS;
-  const int b = wi / NS;
+  // Work order.  A key block's work is the number of query groups that selected it; under a
+  // causal chunk mask the early blocks are picked by many more groups than the late ones.  Units
+  // u = (b, h, key tile) are split into P classes of blocks (bid mod P), P the smallest with U P a
+  // multiple of 8, so that each XCD (workgroup id mod 8 under round-robin dispatch) gets U P / 8
+  // whole classes of equal expected work.  An XCD runs its classes one after another, each with
+  // its blocks ascending (heavy first), so the workgroups it holds at once share one head's
+  // Q/dO tiles in its L2.  Blocks past the last full round of P come last, units fastest.
+  const int id = static_cast<int>(blockIdx.x), U = static_cast<int>(gridDim.x) / NS;
+  const int P = 8 / ((U & 7) == 0 ? 8 : (U & 3) == 0 ? 4 : (U & 1) == 0 ? 2 : 1);
+  const int nb = NS / P, S = U * P / 8, treg = U * nb * P;
+  int u, bid;
+  if (id < treg) {
+    const int x = id & 7, kk = id >> 3, su = x * S + kk / nb, bi = kk - (kk / nb) * nb;
+    u = su / P;
+    bid = bi * P + (su - u * P);
+  } else {
+    const int r = id - treg;
+    u = r % U;
+    bid = nb * P + r / U;
+  }
+  const int kt = u % nkt; u /= nkt;
+  const int h = u % H;
+  const int b = u / H;
 
   const int t0 = bid * bs + 64 * kt;                         // first token of the tile
   const int nk = min(min(bs - 64 * kt, 64), N - t0);         // tokens of the tile
@@ -755,16 +768,29 @@ __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
   __shared__ float Ds[kVQ * DP];
   __shared__ float Ls[kVQ], Dl[kVQ];
   const int tid = threadIdx.x;
-  // Work order: heads fastest, then blocks ascending, dispatched round-robin over the XCDs.  A
-  // key block's work is the number of query groups that selected it, and under a causal chunk
-  // mask the early blocks are visible to (and picked by) many more groups than the late ones, so
-  // this order launches the heavy items first and spreads them evenly over the XCDs.  Contiguous
-  // per-XCD ranges of (head, block) items left some XCDs a head and a half of early blocks.
-  int wi = static_cast<int>(blockIdx.x);
-  const int kt = wi % nkt; wi /= nkt;
-  const int h = wi % H; wi /= H;
-  const int bid = wi % NS;
-  const int b = wi / NS;
+  // Work order.  A key block's work is the number of query groups that selected it; under a
+  // causal chunk mask the early blocks are picked by many more groups than the late ones.  Units
+  // u = (b, h, key tile) are split into P classes of blocks (bid mod P), P the smallest with U P a
+  // multiple of 8, so that each XCD (workgroup id mod 8 under round-robin dispatch) gets U P / 8
+  // whole classes of equal expected work.  An XCD runs its classes one after another, each with
+  // its blocks ascending (heavy first), so the workgroups it holds at once share one head's
+  // Q/dO tiles in its L2.  Blocks past the last full round of P come last, units fastest.
+  const int id = static_cast<int>(blockIdx.x), U = static_cast<int>(gridDim.x) / NS;
+  const int P = 8 / ((U & 7) == 0 ? 8 : (U & 3) == 0 ? 4 : (U & 1) == 0 ? 2 : 1);
+  const int nb = NS / P, S = U * P / 8, treg = U * nb * P;
+  int u, bid;
+  if (id < treg) {
+    const int x = id & 7, kk = id >> 3, su = x * S + kk / nb, bi = kk - (kk / nb) * nb;
+    u = su / P;
+    bid = bi * P + (su - u * P);
+  } else {
+    const int r = id - treg;
+    u = r % U;
+    bid = nb * P + r / U;
+  }
+  const int kt = u % nkt; u /= nkt;
+  const int h = u % H;
+  const int b = u / H;
   const int t0 = bid * bs + 64 * kt;
   const int nk = min(min(bs - 64 * kt, 64), N - t0);
   if (nk <= 0) return;
