@@ -4,8 +4,9 @@
 // (score desc, id asc; :3, :100-102), -1 padding and output contract (ops.h:11-12).
 //
 // gfx950 design: one workgroup = 12 query rows x one column span of one (b, h), 4 waves.  Two
-// workgroups fit a CU, and 12 rows rather than 16 put config 2's 6144 rows on 516 workgroups,
-// about two per CU, instead of 384 (one CU in two holding two).
+// workgroups fit a CU; 12 rows rather than 16 put the 6144 rows of a 32768-token, 12-head call
+// (64-token groups) on 516 workgroups, about two per CU, instead of 384 (one CU in two holding
+// two while the others held one).
 //   1. rows: pooled query rows are staged in LDS as fp32.  In the fused mode the workgroup
 //      pools them itself from the full-resolution queries (16-byte loads, fp32 sum in ascending
 //      token order, one division, one rounding to the element type -- the omm_block_pool
