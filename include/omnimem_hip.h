@@ -218,8 +218,9 @@ int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr
 
 /* ---- paged block KV cache (a7) ------------------------------------------------------- */
 /* Write chunk cid of every head from k_new / v_new (bf16 [1, chunk_tokens, H, D], unit dim
- * stride, 16-byte aligned rows; chunk_tokens <= chunk_len) into the units unit_table[h][cid]
- * (HBM slots; units whose entry is < 0 are skipped).  Page slots past chunk_tokens are zeroed.
+ * stride, 16-byte aligned rows; chunk_tokens == chunk_len: whole chunks only, so every page
+ * slot attention reads was written) into the units unit_table[h][cid] (HBM slots; units whose
+ * entry is < 0 are skipped).  The last page's slots past chunk_len are zeroed.
  * bf16 cache: bytes copied.  fp8 cache: per (page, head) scale = amax/448 (1 when amax == 0),
  * code = e4m3(clamp(x * (448/amax), +-448)), round to nearest even.  With k_cmp (bf16
  * [1, >= (cid+1)*pages_per_chunk, H, D]) row cid*pages_per_chunk + p receives the mean of page

@@ -87,7 +87,8 @@ class PagedKVCache:
                  chunk_len: int = 4680, page_tokens: int = 64, dtype=torch.bfloat16,
                  hbm_budget_bytes: Optional[int] = None, hbm_slots: Optional[int] = None,
                  host_slots: Optional[int] = None, lru_max_size: int = 0,
-                 window_chunks: int = 3, sink_chunks: int = 0, keep_window_kv: bool = True,
+                 window_chunks: Optional[int] = 3, sink_chunks: int = 0,
+                 keep_window_kv: bool = True,
                  device="cuda"):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -121,7 +122,10 @@ class PagedKVCache:
         self.n_host = int(host_slots)
         self.hbm_budget_bytes = self.n_slots * per_slot
         self.lru_max_size = int(lru_max_size)
-        self.window, self.sink = int(window_chunks), int(sink_chunks)
+        # window None: the sink + window view is every chunk, and no chunk is protected from
+        # eviction (the reference's rule without a window, models/cache.py:1060-1068)
+        self.window = None if window_chunks is None else int(window_chunks)
+        self.sink = int(sink_chunks)
 
         store = torch.uint8 if self.fp8 else torch.bfloat16
         shape = (self.n_slots, self.ppc, self.P, self.D)
@@ -148,13 +152,19 @@ class PagedKVCache:
         self.k_cmp = [torch.zeros((1, ncb, H, self.D), dtype=torch.bfloat16, device=self.device)
                       for _ in range(self.L)]
         self.v_cmp = [torch.zeros_like(self.k_cmp[0]) for _ in range(self.L)]
-        self.keep_window_kv = bool(keep_window_kv) and self.window > 0
+        self.keep_window_kv = bool(keep_window_kv) and bool(self.window)
         if self.keep_window_kv:
             wshape = (self.window, self.chunk_len, H, self.D)
             self.win_k = [torch.zeros(wshape, dtype=torch.bfloat16, device=self.device)
                           for _ in range(self.L)]
             self.win_v = [torch.zeros_like(self.win_k[0]) for _ in range(self.L)]
         self._win_ids: Dict[tuple, torch.Tensor] = {}
+        # update_cache('k_cmp_cache' / 'v_cmp_cache') hands in the caller's pooled rows; from
+        # then on the append kernel leaves the pooled rows to the caller.  The pooled history
+        # has its own window (None = all chunks, the reference pipeline's kv_cmp setting).
+        self._pooled_by_caller = False
+        self.cmp_window: Optional[int] = None
+        self.cmp_sink = 0
         self._table_h = np.full((self.L, H, MC), -1, dtype=np.int32)
         self._stage = torch.empty((H, MC), dtype=torch.int32).pin_memory()
         self.n_chunks = [0] * self.L
@@ -212,7 +222,7 @@ class PagedKVCache:
 
     # ---------------------------------------------------------------- append
     def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, cid: int):
-        """Write chunk ``cid`` (k, v: bf16 [1, S, H, D], S <= chunk_len) of one layer.
+        """Write chunk ``cid`` (k, v: bf16 [1, chunk_len, H, D]) of one layer.
 
         Rewriting a chunk (the reference's 4 denoise + 1 context forwards per AR chunk) reuses its
         units.  Also writes the pooled keys / values of its pages (``k_cmp`` / ``v_cmp``)."""
@@ -225,8 +235,11 @@ class PagedKVCache:
             raise BlockKVBackendError(f"k / v must be [1, S, {self.H}, {self.D}], got "
                                       f"{tuple(k.shape)} / {tuple(v.shape)}")
         S = k.shape[1]
-        if S > self.chunk_len:
-            raise BlockKVBackendError(f"{S} tokens exceed the chunk length {self.chunk_len}")
+        if S != self.chunk_len:
+            # attention reads every page of a written chunk with the token counts chunk_len
+            # fixes, so a shorter write would expose unwritten slots
+            raise BlockKVBackendError(f"{S} tokens for a chunk of {self.chunk_len} (whole chunks "
+                                      "only)")
         if k.stride(3) != 1 or k.stride(1) % 8 or k.stride(2) % 8 or k.data_ptr() % 16:
             k = k.contiguous()
         if v.stride(3) != 1 or v.stride(1) % 8 or v.stride(2) % 8 or v.data_ptr() % 16:
@@ -246,34 +259,137 @@ class PagedKVCache:
                 self._upload_table(layer)
         self.n_chunks[layer] = max(self.n_chunks[layer], cid + 1)
         kv = self.layer_view(layer)
+        pool_k = pool_v = None
+        if not self._pooled_by_caller:
+            pool_k, pool_v = _lib.view4(self.k_cmp[layer]), _lib.view4(self.v_cmp[layer])
         _lib.call("omm_paged_append", ctypes.byref(kv), _lib.view4(k), _lib.view4(v), int(cid),
-                  int(S), _lib.view4(self.k_cmp[layer]), _lib.view4(self.v_cmp[layer]),
-                  self.next_epoch(), _lib.stream_of(k), error=BlockKVBackendError)
+                  int(S), pool_k, pool_v, self.next_epoch(), _lib.stream_of(k),
+                  error=BlockKVBackendError)
         if self.keep_window_kv:
             w = cid % self.window
             self.win_k[layer][w, :S].copy_(k[0])
             self.win_v[layer][w, :S].copy_(v[0])
 
-    def update_cache(self, name: str, hidden_state: torch.Tensor, layer_idx: int, start_id: int):
-        """MMCache-compatible entry (models/cache.py:439): 'k_cache' stages the keys, 'v_cache'
-        commits the chunk; both return the window ([1, tokens, H, D]) like the reference's
-        chunk_per_head branch."""
-        cid = int(start_id) // self.chunk_len
+    @staticmethod
+    def _window_chunks(n_valid: int, window: Optional[int], sink: int):
+        """Chunk ids of the sink + window view of chunks 0..n_valid-1, ascending: all of them
+        without a window; else the first ``sink`` chunks and the last ``window`` (the window
+        never reaches into the sinks), as MMCache._resolve_window_range (models/cache.py:557-570)."""
+        if window is None:
+            return list(range(n_valid))
+        s = min(int(sink), n_valid)
+        start = max(s, n_valid - int(window))
+        return list(range(s)) + list(range(start, n_valid))
+
+    def _gather_chunk(self, layer: int, which: str, cid: int) -> torch.Tensor:
+        """Chunk ``cid`` of every head as bf16 [chunk_len, H, D], read from the pools (fp8 pages
+        dequantised with their scales; host-resident units copied over the host link)."""
+        slots = self._table_h[layer, :, cid]
+        if (slots == -1).any():
+            raise BlockKVBackendError(f"chunk {cid} of layer {layer} was never written")
+        pool = self.pool_k if which == "k" else self.pool_v
+        scales = self.scale_k if which == "k" else self.scale_v
+        rows = []
+        for h, s in enumerate(slots.tolist()):
+            if s >= 0:
+                unit = pool[s]
+                sc = scales[s] if self.fp8 else None
+            else:
+                hs, ub = -2 - s, self.unit_bytes
+                host = (self._host_k if which == "k" else self._host_v).cpu_view()
+                torch.cuda.current_stream(self.device).synchronize()  # pending moves land first
+                unit = host[hs * ub:(hs + 1) * ub].view(pool.dtype).view(pool.shape[1:]).to(
+                    self.device)
+                sc = None
+                if self.fp8:
+                    sb = self.scale_bytes
+                    hsc = (self._host_sk if which == "k" else self._host_sv).cpu_view()
+                    sc = hsc[hs * sb:(hs + 1) * sb].view(torch.float32).to(self.device)
+            if self.fp8:
+                unit = (unit.view(torch.float8_e4m3fn).float() * sc[:, None, None]).to(
+                    torch.bfloat16)
+            rows.append(unit.reshape(self.ppc * self.P, self.D)[:self.chunk_len])
+        return torch.stack(rows, dim=1)
+
+    def _window_tokens(self, layer: int, which: str, cid: int, current: torch.Tensor):
+        """Sink + window K or V up to chunk ``cid`` as [1, tokens, H, D], chunks ascending;
+        chunk ``cid`` itself is ``current`` (the caller's tensor)."""
+        parts = []
+        for c in self._window_chunks(cid + 1, self.window, self.sink):
+            if c == cid:
+                parts.append(current[0])
+            elif self.keep_window_kv and cid - c < self.window:  # keep_window_kv: window > 0
+                ring = self.win_k[layer] if which == "k" else self.win_v[layer]
+                parts.append(ring[c % self.window])
+            else:
+                parts.append(self._gather_chunk(layer, which, c))
+        return parts[0].unsqueeze(0) if len(parts) == 1 else torch.cat(parts, 0).unsqueeze(0)
+
+    def _write_pooled(self, name: str, hidden_state: torch.Tensor, layer_idx: int, start: int):
+        rows = self.k_cmp[layer_idx] if name == "k_cmp_cache" else self.v_cmp[layer_idx]
+        n = hidden_state.shape[1]
+        if hidden_state.dim() != 4 or hidden_state.shape[0] != 1 or n != self.ppc or \
+                tuple(hidden_state.shape[2:]) != (self.H, self.D):
+            raise BlockKVBackendError(
+                f"{name} takes one chunk's pooled rows [1, {self.ppc}, {self.H}, {self.D}], got "
+                f"{tuple(hidden_state.shape)}")
+        if start % self.ppc:
+            raise BlockKVBackendError(f"{name}: start_id {start} is not a chunk boundary")
+        cid = start // self.ppc
+        if not (0 <= cid < self.max_chunks):
+            raise BlockKVBackendError(f"chunk id {cid} outside [0, {self.max_chunks})")
+        self._pooled_by_caller = True
+        rows[:, start:start + n].copy_(hidden_state)
+        keep = self._window_chunks(cid + 1, self.cmp_window, self.cmp_sink)
+        if keep == list(range(keep[0], keep[-1] + 1)):  # one contiguous range: a view
+            return rows[:, keep[0] * self.ppc:(keep[-1] + 1) * self.ppc]
+        return torch.cat([rows[:, c * self.ppc:(c + 1) * self.ppc] for c in keep], 1)
+
+    def update_cache(self, name: str, hidden_state: torch.Tensor, layer_idx: int, start_id):
+        """The reference's ``MMCache.update_cache`` (models/cache.py:439-522) for the four cache
+        names of the NSA model's AR branch (causal_wan_nsa_model.py:479-504):
+
+        * ``'k_cmp_cache'`` / ``'v_cmp_cache'`` (``start_id`` in pooled rows): store one chunk's
+          pooled keys / values and return the pooled history ([1, rows, H, D]; all chunks unless
+          ``cmp_window`` is set), a view valid until the next write of this layer;
+        * ``'k_cache'`` (``start_id`` in tokens): take the chunk's keys and return the sink +
+          window keys ([1, tokens, H, D], chunks ascending, this chunk last);
+        * ``'v_cache'``: write the chunk (keys and values) into its pages and return the sink +
+          window values the same way.
+
+        Chunks are whole (``chunk_len`` tokens).  ``start_id`` may be a tensor (read once)."""
+        start = int(start_id.item()) if isinstance(start_id, torch.Tensor) else int(start_id)
+        if name in ("k_cmp_cache", "v_cmp_cache"):
+            return self._write_pooled(name, hidden_state, layer_idx, start)
+        if name not in ("k_cache", "v_cache"):
+            raise BlockKVBackendError(f"unknown cache name {name!r} (expected 'k_cache', "
+                                      "'v_cache', 'k_cmp_cache' or 'v_cmp_cache')")
+        if start % self.chunk_len:
+            raise BlockKVBackendError(f"{name}: start_id {start} is not a chunk boundary")
+        cid = start // self.chunk_len
         if name == "k_cache":
+            if not (0 <= cid < self.max_chunks):
+                raise BlockKVBackendError(f"chunk id {cid} outside [0, {self.max_chunks})")
             self._staged_k[layer_idx] = (hidden_state, cid)
             if self.keep_window_kv:
-                self.win_k[layer_idx][cid % self.window, :hidden_state.shape[1]].copy_(hidden_state[0])
-                return self.window_kv(layer_idx, upto=cid + 1)[0]
-            return hidden_state
-        if name == "v_cache":
-            if layer_idx not in self._staged_k or self._staged_k[layer_idx][1] != cid:
-                raise BlockKVBackendError("update_cache('v_cache') needs the matching 'k_cache' first")
-            k, _ = self._staged_k.pop(layer_idx)
-            self.append(layer_idx, k, hidden_state, cid)
-            if self.keep_window_kv:
-                return self.window_kv(layer_idx)[1]
-            return hidden_state
-        raise BlockKVBackendError(f"unknown cache name {name!r} (expected 'k_cache' or 'v_cache')")
+                self.win_k[layer_idx][cid % self.window].copy_(hidden_state[0])
+            return self._window_tokens(layer_idx, "k", cid, hidden_state)
+        if layer_idx not in self._staged_k or self._staged_k[layer_idx][1] != cid:
+            raise BlockKVBackendError("update_cache('v_cache') needs the matching 'k_cache' first")
+        k, _ = self._staged_k.pop(layer_idx)
+        self.append(layer_idx, k, hidden_state, cid)
+        return self._window_tokens(layer_idx, "v", cid, hidden_state)
+
+    @property
+    def _has_cpu_chunks(self) -> bool:
+        """Whether any unit lives in the host pool (the reference's flag, models/cache.py:66)."""
+        return bool((self._table_h <= -2).any())
+
+    @property
+    def block_seqlens(self) -> Dict[str, int]:
+        """Tokens (pooled rows for the cmp names) per chunk, as MMCache.block_seqlens."""
+        return {"k_cache": self.chunk_len, "v_cache": self.chunk_len,
+                "k_cmp_cache": self.ppc, "v_cmp_cache": self.ppc}
 
     def window_kv(self, layer: int, upto: Optional[int] = None):
         """K and V of the last ``window_chunks`` chunks as [1, tokens, H, D] (chunk order need not
@@ -289,33 +405,40 @@ class PagedKVCache:
     def window_attention(self, q: torch.Tensor, layer: int, softmax_scale: Optional[float] = None,
                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Sliding-window attention (the reference's SWA branch, causal_wan_nsa_model.py:508, whose
-        window K/V come from the cache, models/cache.py:576-588): softmax attention of q (bf16
-        [1, M, H, D]) over every token of the last ``window_chunks`` chunks written.
+        K/V are the sink + window chunks update_cache returns, models/cache.py:576-588): softmax
+        attention of q (bf16 [1, M, H, D]) over every token of the first ``sink_chunks`` and the
+        last ``window_chunks`` chunks written.
 
-        With ``keep_window_kv`` the dense ring is read (``window_kv``); otherwise the pages of the
-        window chunks are read in place by the paged selection kernel, every page listed for
-        every query group (the window is protected from eviction, and a host-resident page would
-        still be read).  The paged read neither stamps the LRU nor counts page reads."""
+        With ``keep_window_kv`` and no sinks the dense ring is read (``window_kv``); otherwise
+        the pages of those chunks are read in place by the paged selection kernel, every page
+        listed for every query group (sink and window units are protected from eviction, and a
+        host-resident page would still be read).  The paged read neither stamps the LRU nor
+        counts page reads.  An fp8 cache with sinks gathers the dequantised pages first."""
         from .selection import dense_attention
-        if self.keep_window_kv:
-            wk, wv = self.window_kv(layer)
+        n = self.n_chunks[layer]
+        chunks = self._window_chunks(n, self.window, self.sink)
+        if self.keep_window_kv and (self.sink == 0 or self.fp8):
+            if self.sink == 0:
+                wk, wv = self.window_kv(layer)
+            else:
+                wk = torch.cat([self._gather_chunk(layer, "k", c) for c in chunks], 0)[None]
+                wv = torch.cat([self._gather_chunk(layer, "v", c) for c in chunks], 0)[None]
             return dense_attention(q, wk, wv, scale=softmax_scale, out=out)
         _lib.require_cuda((q, "q"))
         if q.dtype != torch.bfloat16:
             raise BlockKVBackendError(f"window attention needs bf16 queries, got {q.dtype}")
         B, M, H, D = q.shape
-        n = self.n_chunks[layer]
-        w = min(n, self.window)
         if out is None:
             out = torch.empty_like(q)
-        if w == 0:
+        if not chunks:
             return out.zero_()
         G = 128  # every group lists the same pages: 128-query groups share each K/V tile
-        T = w * self.ppc
-        key = (q.device, n - w, T)
+        T = len(chunks) * self.ppc
+        key = (q.device, tuple(chunks))
         ids = self._win_ids.get(key)
         if ids is None:
-            ids = torch.arange((n - w) * self.ppc, n * self.ppc, dtype=torch.int32, device=q.device)
+            ids = torch.cat([torch.arange(c * self.ppc, (c + 1) * self.ppc, dtype=torch.int32)
+                             for c in chunks]).to(q.device)
             self._win_ids = {key: ids}
         ids4 = ids.view(1, 1, 1, T).expand(B, -(-M // G), H, T)
         kv = self.layer_view(layer)
@@ -361,6 +484,8 @@ class PagedKVCache:
         c = np.arange(self.max_chunks)
         for l in range(self.L):
             n = self.n_chunks[l]
+            if self.window is None:
+                continue
             prot = (c < min(self.sink, n)) | ((c >= max(0, n - self.window)) & (c < n))
             mask[l, :, :] = prot[None, :]
         return mask
@@ -661,3 +786,80 @@ class PagedKVCache:
     def close(self):
         for p in (self._host_k, self._host_v, self._host_sk, self._host_sv):
             p.free()
+
+
+class MMCache(PagedKVCache):
+    """``PagedKVCache`` behind the reference's ``MMCache`` constructor (models/cache.py:44-60),
+    so the pipeline's cache construction (pipelines/pipeline_wan_causal.py:235-316) runs as is.
+
+    Mapping of the reference's arguments:
+
+    * ``config["cache_type"]`` must name ``k_cache`` and ``v_cache`` (``k_cmp_cache`` /
+      ``v_cmp_cache`` are optional: the pooled history lives in every paged cache);
+    * ``seq_dim`` must be 1; ``available_shape["k_cache"]`` is ``(B, tokens, H, D)`` with B = 1
+      (the paged cache serves one sequence); ``max_chunks = ceil(tokens / chunk)``;
+    * ``block_seqlen_config["k_cache"]`` is the chunk length in tokens, and
+      ``block_seqlen_config["k_cmp_cache"]`` (if given) must equal the pages per chunk;
+    * ``kv_block_size`` is the page size (the selection block; 64 when the reference passes 0);
+    * ``window_config`` / ``sink_config`` give the window and sink chunks of ``k_cache`` and of
+      ``k_cmp_cache`` (None: no window, every chunk is returned);
+    * ``lru_max_size`` keeps the reference's per-(layer, head) chunk count; ``hbm_budget_bytes``
+      (keyword only) replaces it with a byte budget;
+    * ``dtype``, ``per_head_types``, ``chunk_per_head_types``, ``chunk_buffer_types`` are
+      accepted: storage is always per-head chunk pages, in bf16, or fp8 e4m3 with
+      ``cache_dtype="fp8"`` (keyword only).
+    """
+
+    def __init__(self, config, seq_dim, available_shape, device="cuda", dtype=torch.float32,
+                 block_seqlen_config=None, window_config=None, sink_config=None,
+                 num_layers=None, lru_max_size=10, per_head_types=None,
+                 chunk_per_head_types=None, chunk_buffer_types=None, num_heads=None,
+                 kv_block_size=0, *, hbm_budget_bytes: Optional[int] = None,
+                 cache_dtype=torch.bfloat16, keep_window_kv: bool = False):
+        types = set(config.get("cache_type", ()))
+        if not {"k_cache", "v_cache"} <= types:
+            raise BlockKVBackendError(f"MMCache over pages needs 'k_cache' and 'v_cache' in "
+                                      f"config['cache_type'], got {sorted(types)}")
+        if seq_dim != 1:
+            raise BlockKVBackendError(f"the paged cache stores [B, tokens, H, D]: seq_dim must be "
+                                      f"1, got {seq_dim}")
+        if num_layers is None:
+            raise BlockKVBackendError("num_layers is required")
+        blk = dict(block_seqlen_config or {})
+        if "k_cache" not in blk:
+            raise BlockKVBackendError("block_seqlen_config['k_cache'] (the chunk length) is "
+                                      "required: the paged cache is chunked")
+        shape = tuple(available_shape["k_cache"])
+        if len(shape) != 4 or shape[0] != 1:
+            raise BlockKVBackendError(f"available_shape['k_cache'] must be (1, tokens, H, D), got "
+                                      f"{shape}")
+        H = int(num_heads) if num_heads else int(shape[2])
+        if H != shape[2]:
+            raise BlockKVBackendError(f"num_heads {H} != available_shape heads {shape[2]}")
+        chunk = int(blk["k_cache"])
+        page = int(kv_block_size) if kv_block_size else 64
+        win = dict(window_config or {})
+        sink = dict(sink_config or {})
+        window = win.get("k_cache")
+        max_chunks = -(-int(shape[1]) // chunk)
+        super().__init__(int(num_layers), H, int(shape[3]), max_chunks=max_chunks,
+                         chunk_len=chunk, page_tokens=page, dtype=cache_dtype,
+                         hbm_budget_bytes=hbm_budget_bytes,
+                         lru_max_size=0 if hbm_budget_bytes is not None else int(lru_max_size),
+                         window_chunks=None if window is None else int(window),
+                         sink_chunks=int(sink.get("k_cache") or 0),
+                         keep_window_kv=keep_window_kv, device=device)
+        cmp_rows = blk.get("k_cmp_cache")
+        if cmp_rows is not None and int(cmp_rows) != self.ppc:
+            raise BlockKVBackendError(
+                f"block_seqlen_config['k_cmp_cache'] = {cmp_rows} pooled rows per chunk, but "
+                f"{chunk}-token chunks of {page}-token blocks have {self.ppc}")
+        cw = win.get("k_cmp_cache")
+        self.cmp_window = None if cw is None else int(cw)
+        self.cmp_sink = int(sink.get("k_cmp_cache") or 0)
+        self.config = config
+        self.seq_dim = seq_dim
+        self.dtype = dtype
+        self.num_heads = H
+        self.num_layers = int(num_layers)
+        self.kv_block_size = page

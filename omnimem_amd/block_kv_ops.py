@@ -124,77 +124,105 @@ def gather_publish_clear(desc: torch.Tensor, n_fetch: int, n_clear: int, block_t
 
 
 class DeviceBlockDedup:
-    """Fixed-capacity device dedup; unique_keys returns (keys int32 view, n_unique, overflow)."""
+    """Distinct selected (head, block) keys of a block-index tensor, found on the device.
+
+    The kernel (``omm_dedup_run``; contract of K3, cuda_backend/csrc/block_kv_ops.h:25-31)
+    marks every valid entry's key with this call's epoch in a persistent stamp array, counts the
+    marked keys per 1024-key tile, scans the counts and writes ``[n, key_0 < key_1 < ...]``.
+    Entry e of the flattened ``[..., H, T]`` indices is head ``(e // T) % H``; block
+    ``bid = cid * blocks_per_chunk + loc`` gives key ``(cid * H + h) * blocks_per_chunk + loc``,
+    the chunk-major order of a per-head chunk store.
+
+    All device state is one int32 allocation ``[stamps | tile counts | tile offsets | result]``;
+    the result lands in one pinned host buffer.  ``enqueue`` launches and starts that copy,
+    ``wait`` is the one host wait and returns ``(keys, n_unique, overflow)`` with ``keys`` a view
+    of at most ``cap`` ascending keys.  Because the landing buffer is reused, a second
+    ``enqueue`` before ``wait`` raises ``RuntimeError``.  Stamps start at 0 and epochs at 1; when
+    the epoch would leave int32 the stamps are cleared and counting restarts.
+    """
+
+    _TILE = _SCAN_BLOCK
 
     def __init__(self, heads: int, mb: int, blocks_per_group: int, cap: int, device, *,
                  blocks_per_chunk: int, backend: Optional[str] = None):
-        self.H, self.MB, self.T = int(heads), int(mb), int(blocks_per_group)
-        self.bpc = int(blocks_per_chunk)
-        if not (self.bpc > 0 and self.MB % self.bpc == 0):
-            raise BlockKVBackendError(
-                f"blocks_per_chunk {self.bpc} must divide MB {self.MB} for the key to be a bijection")
-        self.n_keys = self.H * self.MB
-        self.cap = int(cap)
         self.backend = resolve_block_kv_backend(backend)
-        self.stamp = torch.full((self.n_keys,), -1, dtype=torch.int32, device=device)
-        self.device = self.stamp.device
-        self.n_tiles = -(-self.n_keys // _SCAN_BLOCK)
+        self.H, self.MB, self.T = int(heads), int(mb), int(blocks_per_group)
+        self.bpc, self.cap = int(blocks_per_chunk), int(cap)
+        if min(self.H, self.MB, self.T) <= 0 or self.cap < 0:
+            raise BlockKVBackendError(
+                f"dedup geometry must be positive: heads={self.H}, mb={self.MB}, "
+                f"blocks_per_group={self.T}, cap={self.cap}")
+        if self.bpc <= 0 or self.MB % self.bpc:
+            raise BlockKVBackendError(
+                f"blocks_per_chunk={self.bpc} must be positive and divide mb={self.MB}: the key "
+                "(cid * heads + h) * blocks_per_chunk + loc is then a bijection")
+        self.n_keys = self.H * self.MB
+        self.n_tiles = -(-self.n_keys // self._TILE)
         if self.n_tiles > 2 ** 15:
-            raise BlockKVBackendError("too many keys for the single-workgroup scan")
-        self.counts = torch.zeros(self.n_tiles, dtype=torch.int32, device=self.device)
-        self.offsets = torch.zeros(self.n_tiles, dtype=torch.int32, device=self.device)
-        self.out = torch.zeros(1 + self.cap, dtype=torch.int32, device=self.device)
-        self.pinned = torch.empty(1 + self.cap, dtype=torch.int32, pin_memory=True)
-        self._pin_np = self.pinned.numpy()
-        self.event = torch.cuda.Event()
-        self.epoch = 0
-        self.launches = 0
-        self.d2h_bytes = 0
-        self._in_flight = False
+            raise BlockKVBackendError(f"{self.n_keys} keys exceed the single-workgroup scan")
+        nt = self.n_tiles
+        self._state = torch.zeros(self.n_keys + 2 * nt + 1 + self.cap, dtype=torch.int32,
+                                  device=device)
+        self.device = self._state.device
+        self._stamps = self._state[:self.n_keys]
+        self._tile_counts = self._state[self.n_keys:self.n_keys + nt]
+        self._tile_offsets = self._state[self.n_keys + nt:self.n_keys + 2 * nt]
+        self._result = self._state[self.n_keys + 2 * nt:]
+        self._landing = torch.empty(1 + self.cap, dtype=torch.int32, pin_memory=True)
+        self._landed = torch.cuda.Event()
+        self._epoch = 0
+        self._pending = False
+        self.calls = 0
 
     @property
     def d2h_bytes_per_call(self) -> int:
-        return self.pinned.numel() * 4
+        """Bytes one call copies to the host: the count plus ``cap`` key slots."""
+        return 4 * (1 + self.cap)
 
     def device_bytes(self) -> int:
-        return sum(t.numel() * t.element_size()
-                   for t in (self.stamp, self.counts, self.offsets, self.out))
+        return self._state.numel() * 4
+
+    def _next_epoch(self) -> int:
+        if self._epoch == 2 ** 31 - 1:
+            self._stamps.zero_()
+            self._epoch = 0
+        self._epoch += 1
+        return self._epoch
 
     def enqueue(self, block_indices: torch.Tensor) -> None:
-        if self._in_flight:
-            raise RuntimeError("DeviceBlockDedup.enqueue() called again before the previous "
-                               "enqueue's wait(); at most one call may be in flight")
-        if not (block_indices.dtype == torch.int32 and block_indices.is_cuda
-                and block_indices.is_contiguous()):
+        """Launch the dedup of ``block_indices`` (contiguous int32 [..., H, T] on this device)
+        and the copy of its result to the host, on the current stream.  No host wait."""
+        if self._pending:
+            raise RuntimeError("DeviceBlockDedup: wait() for the pending call before enqueueing "
+                               "another (the host landing buffer is shared)")
+        t = block_indices
+        if not (isinstance(t, torch.Tensor) and t.dtype == torch.int32 and t.is_cuda
+                and t.is_contiguous()):
             raise BlockKVBackendError("block_indices must be a contiguous int32 GPU tensor")
-        if block_indices.shape[-2] != self.H or block_indices.shape[-1] != self.T:
+        if t.dim() < 2 or tuple(t.shape[-2:]) != (self.H, self.T):
             raise BlockKVBackendError(
-                f"expected [..., H={self.H}, T={self.T}], got {tuple(block_indices.shape)}")
-        if block_indices.device != self.device:
-            raise BlockKVBackendError(
-                f"block_indices live on {block_indices.device}, the dedup buffers on {self.device}")
-        self._in_flight = True
-        self.epoch += 1
-        if self.epoch >= 2 ** 31 - 1:
-            self.stamp.fill_(-1)
-            self.epoch = 1
-        flat = block_indices.view(-1)
-        _lib.call("omm_dedup_run", flat.data_ptr(), flat.numel(), self.stamp.data_ptr(),
-                  self.counts.data_ptr(), self.offsets.data_ptr(), self.out.data_ptr(),
-                  self.epoch, self.MB, self.H, self.T, self.bpc, self.cap,
-                  _lib.stream_of(flat), error=BlockKVBackendError)
-        self.pinned.copy_(self.out, non_blocking=True)
-        self.event.record(torch.cuda.current_stream(self.device))
-        self.launches += 4
-        self.d2h_bytes += self.d2h_bytes_per_call
+                f"block_indices must end in [H={self.H}, T={self.T}], got {tuple(t.shape)}")
+        if t.device != self.device:
+            raise BlockKVBackendError(f"block_indices on {t.device}, dedup state on {self.device}")
+        epoch = self._next_epoch()
+        _lib.call("omm_dedup_run", t.data_ptr() if t.numel() else None, t.numel(),
+                  self._stamps.data_ptr(), self._tile_counts.data_ptr(),
+                  self._tile_offsets.data_ptr(), self._result.data_ptr(), epoch, self.MB, self.H,
+                  self.T, self.bpc, self.cap, _lib.stream_of(t), error=BlockKVBackendError)
+        self._landing.copy_(self._result, non_blocking=True)
+        self._landed.record(torch.cuda.current_stream(self.device))
+        self._pending = True
+        self.calls += 1
 
     def wait(self):
-        try:
-            self.event.synchronize()
-        finally:
-            self._in_flight = False
-        n = int(self._pin_np[0])
-        return self._pin_np[1:1 + min(n, self.cap)], n, n > self.cap
+        """Block until the pending call's result is on the host: (keys, n_unique, overflow)."""
+        if not self._pending:
+            raise RuntimeError("DeviceBlockDedup.wait() without a pending enqueue()")
+        self._pending = False
+        self._landed.synchronize()
+        view = self._landing.numpy()
+        n = int(view[0])
+        return view[1:1 + min(n, self.cap)], n, n > self.cap
 
     def unique_keys(self, block_indices: torch.Tensor):
         self.enqueue(block_indices)

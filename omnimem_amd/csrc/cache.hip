@@ -481,8 +481,12 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
               OMM_EINVAL, "omm_paged_append: inconsistent cache geometry");
   OMM_REQUIRE(cid >= 0 && cid < kv->max_chunks, OMM_EINVAL,
               "omm_paged_append: chunk id %d outside [0, %d)", cid, kv->max_chunks);
-  OMM_REQUIRE(chunk_tokens >= 0 && chunk_tokens <= kv->chunk_len, OMM_EINVAL,
-              "omm_paged_append: %d tokens for a chunk of %d", chunk_tokens, kv->chunk_len);
+  // Whole chunks only: attention reads every page of a written chunk with the token counts
+  // chunk_len fixes (the last page's tail past chunk_len is the only padding), so a shorter
+  // write would expose unwritten slots to the softmax.
+  OMM_REQUIRE(chunk_tokens == kv->chunk_len, OMM_EINVAL,
+              "omm_paged_append: %d tokens for a chunk of %d (whole chunks only)", chunk_tokens,
+              kv->chunk_len);
   for (const omm_view4* x : {k_new, v_new}) {
     OMM_REQUIRE(x->size[0] == 1 && x->size[1] == chunk_tokens && x->size[2] == H &&
                     x->size[3] == D,

@@ -17,7 +17,7 @@ from typing import Optional
 
 import torch
 
-from . import _lib
+from . import _lib, ops
 from .backend import NSABackendError, get_backend
 
 __all__ = [
@@ -33,7 +33,14 @@ __all__ = [
 def block_pool(x: torch.Tensor, group: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Mean of each run of ``group`` consecutive tokens of x [B, T, H, D] (ragged tail allowed).
 
-    The HIP replacement of ``x.view(B, T//g, g, H, D).mean(2)`` in x's dtype."""
+    The HIP replacement of ``x.view(B, T//g, g, H, D).mean(2)`` in x's dtype
+    (``torch.ops.omnimem_nsa.block_pool``; with ``out`` the result is written in place)."""
+    if out is None:
+        return ops.op("block_pool")(x, int(group))
+    return _block_pool_impl(x, group, out)
+
+
+def _block_pool_impl(x: torch.Tensor, group: int, out: Optional[torch.Tensor] = None):
     _lib.require_cuda((x, "x"))
     B, T, H, D = x.shape
     MG = -(-T // group) if T else 0
@@ -74,7 +81,24 @@ def topk(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, block_size: 
     """Op-level adapter, the counterpart of ``omnimem_nsa::topk`` (cuda_backend/ops.py:55-70).
 
     q: pooled rows [B, MG, H, D]; ``chunk_size`` counts rows as in the reference op, so the token
-    chunk of the query side is chunk_size * group_size."""
+    chunk of the query side is chunk_size * group_size.  With the reference's arguments only
+    (``group_size`` 1, ``blocks_per_chunk`` 0) the call goes through the registered
+    ``torch.ops.omnimem_nsa.topk``."""
+    if int(group_size) == 1 and int(blocks_per_chunk) == 0:
+        return ops.op("topk")(q, k, int(topk), float(scale), int(block_size), int(chunk_size),
+                              int(chunk_size_k), bool(causal), int(ex_win), int(ex_sink),
+                              bool(prog_excl), bool(tf_mask), int(q_chunk_offset),
+                              bool(allow_tf32))
+    return _topk_impl(q, k, topk, scale, block_size, chunk_size, chunk_size_k, causal, ex_win,
+                      ex_sink, prog_excl, tf_mask, q_chunk_offset, allow_tf32, group_size,
+                      blocks_per_chunk)
+
+
+def _topk_impl(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, block_size: int,
+               chunk_size: int, chunk_size_k: int, causal: bool, ex_win: int = 0,
+               ex_sink: int = 0, prog_excl: bool = False, tf_mask: bool = False,
+               q_chunk_offset: int = 0, allow_tf32: bool = True, group_size: int = 1,
+               blocks_per_chunk: int = 0) -> torch.Tensor:
     for name, v in (("block_size", block_size), ("chunk_size", chunk_size),
                     ("chunk_size_k", chunk_size_k), ("ex_win", ex_win), ("ex_sink", ex_sink),
                     ("q_chunk_offset", q_chunk_offset)):
@@ -176,12 +200,26 @@ def parallel_nsa_topk(
                     ("q_chunk_offset", q_chunk_offset)):
         _check_int(name, v)
     sc = scale if scale is not None else K ** -0.5
+    return ops.op("topk_fused")(q, k, int(block_counts), float(sc), int(block_size),
+                                int(chunk_size), bool(causal), int(exclude_window_chunks),
+                                int(exclude_sink_chunks), bool(progressive_exclude),
+                                bool(tf_mask), int(q_chunk_offset), G, int(blocks_per_chunk))
+
+
+def _topk_fused_impl(q: torch.Tensor, k: torch.Tensor, S: int, sc: float, block_size: int,
+                     chunk_size: int, causal: bool, ex_win: int, ex_sink: int, prog_excl: bool,
+                     tf_mask: bool, q_chunk_offset: int, G: int,
+                     blocks_per_chunk: int) -> torch.Tensor:
+    """``torch.ops.omnimem_nsa.topk_fused`` on the GPU: query pooling + scores + top-k in one
+    C-ABI call (``chunk_size`` in tokens on both sides)."""
+    _lib.require_cuda((q, "q"), (k, "k"))
+    B, T, H, K = q.shape
+    MG = -(-T // G)
+    NC = k.shape[1]
     q_half = (MG * G) // (2 * chunk_size) if tf_mask else 0
     k_half = (NC * block_size) // (2 * chunk_size) if tf_mask else 0
-    m = _mask(block_size, G, chunk_size, chunk_size, causal, exclude_window_chunks,
-              exclude_sink_chunks, progressive_exclude, tf_mask, q_chunk_offset, q_half, k_half,
-              blocks_per_chunk)
-    S = int(block_counts)
+    m = _mask(block_size, G, chunk_size, chunk_size, causal, ex_win, ex_sink, prog_excl, tf_mask,
+              q_chunk_offset, q_half, k_half, blocks_per_chunk)
     out = torch.empty((B, MG, H, S), dtype=torch.int32, device=q.device)
     dt = _lib.dtype_code(q)
     ws_n = _lib.lib().omm_topk_fused_workspace_bytes(B, T, H, K, NC, G, S, dt)

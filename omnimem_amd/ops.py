@@ -1,0 +1,159 @@
+"""torch.library registration of the selection-path operators, namespace ``omnimem_nsa``.
+
+The reference registers its CUDA kernels as ``torch.ops.omnimem_nsa.*`` (schemas:
+cuda_backend/csrc/bindings.cpp:7-36) and gives each a shape-only fake so ``torch.compile`` can
+trace through them (cuda_backend/ops.py:191-235).  The schemas below are the reference's, so a
+caller of ``torch.ops.omnimem_nsa.topk`` / ``sel_fwd`` / ``sel_bwd`` / ``build_ptr_table`` /
+``sel_fwd_ptr`` runs unchanged.  Two more ops are this build's: ``topk_fused`` (query-group
+pooling, scoring and selection in one call, what ``parallel_nsa_topk`` runs) and ``block_pool``
+(the K block compression), so that the facades trace as a chain of registered ops.
+
+The CUDA-key implementations are the C-ABI calls of ``index_topk``, ``selection`` and
+``padded_ptr`` (ctypes on the current stream, no host synchronisation); they raise
+``NSABackendError`` on a bad argument, as the reference's adapters do.  The fakes compute
+output shapes, dtypes and layouts only.  Importing this module registers everything once.
+"""
+from __future__ import annotations
+
+import torch
+
+NAMESPACE = "omnimem_nsa"
+
+SCHEMAS = {
+    "topk": "topk(Tensor q, Tensor k, int topk, float scale, int block_size, int chunk_size, "
+            "int chunk_size_k, bool causal, int ex_win, int ex_sink, bool prog_excl, "
+            "bool tf_mask, int q_chunk_offset, bool allow_tf32) -> Tensor",
+    "build_ptr_table": "build_ptr_table(Tensor block_indices, Tensor base_k, Tensor base_v, "
+                       "Tensor n_blocks_per_head, int batch_stride, int blocks_per_chunk, "
+                       "int in_chunk_block_bytes) -> (Tensor, Tensor)",
+    "sel_fwd": "sel_fwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, int block_size, "
+               "int chunk_size, float scale, bool causal, int group_size, bool allow_tf32) "
+               "-> (Tensor, Tensor)",
+    "sel_fwd_ptr": "sel_fwd_ptr(Tensor q, Tensor ptr_k, Tensor ptr_v, int block_size, "
+                   "int group_size, int stride_bn, int stride_bd, float scale, "
+                   "str input_precision, Tensor[] owners) -> (Tensor, Tensor)",
+    "sel_bwd": "sel_bwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, Tensor out, "
+               "Tensor lse, Tensor d_out, int block_size, int chunk_size, float scale, "
+               "bool causal, int group_size, bool allow_tf32) -> (Tensor, Tensor, Tensor)",
+    # this build's additions
+    "topk_fused": "topk_fused(Tensor q, Tensor k, int topk, float scale, int block_size, "
+                  "int chunk_size, bool causal, int ex_win, int ex_sink, bool prog_excl, "
+                  "bool tf_mask, int q_chunk_offset, int group_size, int blocks_per_chunk) "
+                  "-> Tensor",
+    "block_pool": "block_pool(Tensor x, int group) -> Tensor",
+}
+
+
+# ---- CUDA-key implementations (C-ABI calls) ------------------------------------------------
+def _topk_cuda(q, k, topk, scale, block_size, chunk_size, chunk_size_k, causal, ex_win, ex_sink,
+               prog_excl, tf_mask, q_chunk_offset, allow_tf32):
+    from .index_topk import _topk_impl
+    return _topk_impl(q, k, topk, scale, block_size, chunk_size, chunk_size_k, causal, ex_win,
+                      ex_sink, prog_excl, tf_mask, q_chunk_offset, allow_tf32)
+
+
+def _topk_fused_cuda(q, k, topk, scale, block_size, chunk_size, causal, ex_win, ex_sink,
+                     prog_excl, tf_mask, q_chunk_offset, group_size, blocks_per_chunk):
+    from .index_topk import _topk_fused_impl
+    return _topk_fused_impl(q, k, topk, scale, block_size, chunk_size, causal, ex_win, ex_sink,
+                            prog_excl, tf_mask, q_chunk_offset, group_size, blocks_per_chunk)
+
+
+def _block_pool_cuda(x, group):
+    from .index_topk import _block_pool_impl
+    return _block_pool_impl(x, group)
+
+
+def _sel_fwd_cuda(q, k, v, block_indices, block_size, chunk_size, scale, causal, group_size,
+                  allow_tf32):
+    from .selection import _sel_fwd_impl
+    return _sel_fwd_impl(q, k, v, block_indices, block_size, chunk_size, scale, causal,
+                         group_size)
+
+
+def _sel_bwd_cuda(q, k, v, block_indices, out, lse, d_out, block_size, chunk_size, scale, causal,
+                  group_size, allow_tf32):
+    from .selection import _sel_bwd_impl
+    return _sel_bwd_impl(q, k, v, block_indices, out, lse, d_out, block_size, chunk_size, scale,
+                         causal, group_size)
+
+
+def _build_ptr_table_cuda(block_indices, base_k, base_v, n_blocks_per_head, batch_stride,
+                          blocks_per_chunk, in_chunk_block_bytes):
+    from .padded_ptr import _build_ptr_table_impl
+    return _build_ptr_table_impl(block_indices, base_k, base_v, n_blocks_per_head, batch_stride,
+                                 blocks_per_chunk, in_chunk_block_bytes)
+
+
+def _sel_fwd_ptr_cuda(q, ptr_k, ptr_v, block_size, group_size, stride_bn, stride_bd, scale,
+                      input_precision, owners):
+    from .padded_ptr import _sel_fwd_ptr_impl
+    return _sel_fwd_ptr_impl(q, ptr_k, ptr_v, block_size, group_size, stride_bn, stride_bd,
+                             scale, input_precision, owners)
+
+
+# ---- fakes (shapes only) ------------------------------------------------------------------
+def _topk_fake(q, k, topk, scale, block_size, chunk_size, chunk_size_k, causal, ex_win, ex_sink,
+               prog_excl, tf_mask, q_chunk_offset, allow_tf32):
+    B, MG, H, _ = q.shape
+    return q.new_empty((B, MG, H, topk), dtype=torch.int32)
+
+
+def _topk_fused_fake(q, k, topk, scale, block_size, chunk_size, causal, ex_win, ex_sink,
+                     prog_excl, tf_mask, q_chunk_offset, group_size, blocks_per_chunk):
+    B, T, H, _ = q.shape
+    return q.new_empty((B, -(-T // group_size), H, topk), dtype=torch.int32)
+
+
+def _block_pool_fake(x, group):
+    B, T, H, D = x.shape
+    return x.new_empty((B, -(-T // group), H, D))
+
+
+def _sel_fwd_fake(q, k, v, block_indices, block_size, chunk_size, scale, causal, group_size,
+                  allow_tf32):
+    B, M, H, _ = q.shape
+    return torch.empty_like(q), q.new_empty((B, H, M), dtype=torch.float32)
+
+
+def _sel_bwd_fake(q, k, v, block_indices, out, lse, d_out, block_size, chunk_size, scale, causal,
+                  group_size, allow_tf32):
+    # dq, dk and dv are fresh contiguous buffers
+    return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
+
+
+def _build_ptr_table_fake(block_indices, base_k, base_v, n_blocks_per_head, batch_stride,
+                          blocks_per_chunk, in_chunk_block_bytes):
+    shape = block_indices.shape
+    return (block_indices.new_empty(shape, dtype=torch.int64),
+            block_indices.new_empty(shape, dtype=torch.int64))
+
+
+def _sel_fwd_ptr_fake(q, ptr_k, ptr_v, block_size, group_size, stride_bn, stride_bd, scale,
+                      input_precision, owners):
+    B, M, H, _ = q.shape
+    return torch.empty_like(q), q.new_empty((B, H, M), dtype=torch.float32)
+
+
+_IMPLS = {
+    "topk": (_topk_cuda, _topk_fake),
+    "topk_fused": (_topk_fused_cuda, _topk_fused_fake),
+    "block_pool": (_block_pool_cuda, _block_pool_fake),
+    "sel_fwd": (_sel_fwd_cuda, _sel_fwd_fake),
+    "sel_bwd": (_sel_bwd_cuda, _sel_bwd_fake),
+    "build_ptr_table": (_build_ptr_table_cuda, _build_ptr_table_fake),
+    "sel_fwd_ptr": (_sel_fwd_ptr_cuda, _sel_fwd_ptr_fake),
+}
+
+_LIBRARY = torch.library.Library(NAMESPACE, "DEF")
+for _name, _schema in SCHEMAS.items():
+    _LIBRARY.define(_schema)
+    _real, _fake = _IMPLS[_name]
+    _LIBRARY.impl(_name, _real, "CUDA")
+    torch.library.register_fake(f"{NAMESPACE}::{_name}", _fake, lib=_LIBRARY)
+del _name, _schema, _real, _fake
+
+
+def op(name: str):
+    """The registered ``torch.ops.omnimem_nsa.<name>`` overload packet."""
+    return getattr(getattr(torch.ops, NAMESPACE), name)

@@ -13,19 +13,29 @@ from typing import Any, Dict, Optional, Sequence, Tuple
 
 import torch
 
-from . import _lib
+from . import _lib, ops
 from .backend import NSABackendError, get_backend
 
 __all__ = ["build_ptr_table", "launch_ptr_fwd", "selection_attention_padded_ptr_fast",
            "selection_attention_block_store", "selection_attention_paged"]
 
 
+@torch.compiler.disable()
 def build_ptr_table(block_indices: torch.Tensor, block_base_ptrs_k: torch.Tensor,
                     block_base_ptrs_v: torch.Tensor, n_blocks_per_head: torch.Tensor,
                     batch_stride: int, blocks_per_chunk: int = 0, in_chunk_block_bytes: int = 0,
                     backend: Optional[str] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """int64 [B, MG, H, T] K and V byte addresses of every selected block (0 = skip)."""
+    """int64 [B, MG, H, T] K and V byte addresses of every selected block (0 = skip), via
+    ``torch.ops.omnimem_nsa.build_ptr_table``.  Raw addresses make this an eager boundary, as in
+    the reference (cuda_backend/ops.py:74)."""
     get_backend() if backend is None else None
+    return ops.op("build_ptr_table")(block_indices, block_base_ptrs_k, block_base_ptrs_v,
+                                     n_blocks_per_head, int(batch_stride), int(blocks_per_chunk),
+                                     int(in_chunk_block_bytes))
+
+
+def _build_ptr_table_impl(block_indices, block_base_ptrs_k, block_base_ptrs_v, n_blocks_per_head,
+                          batch_stride, blocks_per_chunk, in_chunk_block_bytes):
     _lib.require_cuda((block_indices, "block_indices"), (block_base_ptrs_k, "block_base_ptrs_k"),
                       (block_base_ptrs_v, "block_base_ptrs_v"),
                       (n_blocks_per_head, "n_blocks_per_head"))
@@ -58,11 +68,21 @@ def build_ptr_table(block_indices: torch.Tensor, block_base_ptrs_k: torch.Tensor
     return ptr_k, ptr_v
 
 
+@torch.compiler.disable()
 def launch_ptr_fwd(q: torch.Tensor, ptr_table_k: torch.Tensor, ptr_table_v: torch.Tensor,
                    block_size: int, group_size: int, stride_bn: int, stride_bd: int,
                    softmax_scale: float, return_lse: bool, input_precision: str = "tf32",
                    owners: Sequence[torch.Tensor] = (), backend: Optional[str] = None):
-    """Pointer forward: returns (out, lse or None).  bf16 storage only, as the reference."""
+    """Pointer forward via ``torch.ops.omnimem_nsa.sel_fwd_ptr``: returns (out, lse or None).
+    bf16 storage only, as the reference."""
+    out, lse = ops.op("sel_fwd_ptr")(q, ptr_table_k, ptr_table_v, int(block_size),
+                                     int(group_size), int(stride_bn), int(stride_bd),
+                                     float(softmax_scale), str(input_precision), list(owners))
+    return out, (lse if return_lse else None)
+
+
+def _sel_fwd_ptr_impl(q, ptr_table_k, ptr_table_v, block_size, group_size, stride_bn, stride_bd,
+                      softmax_scale, input_precision, owners):
     _lib.require_cuda((q, "q"), (ptr_table_k, "ptr_table_k"), (ptr_table_v, "ptr_table_v"))
     for o in owners:
         if isinstance(o, torch.Tensor) and o.dtype != torch.bfloat16:
@@ -78,12 +98,12 @@ def launch_ptr_fwd(q: torch.Tensor, ptr_table_k: torch.Tensor, ptr_table_v: torc
     if ptr_table_k.stride() != ptr_table_v.stride():
         raise NSABackendError("launch_ptr_fwd: pointer tables must share strides")
     out = torch.empty_like(q)
-    lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device) if return_lse else None
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device)
     strides = (_lib.ctypes.c_int64 * 4)(*ptr_table_k.stride())
     _lib.call("omm_sel_fwd_ptr", _lib.view4(q), ptr_table_k.data_ptr(), ptr_table_v.data_ptr(),
               strides, ptr_table_k.shape[-1], int(block_size), G, int(stride_bn),
               int(stride_bd), float(softmax_scale), _lib.view4(out),
-              lse.data_ptr() if lse is not None else None, _lib.stream_of(q))
+              lse.data_ptr() if lse.numel() else None, _lib.stream_of(q))
     return out, lse
 
 

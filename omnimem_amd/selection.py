@@ -15,7 +15,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import _lib
+from . import _lib, ops
 from .backend import NSABackendError, get_backend
 
 __all__ = ["selection_attention", "sel_fwd", "sel_bwd", "dense_attention"]
@@ -41,6 +41,9 @@ def _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size,
     if block_indices.shape[-1] == 0:
         raise ValueError("top_idx last dim T must be > 0")
     num_blocks = math.ceil(N / block_size)
+    if torch.compiler.is_compiling():
+        # a traced graph cannot branch on tensor values; the kernel skips out-of-range ids
+        return num_blocks
     # One host sync per call, as in the reference; the op-level sel_fwd() skips it.
     valid_mask = block_indices >= 0
     if valid_mask.any() and torch.any(block_indices[valid_mask] >= num_blocks):
@@ -76,7 +79,19 @@ def sel_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: to
             lse: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Op-level adapter (counterpart of ``omnimem_nsa::sel_fwd``): returns (out, lse [B,H,M] f32).
 
-    No host synchronisation; ids outside [0, ceil(N/block_size)) are skipped by the kernel."""
+    No host synchronisation; ids outside [0, ceil(N/block_size)) are skipped by the kernel.
+    Without ``out`` / ``lse`` the call goes through ``torch.ops.omnimem_nsa.sel_fwd``."""
+    if out is None and lse is None:
+        return ops.op("sel_fwd")(q, k, v, block_indices, int(block_size), int(chunk_size),
+                                 float(scale), bool(causal), int(group_size), bool(allow_tf32))
+    return _sel_fwd_impl(q, k, v, block_indices, block_size, chunk_size, scale, causal,
+                         group_size, out, lse)
+
+
+def _sel_fwd_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                  block_size: int, chunk_size: int, scale: float, causal: bool, group_size: int,
+                  out: Optional[torch.Tensor] = None,
+                  lse: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"))
     if not (q.dtype == k.dtype == v.dtype):
         raise NSABackendError(f"sel_fwd: q/k/v must share one dtype, got {q.dtype}/{k.dtype}/{v.dtype}")
@@ -101,7 +116,16 @@ def sel_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: to
     """Op-level adapter (counterpart of ``omnimem_nsa::sel_bwd``): returns (dq, dk, dv) in the
     q / k / v dtypes.  No host synchronisation.  ``allow_tf32`` is accepted for signature
     compatibility: 16-bit inputs use 16-bit MFMA operands with fp32 accumulation, fp32 inputs
-    full fp32 arithmetic."""
+    full fp32 arithmetic.  Runs as ``torch.ops.omnimem_nsa.sel_bwd``."""
+    return ops.op("sel_bwd")(q, k, v, block_indices, out, lse, d_out, int(block_size),
+                             int(chunk_size), float(scale), bool(causal), int(group_size),
+                             bool(allow_tf32))
+
+
+def _sel_bwd_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                  out: torch.Tensor, lse: torch.Tensor, d_out: torch.Tensor, block_size: int,
+                  chunk_size: int, scale: float, causal: bool,
+                  group_size: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"),
                       (out, "out"), (lse, "lse"), (d_out, "d_out"))
     if not (q.dtype == k.dtype == v.dtype == out.dtype == d_out.dtype):
@@ -183,7 +207,7 @@ def selection_attention(
         raise ValueError(f"Unknown bwd_method '{bwd_method}', expected 'auto', 'inverted' or 'mask'")
     get_backend()
     _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size, causal)
-    if _debug_checks_enabled():
+    if not torch.compiler.is_compiling() and _debug_checks_enabled():
         _debug_check_unique(block_indices)
     if block_indices.dtype != torch.int32:
         block_indices = block_indices.to(torch.int32)

@@ -112,10 +112,30 @@ def _pages(x: np.ndarray, C: int, P: int):
     return out.reshape(ppc, P, -1)
 
 
-@pytest.mark.parametrize("S", [4680, 4000])
-def test_paged_append_bf16_bitexact_and_pooled(S):
+def test_paged_append_rejects_partial_chunks():
+    """Whole chunks only: a shorter write would leave page slots that attention reads (every
+    page of a written chunk counts min(page_tokens, chunk_len - p*page_tokens) tokens)."""
+    from omnimem_amd.backend import BlockKVBackendError
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(4000)
+    H, D, C, P = 2, 128, 4680, 64
+    cache = PagedKVCache(1, H, D, max_chunks=2, chunk_len=C, page_tokens=P, hbm_slots=4,
+                         window_chunks=0)
+    k = _chunk(g, 4000, H, D).to(DEV)
+    with pytest.raises(BlockKVBackendError, match="whole chunks"):
+        cache.append(0, k, k, 0)
+    kv = cache.layer_view(0)
+    from omnimem_amd import _lib
+    import ctypes
+    with pytest.raises(BlockKVBackendError, match="whole chunks"):
+        _lib.call("omm_paged_append", ctypes.byref(kv), _lib.view4(k), _lib.view4(k), 0, 4000,
+                  None, None, 0, _lib.stream_of(k), error=BlockKVBackendError)
+
+
+def test_paged_append_bf16_bitexact_and_pooled():
     from omnimem_amd.block_cache import PagedKVCache
     from omnimem_amd.index_topk import block_pool
+    S = 4680
     g = torch.Generator().manual_seed(S)
     H, D, C, P = 3, 128, 4680, 64
     cache = PagedKVCache(1, H, D, max_chunks=4, chunk_len=C, page_tokens=P, hbm_slots=12,

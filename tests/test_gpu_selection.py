@@ -113,22 +113,41 @@ def test_sel_fwd_strided_views():
     _check(out, lse, want_o, want_l, torch.bfloat16)
 
 
-def test_config1_fp32_full_size():
+@pytest.mark.parametrize("causal", [True, False])
+def test_config1_fp32_full_size(causal):
     """fp32, q [1,1560,12,128], k/v [1,4680,12,128] ~ N(0,1)/sqrt(128),
-    64-token blocks, groups of 64, top-16 causal by 1560-token frames (indices from our top-k)."""
+    64-token blocks, groups of 64, top-16 over 1560-token frame chunks.
+
+    causal=True is the dense op's frame-chunk mask with the queries as frame 0
+    (selection_fwd.cu:218, common.cuh:327-332): every group sees frame-0 keys only, so 25 of the
+    74 blocks are candidates and block 24 (tokens 1536..1599) is cut at token 1560.
+    causal=False reads the queries as the last frame, so all three frames are candidates.
+    The top-k indices are checked bit for bit against the oracle on the same pooled inputs
+    before the attention is checked against the float64 oracle."""
     from omnimem_amd.index_topk import parallel_nsa_topk, block_pool
     from omnimem_amd.selection import selection_attention
     gen = torch.Generator().manual_seed(1)
     q, k, v = (torch.randn((1, L, 12, 128), generator=gen) / 128 ** 0.5 for L in (1560, 4680, 4680))
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
-    # queries are the last frame (offset 2 frames) so all three frames are candidates
     kc = block_pool(kd, 64)
-    ids = parallel_nsa_topk(qd, kc, 16, block_size=64, chunk_size=1560, causal=False,
+    np.testing.assert_array_equal(kc.cpu().numpy(), O.pool_mean(k.numpy(), 64, "f32"))
+    ids = parallel_nsa_topk(qd, kc, 16, block_size=64, chunk_size=1560, causal=causal,
                             group_size=64)
-    out, lse = selection_attention(qd, kd, vd, ids, 16, 64, chunk_size=1560, causal=False,
+    want_ids = O.topk(O.pool_mean(q.numpy(), 64, "f32"), O.pool_mean(k.numpy(), 64, "f32"), 16,
+                      128 ** -0.5, O.Mask(block_size=64, group_size=64, chunk_q=1560,
+                                          chunk_k=1560, causal=int(causal)))
+    got_ids = ids.cpu().numpy()
+    np.testing.assert_array_equal(got_ids, want_ids)
+    if causal:
+        assert got_ids.max() <= 24 and (got_ids >= 0).all()  # frame 0 only, 25 candidates
+    else:
+        assert got_ids.max() > 24  # later frames are selected
+    out, lse = selection_attention(qd, kd, vd, ids, 16, 64, chunk_size=1560, causal=causal,
                                    return_lse=True, group_size=64)
-    want_o, want_l = O.selection_attention(q.numpy(), k.numpy(), v.numpy(), ids.cpu().numpy(), 64,
-                                           128 ** -0.5, O.dense_block_tokens(4680, 64, 1560, False))
+    want_o, want_l = O.selection_attention(q.numpy(), k.numpy(), v.numpy(), got_ids, 64,
+                                           128 ** -0.5,
+                                           O.dense_block_tokens(4680, 64, 1560, causal),
+                                           chunk_size=1560, causal=causal)
     _check(out, lse, want_o, want_l, torch.float32)
 
 

@@ -1,0 +1,110 @@
+"""The selection-path operators are registered with torch.library (namespace ``omnimem_nsa``) and
+the reference-signature facades trace under torch.compile with no graph break (CPU only: fake
+CUDA tensors, shape-only kernels).
+
+Reference: the schemas of cuda_backend/csrc/bindings.cpp:7-36 and the fake kernels of
+cuda_backend/ops.py:191-235.
+"""
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+from omnimem_amd import ops
+
+# The reference's schemas (cuda_backend/csrc/bindings.cpp:8-31), as written there.
+REFERENCE_SCHEMAS = {
+    "topk": "topk(Tensor q, Tensor k, int topk, float scale, int block_size, int chunk_size, "
+            "int chunk_size_k, bool causal, int ex_win, int ex_sink, bool prog_excl, "
+            "bool tf_mask, int q_chunk_offset, bool allow_tf32) -> Tensor",
+    "build_ptr_table": "build_ptr_table(Tensor block_indices, Tensor base_k, Tensor base_v, "
+                       "Tensor n_blocks_per_head, int batch_stride, int blocks_per_chunk, "
+                       "int in_chunk_block_bytes) -> (Tensor, Tensor)",
+    "sel_fwd": "sel_fwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, int block_size, "
+               "int chunk_size, float scale, bool causal, int group_size, bool allow_tf32) "
+               "-> (Tensor, Tensor)",
+    "sel_fwd_ptr": "sel_fwd_ptr(Tensor q, Tensor ptr_k, Tensor ptr_v, int block_size, "
+                   "int group_size, int stride_bn, int stride_bd, float scale, "
+                   "str input_precision, Tensor[] owners) -> (Tensor, Tensor)",
+    "sel_bwd": "sel_bwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, Tensor out, "
+               "Tensor lse, Tensor d_out, int block_size, int chunk_size, float scale, "
+               "bool causal, int group_size, bool allow_tf32) -> (Tensor, Tensor, Tensor)",
+}
+
+
+def _norm(schema: str) -> str:
+    return " ".join(schema.replace("omnimem_nsa::", "").split())
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_SCHEMAS))
+def test_reference_schemas_registered(name):
+    got = str(ops.op(name).default._schema)
+    assert _norm(got) == _norm(REFERENCE_SCHEMAS[name])
+
+
+def _fake_inputs(fm, M=1024, N=1024, H=4, D=128, dtype=torch.bfloat16, grad=False):
+    with fm:
+        q, k, v = (torch.empty((1, L, H, D), dtype=dtype, device="cuda") for L in (M, N, N))
+    if grad:
+        for t in (q, k, v):
+            t.requires_grad_(True)
+    return q, k, v
+
+
+def _layer(q, k, v):
+    from omnimem_amd.index_topk import block_pool, parallel_nsa_topk
+    from omnimem_amd.selection import selection_attention
+    kc = block_pool(k, 64)
+    ids = parallel_nsa_topk(q, kc, 4, block_size=64, chunk_size=256, causal=True, group_size=64)
+    return selection_attention(q, k, v, ids, 4, 64, chunk_size=256, causal=True, group_size=64)
+
+
+def test_facades_trace_without_graph_break():
+    """block_pool -> parallel_nsa_topk -> selection_attention compiles as one graph."""
+    torch._dynamo.reset()
+    fm = FakeTensorMode()
+    q, k, v = _fake_inputs(fm)
+    compiled = torch.compile(_layer, backend="eager", fullgraph=True)
+    with fm:
+        out = compiled(q, k, v)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.device.type == "cuda"
+
+
+def test_facades_trace_with_gradients():
+    """With inputs that require grad, the autograd Function wrapping sel_fwd / sel_bwd traces in
+    the same single graph and its output is differentiable.  (Running the backward needs a real
+    device context for the autograd engine; sel_bwd's fake is checked directly below.)"""
+    torch._dynamo.reset()
+    fm = FakeTensorMode()
+    q, k, v = _fake_inputs(fm, M=512, N=512, H=2, grad=True)
+
+    def step(q, k, v):
+        return _layer(q, k, v).float().sum()
+
+    compiled = torch.compile(step, backend="eager", fullgraph=True)
+    with fm:
+        loss = compiled(q, k, v)
+    assert loss.requires_grad and loss.grad_fn is not None
+
+
+def test_fake_shapes_of_every_op():
+    fm = FakeTensorMode()
+    with fm:
+        q = torch.empty((2, 300, 3, 64), dtype=torch.bfloat16, device="cuda")
+        kc = torch.empty((2, 40, 3, 64), dtype=torch.bfloat16, device="cuda")
+        ids = ops.op("topk_fused")(q, kc, 8, 0.125, 16, 120, True, 0, 0, False, False, 0, 64, 0)
+        assert ids.shape == (2, 5, 3, 8) and ids.dtype == torch.int32
+        pooled = ops.op("block_pool")(q, 64)
+        assert pooled.shape == (2, 5, 3, 64) and pooled.dtype == torch.bfloat16
+        rows = ops.op("topk")(pooled, kc, 8, 0.125, 16, 2, 120, True, 0, 0, False, False, 0, True)
+        assert rows.shape == (2, 5, 3, 8)
+        out, lse = ops.op("sel_fwd")(q, q, q, ids, 64, 120, 0.125, True, 64, True)
+        assert out.shape == q.shape and lse.shape == (2, 3, 300) and lse.dtype == torch.float32
+        dq, dk, dv = ops.op("sel_bwd")(q, q, q, ids, out, lse, out, 64, 120, 0.125, True, 64, True)
+        assert dq.shape == dk.shape == dv.shape == q.shape and dq.is_contiguous()
+        base = torch.empty((3, 4), dtype=torch.int64, device="cuda")
+        nb = torch.empty((3,), dtype=torch.int32, device="cuda")
+        pk, pv = ops.op("build_ptr_table")(ids, base, base, nb, 0, 0, 0)
+        assert pk.shape == ids.shape and pk.dtype == torch.int64 and pv.dtype == torch.int64
+        o2, l2 = ops.op("sel_fwd_ptr")(q[:, :256], pk[:, :4], pv[:, :4], 64, 64, 64, 1, 0.125,
+                                       "tf32", [])
+        assert o2.shape == (2, 256, 3, 64) and l2.shape == (2, 3, 256)
