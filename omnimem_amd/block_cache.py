@@ -116,12 +116,17 @@ class PagedKVCache:
             raise BlockKVBackendError(
                 f"HBM pool of {self.n_slots} units cannot hold one chunk of every layer and head "
                 f"({self.L * self.H} units)")
+        self.lru_max_size = int(lru_max_size)
         if host_slots is None:
-            # every unit the HBM pool cannot hold, plus the chunk reserved at a flush
-            host_slots = min(total_units, total_units - self.n_slots + self.L * self.H)
+            if self.lru_max_size > 0:
+                # the per-head count, not the pool, bounds residency: any unit may be evicted
+                # (the reference preallocates a pinned slot per chunk, models/cache.py:970-1016)
+                host_slots = total_units
+            else:
+                # every unit the HBM pool cannot hold, plus the chunk reserved at a flush
+                host_slots = min(total_units, total_units - self.n_slots + self.L * self.H)
         self.n_host = int(host_slots)
         self.hbm_budget_bytes = self.n_slots * per_slot
-        self.lru_max_size = int(lru_max_size)
         # window None: the sink + window view is every chunk, and no chunk is protected from
         # eviction (the reference's rule without a window, models/cache.py:1060-1068)
         self.window = None if window_chunks is None else int(window_chunks)
@@ -323,6 +328,8 @@ class PagedKVCache:
                 parts.append(ring[c % self.window])
             else:
                 parts.append(self._gather_chunk(layer, which, c))
+        if not parts:  # a zero-chunk window: an empty view
+            return current.new_empty((1, 0) + tuple(current.shape[2:]))
         return parts[0].unsqueeze(0) if len(parts) == 1 else torch.cat(parts, 0).unsqueeze(0)
 
     def _write_pooled(self, name: str, hidden_state: torch.Tensor, layer_idx: int, start: int):
