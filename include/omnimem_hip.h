@@ -161,6 +161,17 @@ size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D
 int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t group_size,
                    int32_t topk, float scale, const omm_topk_mask* mask, int32_t* out,
                    void* workspace, size_t workspace_bytes, void* stream);
+/* No counterpart in the reference: omm_topk_fused for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments
+ * and result as omm_topk_fused without the workspace: the workspace is a fixed array of
+ * omm_topk_fused_noalloc_max_bytes() bytes in the library's device memory, one per GPU, held
+ * until the process ends.  A call whose omm_topk_fused_workspace_bytes exceeds that size fails
+ * with OMM_EWORKSPACE.  Calls that overlap on one GPU (two streams, or two threads) race on the
+ * array; serialise them.  Nothing in the array needs to start at zero. */
+size_t omm_topk_fused_noalloc_max_bytes(void);
+int omm_topk_fused_noalloc(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                           int32_t group_size, int32_t topk, float scale,
+                           const omm_topk_mask* mask, int32_t* out, void* stream);
 /* scores: fp32 contiguous [B, MG, H, NC], already scaled; same selection and output as above. */
 int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H, int64_t NC,
                          int32_t topk, const omm_topk_mask* mask, int32_t* out, void* workspace,

@@ -23,6 +23,8 @@
 //   keys and a merge kernel selects again over the per-span winners.
 #include "omm_common.h"
 
+#include <mutex>
+
 namespace omm {
 namespace {
 
@@ -932,4 +934,76 @@ extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, 
   TopkArgs a = base_args(MG, H, NC, 128, topk, 0.0f, *mask, out, workspace);
   a.scores = scores;
   return launch_core<float, kModeScores>(a, B, MG, H, p, 128, s);
+}
+
+// ---- allocation-free variant of omm_topk_fused ----------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture, serving loops
+// that forbid hipMalloc): the workspace is a fixed array in the code object's device memory,
+// one copy per GPU, held until the process ends.
+namespace omm {
+namespace {
+
+constexpr size_t kTopkScratchBytes = size_t(8) << 20;
+
+// In host code this name stands for the symbol, not a device address: host code reaches the
+// array only through the per-device address hipGetSymbolAddress returns (scratch_of_stream).
+static __device__ __align__(256) unsigned char scratch[kTopkScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// The scratch address on the device that owns `stream` (the current device for the null
+// stream), looked up once per device with that device current.
+int scratch_of_stream(hipStream_t stream, void** addr) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(OMM_EHIP, "omm_topk_fused_noalloc: device of the stream: %s",
+                     hipGetErrorString(e));
+  OMM_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, OMM_EUNSUPPORTED,
+              "omm_topk_fused_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess || p == nullptr)
+      return set_error(OMM_EHIP, "omm_topk_fused_noalloc: scratch address on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return OMM_OK;
+}
+
+}  // namespace
+}  // namespace omm
+
+extern "C" size_t omm_topk_fused_noalloc_max_bytes(void) { return omm::kTopkScratchBytes; }
+
+extern "C" int omm_topk_fused_noalloc(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                                      int32_t group_size, int32_t topk, float scale,
+                                      const omm_topk_mask* mask, int32_t* out, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL,
+              "omm_topk_fused_noalloc: null argument");
+  const size_t need = omm_topk_fused_workspace_bytes(q->size[0], q->size[1], q->size[2],
+                                                     q->size[3], k->size[1], group_size, topk,
+                                                     dtype);
+  OMM_REQUIRE(need <= kTopkScratchBytes, OMM_EWORKSPACE,
+              "omm_topk_fused_noalloc: this call needs %zu bytes of scratch but the static "
+              "scratch holds %zu; call omm_topk_fused with a workspace instead",
+              need, kTopkScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_of_stream(static_cast<hipStream_t>(stream), &ws);
+  if (rc != OMM_OK) return rc;
+  return omm_topk_fused(q, k, dtype, group_size, topk, scale, mask, out, ws, kTopkScratchBytes,
+                        stream);
 }
