@@ -161,6 +161,15 @@ size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D
 int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t group_size,
                    int32_t topk, float scale, const omm_topk_mask* mask, int32_t* out,
                    void* workspace, size_t workspace_bytes, void* stream);
+/* Test hook, no reference counterpart: omm_topk_fused that also writes the fp32 scores its
+ * selection ran on into scores ([B, ceil(T/group_size), H, NC], contiguous; entries of columns
+ * a row cannot see may be left unwritten), so the selection can be checked bit for bit against
+ * the reference rule on identical scores.  MFMA path only (bf16 / f16, head dim 64 or 128,
+ * unit dim strides, 16-byte aligned rows); other inputs fail with OMM_EUNSUPPORTED. */
+int omm_topk_fused_debug(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                         int32_t group_size, int32_t topk, float scale,
+                         const omm_topk_mask* mask, int32_t* out, float* scores,
+                         void* workspace, size_t workspace_bytes, void* stream);
 /* No counterpart in the reference: omm_topk_fused for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments
  * and result as omm_topk_fused without the workspace: the workspace is a fixed array of

@@ -66,6 +66,7 @@ PROTOTYPES = {
     "omm_topk": (_i32, [_V, _V, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
     "omm_topk_fused_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32]),
     "omm_topk_fused": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
+    "omm_topk_fused_debug": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _vp, _sz, _vp]),
     "omm_topk_fused_noalloc_max_bytes": (_sz, []),
     "omm_topk_fused_noalloc": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp]),
     "omm_topk_from_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _M, _vp, _vp, _sz, _vp]),

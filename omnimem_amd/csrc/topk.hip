@@ -640,6 +640,549 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
       sv + wave * kSurvCap);
 }
 
+// ---- MFMA scoring path ------------------------------------------------------------------------
+// bf16 / f16 queries and keys with head dim 64 or 128, unit dim strides and 16-byte aligned
+// rows.  Scores are MFMA dot products: each bf16 (f16) product is exact in fp32 and
+// v_mfma_f32_16x16x32 sums them in fp32 over d in 32-wide steps, ascending; the sum is then
+// multiplied by scale.  That is the role of the reference's TF32 WMMA scoring
+// (topk.cu:179-291, an fp32 sum of exact products in the hardware's order); the selection over
+// the scores follows the (score desc, id asc) rule bit for bit.
+//
+// One item = 16 query rows of one (b, h) x one column span, 4 waves:
+//   1. rows -> LDS: pooled from the full-resolution queries (fused mode; each lane sums one
+//      16-byte slice of one row over its tokens in ascending order, one division, one rounding:
+//      the omm_block_pool arithmetic) or loaded as given (pooled mode);
+//   2. S^T = K Qp^T: each wave takes 16-column blocks, K fragments straight from global memory
+//      (no LDS staging), Qp^T fragments held in registers; scores * scale -> LDS;
+//   3. selection, one wave per row: a lane holds its columns' 64-bit keys in registers; theta =
+//      min over 16 (more generally >= topk) lane groups of the group maxima, so at least topk
+//      keys are >= theta; the survivors are compacted and ranked exactly.
+typedef float m2_f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 m2_bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 m2_f16x8;
+
+template <typename T> struct M2Mfma;
+template <> struct M2Mfma<bf16_t> {
+  __device__ __forceinline__ static m2_f32x4 run(uint4 a, uint4 b, m2_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(m2_bf16x8, a),
+                                                   __builtin_bit_cast(m2_bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct M2Mfma<f16_t> {
+  __device__ __forceinline__ static m2_f32x4 run(uint4 a, uint4 b, m2_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(m2_f16x8, a),
+                                                  __builtin_bit_cast(m2_f16x8, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kM2Rows = 16;
+constexpr int kM2Threads = 256;
+constexpr int kM2Waves = kM2Threads / kWave;
+constexpr int kM2SpanCap = 960;   // columns per item: two workgroups' LDS fit a CU
+constexpr int kM2Batch = 4;       // 16-column blocks whose K fragments are loaded together
+
+struct M2Args {
+  const void* q;       // full-resolution [B, T, H, D] (fused) or pooled rows [B, MG, H, D]
+  int64_t qs0, qs1, qs2;
+  const void* k;       // [B, NC, H, D]
+  int64_t ks0, ks1, ks2;
+  int T_len, G;        // fused mode: tokens, tokens per row
+  int MG, H, NC, topk;
+  float scale;
+  MaskDev mk;
+  int span, nspan, rtiles;
+  int32_t* out;        // nspan == 1
+  uint64_t* part;      // nspan > 1: [B*MG*H][nspan][topk] packed keys
+  float* dump;         // optional: the scores, [B, MG, H, NC]
+  uint32_t o_qs, o_sv, o_kc, o_tv;
+};
+
+// LDS row pitch of the scores: whole 64-column steps (the selection reads 64 j + 4 l + e) plus
+// 4 floats, which keeps rows 16-byte aligned and off one another's banks
+__host__ __device__ inline int m2_pitch(int span) { return (span + 63) / 64 * 64 + 4; }
+
+inline size_t m2_lds_bytes(int span, int D) {
+  return static_cast<size_t>(kM2Rows) * m2_pitch(span) * 4         // scores
+         + static_cast<size_t>(kM2Rows) * (D + 8) * 2              // rows (16-bit)
+         + static_cast<size_t>(kM2Waves) * kSurvCap * 8            // survivors
+         + static_cast<size_t>(kM2Rows) * 32 * 4                   // row thresholds
+         + static_cast<size_t>(span) * 4;                          // column chunk ids
+}
+
+// Threshold of a wave's keys for a top-k: lanes in groups of gs consecutive lanes, 64 / gs >=
+// topk groups; theta = the smallest non-empty group maximum (high word) when at least topk
+// groups are non-empty -- each such group holds a key >= theta, so at least topk keys pass --
+// else 1 (every candidate passes: candidates have a high word >= 1).
+__device__ __forceinline__ uint32_t group_threshold(uint32_t lmax, int topk) {
+  const int lane = lane_id();
+  int gs = kWave;
+  while (gs > 1 && kWave / gs < topk) gs >>= 1;
+  uint32_t gmax = lmax;
+  for (int m = 1; m < gs; m <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(gmax), m, kWave));
+    gmax = o > gmax ? o : gmax;
+  }
+  const int groups = popc64(ballot64((lane % gs) == 0 && gmax != 0u));
+  uint32_t gmin = gmax != 0u ? gmax : 0xffffffffu;
+  for (int m = gs; m < kWave; m <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(gmin), m, kWave));
+    gmin = o < gmin ? o : gmin;
+  }
+  return groups >= topk ? gmin : 1u;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Top-k of one row from its fp32 scores in LDS (srow[i], i < n = column c_begin + i), one
+// wave.  vis(i) says whether column i is visible; -inf and NaN are never candidates.  Keys are
+// make_key(score, column): larger = (score desc, id asc).
+//   1. lane maxima of the candidates' high words (columns lane, lane + 64, ...) ->
+//      theta = group_threshold; candidates >= theta are compacted into sv (LDS, wave-private);
+//   2. while more than 64 survive: the survivors (<= 4 per lane) are cut by group_threshold
+//      again;
+//   3. one survivor per lane is ranked exactly by broadcast reads of the others.
+// Ties so massive that a cut removes nothing fall back to taking maxima one at a time.
+template <typename VisF, typename EmitF, typename PadF>
+__device__ __forceinline__ void row_topk_lds(const float* srow, int n, int c_begin, int NC,
+                                             int topk, VisF vis, EmitF emit, PadF pad,
+                                             uint64_t* sv) {
+  const int lane = lane_id();
+  uint32_t lmax = 0;
+  for (int i = lane; i < n; i += kWave) {
+    const float x = srow[i];
+    if (x > kNegInf && vis(i)) {
+      const uint32_t hi = f32_ord(x);
+      lmax = hi > lmax ? hi : lmax;
+    }
+  }
+  uint32_t theta = group_threshold(lmax, topk);
+  int ns = 0;
+  for (int i0 = 0; i0 < n; i0 += kWave) {
+    const int i = i0 + lane;
+    uint64_t k = 0ull;
+    if (i < n) {
+      const float x = srow[i];
+      if (x > kNegInf && f32_ord(x) >= theta && vis(i)) k = make_key(x, c_begin + i, NC);
+    }
+    const uint64_t m = ballot64(k != 0ull);
+    const int pos = ns + lanes_below(m);
+    if (k != 0ull && pos < kSurvCap) sv[pos] = k;
+    ns += popc64(m);
+  }
+  wave_lds_sync();
+  bool exhaustive = ns > kSurvCap;
+  while (!exhaustive && ns > kWave) {
+    uint64_t s4[kSurvCap / kWave];
+    uint32_t smax = 0;
+#pragma unroll
+    for (int j = 0; j < kSurvCap / kWave; ++j) {
+      const int i = kWave * j + lane;
+      s4[j] = i < ns ? sv[i] : 0ull;
+      const uint32_t hi = static_cast<uint32_t>(s4[j] >> 32);
+      smax = hi > smax ? hi : smax;
+    }
+    theta = group_threshold(smax, topk);
+    wave_lds_sync();  // every lane has read sv
+    int ns2 = 0;
+#pragma unroll
+    for (int j = 0; j < kSurvCap / kWave; ++j) {
+      const uint64_t k = s4[j];
+      const bool surv = static_cast<uint32_t>(k >> 32) >= theta && k != 0ull;
+      const uint64_t m = ballot64(surv);
+      if (surv) sv[ns2 + lanes_below(m)] = k;
+      ns2 += popc64(m);
+    }
+    wave_lds_sync();
+    if (ns2 == ns) exhaustive = true;  // no progress: ties
+    ns = ns2;
+  }
+  if (!exhaustive) {
+    const uint64_t mine = lane < ns ? sv[lane] : 0ull;
+    if (lane >= ns && lane < ((ns + 7) & ~7)) sv[lane] = 0ull;  // groups of 8 read below
+    wave_lds_sync();
+    int rank = 0;
+    for (int j = 0; j < ns; j += 8) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const ulonglong2 w = reinterpret_cast<const ulonglong2*>(sv + j)[e];
+        rank += (w.x > mine ? 1 : 0) + (w.y > mine ? 1 : 0);
+      }
+    }
+    if (lane < ns && rank < topk) emit(rank, mine);
+  } else {
+    // the maxima one at a time: each round a wave-wide max over the keys below the previous
+    uint64_t prev = ~0ull;
+    int r = 0;
+    for (; r < topk; ++r) {
+      uint64_t best = 0ull;
+      for (int i = lane; i < n; i += kWave) {
+        const float x = srow[i];
+        if (x > kNegInf && vis(i)) {
+          const uint64_t k = make_key(x, c_begin + i, NC);
+          if (k < prev && k > best) best = k;
+        }
+      }
+#pragma unroll
+      for (int mm = 1; mm < kWave; mm <<= 1) {
+        const uint64_t o = shfl_xor_u64(best, mm);
+        best = o > best ? o : best;
+      }
+      if (best == 0ull) break;
+      if (lane == 0) emit(r, best);
+      prev = best;
+    }
+    ns = r;
+  }
+  for (int p = lane; p < topk; p += kWave)
+    if (p >= ns) pad(p);
+  wave_lds_sync();
+}
+
+// ---- four rows per wave, one row per 16-lane DPP row (topk <= 16) ----------------------------
+// DPP reductions inside a 16-lane row: every lane gets the row's maximum / the inclusive prefix.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t row16_max(uint32_t v) {
+  v = max(v, dpp_u32<0x121>(v));  // row_ror:1
+  v = max(v, dpp_u32<0x122>(v));  // row_ror:2
+  v = max(v, dpp_u32<0x124>(v));  // row_ror:4
+  v = max(v, dpp_u32<0x128>(v));  // row_ror:8
+  return v;
+}
+// inclusive prefix sum over the lanes of a 16-lane row (row_shr with zero fill)
+template <int CTRL>
+__device__ __forceinline__ int dpp_shr0(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);  // bound_ctrl: 0 past the edge
+}
+__device__ __forceinline__ int row16_scan(int v) {
+  v += dpp_shr0<0x111>(v);  // row_shr:1
+  v += dpp_shr0<0x112>(v);  // row_shr:2
+  v += dpp_shr0<0x114>(v);  // row_shr:4
+  v += dpp_shr0<0x118>(v);  // row_shr:8
+  return v;
+}
+
+constexpr int kRowSurv = kSurvCap / 4;  // survivor slots per row (64)
+constexpr int kMaxJ = 16;               // 64-column steps per row: spans up to 1024 columns
+
+// Top-k (k <= 16) of the four rows r = 4 w + (lane >> 4) of a wave.  Lane (row, l) holds the
+// columns 64 j + 4 l + e (j < ceil(n / 64), e < 4) of its row's LDS scores as ordered high
+// words (0 = not a candidate) and its two largest.  The row threshold theta is the topk-th
+// largest of the row's 32 two-largest values: those are high words of distinct keys, so at
+// least topk keys are >= theta, and every key of the top topk is.  Survivors (>= theta, about
+// 18 for top-16 of random scores) are compacted per row and ranked exactly; a row with more
+// than 64 (massive ties) is reported in `overflow` (bit per row) for the caller to redo.
+template <typename VisF, typename EmitF, typename PadF>
+__device__ __forceinline__ uint32_t rows4_topk(const float* sc, int SP, int n, int c_begin,
+                                               int NC, int topk, bool row_live, int lim,
+                                               bool simple, VisF vis, EmitF emit, PadF pad,
+                                               uint64_t* sv, uint32_t* tv) {
+  const int lane = lane_id(), rid = lane >> 4, l16 = lane & 15;
+  const float* srow = sc + rid * SP;  // caller offsets sc to the wave's first row
+  const int J = (n + kWave - 1) / kWave;
+  // visibility of the lane's columns 64 j + 4 l16 + e as bit 4 j + e: plain masks see exactly
+  // the columns below `lim`; other masks evaluate the rule once per column in a rolled loop
+  uint64_t vbits = 0ull;
+  if (row_live) {
+    if (simple) {
+#pragma unroll
+      for (int j = 0; j < kMaxJ; ++j) {
+        const int k = min(max(lim - (kWave * j + 4 * l16), 0), 4);
+        vbits |= static_cast<uint64_t>((1u << k) - 1u) << (4 * j);
+      }
+    } else {
+#pragma nounroll
+      for (int t = 0; t < 4 * J; ++t) {
+        const int i = kWave * (t >> 2) + 4 * l16 + (t & 3);
+        if (i < n && vis(i)) vbits |= 1ull << t;
+      }
+    }
+  }
+  uint32_t hv[kMaxJ][4];
+  uint32_t m1 = 0, m2 = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxJ; ++j) {
+    if (j < J) {
+      const float4 x = *reinterpret_cast<const float4*>(srow + kWave * j + 4 * l16);
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool cand = ((vbits >> (4 * j + e)) & 1ull) != 0ull && xs[e] > kNegInf;
+        const uint32_t hi = cand ? f32_ord(xs[e]) : 0u;
+        hv[j][e] = hi;
+        m2 = max(m2, min(m1, hi));
+        m1 = max(m1, hi);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hv[j][e] = 0u;
+    }
+  }
+  // theta: the topk-th largest of the row's 32 values m1, m2 (0 when fewer are non-zero)
+  uint32_t* trow = tv + rid * 32;
+  trow[2 * l16] = m1;
+  trow[2 * l16 + 1] = m2;
+  wave_lds_sync();
+  int c1 = 0, c2 = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint4 t4 = reinterpret_cast<const uint4*>(trow)[q];
+    c1 += (t4.x >= m1) + (t4.y >= m1) + (t4.z >= m1) + (t4.w >= m1);
+    c2 += (t4.x >= m2) + (t4.y >= m2) + (t4.z >= m2) + (t4.w >= m2);
+  }
+  uint32_t theta = row16_max(max(c1 >= topk ? m1 : 0u, c2 >= topk ? m2 : 0u));
+  if (theta == 0u) theta = 1u;  // fewer than topk values: every candidate survives
+  uint64_t sbits = 0ull;  // survivors, bit 4 j + e
+#pragma unroll
+  for (int j = 0; j < kMaxJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (hv[j][e] >= theta) sbits |= 1ull << (4 * j + e);
+  const int cnt = popc64(sbits);
+  const int incl = row16_scan(cnt);
+  int pos = incl - cnt;
+  // row totals: lane 15 of each row
+  const int t0 = __builtin_amdgcn_readlane(incl, 15), t1 = __builtin_amdgcn_readlane(incl, 31);
+  const int t2 = __builtin_amdgcn_readlane(incl, 47), t3 = __builtin_amdgcn_readlane(incl, 63);
+  const int ns = rid == 0 ? t0 : rid == 1 ? t1 : rid == 2 ? t2 : t3;
+  uint64_t* srv = sv + rid * kRowSurv;
+  wave_lds_sync();  // the threshold buffer may be reused by the caller's next rows
+  // write the set bits' keys (a lane holds a handful): re-read each survivor's score
+  while (sbits != 0ull) {
+    const int t = __builtin_ctzll(sbits);
+    sbits &= sbits - 1ull;
+    const int i = kWave * (t >> 2) + 4 * l16 + (t & 3);
+    if (pos < kRowSurv) srv[pos] = make_key(srow[i], c_begin + i, NC);
+    ++pos;
+  }
+  wave_lds_sync();
+  const uint32_t over = static_cast<uint32_t>(ns > kRowSurv);
+  const int nsr = ns > kRowSurv ? 0 : ns;  // an overflowing row is left to the caller
+  const int nmax = max(max(t0 > kRowSurv ? 0 : t0, t1 > kRowSurv ? 0 : t1),
+                       max(t2 > kRowSurv ? 0 : t2, t3 > kRowSurv ? 0 : t3));
+  const int M = (nmax + 15) / 16;  // survivors per lane to rank (wave-uniform, <= 4)
+  // rank: lane takes survivors l16, l16 + 16, l16 + 32, l16 + 48 of its row
+  uint64_t mine[4];
+  int rank[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    mine[m] = (m < M && 16 * m + l16 < nsr) ? srv[16 * m + l16] : ~0ull;
+    rank[m] = 0;
+  }
+  for (int i = 0; i < nmax; i += 2) {  // wave-uniform bound; entries past a row's count are 0
+    const ulonglong2 w2 = *reinterpret_cast<const ulonglong2*>(srv + i);
+    const uint64_t a = i < nsr ? w2.x : 0ull, b = i + 1 < nsr ? w2.y : 0ull;
+    rank[0] += (a > mine[0] ? 1 : 0) + (b > mine[0] ? 1 : 0);
+    if (M > 1) rank[1] += (a > mine[1] ? 1 : 0) + (b > mine[1] ? 1 : 0);
+    if (M > 2) rank[2] += (a > mine[2] ? 1 : 0) + (b > mine[2] ? 1 : 0);
+    if (M > 3) rank[3] += (a > mine[3] ? 1 : 0) + (b > mine[3] ? 1 : 0);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (m < M && 16 * m + l16 < nsr && rank[m] < topk) emit(rid, rank[m], mine[m]);
+  if (!over && l16 < topk && l16 >= nsr && row_live) pad(rid, l16);
+  wave_lds_sync();
+  // overflow bits of the four rows, wave-uniform
+  const uint64_t ob = ballot64(over != 0u && l16 == 0);
+  return static_cast<uint32_t>((ob & 1ull) | ((ob >> 15) & 2ull) | ((ob >> 30) & 4ull) |
+                               ((ob >> 45) & 8ull));
+}
+
+// Row facts of a 16-row tile, one row per lane (lanes >= 16 repeat them): 4 words each.
+struct RowFacts {
+  int q_cid, q_rel, flags, ub;  // flags: bit 0 q_clean, bit 1 do_excl
+};
+
+template <typename T, int D, bool FUSED>
+__global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int SD = D / 32;      // MFMA k-steps
+  constexpr int CH = D / 8;       // 16-byte slices per row
+  constexpr int QP = D + 8;       // LDS row pitch of the pooled rows (elements)
+  __shared__ RowFacts facts[kM2Rows];
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  const int total = static_cast<int>(gridDim.x);
+  int it = xcd_remap(static_cast<int>(blockIdx.x), total);
+  // item order: (b, h) major, then column span, then row tiles heaviest (latest) first
+  const int rt = a.rtiles - 1 - it % a.rtiles; it /= a.rtiles;
+  const int sp = it % a.nspan; it /= a.nspan;
+  const int h = it % a.H;
+  const int b = it / a.H;
+  const int row0 = rt * kM2Rows;
+  const MaskDev& mk = a.mk;
+  const int SP = m2_pitch(a.span);
+
+  float* sc = reinterpret_cast<float*>(smem);
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem + a.o_qs);
+  uint64_t* sv = reinterpret_cast<uint64_t*>(smem + a.o_sv);
+  int* kc = reinterpret_cast<int*>(smem + a.o_kc);
+
+  // ---- 0. row facts, lane r -> row row0 + r; the tile's column bound by a wave max ----
+  int ub;
+  {
+    const int g = row0 + l16;
+    const RowInfo ri = row_info(mk, g);
+    const int rub = g < a.MG ? row_ub(mk, ri, a.NC) : 0;
+    if (w == 0 && lane < kM2Rows)
+      facts[lane] = RowFacts{ri.q_cid, ri.q_rel, (ri.q_clean ? 1 : 0) | (ri.do_excl ? 2 : 0), rub};
+    ub = rub;
+    for (int m = 1; m < 16; m <<= 1) ub = max(ub, __shfl_xor(ub, m, kWave));
+  }
+  const int c_begin = sp * a.span;
+  const int c_end = min(c_begin + a.span, ub);
+  const int n = max(0, c_end - c_begin);
+  const int nblk = (n + 15) / 16;
+  const bool simple = !mk.tf && mk.ex_sink <= 0 && mk.ex_win <= 0;
+
+  // this wave's first batch of K fragments, in flight during the row pooling
+  const T* kp = static_cast<const T*>(a.k) + b * a.ks0 + h * a.ks2;
+  uint4 kf[kM2Batch][SD];
+  auto load_k = [&](int cb0) {
+#pragma unroll
+    for (int x = 0; x < kM2Batch; ++x) {
+      const int col = min(c_begin + (cb0 + x) * 16 + l16, a.NC - 1);  // in bounds
+#pragma unroll
+      for (int s = 0; s < SD; ++s)
+        kf[x][s] = *reinterpret_cast<const uint4*>(kp + static_cast<int64_t>(col) * a.ks1 +
+                                                   32 * s + 8 * j4);
+    }
+  };
+  if (w * kM2Batch < nblk) load_k(w * kM2Batch);
+
+  // ---- 1. rows -> LDS ----
+  const T* qp = static_cast<const T*>(a.q);
+  if (tid < kM2Rows * CH) {
+    const int r = tid / CH, u = tid - r * CH, g = row0 + r;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (g < a.MG) {
+      if constexpr (FUSED) {
+        constexpr int V = 8;
+        float acc[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+        const int t0 = g * a.G, t1 = min(t0 + a.G, a.T_len);
+        const T* base = qp + b * a.qs0 + h * a.qs2 + u * V;
+        int t = t0;
+        for (; t + 16 <= t1; t += 16) {
+          uint4 rr[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            rr[j] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t + j) * a.qs1);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            float f[V];
+            unpack<T>(rr[j], f);
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] += f[i];
+          }
+        }
+        for (; t < t1; ++t) {
+          const uint4 rr = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t) * a.qs1);
+          float f[V];
+          unpack<T>(rr, f);
+#pragma unroll
+          for (int i = 0; i < V; ++i) acc[i] += f[i];
+        }
+        const float cnt = static_cast<float>(t1 - t0);
+        uint16_t bits[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const T x = from_f32<T>(acc[i] / cnt);
+          bits[i] = __builtin_bit_cast(uint16_t, x);
+        }
+        val = make_uint4(bits[0] | (static_cast<uint32_t>(bits[1]) << 16),
+                         bits[2] | (static_cast<uint32_t>(bits[3]) << 16),
+                         bits[4] | (static_cast<uint32_t>(bits[5]) << 16),
+                         bits[6] | (static_cast<uint32_t>(bits[7]) << 16));
+      } else {
+        val = *reinterpret_cast<const uint4*>(qp + b * a.qs0 + g * a.qs1 + h * a.qs2 + u * 8);
+      }
+    }
+    *reinterpret_cast<uint4*>(qs + r * QP + u * 8) = val;
+  }
+  if (!simple)
+    for (int i = tid; i < n; i += kM2Threads) kc[i] = col_cid(mk, c_begin + i);
+  __syncthreads();
+
+  // ---- 2. S^T = K Qp^T on MFMA -> LDS ----
+  uint4 qb[SD];
+#pragma unroll
+  for (int s = 0; s < SD; ++s)
+    qb[s] = *reinterpret_cast<const uint4*>(qs + l16 * QP + 32 * s + 8 * j4);
+  for (int cb0 = w * kM2Batch; cb0 < nblk; cb0 += kM2Waves * kM2Batch) {
+    if (cb0 != w * kM2Batch) load_k(cb0);
+#pragma unroll
+    for (int x = 0; x < kM2Batch; ++x) {
+      if (cb0 + x >= nblk) break;  // wave-uniform
+      m2_f32x4 acc = m2_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < SD; ++s) acc = M2Mfma<T>::run(kf[x][s], qb[s], acc);
+      // lane holds the scores of row l16, columns (cb0 + x) * 16 + 4 j4 + 0..3 of the span
+      const int c = (cb0 + x) * 16 + 4 * j4;
+      const float4 v = make_float4(acc[0] * a.scale, acc[1] * a.scale, acc[2] * a.scale,
+                                   acc[3] * a.scale);
+      *reinterpret_cast<float4*>(sc + l16 * SP + c) = v;
+      if (a.dump != nullptr && row0 + l16 < a.MG) {
+        float* d = a.dump + ((static_cast<int64_t>(b) * a.MG + row0 + l16) * a.H + h) * a.NC;
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c + e < n) d[c_begin + c + e] = vv[e];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. selection: wave w owns rows 4 w .. 4 w + 3, one per 16-lane DPP row ----
+  uint64_t* wsv = sv + w * kSurvCap;
+  uint32_t* wtv = reinterpret_cast<uint32_t*>(smem + a.o_tv) + w * 128;
+  const int NC = a.NC;
+  const int r = 4 * w + (lane >> 4), g = row0 + r;
+  const RowFacts f = facts[r];
+  const RowInfo ri{f.q_cid, f.q_rel, (f.flags & 1) != 0, (f.flags & 2) != 0};
+  const int rub = f.ub - c_begin;
+  const int64_t orow = (static_cast<int64_t>(b) * a.MG + g) * a.H + h;
+  auto emit_at = [&](int64_t orow_, int rank, uint64_t kk) {
+    if (a.nspan == 1) a.out[orow_ * a.topk + rank] = key_id(kk, NC);
+    else a.part[(orow_ * a.nspan + sp) * a.topk + rank] = kk;
+  };
+  auto pad_at = [&](int64_t orow_, int p) {
+    if (a.nspan == 1) a.out[orow_ * a.topk + p] = -1;
+    else a.part[(orow_ * a.nspan + sp) * a.topk + p] = 0ull;
+  };
+  uint32_t over;
+  {
+    auto vis = [&](int i) { return simple ? (i < rub) : visible(mk, ri, kc[i]); };
+    over = rows4_topk(sc + 4 * w * SP, SP, n, c_begin, NC, a.topk, g < a.MG, min(rub, n), simple,
+                      vis,
+                      [&](int, int rank, uint64_t kk) { emit_at(orow, rank, kk); },
+                      [&](int, int p) { pad_at(orow, p); }, wsv, wtv);
+  }
+  // rows with more than 64 survivors (massive ties): the whole wave redoes them one at a time
+  while (over != 0u) {
+    const int rr = __builtin_ctz(over);
+    over &= over - 1u;
+    const int r2 = 4 * w + rr, g2 = row0 + r2;
+    const RowFacts f2 = facts[r2];
+    const RowInfo ri2{f2.q_cid, f2.q_rel, (f2.flags & 1) != 0, (f2.flags & 2) != 0};
+    const int rub2 = f2.ub - c_begin;
+    const int64_t orow2 = (static_cast<int64_t>(b) * a.MG + g2) * a.H + h;
+    auto vis2 = [&](int i) { return simple ? (i < rub2) : visible(mk, ri2, kc[i]); };
+    row_topk_lds(sc + r2 * SP, n, c_begin, NC, a.topk, vis2,
+                 [&](int rank, uint64_t kk) { emit_at(orow2, rank, kk); },
+                 [&](int p) { pad_at(orow2, p); }, wsv);
+  }
+  (void)lane;
+}
+
 // ---- host planning ---------------------------------------------------------------------------
 int span_cap(int D, int esize, bool scores) {
   for (int s = kSpanCap; s > kTileC; s -= kTileC)
@@ -791,6 +1334,102 @@ void set_k(TopkArgs& a, const omm_view4& k) {
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// ---- MFMA path planning ---------------------------------------------------------------------
+inline bool m2_view_ok(const omm_view4& v) {
+  return v.stride[3] == 1 && v.stride[0] % 8 == 0 && v.stride[1] % 8 == 0 &&
+         v.stride[2] % 8 == 0 && a16(v.data);
+}
+// 16-bit inputs, head dim 64 or 128, unit dim strides, 16-byte aligned rows, topk <= 16.
+bool m2_ok(int32_t dtype, const omm_view4& q, const omm_view4& k, int topk) {
+  if (dtype != OMM_BF16 && dtype != OMM_F16) return false;
+  if (topk > 16) return false;
+  const int64_t D = q.size[3];
+  return (D == 64 || D == 128) && m2_view_ok(q) && m2_view_ok(k);
+}
+
+struct M2Plan {
+  int span, nspan, rtiles;
+  size_t ws_part;
+};
+
+// fused: one item per 16-row tile covers every column (q is pooled once).  Otherwise the columns
+// are split into spans so that about 512 items (two per CU) run, and a merge kernel selects
+// again over the spans' winners.
+M2Plan m2_plan(int64_t B, int64_t MG, int64_t H, int64_t NC, int topk, bool fused) {
+  M2Plan p{};
+  p.rtiles = static_cast<int>(cdiv64(MG, kM2Rows));
+  const int64_t tiles = B * H * p.rtiles;
+  int64_t nspan = cdiv64(NC, kM2SpanCap);
+  if (!fused && tiles * nspan < 512)
+    nspan = std::max(nspan, std::min(cdiv64(512, tiles), cdiv64(NC, 256)));
+  int64_t span = (cdiv64(NC, nspan) + 15) / 16 * 16;
+  if (span < 16) span = 16;
+  p.span = static_cast<int>(span);
+  p.nspan = static_cast<int>(std::max<int64_t>(1, cdiv64(NC, span)));
+  p.ws_part = p.nspan > 1 ? static_cast<size_t>(B * MG * H) * p.nspan * topk * sizeof(uint64_t) : 0;
+  return p;
+}
+
+bool m2_fused_ok(int64_t B, int64_t MG, int64_t H, int64_t NC) {
+  return NC <= kM2SpanCap && B * H * cdiv64(MG, kM2Rows) >= 256;
+}
+
+template <typename T, int D, bool FUSED>
+int launch_m2_typed(M2Args a, int64_t B, int64_t H, const M2Plan& p, hipStream_t s) {
+  const size_t lds = m2_lds_bytes(p.span, D);
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&topk_mfma_kernel<T, D, FUSED>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return set_error(OMM_EHIP, "top-k: LDS attribute: %s", hipGetErrorString(e));
+  }
+  a.span = p.span;
+  a.nspan = p.nspan;
+  a.rtiles = p.rtiles;
+  a.o_qs = static_cast<uint32_t>(align16(static_cast<size_t>(kM2Rows) * m2_pitch(p.span) * 4));
+  a.o_sv = static_cast<uint32_t>(align16(a.o_qs + static_cast<size_t>(kM2Rows) * (D + 8) * 2));
+  a.o_tv = static_cast<uint32_t>(a.o_sv + static_cast<size_t>(kM2Waves) * kSurvCap * 8);
+  a.o_kc = static_cast<uint32_t>(a.o_tv + static_cast<size_t>(kM2Rows) * 32 * 4);
+  const int64_t items = B * H * p.nspan * p.rtiles;
+  OMM_REQUIRE(items <= 2147483647ll, OMM_EUNSUPPORTED, "top-k: grid too large");
+  topk_mfma_kernel<T, D, FUSED><<<static_cast<unsigned>(items), kM2Threads, lds, s>>>(a);
+  int rc = check_launch("top-k (mfma)");
+  if (rc != OMM_OK || p.nspan == 1) return rc;
+  const int64_t rows = B * a.MG * H;
+  topk_merge_kernel<<<static_cast<unsigned>(cdiv64(rows, kWaves)), kThreads, 0, s>>>(
+      a.part, a.out, rows, p.nspan, a.topk, a.NC);
+  return check_launch("top-k merge");
+}
+
+template <bool FUSED>
+int launch_m2(int32_t dtype, int D, M2Args a, int64_t B, int64_t H, const M2Plan& p,
+              hipStream_t s) {
+  if (dtype == OMM_BF16)
+    return D == 128 ? launch_m2_typed<bf16_t, 128, FUSED>(a, B, H, p, s)
+                    : launch_m2_typed<bf16_t, 64, FUSED>(a, B, H, p, s);
+  return D == 128 ? launch_m2_typed<f16_t, 128, FUSED>(a, B, H, p, s)
+                  : launch_m2_typed<f16_t, 64, FUSED>(a, B, H, p, s);
+}
+
+M2Args m2_args(const omm_view4& q, const omm_view4& k, int64_t MG, int64_t H, int64_t NC,
+               int topk, float scale, const omm_topk_mask& mask, int32_t* out, void* part,
+               float* dump) {
+  M2Args a{};
+  a.q = q.data; a.qs0 = q.stride[0]; a.qs1 = q.stride[1]; a.qs2 = q.stride[2];
+  a.k = k.data; a.ks0 = k.stride[0]; a.ks1 = k.stride[1]; a.ks2 = k.stride[2];
+  a.MG = static_cast<int>(MG);
+  a.H = static_cast<int>(H);
+  a.NC = static_cast<int>(NC);
+  a.topk = topk;
+  a.scale = scale;
+  a.mk = to_dev(mask);
+  a.out = out;
+  a.part = static_cast<uint64_t*>(part);
+  a.dump = dump;
+  a.G = 1;
+  return a;
+}
+
 }  // namespace
 }  // namespace omm
 
@@ -804,7 +1443,7 @@ extern "C" size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int
     for (int D : {64, 128, 256})
       for (bool scores : {false, true})
         ws = std::max(ws, omm::make_plan(B, MG, H, NC, topk, D, esize, scores, false).ws_part);
-  return ws;
+  return std::max(ws, omm::m2_plan(B, MG, H, NC, topk, false).ws_part);
 }
 
 extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t topk,
@@ -827,6 +1466,14 @@ extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, i
   if (B == 0 || MG == 0 || H == 0) return OMM_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
+  if (m2_ok(dtype, *q, *k, topk)) {
+    const M2Plan p = m2_plan(B, MG, H, NC, topk, false);
+    OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
+                OMM_EWORKSPACE, "omm_topk: workspace of %zu bytes required, got %zu", p.ws_part,
+                workspace_bytes);
+    const M2Args a = m2_args(*q, *k, MG, H, NC, topk, scale, *mask, out, workspace, nullptr);
+    return launch_m2<false>(dtype, static_cast<int>(D), a, B, H, p, s);
+  }
   const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
   OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
               OMM_EWORKSPACE, "omm_topk: workspace of %zu bytes required, got %zu", p.ws_part,
@@ -850,11 +1497,11 @@ extern "C" size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H
   return pooled + omm_topk_workspace_bytes(B, MG, H, NC, topk);
 }
 
-extern "C" int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype,
-                              int32_t group_size, int32_t topk, float scale,
-                              const omm_topk_mask* mask, int32_t* out, void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  using namespace omm;
+namespace omm {
+namespace {
+int topk_fused_impl(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t group_size,
+                    int32_t topk, float scale, const omm_topk_mask* mask, int32_t* out,
+                    float* dump, void* workspace, size_t workspace_bytes, void* stream) {
   OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL,
               "omm_topk_fused: null argument");
   OMM_REQUIRE(group_size >= 1, OMM_EINVAL, "omm_topk_fused: group_size must be >= 1, got %d",
@@ -880,6 +1527,36 @@ extern "C" int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dt
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   OMM_REQUIRE(q->data != nullptr && k->data != nullptr, OMM_EINVAL, "omm_topk_fused: null data");
+
+  if (m2_ok(dtype, *q, *k, topk)) {
+    if (m2_fused_ok(B, MG, H, NC)) {
+      const M2Plan p = m2_plan(B, MG, H, NC, topk, true);
+      M2Args a = m2_args(*q, *k, MG, H, NC, topk, scale, *mask, out, nullptr, dump);
+      a.T_len = static_cast<int>(T);
+      a.G = group_size;
+      return launch_m2<true>(dtype, static_cast<int>(D), a, B, H, p, s);
+    }
+    // few rows or a long key history: pool once into the workspace, then column spans
+    const size_t pooled_bytes = align256(static_cast<size_t>(B * MG * H * D) * es);
+    const M2Plan p = m2_plan(B, MG, H, NC, topk, false);
+    const size_t need = pooled_bytes + p.ws_part;
+    OMM_REQUIRE(workspace != nullptr && need <= workspace_bytes, OMM_EWORKSPACE,
+                "omm_topk_fused: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    omm_view4 pooled{};
+    pooled.data = workspace;
+    pooled.size[0] = B; pooled.size[1] = MG; pooled.size[2] = H; pooled.size[3] = D;
+    pooled.stride[3] = 1; pooled.stride[2] = D; pooled.stride[1] = H * D;
+    pooled.stride[0] = MG * H * D;
+    OMM_REQUIRE(MG <= 65535 && B <= 65535, OMM_EUNSUPPORTED, "omm_topk_fused: grid limit");
+    rc = pool_launch(*q, pooled, dtype, group_size, s);
+    if (rc) return rc;
+    const M2Args a = m2_args(pooled, *k, MG, H, NC, topk, scale, *mask, out,
+                             static_cast<unsigned char*>(workspace) + pooled_bytes, dump);
+    return launch_m2<false>(dtype, static_cast<int>(D), a, B, H, p, s);
+  }
+  OMM_REQUIRE(dump == nullptr, OMM_EUNSUPPORTED,
+              "omm_topk_fused_debug: the score dump exists on the MFMA path only (bf16 / f16, "
+              "head dim 64 or 128, unit dim strides, 16-byte aligned rows)");
 
   const bool vec = vec_ok(*q, es) && vec_ok(*k, es);
   if (vec && fused_ok(B, MG, H, NC, static_cast<int>(D), es)) {
@@ -911,6 +1588,26 @@ extern "C" int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dt
   set_k(a, *k);
   a.vec = vec_ok(pooled, es) && vec_ok(*k, es);
   return launch_typed<kModePooled>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
+}
+}  // namespace
+}  // namespace omm
+
+extern "C" int omm_topk_fused(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                              int32_t group_size, int32_t topk, float scale,
+                              const omm_topk_mask* mask, int32_t* out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return omm::topk_fused_impl(q, k, dtype, group_size, topk, scale, mask, out, nullptr, workspace,
+                              workspace_bytes, stream);
+}
+
+extern "C" int omm_topk_fused_debug(const omm_view4* q, const omm_view4* k, int32_t dtype,
+                                    int32_t group_size, int32_t topk, float scale,
+                                    const omm_topk_mask* mask, int32_t* out, float* scores,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(scores != nullptr, OMM_EINVAL, "omm_topk_fused_debug: null scores");
+  return topk_fused_impl(q, k, dtype, group_size, topk, scale, mask, out, scores, workspace,
+                         workspace_bytes, stream);
 }
 
 extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H,

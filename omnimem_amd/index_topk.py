@@ -8,7 +8,9 @@ adapter).  Differences, all extensions that leave the reference's accepted input
   rule the selection kernel already uses (cuda_backend/csrc/selection_fwd.cu:218).
 * ``blocks_per_chunk > 0`` selects chunk-aligned key blocks (block c lies in chunk
   c // blocks_per_chunk), the page layout of the paged KV cache.
-* ``allow_tf32`` and ``bt_chunk`` are accepted and ignored: scores are always exact-order fp32.
+* ``allow_tf32`` and ``bt_chunk`` are accepted and ignored.  Scores are fp32 sums of exact
+  products: MFMA dot products for bf16 / f16 inputs with head dim 64 or 128 (the role of the
+  reference's TF32 WMMA), fmaf over d ascending otherwise.
 """
 from __future__ import annotations
 
@@ -227,6 +229,38 @@ def _topk_fused_impl(q: torch.Tensor, k: torch.Tensor, S: int, sc: float, block_
     _lib.call("omm_topk_fused", _lib.view4(q), _lib.view4(k), dt, G, S, float(sc), m,
               out.data_ptr() if out.numel() else None, ws.data_ptr(), ws_n, _lib.stream_of(q))
     return out
+
+
+def parallel_nsa_topk_with_scores(q: torch.Tensor, k: torch.Tensor, block_counts: int,
+                                  block_size: int = 64, scale: Optional[float] = None,
+                                  chunk_size: int = 64, causal: bool = True, group_size: int = 1,
+                                  exclude_window_chunks: int = 0, exclude_sink_chunks: int = 0,
+                                  progressive_exclude: bool = False, tf_mask: bool = False,
+                                  q_chunk_offset: int = 0, blocks_per_chunk: int = 0):
+    """Inspection hook: ``parallel_nsa_topk``'s indices together with the fp32 block scores its
+    selection ran on ([B, ceil(T/G), H, TC]; NaN where a row's columns were not scored because
+    the mask hides them).  bf16 / f16 inputs with head dim 64 or 128 (the MFMA path)."""
+    _lib.require_cuda((q, "q"), (k, "k"))
+    B, T, H, K = q.shape
+    G = int(group_size)
+    MG = -(-T // G)
+    NC = k.shape[1]
+    sc = scale if scale is not None else K ** -0.5
+    q_half = (MG * G) // (2 * chunk_size) if tf_mask else 0
+    k_half = (NC * block_size) // (2 * chunk_size) if tf_mask else 0
+    m = _mask(block_size, G, chunk_size, chunk_size, causal, exclude_window_chunks,
+              exclude_sink_chunks, progressive_exclude, tf_mask, q_chunk_offset, q_half, k_half,
+              blocks_per_chunk)
+    S = int(block_counts)
+    out = torch.empty((B, MG, H, S), dtype=torch.int32, device=q.device)
+    scores = torch.full((B, MG, H, NC), float("nan"), dtype=torch.float32, device=q.device)
+    dt = _lib.dtype_code(q)
+    ws_n = _lib.lib().omm_topk_fused_workspace_bytes(B, T, H, K, NC, G, S, dt)
+    ws = _lib.workspace(ws_n, q.device)
+    _lib.call("omm_topk_fused_debug", _lib.view4(q), _lib.view4(k), dt, G, S, float(sc), m,
+              out.data_ptr() if out.numel() else None, scores.data_ptr(), ws.data_ptr(), ws_n,
+              _lib.stream_of(q))
+    return out, scores
 
 
 def parallel_nsa_topk_grouped_heads(

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from oracle import nsa_oracle as O
+from _topk_checks import check_mfma_topk
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -125,12 +126,12 @@ def test_reference_ar_sequence_against_mmcache():
             assert torch.equal(v_swa.cpu(), torch.cat([vs[c] for c in keep], 1))
             _tol(o_cmp, _dense_ref(q, k_cmp, v_cmp), what="o_cmp")
             _tol(o_swa, _dense_ref(q, k_swa, v_swa), what="o_swa")
-            # top-k on the same pooled inputs as the oracle
-            qp = O.pool_mean(q.float().cpu().numpy(), G, "bf16")
-            want_ids = O.topk(qp, want_kc.float().numpy(), TOPK, D ** -0.5,
-                              O.Mask(block_size=BS, group_size=G, chunk_q=S, chunk_k=S,
-                                     q_chunk_offset=cid, ex_win=EXW, causal=0, prog_excl=1))
-            np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+            # top-k: the oracle's selection rule on the kernel's scores of the same inputs
+            mask = O.Mask(block_size=BS, group_size=G, chunk_q=S, chunk_k=S,
+                          q_chunk_offset=cid, ex_win=EXW, causal=0, prog_excl=1)
+            check_mfma_topk(q, k_cmp, TOPK, mask, D ** -0.5, G, got=ids.cpu().numpy(),
+                            block_size=BS, chunk_size=S, causal=False, exclude_window_chunks=EXW,
+                            progressive_exclude=True, q_chunk_offset=cid)
             k_all = torch.cat(ks, 1).float().numpy()
             v_all = torch.cat(vs, 1).float().numpy()
             want_o, _ = O.selection_attention(q.float().cpu().numpy(), k_all, v_all,

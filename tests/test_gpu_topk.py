@@ -1,7 +1,9 @@
 """GPU parity of block compression, query pooling and top-k against the CPU oracle.
 
-Bit-exact: pooled values, and block indices (given the oracle's fp32 scores, which the kernel
-reproduces operation for operation).  Cases follow the reference's mask modes
+Bit-exact: pooled values; block indices of the exact-order path (fp32, or strides / head dims
+off the MFMA path) against the oracle's own fmaf scores; block indices of the MFMA path (bf16 /
+f16, head dim 64 or 128) against the oracle's selection on the kernel's own scores, whose
+accuracy is bounded separately (tests/_topk_checks.py).  Cases follow the reference's mask modes
 (cuda_backend/csrc/topk.cu:36-97) and BASELINE config 2 at full size.
 """
 import zlib
@@ -11,6 +13,7 @@ import pytest
 import torch
 
 from oracle import nsa_oracle as O
+from _topk_checks import check_mfma_topk
 
 pytestmark = pytest.mark.gpu
 
@@ -117,16 +120,17 @@ def test_parallel_nsa_topk_fused_bitexact(dtype, T, NC, G, chunk, causal, qoff, 
     q = torch.randn((B, T, H, D), generator=g).to(dtype)
     k = torch.randn((B, NC, H, D), generator=g).to(dtype)
     bpc = 74 if not causal else 0
-    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=chunk,
-                            causal=causal, group_size=G, exclude_window_chunks=exw,
-                            progressive_exclude=not causal, q_chunk_offset=qoff,
-                            blocks_per_chunk=bpc).cpu().numpy()
-    dt = "bf16" if dtype == torch.bfloat16 else "f32"
-    qp = O.pool_mean(_img(q), G, dt)
-    want = O.topk(qp, _img(k), 16, D ** -0.5,
-                  O.Mask(block_size=64, group_size=G, chunk_q=chunk, chunk_k=chunk,
-                         blocks_per_chunk=bpc, q_chunk_offset=qoff, ex_win=exw,
-                         causal=int(causal), prog_excl=int(not causal)))
+    kw = dict(block_size=64, chunk_size=chunk, causal=causal, exclude_window_chunks=exw,
+              progressive_exclude=not causal, q_chunk_offset=qoff, blocks_per_chunk=bpc)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, group_size=G, **kw).cpu().numpy()
+    mask = O.Mask(block_size=64, group_size=G, chunk_q=chunk, chunk_k=chunk,
+                  blocks_per_chunk=bpc, q_chunk_offset=qoff, ex_win=exw,
+                  causal=int(causal), prog_excl=int(not causal))
+    if dtype == torch.bfloat16:  # MFMA path
+        check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, D ** -0.5, G, got=got, **kw)
+        return
+    qp = O.pool_mean(_img(q), G, "f32")
+    want = O.topk(qp, _img(k), 16, D ** -0.5, mask)
     np.testing.assert_array_equal(got, want)
 
 
@@ -139,10 +143,9 @@ def test_topk_config2_full_size_bitexact():
     k = torch.randn((1, 512, 12, 128), generator=g).to(torch.bfloat16)
     got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=4680,
                             causal=True, group_size=64).cpu().numpy()
-    qp = O.pool_mean(_img(q), 64, "bf16")
-    want = O.topk(qp, _img(k), 16, 128 ** -0.5,
-                  O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1))
-    np.testing.assert_array_equal(got, want)
+    mask = O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1)
+    check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 64, got=got, block_size=64,
+                    chunk_size=4680, causal=True)
     assert (got >= 0).all()  # every group sees >= 73 blocks
 
 
@@ -156,8 +159,11 @@ def test_grouped_heads_broadcast():
     # head pool (pairs of heads) then query pool, both rounded to bf16
     qh = O.round_to(_img(q).reshape(1, 512, 2, 2, 64).astype(np.float32).sum(3) / 2, "bf16")
     kh = O.round_to(_img(k).reshape(1, 32, 2, 2, 64).astype(np.float32).sum(3) / 2, "bf16")
-    want = O.topk(O.pool_mean(qh, 16, "bf16"), kh, 8, 64 ** -0.5,
-                  O.Mask(block_size=16, group_size=16, chunk_q=128, chunk_k=128, causal=1))
+    mask = O.Mask(block_size=16, group_size=16, chunk_q=128, chunk_k=128, causal=1)
+    qh_t = torch.from_numpy(qh).to(torch.bfloat16).to(DEV)
+    kh_t = torch.from_numpy(kh).to(torch.bfloat16).to(DEV)
+    want = check_mfma_topk(qh_t, kh_t, 8, mask, 64 ** -0.5, 16, block_size=16, chunk_size=128,
+                           causal=True)
     np.testing.assert_array_equal(got[:, :, 0::2], want)
     np.testing.assert_array_equal(got[:, :, 1::2], want)
 
@@ -170,9 +176,9 @@ def test_topk_fused_config3_ragged_tail_bitexact():
     k = torch.randn((1, 512, 12, 128), generator=g).to(torch.bfloat16)
     got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=4680,
                             causal=True, group_size=64).cpu().numpy()
-    want = O.topk(O.pool_mean(_img(q), 64, "bf16"), _img(k), 16, 128 ** -0.5,
-                  O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1))
-    np.testing.assert_array_equal(got, want)
+    mask = O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1)
+    check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 64, got=got, block_size=64,
+                    chunk_size=4680, causal=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -182,13 +188,15 @@ def test_topk_fused_many_heads_bitexact(dtype):
     g = torch.Generator().manual_seed(34)
     q = torch.randn((1, 4096, 64, 64), generator=g).to(dtype)
     k = torch.randn((1, 200, 64, 64), generator=g).to(dtype)
-    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 8, block_size=32, chunk_size=1024,
-                            causal=True, group_size=64, exclude_sink_chunks=1,
-                            exclude_window_chunks=1).cpu().numpy()
-    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dtype]
-    want = O.topk(O.pool_mean(_img(q), 64, dt), _img(k), 8, 64 ** -0.5,
-                  O.Mask(block_size=32, group_size=64, chunk_q=1024, chunk_k=1024, causal=1,
-                         ex_sink=1, ex_win=1))
+    kw = dict(block_size=32, chunk_size=1024, causal=True, exclude_sink_chunks=1,
+              exclude_window_chunks=1)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 8, group_size=64, **kw).cpu().numpy()
+    mask = O.Mask(block_size=32, group_size=64, chunk_q=1024, chunk_k=1024, causal=1,
+                  ex_sink=1, ex_win=1)
+    if dtype != torch.float32:  # MFMA path
+        check_mfma_topk(q.to(DEV), k.to(DEV), 8, mask, 64 ** -0.5, 64, got=got, **kw)
+        return
+    want = O.topk(O.pool_mean(_img(q), 64, "f32"), _img(k), 8, 64 ** -0.5, mask)
     np.testing.assert_array_equal(got, want)
 
 
@@ -216,8 +224,10 @@ def test_topk_prepooled_op_long_history_split_merge():
     got = topk(q.to(DEV), k.to(DEV), 16, 128 ** -0.5, 64, 74, 4680, False, ex_win=3,
                prog_excl=True, q_chunk_offset=80, group_size=64,
                blocks_per_chunk=74).cpu().numpy()
-    want = O.topk(_img(q), _img(k), 16, 128 ** -0.5,
-                  O.Mask(block_size=64, group_size=64, chunk_q=74 * 64, chunk_k=4680,
-                         blocks_per_chunk=74, q_chunk_offset=80, ex_win=3, causal=0,
-                         prog_excl=1))
-    np.testing.assert_array_equal(got, want)
+    # the same rows through the scores hook: one row per "token" (group 1), 74-row query chunks;
+    # keys in chunk-aligned pages of 74
+    mask = O.Mask(block_size=64, group_size=1, chunk_q=74, chunk_k=74, blocks_per_chunk=74,
+                  q_chunk_offset=80, ex_win=3, causal=0, prog_excl=1)
+    check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 1, got=got, block_size=64,
+                    chunk_size=74, causal=False, exclude_window_chunks=3, progressive_exclude=True,
+                    q_chunk_offset=80, blocks_per_chunk=74)
