@@ -24,6 +24,7 @@
 #include "omm_common.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace omm {
 namespace {
@@ -51,9 +52,16 @@ struct RowInfo {
   bool q_clean, do_excl;
 };
 
+// num / den for num >= 0, den >= 1: 32-bit division when num fits (the usual case)
+__device__ __forceinline__ int64_t div_nn(int64_t num, int den) {
+  if (num <= 0xffffffffll)
+    return static_cast<int64_t>(static_cast<uint32_t>(num) / static_cast<uint32_t>(den));
+  return num / den;
+}
+
 __device__ __forceinline__ RowInfo row_info(const MaskDev& m, int g) {
   RowInfo r;
-  r.q_cid = static_cast<int>((static_cast<int64_t>(g) * m.G) / m.chunk_q) + m.qoff;
+  r.q_cid = static_cast<int>(div_nn(static_cast<int64_t>(g) * m.G, m.chunk_q)) + m.qoff;
   if (m.tf) {
     r.q_clean = r.q_cid < m.q_half;
     r.q_rel = r.q_clean ? r.q_cid : r.q_cid - m.q_half;
@@ -346,9 +354,13 @@ template <> __device__ __forceinline__ void unpack<bf16_t>(const uint4& r, float
   }
 }
 template <> __device__ __forceinline__ void unpack<f16_t>(const uint4& r, float* f) {
-  const f16_t* e = reinterpret_cast<const f16_t*>(&r);
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(e[i].v);
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i])));
+    f[2 * i + 1] =
+        static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+  }
 }
 template <> __device__ __forceinline__ void unpack<float>(const uint4& r, float* f) {
   f[0] = __builtin_bit_cast(float, r.x);
@@ -654,9 +666,8 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
 //      the omm_block_pool arithmetic) or loaded as given (pooled mode);
 //   2. S^T = K Qp^T: each wave takes 16-column blocks, K fragments straight from global memory
 //      (no LDS staging), Qp^T fragments held in registers; scores * scale -> LDS;
-//   3. selection, one wave per row: a lane holds its columns' 64-bit keys in registers; theta =
-//      min over 16 (more generally >= topk) lane groups of the group maxima, so at least topk
-//      keys are >= theta; the survivors are compacted and ranked exactly.
+//   3. selection, four rows per wave (one per 16-lane DPP row): a row threshold from the lanes'
+//      two largest candidates, then the survivors are compacted and ranked exactly.
 typedef float m2_f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 m2_bf16x8;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 m2_f16x8;
@@ -678,7 +689,7 @@ template <> struct M2Mfma<f16_t> {
 constexpr int kM2Rows = 16;
 constexpr int kM2Threads = 256;
 constexpr int kM2Waves = kM2Threads / kWave;
-constexpr int kM2SpanCap = 960;   // columns per item: two workgroups' LDS fit a CU
+constexpr int kM2SpanCap = 768;   // columns per item (12 steps of 64 per selecting lane)
 constexpr int kM2Batch = 4;       // 16-column blocks whose K fragments are loaded together
 
 struct M2Args {
@@ -694,19 +705,21 @@ struct M2Args {
   int32_t* out;        // nspan == 1
   uint64_t* part;      // nspan > 1: [B*MG*H][nspan][topk] packed keys
   float* dump;         // optional: the scores, [B, MG, H, NC]
-  uint32_t o_qs, o_sv, o_kc, o_tv;
+  uint32_t o_qs, o_sv, o_tv;
 };
 
-// LDS row pitch of the scores: whole 64-column steps (the selection reads 64 j + 4 l + e) plus
-// 4 floats, which keeps rows 16-byte aligned and off one another's banks
-__host__ __device__ inline int m2_pitch(int span) { return (span + 63) / 64 * 64 + 4; }
+// Column steps of 64 a selecting lane holds (template instances: 4, 8 or 12 for spans up to
+// 256, 512 or 768), and the LDS row pitch of the scores: those whole steps (the selection reads
+// 64 j + 4 l + e for j < JM) plus 4 floats, which keeps rows 16-byte aligned and off one
+// another's banks.
+__host__ __device__ inline int m2_jm(int span) { return span <= 256 ? 4 : span <= 512 ? 8 : 12; }
+__host__ __device__ inline int m2_pitch(int span) { return 64 * m2_jm(span) + 4; }
 
 inline size_t m2_lds_bytes(int span, int D) {
   return static_cast<size_t>(kM2Rows) * m2_pitch(span) * 4         // scores
          + static_cast<size_t>(kM2Rows) * (D + 8) * 2              // rows (16-bit)
          + static_cast<size_t>(kM2Waves) * kSurvCap * 8            // survivors
-         + static_cast<size_t>(kM2Rows) * 32 * 4                   // row thresholds
-         + static_cast<size_t>(span) * 4;                          // column chunk ids
+         + static_cast<size_t>(kM2Rows) * 32 * 4;                  // row thresholds
 }
 
 // Threshold of a wave's keys for a top-k: lanes in groups of gs consecutive lanes, 64 / gs >=
@@ -856,6 +869,15 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
   v = max(v, dpp_u32<0x128>(v));  // row_ror:8
   return v;
 }
+// Row maximum of NaN-free floats (-inf the smallest): float max over the rotated copies.
+__device__ __forceinline__ float row16_max_f(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_u32<0x121>(b)));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_u32<0x122>(__builtin_bit_cast(uint32_t, v))));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_u32<0x124>(__builtin_bit_cast(uint32_t, v))));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_u32<0x128>(__builtin_bit_cast(uint32_t, v))));
+  return v;
+}
 // inclusive prefix sum over the lanes of a 16-lane row (row_shr with zero fill)
 template <int CTRL>
 __device__ __forceinline__ int dpp_shr0(int v) {
@@ -868,105 +890,227 @@ __device__ __forceinline__ int row16_scan(int v) {
   v += dpp_shr0<0x118>(v);  // row_shr:8
   return v;
 }
+// the four rows' values of a per-row quantity (lanes 0, 16, 32, 48), reduced on the scalar unit
+__device__ __forceinline__ int rows4_max(int v) {
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int rows4_min(int v) {
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
 
 constexpr int kRowSurv = kSurvCap / 4;  // survivor slots per row (64)
-constexpr int kMaxJ = 16;               // 64-column steps per row: spans up to 1024 columns
+constexpr float kPosInf = __builtin_huge_valf();
+
+// Visible columns of one row: [lo0, hi0) and [lo1, hi1), disjoint, either possibly empty
+// (lo == hi).  Global columns in the row facts, relative to the item's first column in the
+// selection.
+struct RowCols {
+  int lo0, hi0, lo1, hi1;
+};
+
+// ceil(num / den) for num >= 0, den >= 1: 32-bit division when num fits (the usual case)
+__device__ __forceinline__ int64_t ceil_div_nn(int64_t num, int den) {
+  if (num <= 0xffffffffll) {
+    const uint32_t n32 = static_cast<uint32_t>(num), d32 = static_cast<uint32_t>(den);
+    const uint32_t q = n32 / d32;
+    return static_cast<int64_t>(q) + (n32 - q * d32 != 0u ? 1 : 0);
+  }
+  return (num + den - 1) / den;
+}
+// First column whose chunk id (col_cid) is >= x, clamped to [0, NC].
+__device__ __forceinline__ int chunk_col(const MaskDev& m, int x, int NC) {
+  if (x <= 0) return 0;
+  const int64_t c = m.bpc > 0 ? static_cast<int64_t>(x) * m.bpc
+                              : ceil_div_nn(static_cast<int64_t>(x) * m.chunk_k, m.bs);
+  return c < NC ? static_cast<int>(c) : NC;
+}
+// The visible rule (`visible` above) as at most two intervals of chunk ids, then of columns:
+// the base set is a prefix of the clean chunks (tf: up to the row's own chunk, or the one before
+// for noisy rows; causal: up to the row's chunk; else all), the sink exclusion raises its start,
+// the window exclusion lowers its end, and the second interval is a noisy row's own noisy chunk
+// (tf) or the chunks past a non-causal window.
+__device__ __forceinline__ RowCols row_cols(const MaskDev& m, const RowInfo& r, int NC) {
+  constexpr int kAll = 0x3fffffff;
+  int x0 = 0, y0, x1 = 1, y1 = 0;  // inclusive chunk ids; empty when x > y
+  if (m.tf) {
+    y0 = min(r.q_clean ? r.q_rel : r.q_rel - 1, m.k_half - 1);
+    if (!r.q_clean) x1 = y1 = m.k_half + r.q_rel;
+  } else {
+    y0 = m.causal ? r.q_cid : kAll;
+  }
+  if (r.do_excl) {
+    if (m.ex_sink > 0) x0 = max(x0, m.ex_sink);
+    if (m.ex_win > 0) {
+      if (!m.tf && !m.causal) {
+        x1 = max(x0, r.q_cid + m.ex_win);
+        y1 = y0;
+      }
+      y0 = min(y0, (m.tf ? r.q_rel : r.q_cid) - m.ex_win);
+    }
+  }
+  RowCols c{0, 0, 0, 0};
+  if (x0 <= y0) {
+    c.lo0 = chunk_col(m, x0, NC);
+    c.hi0 = chunk_col(m, y0 + 1, NC);
+  }
+  if (x1 <= y1 && y1 >= 0) {
+    c.lo1 = chunk_col(m, x1, NC);
+    c.hi1 = chunk_col(m, y1 + 1, NC);
+  }
+  if (c.lo0 >= c.hi0) c.lo0 = c.hi0 = 0;
+  if (c.lo1 >= c.hi1) c.lo1 = c.hi1 = 0;
+  return c;
+}
+// a row's intervals relative to column c0 and clipped to [0, n)
+__device__ __forceinline__ RowCols clip_cols(RowCols c, int c0, int n) {
+  RowCols o;
+  o.lo0 = min(max(c.lo0 - c0, 0), n);
+  o.hi0 = min(max(c.hi0 - c0, 0), n);
+  o.lo1 = min(max(c.lo1 - c0, 0), n);
+  o.hi1 = min(max(c.hi1 - c0, 0), n);
+  if (o.lo0 >= o.hi0) o.lo0 = o.hi0 = 0;
+  if (o.lo1 >= o.hi1) o.lo1 = o.hi1 = 0;
+  return o;
+}
+__device__ __forceinline__ bool in_cols(const RowCols& c, int i) {
+  return static_cast<uint32_t>(i - c.lo0) < static_cast<uint32_t>(c.hi0 - c.lo0) ||
+         static_cast<uint32_t>(i - c.lo1) < static_cast<uint32_t>(c.hi1 - c.lo1);
+}
 
 // Top-k (k <= 16) of the four rows r = 4 w + (lane >> 4) of a wave.  Lane (row, l) holds the
-// columns 64 j + 4 l + e (j < ceil(n / 64), e < 4) of its row's LDS scores as ordered high
-// words (0 = not a candidate) and its two largest.  The row threshold theta is the topk-th
-// largest of the row's 32 two-largest values: those are high words of distinct keys, so at
-// least topk keys are >= theta, and every key of the top topk is.  Survivors (>= theta, about
-// 18 for top-16 of random scores) are compacted per row and ranked exactly; a row with more
-// than 64 (massive ties) is reported in `overflow` (bit per row) for the caller to redo.
-template <typename VisF, typename EmitF, typename PadF>
-__device__ __forceinline__ uint32_t rows4_topk(const float* sc, int SP, int n, int c_begin,
-                                               int NC, int topk, bool row_live, int lim,
-                                               bool simple, VisF vis, EmitF emit, PadF pad,
-                                               uint64_t* sv, uint32_t* tv) {
+// columns 64 j + 4 l + e (j < JM, e < 4) of its row's LDS scores; rows hold n <= 64 JM columns
+// at a pitch SP >= 64 JM, so every read stays in its row.  `rc`: the lane's row's visible
+// columns, clipped to [0, n).  The cost is VALU issue (a wave64 instruction takes four cycles),
+// so the per-column work is kept to a handful of instructions:
+//   - 64-column steps that no row of the wave sees are skipped, steps that every row sees in
+//     full take no visibility test, and only the steps at interval edges test each column;
+//   - each lane keeps the two largest of its candidates (m1 >= m2, the new second largest is the
+//     median of m1, m2 and the value); the row threshold theta is the topk-th largest of the
+//     row's 32 values m1, m2, which are scores of distinct columns, so at least topk candidates
+//     are >= theta and every key of the top topk is;
+//   - survivors (>= theta, about 18 for top-16 of random scores) are compacted per row and
+//     ranked exactly.  A row with more than 64 (massive ties) is reported in the returned
+//     overflow bits (bit per row) for the caller to redo.
+template <int JM, typename EmitF, typename PadF>
+__device__ __forceinline__ uint32_t rows4_topk(const float* sc, int SP, int c_begin, int NC,
+                                               int topk, bool row_live, RowCols rc, EmitF emit,
+                                               PadF pad, uint64_t* sv, uint32_t* tv) {
+  using Bits = typename std::conditional<(4 * JM <= 32), uint32_t, uint64_t>::type;
   const int lane = lane_id(), rid = lane >> 4, l16 = lane & 15;
   const float* srow = sc + rid * SP;  // caller offsets sc to the wave's first row
-  const int J = (n + kWave - 1) / kWave;
-  // visibility of the lane's columns 64 j + 4 l16 + e as bit 4 j + e: plain masks see exactly
-  // the columns below `lim`; other masks evaluate the rule once per column in a rolled loop
-  uint64_t vbits = 0ull;
+  // steps [t_lo, t_hi) touch a visible column of some row; [f_lo, f_hi) are inside every row's
+  // first interval (rows past the tile's end constrain neither)
+  int f_lo = 0, f_hi = JM, t_lo = JM, t_hi = 0;
   if (row_live) {
-    if (simple) {
+    const bool e0 = rc.lo0 < rc.hi0, e1 = rc.lo1 < rc.hi1;
+    f_lo = e0 ? (rc.lo0 + 63) >> 6 : JM;
+    f_hi = e0 ? rc.hi0 >> 6 : 0;
+    if (e0) { t_lo = rc.lo0 >> 6; t_hi = (rc.hi0 + 63) >> 6; }
+    if (e1) { t_lo = min(t_lo, rc.lo1 >> 6); t_hi = max(t_hi, (rc.hi1 + 63) >> 6); }
+  }
+  const int F_lo = rows4_max(f_lo), F_hi = rows4_min(f_hi);
+  const int T_lo = rows4_min(t_lo), T_hi = rows4_max(t_hi);
+  // every read is issued before any is used
+  float4 x4[JM];
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
-        const int k = min(max(lim - (kWave * j + 4 * l16), 0), 4);
-        vbits |= static_cast<uint64_t>((1u << k) - 1u) << (4 * j);
-      }
+  for (int j = 0; j < JM; ++j) x4[j] = *reinterpret_cast<const float4*>(srow + kWave * j + 4 * l16);
+  // candidates' scores (-inf for invisible columns) and the lane's two largest.  NaN scores
+  // stay as they are: v_med3_f32 with a NaN operand returns the minimum of the others, so
+  // med3(m1, m2, NaN) = m2 and med3(m1, NaN, +inf) = m1, and NaN >= thr is false below.
+  float xv[JM][4];
+  float m1 = kNegInf, m2 = kNegInf;
+  // +inf the compiler cannot see: med3(m1, x, +inf) would otherwise become a maxnum, which in
+  // IEEE mode costs a canonicalising max per operand
+  float pinf = kPosInf;
+  __asm__("" : "+v"(pinf));
+#pragma unroll
+  for (int j = 0; j < JM; ++j) {
+    const float xs[4] = {x4[j].x, x4[j].y, x4[j].z, x4[j].w};
+    if (j < T_lo || j >= T_hi) {  // wave-uniform: no row sees this step
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[j][e] = kNegInf;
+      continue;
+    }
+    if (j < F_lo || j >= F_hi) {  // wave-uniform: an interval edge in some row
+      __asm__ volatile("" ::: "memory");  // keeps the test off the steps that need none
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[j][e] = in_cols(rc, kWave * j + 4 * l16 + e) ? xs[e] : kNegInf;
     } else {
-#pragma nounroll
-      for (int t = 0; t < 4 * J; ++t) {
-        const int i = kWave * (t >> 2) + 4 * l16 + (t & 3);
-        if (i < n && vis(i)) vbits |= 1ull << t;
-      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[j][e] = xs[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m2 = __builtin_amdgcn_fmed3f(m1, m2, xv[j][e]);
+      m1 = __builtin_amdgcn_fmed3f(m1, xv[j][e], pinf);
     }
   }
-  uint32_t hv[kMaxJ][4];
-  uint32_t m1 = 0, m2 = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
-    if (j < J) {
-      const float4 x = *reinterpret_cast<const float4*>(srow + kWave * j + 4 * l16);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool cand = ((vbits >> (4 * j + e)) & 1ull) != 0ull && xs[e] > kNegInf;
-        const uint32_t hi = cand ? f32_ord(xs[e]) : 0u;
-        hv[j][e] = hi;
-        m2 = max(m2, min(m1, hi));
-        m1 = max(m1, hi);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hv[j][e] = 0u;
-    }
-  }
-  // theta: the topk-th largest of the row's 32 values m1, m2 (0 when fewer are non-zero)
-  uint32_t* trow = tv + rid * 32;
+  // theta: the topk-th largest of the row's 32 values m1, m2 (-inf when fewer are finite)
+  float* trow = reinterpret_cast<float*>(tv + rid * 32);
   trow[2 * l16] = m1;
   trow[2 * l16 + 1] = m2;
   wave_lds_sync();
   int c1 = 0, c2 = 0;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const uint4 t4 = reinterpret_cast<const uint4*>(trow)[q];
+    const float4 t4 = reinterpret_cast<const float4*>(trow)[q];
     c1 += (t4.x >= m1) + (t4.y >= m1) + (t4.z >= m1) + (t4.w >= m1);
     c2 += (t4.x >= m2) + (t4.y >= m2) + (t4.z >= m2) + (t4.w >= m2);
   }
-  uint32_t theta = row16_max(max(c1 >= topk ? m1 : 0u, c2 >= topk ? m2 : 0u));
-  if (theta == 0u) theta = 1u;  // fewer than topk values: every candidate survives
-  uint64_t sbits = 0ull;  // survivors, bit 4 j + e
+  const float theta = row16_max_f(fmaxf(c1 >= topk ? m1 : kNegInf, c2 >= topk ? m2 : kNegInf));
+  // x >= thr is "x >= theta and a candidate": with theta = -inf every candidate passes, and
+  // -inf / NaN never do
+  const float thr = fmaxf(theta, -__FLT_MAX__);
+  // survivors, bit 4 j + e: 32-bit words built as w = 2 w + (x >= thr), highest bit first
+  uint32_t sw[(JM + 7) / 8];
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j)
+  for (int q = 0; q < (JM + 7) / 8; ++q) {
+    uint32_t v = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (hv[j][e] >= theta) sbits |= 1ull << (4 * j + e);
-  const int cnt = popc64(sbits);
+    for (int t = (4 * JM - 1 < 32 * q + 31 ? 4 * JM - 1 : 32 * q + 31); t >= 32 * q; --t)
+      v = v + v + (xv[t >> 2][t & 3] >= thr ? 1u : 0u);
+    sw[q] = row_live ? v : 0u;
+  }
+  Bits sbits = sw[0];
+  if constexpr (JM > 8) sbits |= static_cast<Bits>(sw[(JM + 7) / 8 - 1]) << 32;
+  const int cnt = __builtin_popcountll(static_cast<uint64_t>(sbits));
   const int incl = row16_scan(cnt);
   int pos = incl - cnt;
   // row totals: lane 15 of each row
   const int t0 = __builtin_amdgcn_readlane(incl, 15), t1 = __builtin_amdgcn_readlane(incl, 31);
   const int t2 = __builtin_amdgcn_readlane(incl, 47), t3 = __builtin_amdgcn_readlane(incl, 63);
   const int ns = rid == 0 ? t0 : rid == 1 ? t1 : rid == 2 ? t2 : t3;
+  const int nmax = max(max(t0 > kRowSurv ? 0 : t0, t1 > kRowSurv ? 0 : t1),
+                       max(t2 > kRowSurv ? 0 : t2, t3 > kRowSurv ? 0 : t3));
   uint64_t* srv = sv + rid * kRowSurv;
   wave_lds_sync();  // the threshold buffer may be reused by the caller's next rows
-  // write the set bits' keys (a lane holds a handful): re-read each survivor's score
-  while (sbits != 0ull) {
-    const int t = __builtin_ctzll(sbits);
-    sbits &= sbits - 1ull;
-    const int i = kWave * (t >> 2) + 4 * l16 + (t & 3);
-    if (pos < kRowSurv) srv[pos] = make_key(srow[i], c_begin + i, NC);
-    ++pos;
+  // write the survivors' keys, two per round (a lane holds a handful): re-read their scores
+  while (sbits != 0) {
+    const int ta = __builtin_ctzll(static_cast<uint64_t>(sbits));
+    sbits &= sbits - 1;
+    const bool hb = sbits != 0;
+    const int tb = hb ? __builtin_ctzll(static_cast<uint64_t>(sbits)) : ta;
+    if (hb) sbits &= sbits - 1;
+    const int ia = kWave * (ta >> 2) + 4 * l16 + (ta & 3);
+    const int ib = kWave * (tb >> 2) + 4 * l16 + (tb & 3);
+    const float xa = srow[ia], xb = srow[ib];
+    if (pos < kRowSurv) srv[pos] = make_key(xa, c_begin + ia, NC);
+    if (hb && pos + 1 < kRowSurv) srv[pos + 1] = make_key(xb, c_begin + ib, NC);
+    pos += hb ? 2 : 1;
+  }
+  // zeros after a row's survivors up to the wave's read bound (groups of 8): 0 outranks nothing
+  const int lim8 = (nmax + 7) & ~7;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int p = ns + l16 + 16 * q;
+    if (ns <= kRowSurv && p < lim8) srv[p] = 0ull;
   }
   wave_lds_sync();
   const uint32_t over = static_cast<uint32_t>(ns > kRowSurv);
   const int nsr = ns > kRowSurv ? 0 : ns;  // an overflowing row is left to the caller
-  const int nmax = max(max(t0 > kRowSurv ? 0 : t0, t1 > kRowSurv ? 0 : t1),
-                       max(t2 > kRowSurv ? 0 : t2, t3 > kRowSurv ? 0 : t3));
   const int M = (nmax + 15) / 16;  // survivors per lane to rank (wave-uniform, <= 4)
   // rank: lane takes survivors l16, l16 + 16, l16 + 32, l16 + 48 of its row
   uint64_t mine[4];
@@ -976,13 +1120,17 @@ __device__ __forceinline__ uint32_t rows4_topk(const float* sc, int SP, int n, i
     mine[m] = (m < M && 16 * m + l16 < nsr) ? srv[16 * m + l16] : ~0ull;
     rank[m] = 0;
   }
-  for (int i = 0; i < nmax; i += 2) {  // wave-uniform bound; entries past a row's count are 0
-    const ulonglong2 w2 = *reinterpret_cast<const ulonglong2*>(srv + i);
-    const uint64_t a = i < nsr ? w2.x : 0ull, b = i + 1 < nsr ? w2.y : 0ull;
-    rank[0] += (a > mine[0] ? 1 : 0) + (b > mine[0] ? 1 : 0);
-    if (M > 1) rank[1] += (a > mine[1] ? 1 : 0) + (b > mine[1] ? 1 : 0);
-    if (M > 2) rank[2] += (a > mine[2] ? 1 : 0) + (b > mine[2] ? 1 : 0);
-    if (M > 3) rank[3] += (a > mine[3] ? 1 : 0) + (b > mine[3] ? 1 : 0);
+  for (int i0 = 0; i0 < nmax; i0 += 8) {  // wave-uniform
+    ulonglong2 w8[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w8[q] = *reinterpret_cast<const ulonglong2*>(srv + i0 + 2 * q);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m < M) rank[m] += (w8[q].x > mine[m] ? 1 : 0) + (w8[q].y > mine[m] ? 1 : 0);
+      }
+    }
   }
 #pragma unroll
   for (int m = 0; m < 4; ++m)
@@ -995,18 +1143,33 @@ __device__ __forceinline__ uint32_t rows4_topk(const float* sc, int SP, int n, i
                                ((ob >> 45) & 8ull));
 }
 
-// Row facts of a 16-row tile, one row per lane (lanes >= 16 repeat them): 4 words each.
-struct RowFacts {
-  int q_cid, q_rel, flags, ub;  // flags: bit 0 q_clean, bit 1 do_excl
-};
+// rows4_topk for a score pitch SP = m2_pitch(span): the instance whose JM the pitch was built for
+template <typename EmitF, typename PadF>
+__device__ __forceinline__ uint32_t rows4_topk_sp(const float* sc, int SP, int c_begin, int NC,
+                                                  int topk, bool row_live, RowCols rc,
+                                                  EmitF emit, PadF pad, uint64_t* sv,
+                                                  uint32_t* tv) {
+  if (SP <= 64 * 4 + 4)
+    return rows4_topk<4>(sc, SP, c_begin, NC, topk, row_live, rc, emit, pad, sv, tv);
+  if (SP <= 64 * 8 + 4)
+    return rows4_topk<8>(sc, SP, c_begin, NC, topk, row_live, rc, emit, pad, sv, tv);
+  return rows4_topk<12>(sc, SP, c_begin, NC, topk, row_live, rc, emit, pad, sv, tv);
+}
 
+// One workgroup per (b, h, column span, 16-row tile):
+//   1. the rows' first loads (fused: the first 16 tokens of each query group; else the pooled
+//      rows) and this wave's first K fragments are issued before anything else, then the row
+//      facts (visible column intervals) are worked out while they are in flight;
+//   2. query-group pooling (fp32 sum in token order, one divide, one rounding) -> LDS;
+//   3. S^T = K Qp^T on MFMA, K fragments straight from global memory -> scores * scale in LDS;
+//   4. selection: wave w owns rows 4 w .. 4 w + 3, one per 16-lane DPP row.
 template <typename T, int D, bool FUSED>
 __global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int SD = D / 32;      // MFMA k-steps
   constexpr int CH = D / 8;       // 16-byte slices per row
   constexpr int QP = D + 8;       // LDS row pitch of the pooled rows (elements)
-  __shared__ RowFacts facts[kM2Rows];
+  __shared__ RowCols facts[kM2Rows];
   const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
   const int total = static_cast<int>(gridDim.x);
@@ -1017,80 +1180,97 @@ __global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
   const int h = it % a.H;
   const int b = it / a.H;
   const int row0 = rt * kM2Rows;
-  const MaskDev& mk = a.mk;
   const int SP = m2_pitch(a.span);
+  const int c_begin = sp * a.span;
 
   float* sc = reinterpret_cast<float*>(smem);
   uint16_t* qs = reinterpret_cast<uint16_t*>(smem + a.o_qs);
   uint64_t* sv = reinterpret_cast<uint64_t*>(smem + a.o_sv);
-  int* kc = reinterpret_cast<int*>(smem + a.o_kc);
 
-  // ---- 0. row facts, lane r -> row row0 + r; the tile's column bound by a wave max ----
-  int ub;
-  {
-    const int g = row0 + l16;
-    const RowInfo ri = row_info(mk, g);
-    const int rub = g < a.MG ? row_ub(mk, ri, a.NC) : 0;
-    if (w == 0 && lane < kM2Rows)
-      facts[lane] = RowFacts{ri.q_cid, ri.q_rel, (ri.q_clean ? 1 : 0) | (ri.do_excl ? 2 : 0), rub};
-    ub = rub;
-    for (int m = 1; m < 16; m <<= 1) ub = max(ub, __shfl_xor(ub, m, kWave));
+  // ---- 1. first loads ----
+  const T* qp = static_cast<const T*>(a.q);
+  const int pr = tid / CH, pu = tid - pr * CH, pg = row0 + pr;  // pooling: row, 16-byte slice
+  const bool pooler = tid < kM2Rows * CH && pg < a.MG;
+  const T* qbase = qp + b * a.qs0 + h * a.qs2 + pu * 8;
+  int t0 = 0, t1 = 0;
+  uint4 rr[16];
+  bool first = false;
+  if constexpr (FUSED) {
+    t0 = pg * a.G;
+    t1 = min(t0 + a.G, a.T_len);
+    first = pooler && t0 + 16 <= t1;
+    if (first) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        rr[j] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(t0 + j) * a.qs1);
+    }
+  } else {
+    if (pooler) rr[0] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(pg) * a.qs1);
   }
-  const int c_begin = sp * a.span;
-  const int c_end = min(c_begin + a.span, ub);
-  const int n = max(0, c_end - c_begin);
-  const int nblk = (n + 15) / 16;
-  const bool simple = !mk.tf && mk.ex_sink <= 0 && mk.ex_win <= 0;
-
-  // this wave's first batch of K fragments, in flight during the row pooling
+  // this wave's first batch of K fragments (columns clamped in bounds; unused ones are dropped)
   const T* kp = static_cast<const T*>(a.k) + b * a.ks0 + h * a.ks2;
-  uint4 kf[kM2Batch][SD];
-  auto load_k = [&](int cb0) {
+  // a wave's batches are kM2Stride blocks apart.  The first is issued now and is in flight
+  // during the pooling; the second (when the span has one) once this thread's query loads are
+  // all issued, so that K's L2 traffic does not take miss slots from the HBM-bound pooling but
+  // is in flight across the barrier
+  constexpr int kM2Stride = kM2Waves * kM2Batch;
+  uint4 kf0[kM2Batch][SD], kf1[kM2Batch][SD];
+  auto load_k = [&](uint4 (&kf)[kM2Batch][SD], int cb0) {
 #pragma unroll
     for (int x = 0; x < kM2Batch; ++x) {
-      const int col = min(c_begin + (cb0 + x) * 16 + l16, a.NC - 1);  // in bounds
+      const int col = min(c_begin + (cb0 + x) * 16 + l16, a.NC - 1);
 #pragma unroll
       for (int s = 0; s < SD; ++s)
         kf[x][s] = *reinterpret_cast<const uint4*>(kp + static_cast<int64_t>(col) * a.ks1 +
                                                    32 * s + 8 * j4);
     }
   };
-  if (w * kM2Batch < nblk) load_k(w * kM2Batch);
+  const bool pre1 = a.span > 16 * kM2Stride;  // wave-uniform
+  load_k(kf0, w * kM2Batch);
 
-  // ---- 1. rows -> LDS ----
-  const T* qp = static_cast<const T*>(a.q);
+  // row facts, lane l16 -> row row0 + l16; the tile's column bound by a row maximum
+  int ub;
+  {
+    const int g = row0 + l16;
+    RowCols rc{0, 0, 0, 0};
+    if (g < a.MG) rc = row_cols(a.mk, row_info(a.mk, g), a.NC);
+    if (w == 0 && lane < kM2Rows) facts[lane] = rc;
+    ub = static_cast<int>(row16_max(static_cast<uint32_t>(max(rc.hi0, rc.hi1))));
+    ub = __builtin_amdgcn_readfirstlane(ub);  // rows 0-15 in every 16-lane row: wave-uniform
+  }
+  const int c_end = min(c_begin + a.span, ub);
+  const int n = max(0, c_end - c_begin);
+  const int nblk = (n + 15) / 16;
+
+  // ---- 2. rows -> LDS ----
   if (tid < kM2Rows * CH) {
-    const int r = tid / CH, u = tid - r * CH, g = row0 + r;
     uint4 val = make_uint4(0, 0, 0, 0);
-    if (g < a.MG) {
+    if (pooler) {
       if constexpr (FUSED) {
         constexpr int V = 8;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-        const int t0 = g * a.G, t1 = min(t0 + a.G, a.T_len);
-        const T* base = qp + b * a.qs0 + h * a.qs2 + u * V;
-        int t = t0;
-        for (; t + 16 <= t1; t += 16) {
-          uint4 rr[16];
-#pragma unroll
-          for (int j = 0; j < 16; ++j)
-            rr[j] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t + j) * a.qs1);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            float f[V];
-            unpack<T>(rr[j], f);
-#pragma unroll
-            for (int i = 0; i < V; ++i) acc[i] += f[i];
-          }
-        }
-        for (; t < t1; ++t) {
-          const uint4 rr = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(t) * a.qs1);
+        auto add = [&](const uint4& x) {
           float f[V];
-          unpack<T>(rr, f);
+          unpack<T>(x, f);
 #pragma unroll
           for (int i = 0; i < V; ++i) acc[i] += f[i];
+        };
+        int t = t0;
+        if (first) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) add(rr[j]);
+          t += 16;
         }
+        for (; t + 16 <= t1; t += 16) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            rr[j] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(t + j) * a.qs1);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) add(rr[j]);
+        }
+        for (; t < t1; ++t) add(*reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(t) * a.qs1));
         const float cnt = static_cast<float>(t1 - t0);
         uint16_t bits[V];
 #pragma unroll
@@ -1103,22 +1283,20 @@ __global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
                          bits[4] | (static_cast<uint32_t>(bits[5]) << 16),
                          bits[6] | (static_cast<uint32_t>(bits[7]) << 16));
       } else {
-        val = *reinterpret_cast<const uint4*>(qp + b * a.qs0 + g * a.qs1 + h * a.qs2 + u * 8);
+        val = rr[0];
       }
     }
-    *reinterpret_cast<uint4*>(qs + r * QP + u * 8) = val;
+    *reinterpret_cast<uint4*>(qs + pr * QP + pu * 8) = val;
   }
-  if (!simple)
-    for (int i = tid; i < n; i += kM2Threads) kc[i] = col_cid(mk, c_begin + i);
+  if (pre1) load_k(kf1, w * kM2Batch + kM2Stride);
   __syncthreads();
 
-  // ---- 2. S^T = K Qp^T on MFMA -> LDS ----
+  // ---- 3. S^T = K Qp^T on MFMA -> LDS ----
   uint4 qb[SD];
 #pragma unroll
   for (int s = 0; s < SD; ++s)
     qb[s] = *reinterpret_cast<const uint4*>(qs + l16 * QP + 32 * s + 8 * j4);
-  for (int cb0 = w * kM2Batch; cb0 < nblk; cb0 += kM2Waves * kM2Batch) {
-    if (cb0 != w * kM2Batch) load_k(cb0);
+  auto mfma_batch = [&](const uint4 (&kf)[kM2Batch][SD], int cb0) {
 #pragma unroll
     for (int x = 0; x < kM2Batch; ++x) {
       if (cb0 + x >= nblk) break;  // wave-uniform
@@ -1138,17 +1316,23 @@ __global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
           if (c + e < n) d[c_begin + c + e] = vv[e];
       }
     }
+  };
+  for (int cb0 = w * kM2Batch; cb0 < nblk; cb0 += 2 * kM2Stride) {
+    if (cb0 != w * kM2Batch) load_k(kf0, cb0);
+    mfma_batch(kf0, cb0);
+    const int cb1 = cb0 + kM2Stride;
+    if (cb1 >= nblk) break;
+    if (cb0 != w * kM2Batch || !pre1) load_k(kf1, cb1);
+    mfma_batch(kf1, cb1);
   }
   __syncthreads();
 
-  // ---- 3. selection: wave w owns rows 4 w .. 4 w + 3, one per 16-lane DPP row ----
+  // ---- 4. selection: wave w owns rows 4 w .. 4 w + 3, one per 16-lane DPP row ----
   uint64_t* wsv = sv + w * kSurvCap;
   uint32_t* wtv = reinterpret_cast<uint32_t*>(smem + a.o_tv) + w * 128;
   const int NC = a.NC;
   const int r = 4 * w + (lane >> 4), g = row0 + r;
-  const RowFacts f = facts[r];
-  const RowInfo ri{f.q_cid, f.q_rel, (f.flags & 1) != 0, (f.flags & 2) != 0};
-  const int rub = f.ub - c_begin;
+  const RowCols rc = clip_cols(facts[r], c_begin, n);
   const int64_t orow = (static_cast<int64_t>(b) * a.MG + g) * a.H + h;
   auto emit_at = [&](int64_t orow_, int rank, uint64_t kk) {
     if (a.nspan == 1) a.out[orow_ * a.topk + rank] = key_id(kk, NC);
@@ -1158,29 +1342,21 @@ __global__ __launch_bounds__(kM2Threads, 2) void topk_mfma_kernel(M2Args a) {
     if (a.nspan == 1) a.out[orow_ * a.topk + p] = -1;
     else a.part[(orow_ * a.nspan + sp) * a.topk + p] = 0ull;
   };
-  uint32_t over;
-  {
-    auto vis = [&](int i) { return simple ? (i < rub) : visible(mk, ri, kc[i]); };
-    over = rows4_topk(sc + 4 * w * SP, SP, n, c_begin, NC, a.topk, g < a.MG, min(rub, n), simple,
-                      vis,
-                      [&](int, int rank, uint64_t kk) { emit_at(orow, rank, kk); },
-                      [&](int, int p) { pad_at(orow, p); }, wsv, wtv);
-  }
+  uint32_t over = rows4_topk_sp(
+      sc + 4 * w * SP, SP, c_begin, NC, a.topk, g < a.MG, rc,
+      [&](int, int rank, uint64_t kk) { emit_at(orow, rank, kk); },
+      [&](int, int p) { pad_at(orow, p); }, wsv, wtv);
   // rows with more than 64 survivors (massive ties): the whole wave redoes them one at a time
   while (over != 0u) {
-    const int rr = __builtin_ctz(over);
+    const int rr2 = __builtin_ctz(over);
     over &= over - 1u;
-    const int r2 = 4 * w + rr, g2 = row0 + r2;
-    const RowFacts f2 = facts[r2];
-    const RowInfo ri2{f2.q_cid, f2.q_rel, (f2.flags & 1) != 0, (f2.flags & 2) != 0};
-    const int rub2 = f2.ub - c_begin;
+    const int r2 = 4 * w + rr2, g2 = row0 + r2;
+    const RowCols rc2 = clip_cols(facts[r2], c_begin, n);
     const int64_t orow2 = (static_cast<int64_t>(b) * a.MG + g2) * a.H + h;
-    auto vis2 = [&](int i) { return simple ? (i < rub2) : visible(mk, ri2, kc[i]); };
-    row_topk_lds(sc + r2 * SP, n, c_begin, NC, a.topk, vis2,
+    row_topk_lds(sc + r2 * SP, n, c_begin, NC, a.topk, [&](int i) { return in_cols(rc2, i); },
                  [&](int rank, uint64_t kk) { emit_at(orow2, rank, kk); },
                  [&](int p) { pad_at(orow2, p); }, wsv);
   }
-  (void)lane;
 }
 
 // ---- host planning ---------------------------------------------------------------------------
@@ -1389,7 +1565,6 @@ int launch_m2_typed(M2Args a, int64_t B, int64_t H, const M2Plan& p, hipStream_t
   a.o_qs = static_cast<uint32_t>(align16(static_cast<size_t>(kM2Rows) * m2_pitch(p.span) * 4));
   a.o_sv = static_cast<uint32_t>(align16(a.o_qs + static_cast<size_t>(kM2Rows) * (D + 8) * 2));
   a.o_tv = static_cast<uint32_t>(a.o_sv + static_cast<size_t>(kM2Waves) * kSurvCap * 8);
-  a.o_kc = static_cast<uint32_t>(a.o_tv + static_cast<size_t>(kM2Rows) * 32 * 4);
   const int64_t items = B * H * p.nspan * p.rtiles;
   OMM_REQUIRE(items <= 2147483647ll, OMM_EUNSUPPORTED, "top-k: grid too large");
   topk_mfma_kernel<T, D, FUSED><<<static_cast<unsigned>(items), kM2Threads, lds, s>>>(a);

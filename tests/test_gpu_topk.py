@@ -231,3 +231,103 @@ def test_topk_prepooled_op_long_history_split_merge():
     check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 1, got=got, block_size=64,
                     chunk_size=74, causal=False, exclude_window_chunks=3, progressive_exclude=True,
                     q_chunk_offset=80, blocks_per_chunk=74)
+
+
+def test_topk_fused_massive_ties_bitexact():
+    """Score ties far beyond the survivor buffer (keys of heads 0-1 all zero: every score is 0,
+    the top-16 are the 16 lowest visible ids; heads 2-7 keys in {-1, 0, 1} / 8): rows with more
+    than 64 survivors take the one-row fallback."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(37)
+    q = torch.randn((1, 32768, 8, 128), generator=g).to(torch.bfloat16)
+    k = (torch.randint(-1, 2, (1, 512, 8, 128), generator=g).float() / 8).to(torch.bfloat16)
+    k[:, :, :2] = 0
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, block_size=64, chunk_size=4680,
+                            causal=True, group_size=64).cpu().numpy()
+    mask = O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, causal=1)
+    check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 64, got=got, block_size=64,
+                    chunk_size=4680, causal=True)
+    assert (got[:, :, :2] == np.arange(16)).all()  # all-zero scores: the lowest ids
+
+
+# Mask modes on the MFMA path's four-rows-per-wave selection, whose visibility is a pair of
+# column intervals per row (one visible run, plus a noisy row's own noisy chunk under tf_mask or
+# the chunks past a non-causal exclusion window).  Each case is (T, NC, H, D, G, topk, facade
+# keyword arguments); together they take spans of 4, 8 and 12 column steps, the fused and the
+# pool-to-workspace kernels, column splits with the merge, and every interval shape.
+MFMA_MASK_CASES = {
+    "tf": (1024, 64, 2, 64, 16, 8, dict(block_size=16, chunk_size=128, causal=True,
+                                        tf_mask=True)),
+    "tf_sink_win_prog": (2048, 128, 2, 128, 16, 16,
+                         dict(block_size=16, chunk_size=128, causal=True, tf_mask=True,
+                              exclude_sink_chunks=1, exclude_window_chunks=2,
+                              progressive_exclude=True)),
+    "sink_win_causal": (3000, 100, 2, 128, 30, 16,
+                        dict(block_size=30, chunk_size=600, causal=True, exclude_sink_chunks=1,
+                             exclude_window_chunks=2, progressive_exclude=True)),
+    "window_two_runs": (2048, 128, 2, 64, 16, 16,
+                        dict(block_size=16, chunk_size=256, causal=False,
+                             exclude_window_chunks=2)),
+    "window_two_runs_offset": (4680, 740, 3, 128, 64, 16,
+                               dict(block_size=64, chunk_size=4680, causal=False,
+                                    exclude_window_chunks=2, q_chunk_offset=4,
+                                    blocks_per_chunk=74)),
+    "noncausal_jm12_fused": (4096, 700, 16, 64, 16, 16,
+                             dict(block_size=64, chunk_size=4096, causal=False)),
+    "noncausal_split_merge": (300, 2000, 2, 128, 1, 16,
+                              dict(block_size=64, chunk_size=300, causal=False)),
+    "causal_ragged_small_topk": (4680, 512, 4, 128, 64, 3,
+                                 dict(block_size=64, chunk_size=4680, causal=True)),
+}
+
+
+def _oracle_mask(T, NC, G, kw):
+    chunk = kw["chunk_size"]
+    bs = kw["block_size"]
+    tf = bool(kw.get("tf_mask", False))
+    MG = -(-T // G)
+    return O.Mask(block_size=bs, group_size=G, chunk_q=chunk, chunk_k=chunk,
+                  blocks_per_chunk=kw.get("blocks_per_chunk", 0),
+                  q_chunk_offset=kw.get("q_chunk_offset", 0),
+                  q_half=(MG * G) // (2 * chunk) if tf else 0,
+                  k_half=(NC * bs) // (2 * chunk) if tf else 0,
+                  ex_win=kw.get("exclude_window_chunks", 0),
+                  ex_sink=kw.get("exclude_sink_chunks", 0), causal=int(kw["causal"]),
+                  tf_mask=int(tf), prog_excl=int(kw.get("progressive_exclude", False)))
+
+
+@pytest.mark.parametrize("case", list(MFMA_MASK_CASES))
+def test_mfma_selection_mask_modes(case):
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    T, NC, H, D, G, topk, kw = MFMA_MASK_CASES[case]
+    g = torch.Generator().manual_seed(zlib.crc32(case.encode()) & 0xFFFF)
+    q = _bf16((1, T, H, D), g)
+    k = _bf16((1, NC, H, D), g)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), topk, group_size=G, **kw).cpu().numpy()
+    check_mfma_topk(q.to(DEV), k.to(DEV), topk, _oracle_mask(T, NC, G, kw), D ** -0.5, G,
+                    got=got, **kw)
+
+
+def test_mfma_selection_nan_and_inf_scores():
+    """Keys holding NaN or +-inf give NaN / +-inf scores: NaN and -inf are never selected, +inf
+    wins (cuda_backend/csrc/topk.cu:36-102).  The selection keeps NaN out of its running maxima
+    through v_med3_f32's NaN rule; this pins that on the device."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(91)
+    T, NC, H, D, G = 2048, 300, 2, 128, 16
+    q = _bf16((1, T, H, D), g)
+    k = _bf16((1, NC, H, D), g)
+    k[0, 5::7, 0, 3] = float("nan")
+    k[0, 11::13, 1, 0] = float("inf")
+    k[0, 2::17, :, 1] = float("-inf")
+    kw = dict(block_size=16, chunk_size=T, causal=False)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, group_size=G, **kw).cpu().numpy()
+    mask = _oracle_mask(T, NC, G, kw)
+    # the score bound of check_mfma_topk is meaningless for non-finite scores: compare the
+    # indices with the oracle's selection on the kernel's own scores only
+    from omnimem_amd.index_topk import parallel_nsa_topk_with_scores
+    ids, sc = parallel_nsa_topk_with_scores(q.to(DEV), k.to(DEV), 16, group_size=G, **kw)
+    sc = sc.cpu().numpy()
+    assert np.isnan(sc).any() and np.isposinf(sc).any() and np.isneginf(sc).any()
+    np.testing.assert_array_equal(ids.cpu().numpy(), got)
+    np.testing.assert_array_equal(got, O.topk_select(sc, 16, mask))
