@@ -230,7 +230,9 @@ int omm_build_ptr_table(const omm_view4* ids, const int64_t* base_k, const int64
                         int32_t blocks_per_chunk, int64_t in_chunk_block_bytes, int64_t* ptr_k,
                         int64_t* ptr_v, void* stream);
 /* bf16 only.  ptr tables: int64 [B, MG, H, T] with element strides ptr_stride; a block is
- * block_size full rows at (address + r*stride_bn + d*stride_bd) elements; 0 = skip. */
+ * block_size full rows at (address + r*stride_bn + d*stride_bd) elements; 0 = skip.  Any
+ * 2-byte-aligned address is accepted: blocks that are not 16-byte aligned are detected per
+ * block on the device and read with 2-byte loads (slower, same result). */
 int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr_v,
                     const int64_t* ptr_stride, int64_t T, int32_t block_size, int32_t group_size,
                     int64_t stride_bn, int64_t stride_bd, float scale, const omm_view4* out,

@@ -52,6 +52,7 @@ struct BlockRef {
 // order, so concurrent rows that share blocks tend to read them at the same time).
 template <typename T>
 struct DenseAcc {
+  static constexpr bool kMayMisalign = false;  // 16-byte rows checked on the host
   using KV = T;
   struct Ent {
     int t0, n;  // first token, visible tokens
@@ -87,6 +88,9 @@ struct DenseAcc {
 
 struct PtrAcc {
   using KV = bf16_t;
+  // raw caller addresses: any 2-byte alignment is accepted (the reference's contract), so the
+  // staging checks each block and copies misaligned ones with 2-byte loads
+  static constexpr bool kMayMisalign = true;
   struct Ent {
     int64_t k, v;  // raw addresses (0 = skip)
     int n;
@@ -127,6 +131,7 @@ template <> struct PagedEntOf<uint8_t> { using type = PagedEnt8; };
 
 template <typename KVT>
 struct PagedAcc {
+  static constexpr bool kMayMisalign = false;  // 16-byte rows checked on the host
   using KV = KVT;
   using Ent = typename PagedEntOf<KVT>::type;
   const KVT* pool_k;
@@ -430,6 +435,41 @@ __device__ __forceinline__ void dma_part(const void* base, int rsb, int nrows, c
   }
 }
 #pragma clang diagnostic pop
+
+// dma_part's copy for a block whose address is not 16-byte aligned: the same LDS bytes (rows past
+// nrows as 0), through 2-byte loads and ordinary LDS stores.
+template <int NI>
+__device__ __forceinline__ void copy_part_u16(const void* base, int rsb, int nrows, char* dst,
+                                              int w, const int (&off)[NI]) {
+  const int lim = nrows * rsb;
+  const int lane = lane_id();
+#pragma unroll
+  for (int jj = 0; jj < NI; ++jj) {
+    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+    if (off[jj] < lim) {
+      const uint16_t* p = reinterpret_cast<const uint16_t*>(static_cast<const char*>(base) + off[jj]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        wd[i] = static_cast<uint32_t>(p[2 * i]) | (static_cast<uint32_t>(p[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(dst + 1024 * (NI * w + jj) + 16 * lane) =
+        make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+}
+
+// One wave's part of a K or V tile copy: LDS DMA, or the 2-byte copy for a misaligned block of an
+// accessor that admits them (wave-uniform test; every wave of the workgroup copies the same block).
+template <typename Acc, int NI>
+__device__ __forceinline__ void copy_part(const void* base, int rsb, int nrows, char* dst, int w,
+                                          const int (&off)[NI]) {
+  if constexpr (Acc::kMayMisalign) {
+    if ((reinterpret_cast<uintptr_t>(base) & 15u) != 0u) {
+      copy_part_u16<NI>(base, rsb, nrows, dst, w, off);
+      return;
+    }
+  }
+  dma_part<NI>(base, rsb, nrows, dst, w, off);
+}
 
 }  // namespace
 }  // namespace omm

@@ -85,14 +85,32 @@ struct Stager {
 
   // Rows at or past n are not loaded: their registers keep finite values from an earlier tile
   // (or the initial zeros).  Their scores are masked to -inf, so their V rows get weight 0.
+  // MIS: the accessor admits blocks that are not 16-byte aligned (raw pointer tables); such a
+  // block is read with 2-byte loads (wave-uniform test on the block's addresses).
+  template <bool MIS = false>
   __device__ __forceinline__ void load(const BlockRef& br, int tok0, int n, int tid) {
+    if constexpr (MIS) {
+      if (((reinterpret_cast<uintptr_t>(br.k) | reinterpret_cast<uintptr_t>(br.v)) & 15u) != 0u) {
+        load_impl<false, true>(br, tok0, n, tid);
+        return;
+      }
+    }
     if (n >= 64)
       load_impl<true>(br, tok0, n, tid);
     else
       load_impl<false>(br, tok0, n, tid);
   }
 
-  template <bool FULL>
+  __device__ __forceinline__ static uint4 load_u16(const char* p) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    uint32_t wd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      wd[i] = static_cast<uint32_t>(h[2 * i]) | (static_cast<uint32_t>(h[2 * i + 1]) << 16);
+    return make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+
+  template <bool FULL, bool U16 = false>
   __device__ __forceinline__ void load_impl(const BlockRef& br, int tok0, int n, int tid) {
     const char* kb = static_cast<const char*>(br.k) + static_cast<int64_t>(tok0) * br.sk * ES;
     const char* vb = static_cast<const char*>(br.v) + static_cast<int64_t>(tok0) * br.sv * ES;
@@ -100,14 +118,20 @@ struct Stager {
 #pragma unroll
     for (int j = 0; j < KU; ++j) {
       const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
-      if (FULL || row0 + RS * j < n) k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
+      if (FULL || row0 + RS * j < n) {
+        if constexpr (U16) k[j] = load_u16(p + koff);
+        else k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
+      }
     }
 #pragma unroll
     for (int j = 0; j < VQ; ++j) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const char* p = vb + static_cast<int64_t>(4 * RS * j + r) * br.sv * ES;
-        if (FULL || 4 * (row0 + RS * j) + r < n) v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
+        if (FULL || 4 * (row0 + RS * j) + r < n) {
+          if constexpr (U16) v[j][r] = load_u16(p + voff);
+          else v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
+        }
       }
     }
   }
@@ -223,14 +247,16 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   wk.start(acc, b, g, h, T, qc);
   st.init(tid, wk.br.sk, wk.br.sv);  // row strides are the same for every block of a call
   st.zero();
-  if (wk.valid) st.load(wk.br, wk.tok0, wk.n, tid);
+  // raw pointer tables may hold blocks that are not 16-byte aligned (2-byte loads for those)
+  constexpr bool kMis = Acc::kMayMisalign && sizeof(KVT) == 2;
+  if (wk.valid) st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);
   while (wk.valid) {
     __syncthreads();  // every wave is done reading the previous tile
     st.store(Ks, Vt, tid);
     __syncthreads();
     const int tile_n = wk.n;
     wk.advance(acc, b, g, h, T, qc);
-    if (wk.valid) st.load(wk.br, wk.tok0, wk.n, tid);  // in flight during this tile's MFMAs
+    if (wk.valid) st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);  // in flight during the MFMAs
     if (wave_active) {
       // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks.  A
       // partial tile seeds the accumulators with 0 / -inf per key, so masked keys come out -inf.
@@ -462,9 +488,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
       kdo[jj] = row * rsk + ((c ^ DG::swz_k(row)) << 4);
       vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
     }
-    dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
+    copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
              lds[0], w, kdo);
-    dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
+    copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
              lds[2], w, vdo);
     n_cur = wk.n;
     wk.advance(acc, b, g, h, T, qc);
@@ -485,9 +511,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
     __syncthreads();
     int n_nx = 0;
     if (wk.valid) {
-      dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+      copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
                wk.n, lds[BI ^ 1], w, kdo);
-      dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
+      copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
                wk.n, lds[2 + (BI ^ 1)], w, vdo);
       n_nx = wk.n;
       wk.advance(acc, b, g, h, T, qc);
@@ -914,8 +940,9 @@ extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const i
   if (gm.items == 0) return OMM_OK;
   PtrAcc acc{ptr_k, ptr_v, ptr_stride[0], ptr_stride[1], ptr_stride[2], ptr_stride[3], stride_bn,
              block_size};
-  // pointer rows must be 16-byte aligned for the MFMA staging loads (checked per call on the
-  // host only for the strides; addresses of cache chunks are allocator-aligned)
+  // the MFMA kernels need 16-byte row strides; a block address that is not 16-byte aligned
+  // (any bf16 address is accepted) is detected per block on the device and copied with 2-byte
+  // loads
   const bool mfma = stride_bd == 1 && stride_bn % 8 == 0 && qo_mfma_ok(*q, *out);
   return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, stride_bd, 2 * stride_bn,
                           static_cast<hipStream_t>(stream));

@@ -95,6 +95,44 @@ def test_padded_ptr_fast_reference_geometry(G):
     _check_attn(out, lse, want_o, want_l)
 
 
+@pytest.mark.parametrize("shift,G", [(1, 15), (4, 150), (3, 15)])
+def test_padded_ptr_fast_misaligned_bases(shift, G):
+    """Chunk bases that are only 2- or 8-byte aligned (views `shift` elements into their
+    allocations), as the reference's pointer contract allows (csrc/ptr_table.cu:32-49): the
+    device detects each block's misalignment and copies it with 2-byte loads; results must match
+    the oracle exactly as for aligned bases.  Head 1 mixes aligned and misaligned chunks."""
+    from omnimem_amd.padded_ptr import selection_attention_padded_ptr_fast
+    g = torch.Generator().manual_seed(7 + shift)
+    H, D, C, BS, T, n_chunks = 2, 128, 4680, 30, 8, 3
+
+    def chunk(i, scale):
+        x = (torch.randn((1, C * D + 8), generator=g) * scale).to(torch.bfloat16).to(DEV)
+        off = shift if i % 2 == 0 else 0
+        return x[:, off:off + C * D].view(1, C, D)
+
+    chunks_k = [[chunk(h + c, 0.3) for c in range(n_chunks)] for h in range(H)]
+    chunks_v = [[chunk(h + c + 1, 1.0) for c in range(n_chunks)] for h in range(H)]
+    base_k = torch.tensor([[t.data_ptr() for t in row] for row in chunks_k], dtype=torch.int64)
+    base_v = torch.tensor([[t.data_ptr() for t in row] for row in chunks_v], dtype=torch.int64)
+    assert ((base_k % 16) != 0).any() and ((base_v % 16) != 0).any()
+    M = 150
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    bpc = C // BS
+    ids = torch.stack([torch.randperm(n_chunks * bpc, generator=g)[:T] for _ in range(M // G * H)])
+    ids = ids.view(1, M // G, H, T).to(torch.int32)
+    strides = {"batch_stride_bytes": C * D * 2, "token_stride_bytes": D * 2, "stride_bn": D,
+               "stride_bd": 1, "chunk_len": C}
+    out, lse = selection_attention_padded_ptr_fast(
+        q.to(DEV), ids.to(DEV), BS, G, C, base_k.to(DEV), base_v.to(DEV),
+        torch.full((H,), n_chunks, dtype=torch.int32, device=DEV), strides, return_lse=True)
+    k = torch.stack([torch.cat([c[0] for c in row]) for row in chunks_k], 1)[None].float().cpu()
+    v = torch.stack([torch.cat([c[0] for c in row]) for row in chunks_v], 1)[None].float().cpu()
+    want_o, want_l = O.selection_attention(q.float().numpy(), k.numpy(), v.numpy(), ids.numpy(),
+                                           G, D ** -0.5,
+                                           O.dense_block_tokens(n_chunks * C, BS, 1, False))
+    _check_attn(out, lse, want_o, want_l)
+
+
 # ------------------------------------------------------------------ paged cache
 def _chunk(g, S, H, D, scale=1.0, t_dist=False):
     if t_dist:
