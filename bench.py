@@ -100,7 +100,7 @@ PMC_FILE = os.path.join(ROOT, "profiles", "bench_config3_layer_pmc.json")
 
 # rocprofv3 names of the kernels whose traffic the line reports (config 3 forward, config 2 top-k)
 ROOFLINE_KERNEL = "sel_fwd_dma_kernel<bf16_t, DenseAcc<bf16_t>, 128, 2>"
-TOPK_KERNEL = "topk_kernel<bf16_t, 1>"
+TOPK_KERNEL = "topk_mfma_kernel<bf16_t, 128, true>"
 
 
 def measured_traffic(kernel_prefix: str):
@@ -117,11 +117,40 @@ def measured_traffic(kernel_prefix: str):
     return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (platform's string if unreadable)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_threads():
+    """(threads, note): every CPU this process may run on, bounded by OMP_NUM_THREADS when the
+    host sets it (the GPU box gives each GPU a 16-thread CPU share and sets it so)."""
+    nproc = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = nproc
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = allowed
+    if omp and omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    note = (f"cpu={cpu_model()}, nproc={nproc}, affinity={allowed}, "
+            f"OMP_NUM_THREADS={omp or 'unset'}, torch threads={threads}")
+    return threads, note
+
+
 def cpu_baseline(q, k, v, ids, seconds: float):
     """Time the reference's CPU formulation on random (query group, head) pairs until ~seconds."""
     import torch
     from oracle import cpu_baseline as CB
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    threads, note = cpu_threads()
     torch.set_num_threads(threads)
     qc, kc, vc = (x.float().cpu() for x in (q, k, v))
     idc = ids.cpu().long()
@@ -150,7 +179,76 @@ def cpu_baseline(q, k, v, ids, seconds: float):
         "sample": f"reference select_attention_torch_chunk formulation (fp32, 32-query chunks) on "
                   f"{done} random (64-query group, head) pairs of the config-3 layer "
                   f"({100.0 * done / (MG * Hh):.1f}% of the step), {t_total:.1f} s of CPU time; "
-                  f"cpu={platform.processor() or platform.machine()}, nproc={os.cpu_count()}",
+                  + note,
+    }
+
+
+def cpu_baseline_ar(history: int = 80, q_small: int = 64, q_large: int = 256):
+    """Config 4 on the CPU: one AR layer-forward of the selection path at ``history`` cached
+    chunks (60 s of video at 80), the reference's CPU formulation: query pooling, block scoring
+    + top-16 over the pooled history (window of 3 chunks excluded), then selection attention of
+    the chunk's 4680 queries over their 16 blocks of the 374,400-token bf16 K/V (2.3 GB in RAM).
+
+    The selection call costs a fixed part (the permute of the whole K/V, select_attention.py:85)
+    plus one part per 32-query chunk (:88), so it is timed on ``q_small`` and ``q_large``
+    queries and the line through the two points is evaluated at 4680 queries; the per-layer
+    time is then x150 (5 forwards x 30 layers) for one AR chunk.  Both steps are extrapolations
+    and are labelled so."""
+    import torch
+    from oracle import cpu_baseline as CB
+    threads, note = cpu_threads()
+    torch.set_num_threads(threads)
+    C, P, Gq, W = CHUNK, BS, G, 3
+    Ntok = history * C
+    gdev = "cuda" if torch.cuda.is_available() else "cpu"
+    g = torch.Generator(device=gdev).manual_seed(11)
+    # the cache and the chunk come from the GPU's generator (faster than the CPU's), then live
+    # in host memory
+    k = torch.randn((1, Ntok, H, D), generator=g, device=gdev).to(torch.bfloat16).cpu()
+    v = torch.randn((1, Ntok, H, D), generator=g, device=gdev).to(torch.bfloat16).cpu()
+    q = torch.randn((1, C, H, D), generator=g, device=gdev).to(torch.bfloat16).cpu()
+    nb = Ntok // P
+    kc = k[:, :nb * P].reshape(1, nb, P, H, D).float().mean(2).to(torch.bfloat16)  # pooled history
+    t = time.perf_counter()
+    ng = -(-C // Gq)
+    qp = torch.nn.functional.pad(q.float(), (0, 0, 0, 0, 0, ng * Gq - C)).view(
+        1, ng, Gq, H, D).mean(2)
+    # scores over the history with the progressive window of 3 chunks excluded (the query
+    # chunk is the newest), then top-16 with the (score desc, id asc) rule
+    sc = torch.einsum("bghd,bnhd->bghn", qp, kc.float()) * D ** -0.5
+    sc[..., ((history - W + 1) * C) // P:] = float("-inf")
+    val, idx = torch.topk(sc, TOPK, dim=-1)
+    idx, order = torch.sort(idx, dim=-1)
+    val = torch.gather(val, -1, order)
+    val, order = torch.sort(val, dim=-1, descending=True, stable=True)
+    ids = torch.gather(idx, -1, order)
+    t_topk = time.perf_counter() - t
+    tok = CB.inflate_indices(ids.repeat_interleave(Gq, dim=1)[:, :C], P)
+    pts = []
+    for m in (q_small, q_large):
+        t = time.perf_counter()
+        CB.select_attention_chunked(q[:, :m], k, v, tok[:, :m], scale=D ** -0.5, causal=False)
+        pts.append(time.perf_counter() - t)
+    qch = 32  # the formulation's query chunk
+    per_qchunk = (pts[1] - pts[0]) / ((q_large - q_small) / qch)
+    fixed = max(0.0, pts[0] - per_qchunk * q_small / qch)
+    t_sel = fixed + per_qchunk * (-(-C // qch))
+    layer = t_topk + t_sel
+    del k, v, q, kc, sc, tok
+    return {
+        "ms_per_layer_forward": round(1e3 * layer, 1),
+        "ms_per_ar_chunk_extrapolated": round(1e3 * layer * 150, 1),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one AR layer-forward of the selection path at {history} cached chunks: query "
+                  f"pooling + scores + top-16 over {nb} pooled blocks ({1e3 * t_topk:.0f} ms), "
+                  f"and selection attention of {C} queries x {H} heads over {TOPK} x {P}-token "
+                  f"blocks of a {Ntok}-token bf16 K/V cache in RAM, timed on {q_small} and "
+                  f"{q_large} queries ({1e3 * pts[0]:.0f} / {1e3 * pts[1]:.0f} ms) and "
+                  f"extrapolated linearly to {C} (fixed {1e3 * fixed:.0f} ms + "
+                  f"{1e3 * per_qchunk:.0f} ms per 32-query chunk); x150 (5 forwards x 30 layers) "
+                  f"= extrapolated ms per AR chunk; " + note,
     }
 
 
@@ -187,26 +285,30 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
     torch.cuda.synchronize()
     s0 = dict(cache.stats)
     times = []
+    cats = {}
+    # the timed chunks carry the per-category event timers themselves, so the breakdown and the
+    # mean describe the same chunks
     for _ in range(steps):
         x = noise()
         torch.cuda.synchronize()
+        model.timers = {}
         t0 = time.perf_counter()
         model.step(cid, x)
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
+        for name, pairs in model.timers.items():
+            cats[name] = cats.get(name, 0.0) + sum(a.elapsed_time(b) for a, b in pairs)
         cid += 1
-    s1 = dict(cache.stats)
-    # one more chunk with per-category event timers (not part of the timed mean)
-    model.timers = {}
-    model.step(cid, noise())
-    torch.cuda.synchronize()
-    breakdown = {k: round(sum(a.elapsed_time(b) for a, b in v), 3) for k, v in model.timers.items()}
     model.timers = None
+    s1 = dict(cache.stats)
+    breakdown = {k: round(v / steps, 3) for k, v in sorted(cats.items())}
+    ms_chunk = 1e3 * sum(times) / len(times)
     moved = (s1["evicted_bytes"] - s0["evicted_bytes"]) + (s1["promoted_bytes"] - s0["promoted_bytes"])
     page_bytes = 2 * cfg.page_tokens * cfg.head_dim * cache.elem  # one K page + one V page
+    d = lambda key: (s1[key] - s0[key]) // steps
     res = {
         "dtype": "fp8e4m3" if dtype == "fp8" else "bf16",
-        "ms_per_ar_chunk": round(1e3 * sum(times) / len(times), 2),
+        "ms_per_ar_chunk": round(ms_chunk, 2),
         "steps": steps,
         "cached_chunks_at_start": history,
         "cached_tokens_per_layer": history * cfg.chunk_tokens,
@@ -215,18 +317,29 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
         "hbm_unit_slots": cache.n_slots,
         "host_unit_slots": cache.n_host,
         "per_chunk": {
-            "evicted_bytes": (s1["evicted_bytes"] - s0["evicted_bytes"]) // steps,
-            "promoted_bytes": (s1["promoted_bytes"] - s0["promoted_bytes"]) // steps,
-            "host_units_touched": (s1["misses"] - s0["misses"]) // steps,
-            "hbm_units_touched": (s1["hits"] - s0["hits"]) // steps,
-            "host_page_reads": (s1["host_page_reads"] - s0["host_page_reads"]) // steps,
-            "hbm_page_reads": (s1["hbm_page_reads"] - s0["hbm_page_reads"]) // steps,
+            "evicted_bytes": d("evicted_bytes"),
+            "promoted_bytes": d("promoted_bytes"),
+            "host_units_touched": d("misses"),
+            "hbm_units_touched": d("hits"),
+            # (layer, head, page) triples read from each pool, each counted once per chunk
+            "host_pages_unique": d("host_pages_unique"),
+            "hbm_pages_unique": d("hbm_pages_unique"),
+            # page listings: a page selected by k (query group, forward) pairs counts k times
+            "host_page_listings": d("host_page_reads"),
+            "hbm_page_listings": d("hbm_page_reads"),
         },
-        "host_link_bytes_per_chunk": moved // steps + page_bytes *
-        (s1["host_page_reads"] - s0["host_page_reads"]) // steps,
+        # host-link bytes per chunk: the evict / promote copies, plus the zero-copy reads of
+        # host-resident pages between two bounds (each page once / each listing once)
+        "host_link_bytes_per_chunk": {
+            "moved": moved // steps,
+            "zero_copy_unique_pages": page_bytes * d("host_pages_unique"),
+            "zero_copy_listings_upper_bound": page_bytes * d("host_page_reads"),
+        },
         "lru_hit_rate": round((s1["hits"] - s0["hits"]) /
                               max(1, (s1["hits"] - s0["hits"]) + (s1["misses"] - s0["misses"])), 4),
-        "breakdown_ms_one_chunk": breakdown,
+        "breakdown_ms_per_chunk": breakdown,
+        "breakdown_sum_ms": round(sum(breakdown.values()), 2),
+        "unattributed_ms": round(ms_chunk - sum(breakdown.values()), 2),
         "setup_s": {"alloc": round(t_alloc, 1), "prefill": round(t_prefill, 1)},
         "selection_useful_tflop_per_chunk": round(
             (cfg.denoise_steps + 1) * cfg.layers * 4 * cfg.chunk_tokens * cfg.heads * cfg.head_dim *
@@ -384,6 +497,10 @@ def main():
         }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(q, k, v, ids, args.cpu_seconds)
+        if not args.no_ar:
+            del q, k, v, out, lse
+            torch.cuda.empty_cache()
+            res["cpu_baseline"]["config4_ar"] = cpu_baseline_ar(args.ar_history)
     print(json.dumps(res), flush=True)
 
 

@@ -123,11 +123,14 @@ typedef struct omm_paged_kv {
   int32_t dtype;              /* OMM_BF16 or OMM_FP8E4M3 */
   int32_t n_slots;            /* HBM unit slots */
   int32_t n_host_slots;
+  uint8_t* page_seen;         /* [num_heads][max_chunks][pages_per_chunk]: set to 1 for every
+                                 page a selection lists since the caller last cleared it (unique
+                                 pages read, e.g. host-link bytes), or NULL */
 } omm_paged_kv;
 
 /* ---- library ------------------------------------------------------------------------- */
 const char* omm_last_error(void);
-int omm_abi_version(void); /* 1 */
+int omm_abi_version(void); /* 2 */
 
 /* Pinned, device-mapped host memory for the cache's host pool; *dev receives the device
  * address (equal to *host on ROCm with unified addressing, but always use *dev on device). */

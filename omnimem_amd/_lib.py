@@ -47,6 +47,7 @@ class PagedKV(ctypes.Structure):
         ("page_tokens", ctypes.c_int32), ("pages_per_chunk", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32),
         ("n_slots", ctypes.c_int32), ("n_host_slots", ctypes.c_int32),
+        ("page_seen", ctypes.c_void_p),
     ]
 
 

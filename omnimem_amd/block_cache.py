@@ -40,6 +40,32 @@ from .backend import BlockKVBackendError
 __all__ = ["PagedKVCache"]
 
 
+class _UploadRing:
+    """Pinned staging for asynchronous host -> device copies of small int32 arrays (unit
+    tables, slot indices).  Each of the ``n`` buffers is rewritten only after an event says its
+    previous copy has left, so no upload synchronises the stream."""
+
+    def __init__(self, n: int, elems: int):
+        self.bufs = [torch.empty(max(1, int(elems)), dtype=torch.int32).pin_memory()
+                     for _ in range(n)]
+        self.events = [None] * n
+        self.i = 0
+
+    def upload(self, src: np.ndarray, dst: torch.Tensor):
+        """dst (device int32, contiguous) <- src (host), enqueued on the current stream."""
+        j = self.i
+        self.i = (j + 1) % len(self.bufs)
+        if self.events[j] is not None:
+            self.events[j].synchronize()
+        n = src.size
+        buf = self.bufs[j][:n]
+        buf.numpy()[...] = src.reshape(-1)
+        dst.view(-1)[:n].copy_(buf, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events[j] = ev
+
+
 class _HostPool:
     """Pinned, device-mapped host memory (omm_host_alloc), viewable from torch on the CPU."""
 
@@ -146,13 +172,23 @@ class PagedKVCache:
         self._host_sk = _HostPool(self.n_host * self.scale_bytes)
         self._host_sv = _HostPool(self.n_host * self.scale_bytes)
 
-        H, MC = self.H, self.max_chunks
-        self.unit_table = [torch.full((H, MC), -1, dtype=torch.int32, device=self.device)
-                           for _ in range(self.L)]
-        self.stamp = [torch.zeros((H, MC), dtype=torch.int32, device=self.device)
-                      for _ in range(self.L)]
-        self.reads = [torch.zeros((H, MC), dtype=torch.int32, device=self.device)
-                      for _ in range(self.L)]
+        H, MC, L = self.H, self.max_chunks, self.L
+        # one allocation each for every layer (the per-layer lists are views), so that a flush
+        # reads all counters back with one synchronisation and a table upload is one copy
+        self._unit_all = torch.full((L, H, MC), -1, dtype=torch.int32, device=self.device)
+        self._stamp_all = torch.zeros((L, H, MC), dtype=torch.int32, device=self.device)
+        self._reads_all = torch.zeros((L, H, MC), dtype=torch.int32, device=self.device)
+        self._seen_all = torch.zeros((L, H, MC, self.ppc), dtype=torch.uint8, device=self.device)
+        self.unit_table = list(self._unit_all.unbind(0))
+        self.stamp = list(self._stamp_all.unbind(0))
+        self.reads = list(self._reads_all.unbind(0))
+        self.seen = list(self._seen_all.unbind(0))
+        self._h_stamp = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
+        self._h_reads = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
+        self._h_seen = torch.empty((L, H, MC, self.ppc), dtype=torch.uint8).pin_memory()
+        self._ring = _UploadRing(8, max(L * H * MC, 2 * (self.n_slots + self.n_host)))
+        self._d_idx = torch.empty(2 * (self.n_slots + self.n_host), dtype=torch.int32,
+                                  device=self.device)
         ncb = MC * self.ppc
         self.k_cmp = [torch.zeros((1, ncb, H, self.D), dtype=torch.bfloat16, device=self.device)
                       for _ in range(self.L)]
@@ -171,7 +207,6 @@ class PagedKVCache:
         self.cmp_window: Optional[int] = None
         self.cmp_sink = 0
         self._table_h = np.full((self.L, H, MC), -1, dtype=np.int32)
-        self._stage = torch.empty((H, MC), dtype=torch.int32).pin_memory()
         self.n_chunks = [0] * self.L
         self._epoch = 0
         self._flush_epoch = 0
@@ -184,17 +219,18 @@ class PagedKVCache:
         self._free_hbm = list(range(self.n_slots - 1, -1, -1))
         self._free_host = list(range(self.n_host - 1, -1, -1))
         self._table_h.fill(-1)
-        for l in range(self.L):
-            self.unit_table[l].fill_(-1)
-            self.stamp[l].zero_()
-            self.reads[l].zero_()
+        self._unit_all.fill_(-1)
+        self._stamp_all.zero_()
+        self._reads_all.zero_()
+        self._seen_all.zero_()
         self.n_chunks = [0] * self.L
         self._staged_k.clear()
         self._epoch = 0
         self._flush_epoch = 0
         self.stats = {"hits": 0, "misses": 0, "evicted_units": 0, "promoted_units": 0,
                       "evicted_bytes": 0, "promoted_bytes": 0, "flushes": 0,
-                      "hbm_page_reads": 0, "host_page_reads": 0}
+                      "hbm_page_reads": 0, "host_page_reads": 0,
+                      "hbm_pages_unique": 0, "host_pages_unique": 0}
 
     def next_epoch(self) -> int:
         self._epoch += 1
@@ -202,10 +238,12 @@ class PagedKVCache:
             raise BlockKVBackendError("epoch counter exhausted; call reset()")
         return self._epoch
 
-    def _upload_table(self, layer: int):
-        self._stage.copy_(torch.from_numpy(self._table_h[layer]))
-        self.unit_table[layer].copy_(self._stage, non_blocking=True)
-        torch.cuda.current_stream(self.device).synchronize()  # the staging buffer is reused
+    def _upload_table(self, layer: Optional[int] = None):
+        """Device unit table of one layer (or all) from the host's, asynchronously."""
+        if layer is None:
+            self._ring.upload(self._table_h, self._unit_all)
+        else:
+            self._ring.upload(self._table_h[layer], self.unit_table[layer])
 
     def layer_view(self, layer: int) -> _lib.PagedKV:
         """The omm_paged_kv struct of one layer."""
@@ -218,6 +256,7 @@ class PagedKVCache:
         kv.unit_table = self.unit_table[layer].data_ptr()
         kv.stamp = self.stamp[layer].data_ptr()
         kv.reads = self.reads[layer].data_ptr()
+        kv.page_seen = self.seen[layer].data_ptr()
         kv.num_heads, kv.max_chunks, kv.n_chunks = self.H, self.max_chunks, self.n_chunks[layer]
         kv.chunk_len, kv.page_tokens, kv.pages_per_chunk = self.chunk_len, self.P, self.ppc
         kv.head_dim = self.D
@@ -451,6 +490,7 @@ class PagedKVCache:
         kv = self.layer_view(layer)
         kv.stamp = None
         kv.reads = None
+        kv.page_seen = None
         scale = softmax_scale if softmax_scale is not None else D ** -0.5
         _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(ids4), ctypes.byref(kv), G,
                   float(scale), _lib.view4(out), None, 0, _lib.stream_of(q),
@@ -572,10 +612,9 @@ class PagedKVCache:
             j += 1
         return desired.reshape(self._table_h.shape)
 
-    def _move(self, layer_units, to_host: bool):
-        """Copy units (list of (l, h, c)) between the pools; returns bytes moved."""
-        if not layer_units:
-            return 0
+    def _take_slots(self, layer_units, to_host: bool):
+        """Host side of one batch of moves: reassign the units' slots in the host table and the
+        free lists; returns (src slots, dst slots)."""
         src, dst = [], []
         for (l, h, c) in layer_units:
             s = int(self._table_h[l, h, c])
@@ -592,9 +631,17 @@ class PagedKVCache:
                 dst.append(d)
                 self._table_h[l, h, c] = d
                 self._free_host.append(hs)
-        dev = self.device
-        s_t = torch.tensor(src, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
-        d_t = torch.tensor(dst, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
+        return src, dst
+
+    def _copy_batches(self, batches):
+        """Enqueue the copies of planned batches [(to_host, src, dst)]: one upload of every
+        batch's slot indices, then one omm_copy_units launch per batch.  Nothing synchronises:
+        the copies and the index upload are ordered on the stream before any later kernel."""
+        if not batches:
+            return
+        idx = np.concatenate([np.asarray(sd, dtype=np.int32) for _, src, dst in batches
+                              for sd in (src, dst)])
+        self._ring.upload(idx, self._d_idx)
         hk, hv = self._host_k.dev_ptr, self._host_v.dev_ptr
         pk, pv = self.pool_k.data_ptr(), self.pool_v.data_ptr()
         if self.fp8:
@@ -602,30 +649,34 @@ class PagedKVCache:
             psk, psv = self.scale_k.data_ptr(), self.scale_v.data_ptr()
         else:
             hsk = hsv = psk = psv = None
-        if to_host:
-            args = (pk, hk, pv, hv, psk, hsk, psv, hsv)
-            limits = (self.n_slots, self.n_host)
-        else:
-            args = (hk, pk, hv, pv, hsk, psk, hsv, psv)
-            limits = (self.n_host, self.n_slots)
-        _lib.call("omm_copy_units", *args, s_t.data_ptr(), d_t.data_ptr(), len(src), *limits,
-                  self.unit_bytes, self.scale_bytes, _lib.stream_of(self.pool_k),
-                  error=BlockKVBackendError)
-        torch.cuda.current_stream(dev).synchronize()  # slot index tensors die with this frame
-        return len(src) * 2 * (self.unit_bytes + self.scale_bytes)
+        base = self._d_idx.data_ptr()
+        off = 0
+        for to_host, src, dst in batches:
+            n = len(src)
+            if to_host:
+                args = (pk, hk, pv, hv, psk, hsk, psv, hsv)
+                limits = (self.n_slots, self.n_host)
+            else:
+                args = (hk, pk, hv, pv, hsk, psk, hsv, psv)
+                limits = (self.n_host, self.n_slots)
+            _lib.call("omm_copy_units", *args, base + 4 * off, base + 4 * (off + n), n, *limits,
+                      self.unit_bytes, self.scale_bytes, _lib.stream_of(self.pool_k),
+                      error=BlockKVBackendError)
+            off += 2 * n
 
-    def _apply(self, desired: np.ndarray):
+    def _apply(self, desired: np.ndarray, st: Optional[np.ndarray] = None):
         """Move units so that HBM holds exactly the desired written units.  Evictions and
         promotions alternate in batches bounded by the free slots of the receiving pool (a
         promotion frees a host slot, an eviction an HBM slot), so a full host pool never
-        blocks a swap; the least recent units leave first, the most recent arrive first."""
+        blocks a swap; the least recent units leave first, the most recent arrive first.
+        ``st``: host copy of the stamps (read back when needed and not given)."""
         resident = self._table_h >= 0
         on_host = self._table_h <= -2
-        st = None
         evict = np.argwhere(resident & ~desired)
         promote = np.argwhere(on_host & desired)
         if len(evict) > 1 or len(promote) > 1:
-            st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
+            if st is None:
+                st = self._counts()[0]
             key = lambda u: st[u[:, 0], u[:, 1], u[:, 2]] * (1 << 20) + u[:, 2]
             if len(evict) > 1:
                 evict = evict[np.argsort(key(evict), kind="stable")]
@@ -633,82 +684,93 @@ class PagedKVCache:
                 promote = promote[np.argsort(-key(promote), kind="stable")]
         evict = [tuple(u) for u in evict]
         promote = [tuple(u) for u in promote]
-        n_ev = n_pr = eb = pb = 0
-        touched = set()
+        n_ev = n_pr = 0
+        batches = []
         while evict or promote:
             ne = min(len(evict), len(self._free_host))
             if ne:
-                eb += self._move(evict[:ne], to_host=True)
-                touched.update(u[0] for u in evict[:ne])
+                batches.append((True,) + self._take_slots(evict[:ne], to_host=True))
                 evict, n_ev = evict[ne:], n_ev + ne
             npr = min(len(promote), len(self._free_hbm))
             if npr:
-                pb += self._move(promote[:npr], to_host=False)
-                touched.update(u[0] for u in promote[:npr])
+                batches.append((False,) + self._take_slots(promote[:npr], to_host=False))
                 promote, n_pr = promote[npr:], n_pr + npr
             if ne == 0 and npr == 0:
                 raise BlockKVBackendError(
                     f"no free slot to swap through ({len(evict)} evictions, {len(promote)} "
                     f"promotions pending)")
-        for l in sorted(touched):
-            self._upload_table(int(l))
+        self._copy_batches(batches)
+        if batches:
+            self._upload_table()
+        unit = 2 * (self.unit_bytes + self.scale_bytes)
         self.stats["evicted_units"] += n_ev
         self.stats["promoted_units"] += n_pr
-        self.stats["evicted_bytes"] += eb
-        self.stats["promoted_bytes"] += pb
+        self.stats["evicted_bytes"] += n_ev * unit
+        self.stats["promoted_bytes"] += n_pr * unit
         return n_ev, n_pr
 
     def _counts(self):
-        """Host copies of every layer's stamps and page-read counts (one synchronisation)."""
-        st = torch.stack(self.stamp).cpu().numpy().astype(np.int64)
-        rd = torch.stack(self.reads).cpu().numpy()
-        return st, rd
+        """Host copies of every layer's stamps, page-read counts and pages seen (one
+        synchronisation); the arrays are reused by the next call."""
+        self._h_stamp.copy_(self._stamp_all, non_blocking=True)
+        self._h_reads.copy_(self._reads_all, non_blocking=True)
+        self._h_seen.copy_(self._seen_all, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        return (self._h_stamp.numpy().astype(np.int64), self._h_reads.numpy(),
+                self._h_seen.numpy())
 
     def _make_room(self, need: int):
-        st, rd = self._counts()
+        st, rd, _ = self._counts()
         desired = self._plan(st, reserve=need, rd=rd)
-        self._apply(desired)
+        self._apply(desired, st)
         if len(self._free_hbm) < need:
             raise BlockKVBackendError(f"cannot free {need} HBM slots")
 
     def flush(self, reserve_next_chunk: bool = True) -> dict:
         """Chunk-boundary residency update (MMCache.flush_offload, models/cache.py:1032): one
-        read of the stamps and page counts, then batched evict / promote copies.  With
-        ``reserve_next_chunk`` the HBM slots of the next chunk of every layer and head are
-        assigned here, so the appends of the next AR step never touch the host.  Returns this
-        flush's counts."""
-        st, rd = self._counts()
+        read of the stamps and page counts, then batched evict / promote copies enqueued without
+        synchronising.  With ``reserve_next_chunk`` the HBM slots of the next chunk of every
+        layer and head are assigned here, so the appends of the next AR step never touch the
+        host.  Returns this flush's counts: units touched in HBM / on the host, page listings
+        (a page read by k selections counts k times) and unique pages read per pool."""
+        st, rd, sn = self._counts()
         touched = st > self._flush_epoch
         written = self._table_h != -1
         res, host = self._table_h >= 0, self._table_h <= -2
         hits = int((touched & res).sum())
         misses = int((touched & host).sum())
         hbm_reads, host_reads = int(rd[res].sum()), int(rd[host].sum())
+        pages = sn.sum(-1, dtype=np.int64)
+        hbm_unique, host_unique = int(pages[res].sum()), int(pages[host].sum())
         self.stats["hits"] += hits
         self.stats["misses"] += misses
         self.stats["hbm_page_reads"] += hbm_reads
         self.stats["host_page_reads"] += host_reads
+        self.stats["hbm_pages_unique"] += hbm_unique
+        self.stats["host_pages_unique"] += host_unique
         reserve = self.L * self.H if reserve_next_chunk else 0
         desired = self._plan(st, reserve=reserve, rd=rd) & written
-        ev, pr = self._apply(desired)
+        ev, pr = self._apply(desired, st)
         if reserve_next_chunk:
+            changed = False
             for l in range(self.L):
                 c = self.n_chunks[l]
                 if c >= self.max_chunks:
                     continue
                 row = self._table_h[l, :, c]
                 free = np.nonzero(row == -1)[0]
-                if free.size == 0:
-                    continue
                 for h in free:
                     row[h] = self._free_hbm.pop()
-                self._upload_table(l)
-        for r in self.reads:
-            r.zero_()
+                    changed = True
+            if changed:
+                self._upload_table()
+        self._reads_all.zero_()
+        self._seen_all.zero_()
         self._flush_epoch = self._epoch
         self.stats["flushes"] += 1
         return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr,
-                "hbm_page_reads": hbm_reads, "host_page_reads": host_reads}
+                "hbm_page_reads": hbm_reads, "host_page_reads": host_reads,
+                "hbm_pages_unique": hbm_unique, "host_pages_unique": host_unique}
 
     def flush_offload(self, layer_idx: Optional[int] = None) -> dict:
         """MMCache-compatible name of ``flush`` (models/cache.py:1032).  Residency is planned for

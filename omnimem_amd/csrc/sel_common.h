@@ -146,6 +146,7 @@ struct PagedAcc {
   const int32_t* ids;
   int32_t* stamp;
   int32_t* reads;
+  uint8_t* seen;
   int64_t is0, is1, is2, is3;
   int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
   __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
@@ -181,10 +182,11 @@ struct PagedAcc {
   }
   __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.bid; }
   // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
-  // epoch, so the races are benign) and count its pages read (vector atomics)
+  // epoch, so the races are benign), count its pages read (vector atomics) and mark each listed
+  // page seen (duplicates store the same 1)
   __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
     const bool st = stamp != nullptr && epoch > 0;
-    if (!st && reads == nullptr) return;
+    if (!st && reads == nullptr && seen == nullptr) return;
     for (int t = threadIdx.x; t < T; t += blockDim.x) {
       const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
       if (bid < 0) continue;
@@ -194,6 +196,7 @@ struct PagedAcc {
       if (unit[u] == -1) continue;
       if (st) stamp[u] = epoch;
       if (reads != nullptr) atomicAdd(reads + u, 1);
+      if (seen != nullptr) seen[u * ppc + (bid - cid * ppc)] = 1;
     }
   }
 };

@@ -978,7 +978,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
                          nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
                          static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
-                         idp, kv->stamp, kv->reads, ids->stride[0], ids->stride[1], ids->stride[2],
+                         idp, kv->stamp, kv->reads, kv->page_seen, ids->stride[0], ids->stride[1], ids->stride[2],
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
                          kv->n_slots, kv->n_host_slots};
@@ -990,7 +990,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
     PagedAcc<uint8_t> acc{static_cast<const uint8_t*>(kv->pool_k), static_cast<const uint8_t*>(kv->pool_v),
                           kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
                           static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
-                          kv->host_scale_v, kv->unit_table, idp, kv->stamp, kv->reads,
+                          kv->host_scale_v, kv->unit_table, idp, kv->stamp, kv->reads, kv->page_seen,
                           ids->stride[0],
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,

@@ -331,3 +331,24 @@ def test_mfma_selection_nan_and_inf_scores():
     assert np.isnan(sc).any() and np.isposinf(sc).any() and np.isneginf(sc).any()
     np.testing.assert_array_equal(ids.cpu().numpy(), got)
     np.testing.assert_array_equal(got, O.topk_select(sc, 16, mask))
+
+
+def test_ar_shape_fused_topk_80_chunks():
+    """The call the AR driver makes at 80 cached chunks (omnimem_amd/wan_ar.py, reference
+    causal_wan_nsa_model.py:496-505): one 4680-token chunk of full-resolution bf16 queries
+    (groups of 64, ragged last group) against 5920 pooled keys (74 per chunk), window of 3 chunks
+    excluded progressively, q_chunk_offset 80.  This takes the pool-to-workspace kernel, the
+    column-split MFMA kernel and the merge; checked against the oracle's selection on the
+    kernel's scores and the fp32 score bound."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(80)
+    q = _bf16((1, 4680, 12, 128), g)
+    k = _bf16((1, 80 * 74, 12, 128), g)
+    kw = dict(block_size=64, chunk_size=4680, causal=False, exclude_window_chunks=3,
+              exclude_sink_chunks=0, progressive_exclude=True, q_chunk_offset=80,
+              blocks_per_chunk=74)
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), 16, group_size=64, **kw).cpu().numpy()
+    mask = O.Mask(block_size=64, group_size=64, chunk_q=4680, chunk_k=4680, blocks_per_chunk=74,
+                  q_chunk_offset=80, ex_win=3, causal=0, prog_excl=1)
+    check_mfma_topk(q.to(DEV), k.to(DEV), 16, mask, 128 ** -0.5, 64, got=got, **kw)
+    assert (got >= 0).all() and got.max() < 78 * 74  # the window chunks 78, 79 are excluded
