@@ -45,6 +45,49 @@ C2_T, C2_NC = 32768, 512
 C2_BYTES = C2_T * H * D * 2 + C2_NC * H * D * 2 + (C2_T // 64) * H * TOPK * 4
 
 
+# Algorithmic work per dispatch of the kernels the rocprof summaries price (bytes for HBM-bound
+# kernels, FLOPs for MFMA-bound ones), keyed by rocprofv3 kernel-name prefix, per workload.
+# AR shapes: one 4680-token chunk, 12 heads x 128, 64-token pages (74 per chunk), 80 cached
+# chunks (5920 pooled blocks), top-16, a window of 3 chunks.
+_AR_C, _AR_PPC, _AR_HIST, _AR_WIN = CHUNK, -(-CHUNK // BS), 80, 3
+ALGO = {
+    "c3": {
+        # config 2 and the config-3 layer's top-k (32768 / 32760 tokens: the same to 0.03 %)
+        "topk_mfma_kernel<bf16_t, 128, true>": ("bytes", C2_BYTES),
+        # K compression of the config-3 layer: read k, write k_cmp
+        "pool_rows_kernel<bf16_t>": ("bytes", M * H * D * 2 + (M // BS + 1) * H * D * 2),
+    },
+    "ar": {
+        # append of one layer-forward: read the chunk's K and V, write their pages (74 x 64
+        # slots each) and pooled rows; fp8 writes 1-byte codes and a scale per (page, head)
+        "paged_append_kernel<false>": ("bytes", 2 * _AR_C * H * D * 2
+                                       + 2 * _AR_PPC * BS * H * D * 2 + 2 * _AR_PPC * H * D * 2),
+        "paged_append_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2 + 2 * _AR_PPC * BS * H * D
+                                      + 2 * _AR_PPC * H * 4 + 2 * _AR_PPC * H * D * 2),
+        # selection over the history (cache.select): 4680 queries x 12 heads x 16 pages x 64
+        # tokens, 4 D FLOPs each (bf16 pages, some host-resident; fp8 pages)
+        "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 2>": (
+            "flops", 4 * D * _AR_C * H * TOPK * BS),
+        "sel_fwd_mfma_kernel<bf16_t, PagedAcc<unsigned char>, 128>": (
+            "flops", 4 * D * _AR_C * H * TOPK * BS),
+        # bf16 window attention over the window's pages: 4680 queries x 3 chunks of keys
+        "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 4>": (
+            "flops", 4 * D * _AR_C * H * _AR_WIN * _AR_C),
+    },
+}
+# kernels one call launches together, priced as a whole: the AR top-k (query pooling into the
+# workspace, split scoring + selection, merge) reads the chunk's q and the pooled history
+ALGO_GROUPS = {
+    "ar": {
+        "AR top-k call (pool_rows + topk_mfma + merge)": (
+            ["pool_rows_kernel<bf16_t>", "topk_mfma_kernel<bf16_t, 128, false>",
+             "topk_merge_kernel"],
+            "bytes", _AR_C * H * D * 2 + _AR_HIST * _AR_PPC * H * D * 2
+            + _AR_PPC * H * TOPK * 4),
+    },
+}
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -57,6 +100,18 @@ def parse():
                    help="cached chunks before the timed AR steps (80 chunks = 240 latent frames)")
     p.add_argument("--ar-steps", type=int, default=3, help="timed AR chunks per cache dtype")
     p.add_argument("--no-ar", action="store_true", help="skip the AR (configs 4 and 5) leg")
+    p.add_argument("--ar-only", action="store_true",
+                   help="run only the AR leg (configs 4 and 5) and print its results (profiling "
+                        "runs of the cache kernels)")
+    p.add_argument("--rocprof-summary", nargs=2, metavar=("OUT", "DIR"),
+                   help="summarise the rocprofv3 runs under DIR (stats/, fetch/, write/, "
+                        "copy_fetch/, copy_write/) into OUT.json and OUT.md, then exit")
+    p.add_argument("--rocprof-md", metavar="JSON",
+                   help="rewrite the text form (.md) of a committed rocprof summary and exit")
+    p.add_argument("--summary-command", default="",
+                   help="the command lines that produced the runs, recorded in the summary")
+    p.add_argument("--summary-workload", default="c3", choices=sorted(ALGO),
+                   help="which algorithmic-work table prices the summary's kernels")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 5 device copies of 256 MiB (the reference kernel for scaling "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
@@ -77,6 +132,153 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n, "copies": 5}))
 
 
+def _short_kernel_name(n: str) -> str:
+    n = n.replace("omm::(anonymous namespace)::", "").replace("omm::", "").replace("void ", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return n[:i]
+    return n
+
+
+def _csv_rows(d: str, suffix: str):
+    import csv
+    import glob
+    for path in glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True):
+        with open(path) as f:
+            yield from csv.DictReader(f)
+
+
+def rocprof_summary(out: str, d: str, command: str, workload: str = "c3"):
+    """Kernel durations (``--kernel-trace --stats``) and HBM bytes per dispatch (``--pmc
+    FETCH_SIZE`` / ``WRITE_SIZE``, medians in KiB, scaled by the same counters' reading of a
+    256 MiB device copy) of every kernel of one workload, with the ALGO figures priced against
+    the MI355X peaks."""
+    import statistics
+    stats = {}
+    for r in _csv_rows(os.path.join(d, "stats"), "kernel_stats.csv"):
+        stats[_short_kernel_name(r["Name"])] = (int(r["Calls"]), float(r["AverageNs"]))
+    med = {}
+    for c, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write"),
+                   ("COPY_FETCH", "copy_fetch"), ("COPY_WRITE", "copy_write")):
+        vals = {}
+        for r in _csv_rows(os.path.join(d, sub), "counter_collection.csv"):
+            vals.setdefault(_short_kernel_name(r["Kernel_Name"]), []).append(
+                float(r["Counter_Value"]))
+        med[c] = {k: statistics.median(v) for k, v in vals.items()}
+    scale = {}
+    for c, cc in (("FETCH_SIZE", "COPY_FETCH"), ("WRITE_SIZE", "COPY_WRITE")):
+        cp = [v for k, v in med[cc].items() if "copyBuffer" in k]
+        scale[c] = (256 * 1024) / cp[0] if cp else None
+    kernels = {}
+    for name, (calls, avg_ns) in sorted(stats.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        if "at::native" in name or "copyBuffer" in name:
+            continue
+        k = {"calls": calls, "avg_us": round(avg_ns / 1e3, 2)}
+        f, w = med["FETCH_SIZE"].get(name), med["WRITE_SIZE"].get(name)
+        if f is not None and w is not None and scale["FETCH_SIZE"] and scale["WRITE_SIZE"]:
+            k["FETCH_SIZE"], k["WRITE_SIZE"] = f, w
+            k["hbm_bytes_scaled"] = round(1024 * (f * scale["FETCH_SIZE"] + w * scale["WRITE_SIZE"]))
+            k["hbm_GBps"] = round(k["hbm_bytes_scaled"] / avg_ns, 1)
+        algo = next((v for p_, v in ALGO[workload].items() if name.startswith(p_)), None)
+        if algo is not None:
+            unit, amount = algo
+            if unit == "bytes":
+                k["algorithmic_bytes"] = amount
+                k["algorithmic_GBps"] = round(amount / avg_ns, 1)
+                k["frac_hbm_8TBps"] = round(amount / avg_ns / PEAK_HBM_GBS, 4)
+            else:
+                k["useful_flops"] = amount
+                k["useful_TFLOPs"] = round(amount / avg_ns / 1e3, 1)
+                k["frac_bf16_peak"] = round(amount / avg_ns / 1e3 / PEAK_BF16_TFLOPS, 4)
+        kernels[name] = k
+    # further counter passes (directories pmc_*): medians per dispatch, and for MFMA kernels the
+    # executed bf16 MFMA rate (SQ_INSTS_VALU_MFMA_MOPS_BF16 counts units of 512 FLOPs), the MFMA
+    # busy share of the busy CU-SIMD cycles and VALU instructions per MFMA instruction
+    import glob as _glob
+    for sub in sorted(_glob.glob(os.path.join(d, "pmc_*"))):
+        vals = {}
+        for r in _csv_rows(sub, "counter_collection.csv"):
+            vals.setdefault((_short_kernel_name(r["Kernel_Name"]), r["Counter_Name"]), []).append(
+                float(r["Counter_Value"]))
+        for (name, cname), v in vals.items():
+            if name in kernels:
+                kernels[name].setdefault("counters", {})[cname] = statistics.median(v)
+    for name, k in kernels.items():
+        c = k.get("counters", {})
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+            fl = 512.0 * c["SQ_INSTS_VALU_MFMA_MOPS_BF16"]
+            k["mfma_bf16_executed_TFLOPs"] = round(fl / (k["avg_us"] * 1e6), 1)
+            k["mfma_bf16_executed_frac_peak"] = round(fl / (k["avg_us"] * 1e6) / PEAK_BF16_TFLOPS, 4)
+        if c.get("SQ_BUSY_CU_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            k["mfma_busy_share"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] /
+                                         (4.0 * c["SQ_BUSY_CU_CYCLES"]), 4)
+        if c.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in c:
+            k["valu_insts_per_mfma"] = round(c["SQ_INSTS_VALU"] / c["SQ_INSTS_MFMA"], 2)
+        if c.get("TCC_HIT_sum") is not None and c.get("TCC_MISS_sum") is not None:
+            tot = c["TCC_HIT_sum"] + c["TCC_MISS_sum"]
+            k["l2_hit_rate"] = round(c["TCC_HIT_sum"] / tot, 4) if tot else None
+    groups = {}
+    for gname, (members, unit, amount) in ALGO_GROUPS.get(workload, {}).items():
+        if all(m in kernels for m in members):
+            us = sum(kernels[m]["avg_us"] for m in members)
+            groups[gname] = {"avg_us_sum": round(us, 2), "algorithmic_bytes": amount,
+                             "algorithmic_GBps": round(amount / (us * 1e3), 1),
+                             "frac_hbm_8TBps": round(amount / (us * 1e3) / PEAK_HBM_GBS, 4)}
+    res = {"command": command, "counters": "FETCH_SIZE / WRITE_SIZE median KiB per dispatch",
+           "calibration": {"copy_bytes": 256 * 1024 * 1024,
+                           **{f"{c}_scale": round(v, 4) for c, v in scale.items() if v},
+                           "note": "scale = true bytes of a 256 MiB device copy / counter "
+                                   "reading of that copy"},
+           "kernels": kernels, "groups": groups}
+    with open(out + ".json", "w") as f:
+        json.dump(res, f, indent=1)
+    summary_md(res, out + ".md")
+
+
+def summary_md(res: dict, path: str):
+    """The short text form of a rocprof summary (kernel table, groups, counter passes)."""
+    kernels, groups = res["kernels"], res.get("groups", {})
+    title = os.path.splitext(os.path.basename(path))[0]
+    lines = [f"# {title}", "", "Command:", "", "    " + res["command"], "",
+             "| kernel | calls | avg µs | HBM bytes (scaled) | GB/s | algorithmic | achieved | frac |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, k in kernels.items():
+        if k["calls"] * k["avg_us"] < 1.0 and "algorithmic_bytes" not in k and "useful_flops" not in k:
+            continue
+        alg = (f"{k['algorithmic_bytes']:,} B" if "algorithmic_bytes" in k else
+               f"{k['useful_flops']:,} FLOP" if "useful_flops" in k else "")
+        ach = (f"{k['algorithmic_GBps']} GB/s" if "algorithmic_bytes" in k else
+               f"{k['useful_TFLOPs']} TFLOP/s" if "useful_flops" in k else "")
+        frac = k.get("frac_hbm_8TBps", k.get("frac_bf16_peak", ""))
+        shown = name if len(name) <= 72 else name[:69] + "..."
+        lines.append(f"| `{shown}` | {k['calls']} | {k['avg_us']} | "
+                     f"{k.get('hbm_bytes_scaled', ''):,} | {k.get('hbm_GBps', '')} | {alg} | "
+                     f"{ach} | {frac} |" if "hbm_bytes_scaled" in k else
+                     f"| `{shown}` | {k['calls']} | {k['avg_us']} |  |  | {alg} | {ach} | {frac} |")
+    for gname, g in groups.items():
+        lines.append(f"| {gname} | | {g['avg_us_sum']} | | | {g['algorithmic_bytes']:,} B | "
+                     f"{g['algorithmic_GBps']} GB/s | {g['frac_hbm_8TBps']} |")
+    derived = ("mfma_bf16_executed_TFLOPs", "mfma_bf16_executed_frac_peak", "mfma_busy_share",
+               "valu_insts_per_mfma", "l2_hit_rate")
+    rows = [(n, k) for n, k in kernels.items() if any(x in k for x in derived)]
+    if rows:
+        lines += ["", "Counter passes (medians per dispatch; MFMA FLOPs = 512 x "
+                  "SQ_INSTS_VALU_MFMA_MOPS_BF16; busy share = SQ_VALU_MFMA_BUSY_CYCLES / "
+                  "(4 x SQ_BUSY_CU_CYCLES); L2 hit = TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)):", "",
+                  "| kernel | " + " | ".join(derived) + " |", "|---|" + "---|" * len(derived)]
+        for n, k in rows:
+            lines.append(f"| `{n}` | " + " | ".join(str(k.get(x, "")) for x in derived) + " |")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+
+
 def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
     """4 * D * sum over queries and heads of the visible tokens of their selected blocks.
 
@@ -95,7 +297,7 @@ def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
     return int((n.sum(-1, keepdim=True) * nq).sum().item()) * 4 * D
 
 
-PMC_FILE = os.path.join(ROOT, "profiles", "bench_config3_layer_pmc.json")
+PMC_FILE = os.path.join(ROOT, "profiles", "config3_layer_kernels.json")
 
 
 # rocprofv3 names of the kernels whose traffic the line reports (config 3 forward, config 2 top-k)
@@ -354,6 +556,14 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
 
 def main():
     args = parse()
+    if args.rocprof_md:
+        with open(args.rocprof_md) as f:
+            summary_md(json.load(f), os.path.splitext(args.rocprof_md)[0] + ".md")
+        return
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary[0], args.rocprof_summary[1], args.summary_command,
+                        args.summary_workload)
+        return
     if args.copy_calibration:
         copy_calibration()
         return
@@ -366,6 +576,11 @@ def main():
     from omnimem_amd.selection import sel_fwd
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.ar_only:
+        print(json.dumps({"ms_per_ar_chunk": {
+            "bf16": run_ar(torch.bfloat16, args.ar_history, args.ar_steps),
+            "fp8": run_ar("fp8", args.ar_history, args.ar_steps)}}), flush=True)
+        return
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(3)
     q, k, v = (torch.randn((1, L, H, D), generator=gen).to(torch.bfloat16).to(dev)

@@ -92,7 +92,11 @@ __device__ __forceinline__ uint4 mean8(const float (&sum)[8], float cnt, int n) 
 }
 
 // One wave per (page, heads of the wave); lane = (head in wave, 8-dim slice).  Every lane walks
-// the page's tokens in ascending order, so the pooled key is the omm_block_pool arithmetic.
+// the page's tokens in ascending order, so the pooled key is the omm_block_pool arithmetic; the
+// walk loads kAppendBatch tokens of K and V at a time (all in flight together) and then adds them
+// in order, so a lane waits for memory once per batch, not once per token.
+constexpr int kAppendBatch = 16;
+
 template <bool FP8>
 __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
   const int lane = lane_id();
@@ -108,6 +112,19 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
   const int64_t page = static_cast<int64_t>(slot) * a.ppc + p;
   const bf16_t* ksrc = a.k + static_cast<int64_t>(h) * a.ks2 + dc * 8;
   const bf16_t* vsrc = a.v + static_cast<int64_t>(h) * a.vs2 + dc * 8;
+  constexpr int NB = kAppendBatch;
+  // tokens t0 .. t0 + NB - 1 of the page (zeros past the valid ones)
+  auto load_batch = [&](int t0, uint4 (&kr)[NB], uint4 (&vr)[NB]) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int t = t0 + j;
+      kr[j] = vr[j] = make_uint4(0, 0, 0, 0);
+      if (t < nvalid) {
+        kr[j] = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
+        vr[j] = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
+      }
+    }
+  };
 
   float ksum[8], vsum[8];
 #pragma unroll
@@ -118,39 +135,49 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
     uint4* vd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_v) + page * a.P * a.D + dc * 8);
     const int64_t row = a.D / 8;  // uint4 per page row
     if (go) {
-      for (int t = 0; t < a.P; ++t) {
-        uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
-        if (t < nvalid) {
-          kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
-          vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
-          float f[8], g[8];
-          unpack_bf16x8(kr, f);
-          unpack_bf16x8(vr, g);
+      for (int t0 = 0; t0 < a.P; t0 += NB) {
+        uint4 kr[NB], vr[NB];
+        load_batch(t0, kr, vr);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            ksum[i] += f[i];
-            vsum[i] += g[i];
+        for (int j = 0; j < NB; ++j) {
+          const int t = t0 + j;
+          if (t < nvalid) {
+            float f[8], g[8];
+            unpack_bf16x8(kr[j], f);
+            unpack_bf16x8(vr[j], g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              ksum[i] += f[i];
+              vsum[i] += g[i];
+            }
+          }
+          if (t < a.P) {
+            kd[t * row] = kr[j];
+            vd[t * row] = vr[j];
           }
         }
-        kd[t * row] = kr;
-        vd[t * row] = vr;
       }
     }
   } else {
     float amax_k = 0.0f, amax_v = 0.0f;
     if (go) {
-      for (int t = 0; t < nvalid; ++t) {
-        const uint4 kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
-        const uint4 vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
-        float fk[8], fv[8];
-        unpack_bf16x8(kr, fk);
-        unpack_bf16x8(vr, fv);
+      for (int t0 = 0; t0 < nvalid; t0 += NB) {
+        uint4 kr[NB], vr[NB];
+        load_batch(t0, kr, vr);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          ksum[i] += fk[i];
-          vsum[i] += fv[i];
-          amax_k = fmaxf(amax_k, fabsf(fk[i]));
-          amax_v = fmaxf(amax_v, fabsf(fv[i]));
+        for (int j = 0; j < NB; ++j) {
+          if (t0 + j < nvalid) {
+            float fk[8], fv[8];
+            unpack_bf16x8(kr[j], fk);
+            unpack_bf16x8(vr[j], fv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              ksum[i] += fk[i];
+              vsum[i] += fv[i];
+              amax_k = fmaxf(amax_k, fabsf(fk[i]));
+              amax_v = fmaxf(amax_v, fabsf(fv[i]));
+            }
+          }
         }
       }
     }
@@ -167,19 +194,26 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
       uint2* kd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_k) + page * a.P * a.D + dc * 8);
       uint2* vd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_v) + page * a.P * a.D + dc * 8);
       const int64_t row = a.D / 8;  // uint2 per page row
-      for (int t = 0; t < a.P; ++t) {
-        uint2 kq = make_uint2(0, 0), vq = make_uint2(0, 0);
-        if (t < nvalid) {
-          const uint4 kr = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + t) * a.ks1);
-          const uint4 vr = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + t) * a.vs1);
-          float fk[8], fv[8];
-          unpack_bf16x8(kr, fk);
-          unpack_bf16x8(vr, fv);
-          kq = quant8(fk, ik);
-          vq = quant8(fv, iv);
+      // second pass over the page (its rows were just read: L2 hits)
+      for (int t0 = 0; t0 < a.P; t0 += NB) {
+        uint4 kr[NB], vr[NB];
+        load_batch(t0, kr, vr);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int t = t0 + j;
+          uint2 kq = make_uint2(0, 0), vq = make_uint2(0, 0);
+          if (t < nvalid) {
+            float fk[8], fv[8];
+            unpack_bf16x8(kr[j], fk);
+            unpack_bf16x8(vr[j], fv);
+            kq = quant8(fk, ik);
+            vq = quant8(fv, iv);
+          }
+          if (t < a.P) {
+            kd[t * row] = kq;
+            vd[t * row] = vq;
+          }
         }
-        kd[t * row] = kq;
-        vd[t * row] = vq;
       }
       if (dc == 0) {
         a.scale_k[page] = sk;
