@@ -60,10 +60,12 @@ ALGO = {
     "ar": {
         # append of one layer-forward: read the chunk's K and V, write their pages (74 x 64
         # slots each) and pooled rows; fp8 writes 1-byte codes and a scale per (page, head)
-        "paged_append_kernel<false>": ("bytes", 2 * _AR_C * H * D * 2
-                                       + 2 * _AR_PPC * BS * H * D * 2 + 2 * _AR_PPC * H * D * 2),
-        "paged_append_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2 + 2 * _AR_PPC * BS * H * D
-                                      + 2 * _AR_PPC * H * 4 + 2 * _AR_PPC * H * D * 2),
+        "paged_append_wg_kernel<false>": ("bytes", 2 * _AR_C * H * D * 2
+                                          + 2 * _AR_PPC * BS * H * D * 2
+                                          + 2 * _AR_PPC * H * D * 2),
+        "paged_append_wg_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2
+                                         + 2 * _AR_PPC * BS * H * D + 2 * _AR_PPC * H * 4
+                                         + 2 * _AR_PPC * H * D * 2),
         # selection over the history (cache.select): 4680 queries x 12 heads x 16 pages x 64
         # tokens, 4 D FLOPs each (bf16 pages, some host-resident; fp8 pages)
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 2>": (

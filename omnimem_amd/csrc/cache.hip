@@ -231,6 +231,161 @@ __global__ __launch_bounds__(64) void paged_append_kernel(AppendArgs a) {
     a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
 }
 
+// The same append with a workgroup of 4 waves per (page, heads of a wave), for pages of at most
+// 64 tokens: all 256 threads load the page's K and V rows (16-byte columns c = tid % 64, rows
+// tid / 64 + 4 j, every load of a thread in flight at once), write the bf16 pages straight from
+// registers and stage the rows in LDS; then wave 0 (K) and wave 1 (V) add the staged rows in
+// token order per column, so the pooled rows keep the omm_block_pool arithmetic.  fp8 pages take
+// the per-(page, head) amax from the registers (wave shuffles, then a 4-wave LDS reduction) and
+// quantise the registers: one read of the chunk.  222 workgroups x 256 threads x 32 loads keep
+// about 29 MB in flight, against 7 MB for one wave per (page, heads).
+constexpr int kAppendThreads = 256;
+constexpr int kAppendMaxP = 64;
+constexpr int kAppendRows = kAppendMaxP / (kAppendThreads / kWave);  // rows per thread (16)
+
+template <bool FP8>
+__global__ __launch_bounds__(kAppendThreads) void paged_append_wg_kernel(AppendArgs a) {
+  extern __shared__ __align__(16) uint4 stage[];  // [2][P][64]: K rows, then V rows
+  __shared__ float amx[2][kAppendThreads / kWave][kWave];
+  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
+  const int c = lane, hl = c / a.lph, dc = c - hl * a.lph;
+  const int hpw = kWave / a.lph;  // heads per wave (lph divides 64)
+  const int h = blockIdx.y * hpw + hl;
+  const int p = blockIdx.x;
+  const int P = a.P;
+  const bool col_ok = h < a.H;
+  int32_t slot = -1;
+  if (col_ok) slot = a.unit_table[static_cast<int64_t>(h) * a.max_chunks + a.cid];
+  const bool go = col_ok && slot >= 0 && slot < a.n_slots;
+  const int t_first = p * P;
+  const int nvalid = max(0, min(P, a.tokens - t_first));
+  const int64_t page = static_cast<int64_t>(slot) * a.ppc + p;
+  const bf16_t* ksrc = a.k + static_cast<int64_t>(h) * a.ks2 + dc * 8;
+  const bf16_t* vsrc = a.v + static_cast<int64_t>(h) * a.vs2 + dc * 8;
+  constexpr int NR = kAppendRows;
+  uint4 kr[NR], vr[NR];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int r = w + 4 * j;
+    kr[j] = vr[j] = make_uint4(0, 0, 0, 0);
+    if (go && r < nvalid) {
+      kr[j] = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + r) * a.ks1);
+      vr[j] = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + r) * a.vs1);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int r = w + 4 * j;
+    if (r < nvalid) {
+      stage[r * kWave + c] = kr[j];
+      stage[(P + r) * kWave + c] = vr[j];
+    }
+  }
+  if constexpr (!FP8) {
+    if (go) {
+      uint4* kd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_k) + page * P * a.D + dc * 8);
+      uint4* vd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_v) + page * P * a.D + dc * 8);
+      const int64_t row = a.D / 8;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const int r = w + 4 * j;
+        if (r < P) {
+          kd[r * row] = kr[j];
+          vd[r * row] = vr[j];
+        }
+      }
+    }
+  } else {
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      float fk[8], fv[8];
+      unpack_bf16x8(kr[j], fk);
+      unpack_bf16x8(vr[j], fv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mk = fmaxf(mk, fabsf(fk[i]));
+        mv = fmaxf(mv, fabsf(fv[i]));
+      }
+    }
+    // max over the lanes of one head in this wave (exact, order-free), then over the 4 waves
+    for (int m = 1; m < a.lph; m <<= 1) {
+      mk = fmaxf(mk, __shfl_xor(mk, m, kWave));
+      mv = fmaxf(mv, __shfl_xor(mv, m, kWave));
+    }
+    amx[0][w][lane] = mk;
+    amx[1][w][lane] = mv;
+    __syncthreads();
+#pragma unroll
+    for (int ww = 0; ww < kAppendThreads / kWave; ++ww) {
+      mk = fmaxf(mk, amx[0][ww][lane]);
+      mv = fmaxf(mv, amx[1][ww][lane]);
+    }
+    if (go) {
+      const float ik = mk > 0.0f ? 448.0f / mk : 1.0f;
+      const float iv = mv > 0.0f ? 448.0f / mv : 1.0f;
+      uint2* kd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_k) + page * P * a.D + dc * 8);
+      uint2* vd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_v) + page * P * a.D + dc * 8);
+      const int64_t row = a.D / 8;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const int r = w + 4 * j;
+        if (r < P) {
+          uint2 kq = make_uint2(0, 0), vq = make_uint2(0, 0);
+          if (r < nvalid) {
+            float fk[8], fv[8];
+            unpack_bf16x8(kr[j], fk);
+            unpack_bf16x8(vr[j], fv);
+            kq = quant8(fk, ik);
+            vq = quant8(fv, iv);
+          }
+          kd[r * row] = kq;
+          vd[r * row] = vq;
+        }
+      }
+      if (w == 0 && dc == 0) {
+        a.scale_k[page] = mk > 0.0f ? mk / 448.0f : 1.0f;
+        a.scale_v[page] = mv > 0.0f ? mv / 448.0f : 1.0f;
+      }
+    }
+  }
+  __syncthreads();
+  // pooled rows: wave 0 adds the K rows, wave 1 the V rows, each column in token order
+  if (w < 2 && go) {
+    const uint4* src = stage + (w == 0 ? 0 : P * kWave) + c;
+    float sum[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
+    int r = 0;
+    for (; r + 8 <= nvalid; r += 8) {
+      uint4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = src[(r + u) * kWave];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        float f[8];
+        unpack_bf16x8(x[u], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum[i] += f[i];
+      }
+    }
+    for (; r < nvalid; ++r) {
+      float f[8];
+      unpack_bf16x8(src[r * kWave], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum[i] += f[i];
+    }
+    const float cnt = static_cast<float>(nvalid);
+    const int64_t crow = static_cast<int64_t>(a.cid) * a.ppc + p;
+    if (w == 0 && a.k_cmp != nullptr)
+      *reinterpret_cast<uint4*>(a.k_cmp + crow * a.cs1 + h * a.cs2 + dc * 8) = mean8(sum, cnt, nvalid);
+    if (w == 1 && a.v_cmp != nullptr)
+      *reinterpret_cast<uint4*>(a.v_cmp + crow * a.vcs1 + h * a.vcs2 + dc * 8) = mean8(sum, cnt, nvalid);
+  }
+  if (go && w == 0 && p == 0 && dc == 0 && a.stamp != nullptr && a.epoch > 0)
+    a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
+}
+
 // ---- batched unit copies (evict to the host pool, promote to HBM) ---------------------------
 constexpr int64_t kCopyPart = 64 * 1024;  // bytes per workgroup
 
@@ -565,6 +720,23 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
   OMM_REQUIRE(kWave % a.lph == 0, OMM_EUNSUPPORTED, "omm_paged_append: head dim %d", D);
   const dim3 grid(static_cast<unsigned>(ppc), static_cast<unsigned>(cdiv64(H, kWave / a.lph)));
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (P <= kAppendMaxP) {
+    const size_t lds = static_cast<size_t>(2) * P * kWave * sizeof(uint4);
+    const void* fn = kv->dtype == OMM_BF16
+                         ? reinterpret_cast<const void*>(&paged_append_wg_kernel<false>)
+                         : reinterpret_cast<const void*>(&paged_append_wg_kernel<true>);
+    if (lds > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(lds));
+      OMM_REQUIRE(e == hipSuccess, OMM_EHIP, "omm_paged_append: LDS attribute: %s",
+                  hipGetErrorString(e));
+    }
+    if (kv->dtype == OMM_BF16)
+      paged_append_wg_kernel<false><<<grid, kAppendThreads, lds, s>>>(a);
+    else
+      paged_append_wg_kernel<true><<<grid, kAppendThreads, lds, s>>>(a);
+    return check_launch("omm_paged_append");
+  }
   if (kv->dtype == OMM_BF16)
     paged_append_kernel<false><<<grid, kWave, 0, s>>>(a);
   else

@@ -170,12 +170,18 @@ def test_paged_append_rejects_partial_chunks():
                   None, None, 0, _lib.stream_of(k), error=BlockKVBackendError)
 
 
-def test_paged_append_bf16_bitexact_and_pooled():
+# (heads, head dim, page tokens): pages of at most 64 tokens take the 4-wave staged kernel
+# (partial head groups: 3 of 4 heads, 5 of 8), longer pages the one-wave kernel
+APPEND_GEOMS = [(3, 128, 64), (5, 64, 30), (2, 128, 96)]
+
+
+@pytest.mark.parametrize("H,D,P", APPEND_GEOMS)
+def test_paged_append_bf16_bitexact_and_pooled(H, D, P):
     from omnimem_amd.block_cache import PagedKVCache
     from omnimem_amd.index_topk import block_pool
     S = 4680
-    g = torch.Generator().manual_seed(S)
-    H, D, C, P = 3, 128, 4680, 64
+    g = torch.Generator().manual_seed(S + P)
+    C = 4680
     cache = PagedKVCache(1, H, D, max_chunks=4, chunk_len=C, page_tokens=P, hbm_slots=12,
                          window_chunks=0)
     k, v = _chunk(g, S, H, D), _chunk(g, S, H, D)
@@ -196,10 +202,11 @@ def test_paged_append_bf16_bitexact_and_pooled():
     np.testing.assert_array_equal(got_k[:, :nfull], block_pool(k.to(DEV), P).float().cpu().numpy())
 
 
-def test_paged_append_fp8_codes_and_scales_bitexact():
+@pytest.mark.parametrize("H,D,P", [(2, 128, 64), (3, 64, 30), (2, 128, 80)])
+def test_paged_append_fp8_codes_and_scales_bitexact(H, D, P):
     from omnimem_amd.block_cache import PagedKVCache
-    torch.manual_seed(7)
-    H, D, C, P = 2, 128, 4680, 64
+    torch.manual_seed(7 + P)
+    C = 4680
     cache = PagedKVCache(1, H, D, max_chunks=2, chunk_len=C, page_tokens=P, dtype="fp8",
                          hbm_slots=4, window_chunks=0)
     k, v = _chunk(None, C, H, D, 3.0, True), _chunk(None, C, H, D, 2.0, True)
