@@ -36,6 +36,7 @@ if ROOT not in sys.path:
 METRIC = "sel-attn TFLOP/s + %MFMA peak; top-k GB/s; ms per AR chunk at 60s cache"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 
 # config 3, one layer
 M = N = 32760
@@ -70,8 +71,11 @@ ALGO = {
         # tokens, 4 D FLOPs each (bf16 pages, some host-resident; fp8 pages)
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 2>": (
             "flops", 4 * D * _AR_C * H * TOPK * BS),
-        "sel_fwd_mfma_kernel<bf16_t, PagedAcc<unsigned char>, 128>": (
+        "sel_fwd_mfma_kernel<bf16_t, PagedAcc<unsigned char>, 128, false>": (
             "flops", 4 * D * _AR_C * H * TOPK * BS),
+        # the fp8 Q K^T variant: half the FLOPs (Q K^T) on fp8 MFMA, half (P V) on bf16
+        "sel_fwd_mfma_kernel<bf16_t, PagedAcc<unsigned char>, 128, true>": (
+            "flops_qk8", 4 * D * _AR_C * H * TOPK * BS),
         # bf16 window attention over the window's pages: 4680 queries x 3 chunks of keys
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 4>": (
             "flops", 4 * D * _AR_C * H * _AR_WIN * _AR_C),
@@ -197,6 +201,11 @@ def rocprof_summary(out: str, d: str, command: str, workload: str = "c3"):
                 k["useful_flops"] = amount
                 k["useful_TFLOPs"] = round(amount / avg_ns / 1e3, 1)
                 k["frac_bf16_peak"] = round(amount / avg_ns / 1e3 / PEAK_BF16_TFLOPS, 4)
+                if unit == "flops_qk8":
+                    # time at peak: the Q K^T half at the fp8 rate, the P V half at bf16's
+                    ideal_ns = (amount / 2) / (PEAK_FP8_TFLOPS * 1e3) + \
+                               (amount / 2) / (PEAK_BF16_TFLOPS * 1e3)
+                    k["frac_mixed_fp8_bf16_peak"] = round(ideal_ns / avg_ns, 4)
         kernels[name] = k
     # further counter passes (directories pmc_*): medians per dispatch, and for MFMA kernels the
     # executed bf16 MFMA rate (SQ_INSTS_VALU_MFMA_MOPS_BF16 counts units of 512 FLOPs), the MFMA
@@ -256,7 +265,8 @@ def summary_md(res: dict, path: str):
                f"{k['useful_flops']:,} FLOP" if "useful_flops" in k else "")
         ach = (f"{k['algorithmic_GBps']} GB/s" if "algorithmic_bytes" in k else
                f"{k['useful_TFLOPs']} TFLOP/s" if "useful_flops" in k else "")
-        frac = k.get("frac_hbm_8TBps", k.get("frac_bf16_peak", ""))
+        frac = k.get("frac_hbm_8TBps", k.get("frac_mixed_fp8_bf16_peak",
+                                              k.get("frac_bf16_peak", "")))
         shown = name if len(name) <= 72 else name[:69] + "..."
         lines.append(f"| `{shown}` | {k['calls']} | {k['avg_us']} | "
                      f"{k.get('hbm_bytes_scaled', ''):,} | {k.get('hbm_GBps', '')} | {alg} | "
@@ -457,7 +467,7 @@ def cpu_baseline_ar(history: int = 80, q_small: int = 64, q_large: int = 256):
 
 
 def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
-           keep_window_kv: Optional[bool] = None):
+           keep_window_kv: Optional[bool] = None, qk_fp8: bool = False):
     """Configs 4 / 5: ms per AR chunk with ``history`` chunks cached, 48 GB HBM budget.  The
     sliding window of a bf16 cache is read from the cache's pages; an fp8 cache keeps a dense
     bf16 ring of the window (``keep_window_kv`` overrides either choice)."""
@@ -472,7 +482,7 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
                          chunk_len=cfg.chunk_tokens, page_tokens=cfg.page_tokens, dtype=dtype,
                          hbm_budget_bytes=int(budget_bytes), window_chunks=cfg.window_chunks,
                          keep_window_kv=(dtype == "fp8") if keep_window_kv is None
-                         else keep_window_kv)
+                         else keep_window_kv, qk_fp8=qk_fp8)
     model = WanNSAAR(cfg, cache, seed=4)
     t_alloc = time.perf_counter() - t0
     t0 = time.perf_counter()
@@ -512,6 +522,7 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
     d = lambda key: (s1[key] - s0[key]) // steps
     res = {
         "dtype": "fp8e4m3" if dtype == "fp8" else "bf16",
+        "qk": "fp8 MFMA (queries quantised per row)" if qk_fp8 else "bf16 MFMA",
         "ms_per_ar_chunk": round(ms_chunk, 2),
         "steps": steps,
         "cached_chunks_at_start": history,
@@ -581,7 +592,8 @@ def main():
     if args.ar_only:
         print(json.dumps({"ms_per_ar_chunk": {
             "bf16": run_ar(torch.bfloat16, args.ar_history, args.ar_steps),
-            "fp8": run_ar("fp8", args.ar_history, args.ar_steps)}}), flush=True)
+            "fp8": run_ar("fp8", args.ar_history, args.ar_steps),
+            "fp8_qk8": run_ar("fp8", args.ar_history, args.ar_steps, qk_fp8=True)}}), flush=True)
         return
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(3)
@@ -711,6 +723,7 @@ def main():
         res["ms_per_ar_chunk"] = {
             "bf16": run_ar(torch.bfloat16, args.ar_history, args.ar_steps),
             "fp8": run_ar("fp8", args.ar_history, args.ar_steps),
+            "fp8_qk8": run_ar("fp8", args.ar_history, args.ar_steps, qk_fp8=True),
         }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(q, k, v, ids, args.cpu_seconds)

@@ -126,11 +126,14 @@ typedef struct omm_paged_kv {
   uint8_t* page_seen;         /* [num_heads][max_chunks][pages_per_chunk]: set to 1 for every
                                  page a selection lists since the caller last cleared it (unique
                                  pages read, e.g. host-link bytes), or NULL */
+  int32_t qk_fp8;             /* fp8 caches: 1 = quantise the queries to e4m3 per query row
+                                 (scale amax / 448) and compute Q K^T on fp8 MFMA with the K page
+                                 codes (head dim 64 / 128); 0 = dequantise K to bf16 */
 } omm_paged_kv;
 
 /* ---- library ------------------------------------------------------------------------- */
 const char* omm_last_error(void);
-int omm_abi_version(void); /* 2 */
+int omm_abi_version(void); /* 3 */
 
 /* Pinned, device-mapped host memory for the cache's host pool; *dev receives the device
  * address (equal to *host on ROCm with unified addressing, but always use *dev on device). */

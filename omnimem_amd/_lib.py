@@ -48,6 +48,7 @@ class PagedKV(ctypes.Structure):
         ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32),
         ("n_slots", ctypes.c_int32), ("n_host_slots", ctypes.c_int32),
         ("page_seen", ctypes.c_void_p),
+        ("qk_fp8", ctypes.c_int32),
     ]
 
 

@@ -107,6 +107,8 @@ class PagedKVCache:
     (page, head) for K and for V).  Capacity: ``hbm_slots`` units per pool, or derived from
     ``hbm_budget_bytes`` (K + V + scales).  ``host_slots`` defaults to the units the HBM pool
     cannot hold plus one chunk of every layer and head (the slack a flush reserves).
+    ``qk_fp8`` (fp8 caches): the selection quantises the queries to e4m3 per query row and runs
+    Q K^T on fp8 MFMA with the K page codes, instead of dequantising K to bf16.
     """
 
     def __init__(self, num_layers: int, num_heads: int, head_dim: int, max_chunks: int,
@@ -114,7 +116,7 @@ class PagedKVCache:
                  hbm_budget_bytes: Optional[int] = None, hbm_slots: Optional[int] = None,
                  host_slots: Optional[int] = None, lru_max_size: int = 0,
                  window_chunks: Optional[int] = 3, sink_chunks: int = 0,
-                 keep_window_kv: bool = True,
+                 keep_window_kv: bool = True, qk_fp8: bool = False,
                  device="cuda"):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -126,6 +128,9 @@ class PagedKVCache:
         self.fp8 = dtype == "fp8" or dtype == torch.float8_e4m3fn
         if not self.fp8 and dtype != torch.bfloat16:
             raise BlockKVBackendError(f"cache dtype must be bfloat16 or fp8, got {dtype}")
+        if qk_fp8 and not self.fp8:
+            raise BlockKVBackendError("qk_fp8 needs an fp8 cache")
+        self.qk_fp8 = bool(qk_fp8)
         self.elem = 1 if self.fp8 else 2
         self.unit_elems = self.ppc * self.P * self.D
         self.unit_bytes = self.unit_elems * self.elem
@@ -262,6 +267,7 @@ class PagedKVCache:
         kv.head_dim = self.D
         kv.dtype = _lib.OMM_FP8E4M3 if self.fp8 else _lib.OMM_BF16
         kv.n_slots, kv.n_host_slots = self.n_slots, self.n_host
+        kv.qk_fp8 = 1 if self.qk_fp8 else 0
         return kv
 
     # ---------------------------------------------------------------- append

@@ -34,6 +34,23 @@ template <> struct Mfma<f16_t> {
   }
 };
 
+// e4m3 x e4m3 -> fp32, 16 x 16 x 32: lane l holds A row l % 16 and B column l % 16, k = 8 (l / 16)
+// .. + 7 as 8 bytes (the 16x16x32 bf16 layout with 8-bit elements); products are exact in fp32.
+__device__ __forceinline__ f32x4 mfma_fp8(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a),
+                                                    __builtin_bit_cast(long, b), c, 0, 0, 0);
+}
+
+// 8 packed bf16 -> 8 floats (exact)
+__device__ __forceinline__ void unpack_bf16x8_sel(const uint4& r, float (&f)[8]) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+    f[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+  }
+}
+
 // ---- block accessors ---------------------------------------------------------------------
 // A resolved block: nvalid tokens visible from row 0, rows at k + r*sk (elements of its storage
 // type), k == nullptr when the block is skipped.

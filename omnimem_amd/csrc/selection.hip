@@ -58,14 +58,18 @@ template <> struct Row8<uint8_t> {
 //   V: quad q = tid + 128 j -> dims slice tid % DC, keys 4 (tid / DC + (128 / DC) j) + r, r < 4
 // Each thread's byte offset inside a tile is computed once; a tile adds a wave-uniform base, so
 // the loads take the scalar-base + 32-bit-offset form with no per-load address arithmetic.
-template <typename KVT, int D>
+// RAWK (fp8 pages): K stays in e4m3 codes (8 bytes per unit) for the fp8 QK^T MFMA; V is
+// dequantised as usual.
+template <typename KVT, int D, bool RAWK = false>
 struct Stager {
   static constexpr int DC = D / 8;                 // 16-byte slices per row
   static constexpr int KU = 64 * DC / 128;         // K units per thread
   static constexpr int VQ = 16 * DC / 128;         // V quads per thread
   static constexpr int RS = 128 / DC;              // rows between a thread's units
   static constexpr int ES = static_cast<int>(sizeof(KVT));
-  uint4 k[KU];
+  static constexpr int KP8 = D + 16;               // LDS row pitch of raw K codes (bytes)
+  uint4 k[RAWK ? 1 : KU];
+  uint2 k8[RAWK ? KU : 1];
   uint4 v[VQ][4];
   uint32_t koff, voff;                             // bytes, within a tile
 
@@ -76,7 +80,10 @@ struct Stager {
 
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int j = 0; j < KU; ++j) k[j] = make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < KU; ++j) {
+      if constexpr (RAWK) k8[j] = make_uint2(0, 0);
+      else k[j] = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < VQ; ++j)
 #pragma unroll
@@ -119,7 +126,8 @@ struct Stager {
     for (int j = 0; j < KU; ++j) {
       const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
       if (FULL || row0 + RS * j < n) {
-        if constexpr (U16) k[j] = load_u16(p + koff);
+        if constexpr (RAWK) k8[j] = *reinterpret_cast<const uint2*>(p + koff);
+        else if constexpr (U16) k[j] = load_u16(p + koff);
         else k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
       }
     }
@@ -142,7 +150,10 @@ struct Stager {
 #pragma unroll
     for (int j = 0; j < KU; ++j) {
       const int key = tid / DC + RS * j;
-      *reinterpret_cast<uint4*>(Ks + key * KP + dc * 8) = k[j];
+      if constexpr (RAWK)
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(Ks) + key * KP8 + dc * 8) = k8[j];
+      else
+        *reinterpret_cast<uint4*>(Ks + key * KP + dc * 8) = k[j];
     }
 #pragma unroll
     for (int j = 0; j < VQ; ++j) {
@@ -173,7 +184,11 @@ struct Stager {
 // bytes per MFMA FLOP are half those of 16 queries per wave.
 constexpr int kMfmaThreads = 128;
 
-template <typename QT, typename Acc, int D>
+// QK8 (fp8 pages only): the queries are quantised to e4m3 per query row (scale amax / 448), K
+// stays in its page codes, S = (Qc Kc^T) * s_q * s_k on v_mfma_f32_16x16x32_fp8_fp8 (products
+// of e4m3 codes are exact in fp32), the K page scale s_k is one per 64-key tile and s_q one per
+// query column, both folded into the softmax's exponent scale.  PV stays bf16.
+template <typename QT, typename Acc, int D, bool QK8 = false>
 __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
     int MG, int T, int chunk, float scale, int nsub) {
@@ -181,6 +196,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   constexpr int KS = 64 * KP, VS = D * kVP;
   constexpr int SD = D / 32;   // k-steps of QK^T
   constexpr int ND = D / 16;   // d-tiles of PV
+  static_assert(!QK8 || sizeof(typename Acc::KV) == 1, "fp8 QK^T needs fp8 pages");
   __shared__ __align__(16) uint16_t lds[KS + VS];
   uint16_t* Ks = lds;
   uint16_t* Vt = lds + KS;
@@ -212,6 +228,35 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
       qb[x][s] = q_ok[x] ? *reinterpret_cast<const uint4*>(q.at(b, my_q[x], h, 32 * s + 8 * j4))
                          : make_uint4(0, 0, 0, 0);
   }
+  // fp8 queries: per-row amax over the 4 lane groups holding the row's dims, scale amax / 448,
+  // codes by round-to-nearest-even (v_cvt_pk_fp8_f32)
+  uint2 qb8[2][SD];
+  float sq[2] = {1.0f, 1.0f};
+  if constexpr (QK8) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      float f[SD][8];
+      float am = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        unpack_bf16x8_sel(qb[x][s], f[s]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(f[s][e]));
+      }
+      am = fmaxf(am, __shfl_xor(am, 16, kWave));
+      am = fmaxf(am, __shfl_xor(am, 32, kWave));
+      sq[x] = am > 0.0f ? am / 448.0f : 1.0f;
+      const float inv = am > 0.0f ? 448.0f / am : 1.0f;
+#pragma unroll
+      for (int s = 0; s < SD; ++s) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(f[s][e] * inv, -448.0f), 448.0f);
+        qb8[x][s] = make_uint2(f32x4_to_e4m3(y[0], y[1], y[2], y[3]),
+                               f32x4_to_e4m3(y[4], y[5], y[6], y[7]));
+      }
+    }
+  }
   const bool wave_active = (m0 + 32 * w) < m_end;
   // PV operand row bases (see the V^T swizzle): bit 0 of the chunk is j4_0 ^ (l16 >> 3), bit 1
   // is j4_1 ^ (i & 1)
@@ -238,25 +283,42 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
         qb[x][s].y ^= 0x80008000u;
         qb[x][s].z ^= 0x80008000u;
         qb[x][s].w ^= 0x80008000u;
+        qb8[x][s].x ^= 0x80808080u;  // e4m3 sign bits
+        qb8[x][s].y ^= 0x80808080u;
       }
   }
 
   using KVT = typename Acc::KV;
-  Stager<KVT, D> st;
+  Stager<KVT, D, QK8> st;
+  float sk_next = 1.0f;  // K page scale of the tile being staged (QK8)
   WaveWalk<Acc> wk;
   wk.start(acc, b, g, h, T, qc);
   st.init(tid, wk.br.sk, wk.br.sv);  // row strides are the same for every block of a call
   st.zero();
   // raw pointer tables may hold blocks that are not 16-byte aligned (2-byte loads for those)
   constexpr bool kMis = Acc::kMayMisalign && sizeof(KVT) == 2;
-  if (wk.valid) st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);
+  if (wk.valid) {
+    st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);
+    sk_next = wk.br.scale_k;
+  }
   while (wk.valid) {
     __syncthreads();  // every wave is done reading the previous tile
     st.store(Ks, Vt, tid);
     __syncthreads();
     const int tile_n = wk.n;
+    const float sk_cur = sk_next;
     wk.advance(acc, b, g, h, T, qc);
-    if (wk.valid) st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);  // in flight during the MFMAs
+    if (wk.valid) {
+      st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);  // in flight during the MFMAs
+      sk_next = wk.br.scale_k;
+    }
+    // exponent scale per query block: the softmax scale, and for fp8 scores the two
+    // dequantisation scales
+    float c2x[2] = {c2, c2};
+    if constexpr (QK8) {
+      c2x[0] = c2 * sq[0] * sk_cur;
+      c2x[1] = c2 * sq[1] * sk_cur;
+    }
     if (wave_active) {
       // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks.  A
       // partial tile seeds the accumulators with 0 / -inf per key, so masked keys come out -inf.
@@ -268,9 +330,17 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
           s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int s = 0; s < SD; ++s) {
-            const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
-            s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
-            s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+            if constexpr (QK8) {
+              const uint2 a8 = *reinterpret_cast<const uint2*>(
+                  reinterpret_cast<const uint8_t*>(Ks) + (16 * t + l16) * Stager<KVT, D, true>::KP8 +
+                  32 * s + 8 * j4);
+              s4[0][t] = mfma_fp8(a8, qb8[0][s], s4[0][t]);
+              s4[1][t] = mfma_fp8(a8, qb8[1][s], s4[1][t]);
+            } else {
+              const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
+              s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+              s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);  // bound the operand reads in flight (registers)
         }
@@ -284,9 +354,17 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
           s4[1][t] = bias;
 #pragma unroll
           for (int s = 0; s < SD; ++s) {
-            const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
-            s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
-            s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+            if constexpr (QK8) {
+              const uint2 a8 = *reinterpret_cast<const uint2*>(
+                  reinterpret_cast<const uint8_t*>(Ks) + (16 * t + l16) * Stager<KVT, D, true>::KP8 +
+                  32 * s + 8 * j4);
+              s4[0][t] = mfma_fp8(a8, qb8[0][s], s4[0][t]);
+              s4[1][t] = mfma_fp8(a8, qb8[1][s], s4[1][t]);
+            } else {
+              const uint4 a = *reinterpret_cast<const uint4*>(Ks + (16 * t + l16) * KP + 32 * s + 8 * j4);
+              s4[0][t] = Mfma<QT>::run(a, qb[0][s], s4[0][t]);
+              s4[1][t] = Mfma<QT>::run(a, qb[1][s], s4[1][t]);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -301,10 +379,10 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           mt = fmaxf(mt, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
-        if (__ballot(mt * c2 > m2[x] + 8.0f) != 0ull) {
+        if (__ballot(mt * c2x[x] > m2[x] + 8.0f) != 0ull) {
           mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
           mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-          const float mcand = fmaxf(m2[x], mt * c2);
+          const float mcand = fmaxf(m2[x], mt * c2x[x]);
           const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
           const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
           lsum[x] *= alpha;
@@ -318,7 +396,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, -msafe));
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2x[x], -msafe));
             s4[x][t][r] = pv;
             ps += pv;
           }
@@ -783,6 +861,16 @@ int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float*
   return check_launch("selection attention (mfma)");
 }
 
+// fp8 pages with the fp8 QK^T (queries quantised per row), head dim 64 or 128
+template <typename Acc, int D>
+int launch_qk8(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
+               const Acc& acc, int chunk, float scale, hipStream_t s) {
+  sel_fwd_mfma_kernel<bf16_t, Acc, D, true><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
+      make_view<const bf16_t>(q), make_view<bf16_t>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
+      chunk, scale, gm.nsub);
+  return check_launch("selection attention (fp8 QK)");
+}
+
 template <typename QT, typename Acc, int D>
 int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
                const Acc& acc, int chunk, float scale, hipStream_t s) {
@@ -995,6 +1083,15 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
                           kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};
+    if (kv->qk_fp8) {
+      OMM_REQUIRE(mfma && scale != 0.0f && __builtin_isfinite(scale) &&
+                      (kv->head_dim == 64 || kv->head_dim == 128),
+                  OMM_EUNSUPPORTED,
+                  "omm_sel_fwd_paged: the fp8 QK^T variant needs head dim 64 or 128, 16-byte q / "
+                  "out rows and a finite non-zero scale");
+      return kv->head_dim == 128 ? launch_qk8<PagedAcc<uint8_t>, 128>(gm, *q, *out, lse, acc, 1, scale, s)
+                                 : launch_qk8<PagedAcc<uint8_t>, 64>(gm, *q, *out, lse, acc, 1, scale, s);
+    }
     return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s);
   }
   return set_error(OMM_EINVAL, "omm_sel_fwd_paged: unsupported cache dtype %d", kv->dtype);

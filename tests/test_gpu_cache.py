@@ -290,6 +290,101 @@ def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype, G):
     assert torch.equal(out, out3)
 
 
+def _quantized_rows(q: torch.Tensor) -> np.ndarray:
+    """The e4m3 image of q [1, M, H, D] quantised per (query, head) row with the page rule
+    (scale amax / 448, round to nearest even): codes * scale, fp32."""
+    x = q.float().numpy()
+    out = np.empty_like(x)
+    for m in range(x.shape[1]):
+        for h in range(x.shape[2]):
+            c, sc = O.quantize_pages(x[0, m, h][None, :], 1)
+            out[0, m, h] = O.dequantize_pages(c, sc)[0]
+    return out
+
+
+def _fp8_cache_images(cache, n, round_k: bool):
+    """K and V as the kernels see them: codes * page scale (K rounded to bf16 when the kernel
+    stages it in bf16), V rounded to bf16."""
+    H, D, C = cache.H, cache.D, cache.chunk_len
+    kk = np.zeros((1, n * C, H, D), np.float32)
+    vv = np.zeros_like(kk)
+    for cid in range(n):
+        for h in range(H):
+            kc, vc, sk, sv = cache.read_unit(0, h, cid)
+            k = O.dequantize_pages(kc.numpy(), sk.numpy()[:, None, None]).reshape(-1, D)[:C]
+            v = O.dequantize_pages(vc.numpy(), sv.numpy()[:, None, None]).reshape(-1, D)[:C]
+            kk[0, cid * C:(cid + 1) * C, h] = O.round_to(k, "bf16") if round_k else k
+            vv[0, cid * C:(cid + 1) * C, h] = O.round_to(v, "bf16")
+    return kk, vv
+
+
+@pytest.mark.parametrize("D,G,sign", [(128, 64, 1.0), (64, 128, 1.0), (128, 64, -1.0)])
+def test_paged_selection_fp8_qk_matches_oracle(D, G, sign):
+    """The fp8 Q K^T variant (qk_fp8): queries quantised to e4m3 per query row, K page codes on
+    fp8 MFMA.  Checked against the float64 oracle run on the quantised queries and the
+    dequantised K (V dequantised and rounded to bf16, as staged), at the bf16 tolerances; a
+    negative scale exercises the codes' sign flip."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(int(D + G + (sign < 0)))
+    torch.manual_seed(D + G)
+    H, C, P, T, n = 3, 4680, 64, 16, 3
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype="fp8",
+                         qk_fp8=True, hbm_slots=H * n, host_slots=H * n, window_chunks=0)
+    ks = [_chunk(g, C, H, D, 0.3, True) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, True) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    M = 1000
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    MG = -(-M // G)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32)
+    ids[0, 2, 1, :5] = -1
+    scale = sign * D ** -0.5
+    out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, softmax_scale=scale, return_lse=True)
+    kk, vv = _fp8_cache_images(cache, n, round_k=False)
+    want_o, want_l = O.selection_attention(_quantized_rows(q), kk, vv, ids.numpy(), G, scale,
+                                           O.paged_block_tokens(C, P, n))
+    _check_attn(out, lse, want_o, want_l)
+
+
+def test_fp8_quantisation_error_against_bf16_cache():
+    """Config 5's error budget, per variant: selection-attention output over
+    Student-t(4) K/V against float64 on the original bf16 values, for the bf16 cache, the fp8
+    cache with bf16 queries, and the fp8 cache with fp8 queries (qk_fp8).  The fp8 cache errors
+    are the quantisation's; the test bounds them and prints them."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(55)
+    torch.manual_seed(55)
+    H, D, C, P, T, n, G = 4, 128, 4680, 64, 16, 3, 64
+    ks = [_chunk(g, C, H, D, 1.0, True) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, True) for _ in range(n)]
+    M = 2048
+    q = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16)
+    MG = M // G
+    ids = torch.stack([torch.randperm(n * -(-C // P), generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32)
+    ref, _ = O.selection_attention(q.float().numpy(), torch.cat(ks, 1).float().numpy(),
+                                   torch.cat(vs, 1).float().numpy(), ids.numpy(), G, D ** -0.5,
+                                   O.paged_block_tokens(C, P, n))
+    errs = {}
+    for name, kw in (("bf16", dict(dtype=torch.bfloat16)), ("fp8", dict(dtype="fp8")),
+                     ("fp8_qk", dict(dtype="fp8", qk_fp8=True))):
+        cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P,
+                             hbm_slots=H * n, host_slots=H * n, window_chunks=0, **kw)
+        for cid in range(n):
+            cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+        out = cache.select(q.to(DEV), ids.to(DEV), 0, G).float().cpu().numpy()
+        d = np.abs(out.astype(np.float64) - ref)
+        rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
+        errs[name] = (float(d.max()), float(d.mean()), float(rel))
+        cache.close()
+    print("selection output error vs float64 on bf16 K/V (max-abs, mean-abs, rel-L2):", errs)
+    assert errs["bf16"][2] < 5e-3
+    assert errs["fp8"][2] < 0.06 and errs["fp8_qk"][2] < 0.08
+    assert errs["fp8_qk"][2] >= errs["fp8"][2] * 0.9  # quantising q adds error, not removes it
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
 def test_window_attention_reads_pages_in_place(dtype):
     """SWA over the paged cache (window_attention without the dense ring) against float64
