@@ -270,6 +270,17 @@ int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_v
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
                       int32_t epoch, void* stream);
+/* The same selection with the NSA branch mix fused into its epilogue:
+ *   out = g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa
+ * per (query, head), in fp32 with one rounding to bf16, where o_slc is the selection output
+ * (never written separately) and lse, when given, is the selection's.  gates: bf16 [1, M, H, 3]
+ * (the branch gates after their sigmoid), o_cmp / o_swa: bf16 [1, M, H, D] with unit dim
+ * stride.  Needs the MFMA path (head dim 64 or 128, 16-byte q / out rows, finite non-zero scale).
+ * Reference: the gate combine of causal_wan_nsa_model.py:541-546 after the three branches. */
+int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
+                            int32_t group_size, float scale, const omm_view4* gates,
+                            const omm_view4* o_cmp, const omm_view4* o_swa, const omm_view4* out,
+                            float* lse, int32_t epoch, void* stream);
 /* Batched unit copies: for i < n copy unit_bytes from src_k + src_slot[i]*unit_bytes to
  * dst_k + dst_slot[i]*unit_bytes (either side may be the mapped host pool), the same for the
  * optional V pair and the optional scale pairs (scale_bytes per unit).  src_slot / dst_slot are

@@ -511,9 +511,14 @@ class PagedKVCache:
     # ---------------------------------------------------------------- selection
     def select(self, q: torch.Tensor, block_indices: torch.Tensor, layer: int, group_size: int,
                softmax_scale: Optional[float] = None, return_lse: bool = False,
-               out: Optional[torch.Tensor] = None):
+               out: Optional[torch.Tensor] = None, gates: Optional[torch.Tensor] = None,
+               o_cmp: Optional[torch.Tensor] = None, o_swa: Optional[torch.Tensor] = None):
         """Selection attention of q (bf16 [1, M, H, D]) over the pages listed in block_indices
-        (int32 [1, ceil(M/G), H, T], page id = chunk * pages_per_chunk + page)."""
+        (int32 [1, ceil(M/G), H, T], page id = chunk * pages_per_chunk + page).
+
+        With ``gates`` (bf16 [1, M, H, 3], after the sigmoid) and the other two branch outputs
+        ``o_cmp`` / ``o_swa`` the kernel writes the NSA branch mix g0*o_cmp + g1*o_slc + g2*o_swa
+        (causal_wan_nsa_model.py:541-546) instead of o_slc, in one fp32 pass."""
         _lib.require_cuda((q, "q"), (block_indices, "block_indices"))
         if q.dtype != torch.bfloat16:
             raise BlockKVBackendError(f"paged selection needs bf16 queries, got {q.dtype}")
@@ -525,10 +530,22 @@ class PagedKVCache:
             out = torch.empty_like(q)
         lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device) if return_lse else None
         kv = self.layer_view(layer)
-        _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(block_indices), ctypes.byref(kv),
-                  int(group_size), float(scale), _lib.view4(out),
-                  lse.data_ptr() if lse is not None else None, self.next_epoch(),
-                  _lib.stream_of(q), error=BlockKVBackendError)
+        if gates is not None:
+            if o_cmp is None or o_swa is None:
+                raise BlockKVBackendError("the gated selection needs o_cmp and o_swa")
+            for t, name in ((gates, "gates"), (o_cmp, "o_cmp"), (o_swa, "o_swa")):
+                if t.dtype != torch.bfloat16 or not t.is_cuda:
+                    raise BlockKVBackendError(f"{name} must be a bf16 CUDA tensor")
+            _lib.call("omm_sel_fwd_paged_gated", _lib.view4(q), _lib.view4(block_indices),
+                      ctypes.byref(kv), int(group_size), float(scale), _lib.view4(gates),
+                      _lib.view4(o_cmp), _lib.view4(o_swa), _lib.view4(out),
+                      lse.data_ptr() if lse is not None else None, self.next_epoch(),
+                      _lib.stream_of(q), error=BlockKVBackendError)
+        else:
+            _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(block_indices),
+                      ctypes.byref(kv), int(group_size), float(scale), _lib.view4(out),
+                      lse.data_ptr() if lse is not None else None, self.next_epoch(),
+                      _lib.stream_of(q), error=BlockKVBackendError)
         return (out, lse) if return_lse else out
 
     # ---------------------------------------------------------------- residency

@@ -51,6 +51,44 @@ __device__ __forceinline__ void unpack_bf16x8_sel(const uint4& r, float (&f)[8])
   }
 }
 
+// Optional gate combine in the attention epilogue (the NSA branch mix): out = g[0] * o_cmp +
+// g[1] * o_slc + g[2] * o_swa per (query, head), fp32 arithmetic and one rounding; g == nullptr
+// writes o_slc alone.  Gates bf16 [B, M, H, 3] and the branch outputs bf16 [B, M, H, D] (unit
+// dim stride), element strides.
+struct GateArgs {
+  const bf16_t* g = nullptr;
+  int64_t gs0 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
+  const bf16_t* oc = nullptr;
+  int64_t cs0 = 0, cs1 = 0, cs2 = 0;
+  const bf16_t* ow = nullptr;
+  int64_t ws0 = 0, ws1 = 0, ws2 = 0;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+// One lane's 4 consecutive output dims (d0 .. d0 + 3) of query (b, m, h): o4 = o_slc (fp32,
+// normalised) -> the gated mix packed as 4 bf16.
+__device__ __forceinline__ uint2 gate_mix4(const GateArgs& ga, int b, int m, int h, int d0,
+                                           const float (&o4)[4]) {
+  const uint16_t* gp = reinterpret_cast<const uint16_t*>(ga.g + b * ga.gs0 + m * ga.gs1 + h * ga.gs2);
+  const float g0 = bf16_bits_to_f32(gp[0]), g1 = bf16_bits_to_f32(gp[ga.gs3]);
+  const float g2 = bf16_bits_to_f32(gp[2 * ga.gs3]);
+  const uint2 c = *reinterpret_cast<const uint2*>(ga.oc + b * ga.cs0 + m * ga.cs1 + h * ga.cs2 + d0);
+  const uint2 w = *reinterpret_cast<const uint2*>(ga.ow + b * ga.ws0 + m * ga.ws1 + h * ga.ws2 + d0);
+  const uint32_t cw[2] = {c.x, c.y}, ww[2] = {w.x, w.y};
+  float r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t cb = e & 1 ? cw[e >> 1] & 0xffff0000u : cw[e >> 1] << 16;
+    const uint32_t wb = e & 1 ? ww[e >> 1] & 0xffff0000u : ww[e >> 1] << 16;
+    r[e] = __builtin_fmaf(g2, __builtin_bit_cast(float, wb),
+                          __builtin_fmaf(g1, o4[e], g0 * __builtin_bit_cast(float, cb)));
+  }
+  return make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+}
+
 // ---- block accessors ---------------------------------------------------------------------
 // A resolved block: nvalid tokens visible from row 0, rows at k + r*sk (elements of its storage
 // type), k == nullptr when the block is skipped.

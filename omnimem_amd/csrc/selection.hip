@@ -191,7 +191,7 @@ constexpr int kMfmaThreads = 128;
 template <typename QT, typename Acc, int D, bool QK8 = false>
 __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
-    int MG, int T, int chunk, float scale, int nsub) {
+    int MG, int T, int chunk, float scale, int nsub, GateArgs gate) {
   constexpr int KP = D + 8;
   constexpr int KS = 64 * KP, VS = D * kVP;
   constexpr int SD = D / 32;   // k-steps of QK^T
@@ -444,6 +444,15 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
       for (int i = 0; i < ND; ++i) {
         const int d0 = 16 * i + 4 * j4;
         uint2 w2;
+        if constexpr (sizeof(QT) == 2) {
+          if (gate.g != nullptr) {  // launch-uniform
+            const float o4[4] = {o[x][i][0] * inv, o[x][i][1] * inv, o[x][i][2] * inv,
+                                 o[x][i][3] * inv};
+            w2 = gate_mix4(gate, b, my_q[x], h, d0, o4);
+            *reinterpret_cast<uint2*>(op + d0) = w2;
+            continue;
+          }
+        }
         w2.x = Mfma<QT>::pack2(o[x][i][0] * inv, o[x][i][1] * inv);
         w2.y = Mfma<QT>::pack2(o[x][i][2] * inv, o[x][i][3] * inv);
         *reinterpret_cast<uint2*>(op + d0) = w2;
@@ -475,7 +484,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 template <typename QT, typename Acc, int D, int NW>
 __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
-    int MG, int T, int chunk, float scale, int nsub) {
+    int MG, int T, int chunk, float scale, int nsub, GateArgs gate) {
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
   constexpr int SPW = NW / 2;  // 64-query subgroups per workgroup
   constexpr int NI = 8 / NW;   // copy instructions per wave per K or V tile
@@ -726,6 +735,15 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
 #pragma unroll
       for (int i2 = 0; i2 < ND; ++i2) {
         uint2 w2;
+        if constexpr (sizeof(QT) == 2) {
+          if (gate.g != nullptr) {  // launch-uniform
+            const float o4[4] = {o[x][i2][0] * inv, o[x][i2][1] * inv, o[x][i2][2] * inv,
+                                 o[x][i2][3] * inv};
+            *reinterpret_cast<uint2*>(op + 16 * i2 + 4 * j4) =
+                gate_mix4(gate, b, mq, h, 16 * i2 + 4 * j4, o4);
+            continue;
+          }
+        }
         w2.x = Mfma<QT>::pack2(o[x][i2][0] * inv, o[x][i2][1] * inv);
         w2.y = Mfma<QT>::pack2(o[x][i2][2] * inv, o[x][i2][3] * inv);
         *reinterpret_cast<uint2*>(op + 16 * i2 + 4 * j4) = w2;
@@ -854,35 +872,35 @@ inline int geom(const omm_view4& q, int64_t MGv, int64_t T, int G, Geom& g) {
 
 template <typename QT, typename Acc, int D>
 int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
-                const Acc& acc, int chunk, float scale, hipStream_t s) {
+                const Acc& acc, int chunk, float scale, hipStream_t s, const GateArgs& gate) {
   sel_fwd_mfma_kernel<QT, Acc, D><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
       make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T, chunk,
-      scale, gm.nsub);
+      scale, gm.nsub, gate);
   return check_launch("selection attention (mfma)");
 }
 
 // fp8 pages with the fp8 QK^T (queries quantised per row), head dim 64 or 128
 template <typename Acc, int D>
 int launch_qk8(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
-               const Acc& acc, int chunk, float scale, hipStream_t s) {
+               const Acc& acc, int chunk, float scale, hipStream_t s, const GateArgs& gate) {
   sel_fwd_mfma_kernel<bf16_t, Acc, D, true><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
       make_view<const bf16_t>(q), make_view<bf16_t>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
-      chunk, scale, gm.nsub);
+      chunk, scale, gm.nsub, gate);
   return check_launch("selection attention (fp8 QK)");
 }
 
 template <typename QT, typename Acc, int D>
 int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
-               const Acc& acc, int chunk, float scale, hipStream_t s) {
+               const Acc& acc, int chunk, float scale, hipStream_t s, const GateArgs& gate) {
   if (gm.nsub >= 2) {  // two 64-query subgroups per workgroup
     const int64_t grid = gm.items / gm.nsub * ((gm.nsub + 1) / 2);
     sel_fwd_dma_kernel<QT, Acc, D, 4><<<static_cast<unsigned>(grid), 4 * kWave, 0, s>>>(
         make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
-        chunk, scale, gm.nsub);
+        chunk, scale, gm.nsub, gate);
   } else {
     sel_fwd_dma_kernel<QT, Acc, D, 2><<<static_cast<unsigned>(gm.items), 2 * kWave, 0, s>>>(
         make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
-        chunk, scale, gm.nsub);
+        chunk, scale, gm.nsub, gate);
   }
   return check_launch("selection attention (dma)");
 }
@@ -921,20 +939,23 @@ inline bool qo_mfma_ok(const omm_view4& q, const omm_view4& out) {
 template <typename QT, typename Acc>
 int dispatch(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse, const Acc& acc,
              int chunk, float scale, bool mfma_ok, int64_t kv_sd, int64_t kv_row_bytes,
-             hipStream_t s) {
+             hipStream_t s, const GateArgs& gate = GateArgs{}) {
   if constexpr (sizeof(QT) == 2) {
     // the MFMA softmax needs a finite non-zero scale (its masking uses -inf scores)
     const bool ok = mfma_ok && scale != 0.0f && __builtin_isfinite(scale);
     if constexpr (sizeof(typename Acc::KV) == 2) {
       const bool rows_ok = kv_row_bytes >= 2 * gm.D && kv_row_bytes * 64 < (int64_t{1} << 31);
       if (ok && rows_ok && gm.D == 128)
-        return launch_dma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
+        return launch_dma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s, gate);
       if (ok && rows_ok && gm.D == 64)
-        return launch_dma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
+        return launch_dma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s, gate);
     }
-    if (ok && gm.D == 128) return launch_mfma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s);
-    if (ok && gm.D == 64) return launch_mfma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s);
+    if (ok && gm.D == 128) return launch_mfma<QT, Acc, 128>(gm, q, out, lse, acc, chunk, scale, s, gate);
+    if (ok && gm.D == 64) return launch_mfma<QT, Acc, 64>(gm, q, out, lse, acc, chunk, scale, s, gate);
   }
+  OMM_REQUIRE(gate.g == nullptr, OMM_EUNSUPPORTED,
+              "selection attention: the gated epilogue needs the MFMA path (bf16 q / out with "
+              "16-byte rows, head dim 64 or 128, a finite non-zero scale)");
   return launch_valu<QT, Acc>(gm, q, out, lse, acc, chunk, scale, kv_sd, s);
 }
 
@@ -1036,10 +1057,11 @@ extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const i
                           static_cast<hipStream_t>(stream));
 }
 
-extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
-                                 int32_t group_size, float scale, const omm_view4* out, float* lse,
-                                 int32_t epoch, void* stream) {
-  using namespace omm;
+namespace omm {
+namespace {
+int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
+                       int32_t group_size, float scale, const omm_view4* out, float* lse,
+                       int32_t epoch, void* stream, const GateArgs& gate) {
   int rc = check_q_out("omm_sel_fwd_paged", q, out);
   if (rc) return rc;
   OMM_REQUIRE(ids != nullptr && kv != nullptr, OMM_EINVAL, "omm_sel_fwd_paged: null argument");
@@ -1070,7 +1092,7 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
                          kv->n_slots, kv->n_host_slots};
-    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s);
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s, gate);
   }
   if (kv->dtype == OMM_FP8E4M3) {
     OMM_REQUIRE(kv->scale_k != nullptr && kv->scale_v != nullptr, OMM_EINVAL,
@@ -1089,10 +1111,51 @@ extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const
                   OMM_EUNSUPPORTED,
                   "omm_sel_fwd_paged: the fp8 QK^T variant needs head dim 64 or 128, 16-byte q / "
                   "out rows and a finite non-zero scale");
-      return kv->head_dim == 128 ? launch_qk8<PagedAcc<uint8_t>, 128>(gm, *q, *out, lse, acc, 1, scale, s)
-                                 : launch_qk8<PagedAcc<uint8_t>, 64>(gm, *q, *out, lse, acc, 1, scale, s);
+      return kv->head_dim == 128 ? launch_qk8<PagedAcc<uint8_t>, 128>(gm, *q, *out, lse, acc, 1, scale, s, gate)
+                                 : launch_qk8<PagedAcc<uint8_t>, 64>(gm, *q, *out, lse, acc, 1, scale, s, gate);
     }
-    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s);
+    return dispatch<bf16_t>(gm, *q, *out, lse, acc, 1, scale, mfma, 1, 2 * kv->head_dim, s, gate);
   }
   return set_error(OMM_EINVAL, "omm_sel_fwd_paged: unsupported cache dtype %d", kv->dtype);
+}
+}  // namespace
+}  // namespace omm
+
+extern "C" int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
+                                 int32_t group_size, float scale, const omm_view4* out, float* lse,
+                                 int32_t epoch, void* stream) {
+  return omm::sel_fwd_paged_impl(q, ids, kv, group_size, scale, out, lse, epoch, stream,
+                                 omm::GateArgs{});
+}
+
+extern "C" int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids,
+                                       const omm_paged_kv* kv, int32_t group_size, float scale,
+                                       const omm_view4* gates, const omm_view4* o_cmp,
+                                       const omm_view4* o_swa, const omm_view4* out, float* lse,
+                                       int32_t epoch, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(q != nullptr && gates != nullptr && o_cmp != nullptr && o_swa != nullptr,
+              OMM_EINVAL, "omm_sel_fwd_paged_gated: null argument");
+  OMM_REQUIRE(gates->size[0] == q->size[0] && gates->size[1] == q->size[1] &&
+                  gates->size[2] == q->size[2] && gates->size[3] == 3,
+              OMM_EINVAL, "omm_sel_fwd_paged_gated: gates must be [B, M, H, 3]");
+  for (const omm_view4* o : {o_cmp, o_swa}) {
+    for (int i = 0; i < 4; ++i)
+      OMM_REQUIRE(o->size[i] == q->size[i], OMM_EINVAL,
+                  "omm_sel_fwd_paged_gated: o_cmp / o_swa must have q's shape");
+    OMM_REQUIRE(o->stride[3] == 1 && o->stride[0] % 4 == 0 && o->stride[1] % 4 == 0 &&
+                    o->stride[2] % 4 == 0 && (reinterpret_cast<uintptr_t>(o->data) & 7u) == 0,
+                OMM_EUNSUPPORTED,
+                "omm_sel_fwd_paged_gated: o_cmp / o_swa need unit dim stride and 8-byte "
+                "aligned 4-element groups");
+  }
+  GateArgs ga;
+  ga.g = static_cast<const bf16_t*>(gates->data);
+  ga.gs0 = gates->stride[0]; ga.gs1 = gates->stride[1]; ga.gs2 = gates->stride[2];
+  ga.gs3 = gates->stride[3];
+  ga.oc = static_cast<const bf16_t*>(o_cmp->data);
+  ga.cs0 = o_cmp->stride[0]; ga.cs1 = o_cmp->stride[1]; ga.cs2 = o_cmp->stride[2];
+  ga.ow = static_cast<const bf16_t*>(o_swa->data);
+  ga.ws0 = o_swa->stride[0]; ga.ws1 = o_swa->stride[1]; ga.ws2 = o_swa->stride[2];
+  return sel_fwd_paged_impl(q, ids, kv, group_size, scale, out, lse, epoch, stream, ga);
 }

@@ -222,10 +222,10 @@ class WanNSAAR:
                                 q_chunk_offset=cid, blocks_per_chunk=cache.ppc)
         self._toc(tk)
         tk = self._tic("sel_attn")
-        o_slc = cache.select(q, ids, layer, cfg.group_size)
+        # selection with the branch mix g_cmp*o_cmp + g_slc*o_slc + g_swa*o_swa in its epilogue
+        o = cache.select(q, ids, layer, cfg.group_size, gates=g, o_cmp=o_cmp, o_swa=o_swa)
         self._toc(tk)
         tk = self._tic("linear")
-        o = g[..., 0:1] * o_cmp + g[..., 1:2] * o_slc + g[..., 2:3] * o_swa
         out = F.linear(o.flatten(2), *blk.o)
         self._toc(tk)
         return out

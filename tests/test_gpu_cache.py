@@ -348,6 +348,56 @@ def test_paged_selection_fp8_qk_matches_oracle(D, G, sign):
     _check_attn(out, lse, want_o, want_l)
 
 
+@pytest.mark.parametrize("dtype,qk8,G", [(torch.bfloat16, False, 64), (torch.bfloat16, False, 128),
+                                         ("fp8", False, 64), ("fp8", True, 64)])
+def test_gated_selection_mix_matches_float64(dtype, qk8, G):
+    """The NSA branch mix fused into the selection epilogue (causal_wan_nsa_model.py:541-546):
+    out = g0 * o_cmp + g1 * o_slc + g2 * o_swa against float64, with o_slc from the float64
+    oracle on the cache's values; the bf16 tolerances of attention outputs.  The plain
+    selection of the same call must equal the gated one with gates (0, 1, 0)."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(77 + G)
+    torch.manual_seed(77)
+    H, D, C, P, T, n = 3, 128, 4680, 64, 16, 3
+    fp8 = dtype == "fp8"
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         qk_fp8=qk8, hbm_slots=H * n, host_slots=H * n, window_chunks=0)
+    ks = [_chunk(g, C, H, D, 0.3, fp8) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, fp8) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    M = 1500
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    MG = -(-M // G)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32)
+    gates = torch.sigmoid(torch.randn((1, M, H, 3), generator=g) * 2).to(torch.bfloat16)
+    o_cmp = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16)
+    o_swa = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16)
+    qd, idd = q.to(DEV), ids.to(DEV)
+    mix, lse = cache.select(qd, idd, 0, G, gates=gates.to(DEV), o_cmp=o_cmp.to(DEV),
+                            o_swa=o_swa.to(DEV), return_lse=True)
+    if fp8:
+        kk, vv = _fp8_cache_images(cache, n, round_k=not qk8)
+        qq = _quantized_rows(q) if qk8 else q.float().numpy()
+    else:
+        kk, vv = torch.cat(ks, 1).float().numpy(), torch.cat(vs, 1).float().numpy()
+        qq = q.float().numpy()
+    o_slc, want_l = O.selection_attention(qq, kk, vv, ids.numpy(), G, D ** -0.5,
+                                          O.paged_block_tokens(C, P, n))
+    gg = gates.float().numpy().astype(np.float64)
+    want = (gg[..., 0:1] * o_cmp.float().numpy() + gg[..., 1:2] * o_slc
+            + gg[..., 2:3] * o_swa.float().numpy())
+    # the mix is O(1) (o_cmp, o_swa ~ N(0, 1)): its bf16 rounding alone is about 1e-3 mean-abs
+    _check_attn(mix, lse, want, want_l, mx=4e-2, mean=3e-3)
+    one = torch.zeros_like(gates)
+    one[..., 1] = 1.0
+    plain = cache.select(qd, idd, 0, G)
+    via_gate = cache.select(qd, idd, 0, G, gates=one.to(DEV), o_cmp=o_cmp.to(DEV),
+                            o_swa=o_swa.to(DEV))
+    assert torch.equal(plain, via_gate)
+
+
 def test_fp8_quantisation_error_against_bf16_cache():
     """Config 5's error budget, per variant: selection-attention output over
     Student-t(4) K/V against float64 on the original bf16 values, for the bf16 cache, the fp8
