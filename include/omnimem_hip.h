@@ -27,6 +27,9 @@
  *                              selection_fwd.cu:968-992)
  *   omm_build_ptr_table     <- torch.ops.omnimem_nsa.build_ptr_table (bindings.cpp:12-15,
  *                              ptr_table.cu:59-127)
+ *   omm_sel_bwd_ptr         <- torch.ops.omnimem_nsa.sel_bwd_ptr (bindings.cpp:29-35,
+ *                              selection_bwd.cu:1409-1529; Triton twin
+ *                              padded_ptr/kernels/select_bwd.py:564-711)
  *   omm_paged_append        <- MMCache.update_cache chunk_per_head branch (models/cache.py:478-502)
  *                              fused with the K / V block compression
  *                              (causal_wan_nsa_model.py:479-490)
@@ -243,6 +246,40 @@ int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr
                     const int64_t* ptr_stride, int64_t T, int32_t block_size, int32_t group_size,
                     int64_t stride_bn, int64_t stride_bd, float scale, const omm_view4* out,
                     float* lse, void* stream);
+/* Pointer-table backward (the padded-pointer training path).  q, out, d_out, dq: bf16
+ * [B, M, H, D]; lse: the forward's fp32 contiguous [B, H, M]; ids: int32 [B, MG, H, T]; ptr_k /
+ * ptr_v: the forward's address tables (element strides ptr_stride[4]).  Writes dq (q dtype) and
+ * delta (fp32 contiguous [B, H, M], delta_m = sum_d out[m,d] d_out[m,d]).
+ * dQ: P = exp(q.k * scale - lse) over the block_size rows of every nonzero (ptr_k, ptr_v) slot
+ * (0 for rows with lse = -inf), dS = P (d_out.v - delta) scale, dq = dS K.
+ * With compute_dkv: block id bid of head h resolves, as omm_build_ptr_table does, through the
+ * [H, max_base] base tables (element strides base_stride[0], base_stride[1]) to K / V at
+ * base_k/v[h, bid / bpc] + b*batch_stride_kv_bytes + (bid % bpc)*in_chunk_block_bytes_kv (bpc =
+ * blocks_per_chunk > 0; else base[h, bid]) and to fp32 dK / dV scratch at base_dk/dv[...] +
+ * b*batch_stride_dkv_bytes + (bid % bpc)*in_chunk_block_bytes_dkv, rows stride_dbn / dims
+ * stride_dbd elements.  It is skipped (nothing read or written) when bid >= n_blocks_per_head[h]
+ * (if given), bid / bpc >= max_base or any of its four bases is 0.  Every resolved block of
+ * bid < max_base*bpc (max_base when bpc == 0) gets dK = sum dS^T Q and dV = sum P^T d_out over the
+ * (group, slot) pairs that list it with 0 <= id < n_blocks_per_head[h] (all block_size rows
+ * written; 0 when none does; stored, not added).  Duplicated ids count twice.  MFMA kernels for
+ * head dim 64 / 128 with stride_bd == 1 and stride_bn % 8 == 0 (block addresses may be 2-byte
+ * aligned), VALU fp32 kernels otherwise (head dim <= 256).  Workspace (256-byte aligned): -lse
+ * log2 e and, with compute_dkv, the per-block CSR offsets and bucket lists. */
+size_t omm_sel_bwd_ptr_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t max_base,
+                                       int32_t blocks_per_chunk, int32_t group_size, int64_t T,
+                                       int32_t compute_dkv);
+int omm_sel_bwd_ptr(const omm_view4* q, const omm_view4* out, const float* lse,
+                    const omm_view4* d_out, const omm_view4* ids, const int64_t* ptr_k,
+                    const int64_t* ptr_v, const int64_t* ptr_stride, const int64_t* base_k,
+                    const int64_t* base_v, const int64_t* base_dk, const int64_t* base_dv,
+                    const int64_t* base_stride, int64_t max_base,
+                    const int32_t* n_blocks_per_head, int32_t block_size, int32_t group_size,
+                    int64_t batch_stride_kv_bytes, int64_t batch_stride_dkv_bytes,
+                    int64_t stride_bn, int64_t stride_bd, int64_t stride_dbn, int64_t stride_dbd,
+                    int32_t blocks_per_chunk, int64_t in_chunk_block_bytes_kv,
+                    int64_t in_chunk_block_bytes_dkv, float scale, int32_t compute_dkv,
+                    const omm_view4* dq, float* delta, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 /* ---- paged block KV cache (a7) ------------------------------------------------------- */
 /* Write chunk cid of every head from k_new / v_new (bf16 [1, chunk_tokens, H, D], unit dim

@@ -80,6 +80,10 @@ PROTOTYPES = {
                                _vp]),
     "omm_build_ptr_table": (_i32, [_V, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _i64, _vp,
                                    _vp, _vp]),
+    "omm_sel_bwd_ptr_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32, _i64, _i32]),
+    "omm_sel_bwd_ptr": (_i32, [_V, _V, _vp, _V, _V, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                               _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
+                               _i64, _f32, _i32, _V, _vp, _vp, _sz, _vp]),
     "omm_paged_append": (_i32, [_P, _V, _V, _i32, _i32, _V, _V, _i32, _vp]),
     "omm_sel_fwd_paged": (_i32, [_V, _V, _P, _i32, _f32, _V, _vp, _i32, _vp]),
     "omm_sel_fwd_paged_gated": (_i32, [_V, _V, _P, _i32, _f32, _V, _V, _V, _V, _vp, _i32, _vp]),

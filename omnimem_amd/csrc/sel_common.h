@@ -64,10 +64,6 @@ struct GateArgs {
   int64_t ws0 = 0, ws1 = 0, ws2 = 0;
 };
 
-__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
-  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
-}
-
 // One lane's 4 consecutive output dims (d0 .. d0 + 3) of query (b, m, h): o4 = o_slc (fp32,
 // normalised) -> the gated mix packed as 4 bf16.
 __device__ __forceinline__ uint2 gate_mix4(const GateArgs& ga, int b, int m, int h, int d0,

@@ -157,9 +157,9 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
       kdo[jj] = row * rsk + ((c ^ DG::swz_v(row)) << 4);
       vdo[jj] = row * rsv + ((c ^ DG::swz_v(row)) << 4);
     }
-    dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
+    copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk, wk.n,
              lds[0], w, kdo);
-    dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
+    copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv, wk.n,
              lds[2], w, vdo);
     n_cur = wk.n;
     wk.advance(acc, b, g, h, T, qc);
@@ -171,9 +171,9 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     __syncthreads();
     int n_nx = 0;
     if (wk.valid) {
-      dma_part(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+      copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
                wk.n, lds[BI ^ 1], w, kdo);
-      dma_part(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
+      copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
                wk.n, lds[2 + (BI ^ 1)], w, vdo);
       n_nx = wk.n;
       wk.advance(acc, b, g, h, T, qc);
@@ -256,20 +256,24 @@ constexpr int kIdxThreads = 512;
 constexpr int kIdxWaves = kIdxThreads / kWave;
 constexpr int kIdxBuckets = 64;  // buckets per workgroup
 
-// Bucket of (group g, slot t) of row (b, h), or -1 when the pair reaches no key.
+// Bucket of (group g, slot t) of row (b, h), or -1 when the pair reaches no key.  Ids at or past
+// the row's limit (NS, or n_blocks[h] when that is smaller) reach none.
 struct PairBucket {
   const int32_t* ids;
   int64_t is0, is1, is2, is3;
   int T, NS, bs, chunk, G;
   bool causal;
+  const int32_t* n_blocks;  // per-head bound, or nullptr
   __device__ __forceinline__ int32_t id(int b, int h, int p) const {
     const int g = p / T, t = p - g * T;
     return ids[b * is0 + g * is1 + h * is2 + t * is3];
   }
-  __device__ __forceinline__ int operator()(int b, int h, int p) const { return bucket(id(b, h, p), p); }
-  __device__ __forceinline__ int bucket(int32_t bid, int p) const {
+  __device__ __forceinline__ int limit(int h) const {
+    return n_blocks != nullptr ? min(NS, n_blocks[h]) : NS;
+  }
+  __device__ __forceinline__ int bucket(int32_t bid, int p, int lim) const {
     const int g = p / T;
-    if (bid < 0 || bid >= NS) return -1;
+    if (bid < 0 || bid >= lim) return -1;
     // 32-bit unsigned: bid * bs < N + bs and g * G < M + G, with M, N < 2^31
     if (causal && (static_cast<uint32_t>(bid) * static_cast<uint32_t>(bs)) / static_cast<uint32_t>(chunk) >
                       (static_cast<uint32_t>(g) * static_cast<uint32_t>(G)) / static_cast<uint32_t>(chunk))
@@ -309,6 +313,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
   int32_t* grp = groups + static_cast<int64_t>(row) * P;
   const int per = (P + NW - 1) / NW;
   const int p0 = min(P, w * per), p1 = min(P, p0 + per);
+  const int lim = pb.limit(h);
 
   // a wave's pairs are read PL per lane at a time, all loads in flight together
   constexpr int PL = 16;
@@ -319,7 +324,7 @@ __global__ __launch_bounds__(kIdxThreads) void sel_bwd_index_kernel(
 #pragma unroll
     for (int j = 0; j < PL; ++j) {
       const int p = c0 + j * kWave + lane;
-      kk[j] = p < p1 ? pb.bucket(raw[j], p) : -1;
+      kk[j] = p < p1 ? pb.bucket(raw[j], p, lim) : -1;
     }
   };
 
@@ -420,13 +425,128 @@ __device__ __forceinline__ void dma_f32x64(const float* base, int nvalid, float*
 }
 #pragma clang diagnostic pop
 
-template <typename QT, int D>
+// ---- dK / dV targets --------------------------------------------------------------------------
+// One key tile (up to 64 tokens) of one (b, h, block): element pointers of its first K / V row and
+// first dK / dV row, element strides, its row count and the token id of its first row (used by the
+// chunk-causal mask only).
+template <typename KT, typename GT>
+struct KvTile {
+  const KT* k;
+  const KT* v;
+  GT* dk;
+  GT* dv;
+  int64_t k_sn, k_sd, v_sn, v_sd, dk_sn, dk_sd, dv_sn, dv_sd;
+  int nk, t0;
+};
+
+// Dense K / V and dK / dV [B, N, H, D]: block bid is tokens bid*bs .. min(bid*bs + bs, N).
+template <typename QT>
+struct DenseGrad {
+  using KT = QT;
+  using GT = QT;
+  static constexpr bool kMayMisalign = false;  // 16-byte rows checked on the host
+  View4<const QT> k, v;
+  View4<QT> dk, dv;
+  int N, bs;
+  __device__ __forceinline__ bool tile(int b, int h, int bid, int kt, KvTile<QT, QT>& r) const {
+    const int t0 = bid * bs + 64 * kt;
+    const int nk = min(min(bs - 64 * kt, 64), N - t0);
+    if (nk <= 0) return false;
+    r = KvTile<QT, QT>{k.at(b, t0, h), v.at(b, t0, h), dk.at(b, t0, h), dv.at(b, t0, h),
+                       k.s1, k.s3, v.s1, v.s3, dk.s1, dk.s3, dv.s1, dv.s3, nk, t0};
+    return true;
+  }
+};
+
+// Raw block addresses of a pointer-table caller (bf16 K / V, fp32 dK / dV scratch), from [H, MAXB]
+// base tables: with blocks_per_chunk > 0 the base of (h, bid / blocks_per_chunk) plus
+// (bid % blocks_per_chunk) in-chunk block strides, else the base of (h, bid); plus b batch
+// strides.  A block is skipped (nothing read or written) when bid is at or past n_blocks[h] (if
+// given) or past the table, or when any of its four bases is 0 (reference contract:
+// bwd_common.cuh:66-121).  Every block holds bs tokens.
+struct PtrGrad {
+  using KT = bf16_t;
+  using GT = float;
+  static constexpr bool kMayMisalign = true;  // any 2-byte aligned K / V address is accepted
+  const int64_t* base_k;
+  const int64_t* base_v;
+  const int64_t* base_dk;
+  const int64_t* base_dv;
+  int64_t bsh, bsc;  // element strides of the base tables
+  int64_t max_base;
+  const int32_t* n_blocks;
+  int64_t batch_kv, batch_dkv, chunk_kv, chunk_dkv;  // bytes
+  int64_t s_bn, s_bd, s_dbn, s_dbd;                  // element strides
+  int bpc, bs;
+  __device__ __forceinline__ bool tile(int b, int h, int bid, int kt, KvTile<bf16_t, float>& r) const {
+    if (n_blocks != nullptr && bid >= n_blocks[h]) return false;
+    const int64_t idx = bpc > 0 ? bid / bpc : bid;
+    const int64_t loc = bpc > 0 ? bid - idx * bpc : 0;
+    if (idx >= max_base) return false;
+    const int64_t o = h * bsh + idx * bsc;
+    const int64_t bk = base_k[o], bv = base_v[o], bdk = base_dk[o], bdv = base_dv[o];
+    if (bk == 0 || bv == 0 || bdk == 0 || bdv == 0) return false;
+    const int nk = min(bs - 64 * kt, 64);
+    if (nk <= 0) return false;
+    const int64_t okv = b * batch_kv + loc * chunk_kv, od = b * batch_dkv + loc * chunk_dkv;
+    const int64_t row0 = 64 * static_cast<int64_t>(kt);
+    r.k = reinterpret_cast<const bf16_t*>(static_cast<uintptr_t>(bk + okv)) + row0 * s_bn;
+    r.v = reinterpret_cast<const bf16_t*>(static_cast<uintptr_t>(bv + okv)) + row0 * s_bn;
+    r.dk = reinterpret_cast<float*>(static_cast<uintptr_t>(bdk + od)) + row0 * s_dbn;
+    r.dv = reinterpret_cast<float*>(static_cast<uintptr_t>(bdv + od)) + row0 * s_dbn;
+    r.k_sn = r.v_sn = s_bn;
+    r.k_sd = r.v_sd = s_bd;
+    r.dk_sn = r.dv_sn = s_dbn;
+    r.dk_sd = r.dv_sd = s_dbd;
+    r.nk = nk;
+    r.t0 = 0;
+    return true;
+  }
+};
+
+// 8 consecutive 16-bit elements (unit stride) as one MFMA operand; a target that admits 2-byte
+// aligned rows reads a misaligned row with 2-byte loads.
+template <bool MIS>
+__device__ __forceinline__ uint4 load_row8(const void* p) {
+  if constexpr (MIS) {
+    if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0u) {
+      const uint16_t* e = static_cast<const uint16_t*>(p);
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = static_cast<uint32_t>(e[2 * i]) | (static_cast<uint32_t>(e[2 * i + 1]) << 16);
+      return make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  return *static_cast<const uint4*>(p);
+}
+
+// 8 fp32 results of one row, dims d .. d + 7: 16-bit rows (unit stride, 16-byte aligned) get one
+// packed 16-byte store; fp32 rows two 16-byte stores when contiguous and aligned, else 8 stores.
+template <typename QT>
+__device__ __forceinline__ void store_row8(QT* p, int64_t, const float4& x0, const float4& x1) {
+  *reinterpret_cast<uint4*>(p) =
+      make_uint4(Mfma<QT>::pack2(x0.x, x0.y), Mfma<QT>::pack2(x0.z, x0.w),
+                 Mfma<QT>::pack2(x1.x, x1.y), Mfma<QT>::pack2(x1.z, x1.w));
+}
+__device__ __forceinline__ void store_row8(float* p, int64_t sd, const float4& x0,
+                                           const float4& x1) {
+  if (sd == 1 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0u) {
+    reinterpret_cast<float4*>(p)[0] = x0;
+    reinterpret_cast<float4*>(p)[1] = x1;
+    return;
+  }
+  const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i * sd] = x[i];
+}
+
+template <typename QT, int D, typename KG>
 __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
-    View4<const QT> q, View4<const QT> dout, View4<const QT> k, View4<const QT> v, View4<QT> dk,
-    View4<QT> dv, const float* __restrict__ nl2, const float* __restrict__ delta,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ groups, int M, int N, int H,
-    int G, int MG, int T, int NS, int bs, int nkt, int chunk, bool causal, float scale,
-    int nsub) {
+    View4<const QT> q, View4<const QT> dout, KG kg, const float* __restrict__ nl2,
+    const float* __restrict__ delta, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ groups, int M, int H, int G, int MG, int T, int NS, int nkt,
+    int chunk, bool causal, float scale, int nsub) {
   using DG = DmaGeom<D>;
   constexpr int ROWB = DG::ROWB, CPR = DG::CPR, RPI = DG::RPI;
   constexpr int SD = DG::SD, ND = DG::ND;
@@ -462,9 +582,9 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
   const int h = u % H;
   const int b = u / H;
 
-  const int t0 = bid * bs + 64 * kt;                         // first token of the tile
-  const int nk = min(min(bs - 64 * kt, 64), N - t0);         // tokens of the tile
-  if (nk <= 0) return;
+  KvTile<typename KG::KT, typename KG::GT> tl;
+  if (!kg.tile(b, h, bid, kt, tl)) return;
+  const int t0 = tl.t0, nk = tl.nk;  // first token and tokens of the tile
 
   // K^T and V^T operands of this wave's key 16 w + l16, dims 32 s + 8 j4 ..
   uint4 kb[SD], vb[SD];
@@ -473,9 +593,9 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
     const bool ok = key < nk;
 #pragma unroll
     for (int s = 0; s < SD; ++s) {
-      kb[s] = ok ? *reinterpret_cast<const uint4*>(k.at(b, t0 + key, h, 32 * s + 8 * j4))
+      kb[s] = ok ? load_row8<KG::kMayMisalign>(tl.k + key * tl.k_sn + 32 * s + 8 * j4)
                  : make_uint4(0, 0, 0, 0);
-      vb[s] = ok ? *reinterpret_cast<const uint4*>(v.at(b, t0 + key, h, 32 * s + 8 * j4))
+      vb[s] = ok ? load_row8<KG::kMayMisalign>(tl.v + key * tl.v_sn + 32 * s + 8 * j4)
                  : make_uint4(0, 0, 0, 0);
     }
   }
@@ -656,9 +776,10 @@ __global__ __launch_bounds__(kKvThreads, 2) void sel_bwd_dkv_kernel(
     if (key >= nk) continue;
     const float4 x0 = *reinterpret_cast<const float4*>(stage + row * D + 8 * ch);
     const float4 x1 = *reinterpret_cast<const float4*>(stage + row * D + 8 * ch + 4);
-    *reinterpret_cast<uint4*>((row < 64 ? dk : dv).at(b, t0 + key, h, 8 * ch)) =
-        make_uint4(Mfma<QT>::pack2(x0.x, x0.y), Mfma<QT>::pack2(x0.z, x0.w),
-                   Mfma<QT>::pack2(x1.x, x1.y), Mfma<QT>::pack2(x1.z, x1.w));
+    if (row < 64)
+      store_row8(tl.dk + key * tl.dk_sn + 8 * ch * tl.dk_sd, tl.dk_sd, x0, x1);
+    else
+      store_row8(tl.dv + key * tl.dv_sn + 8 * ch * tl.dv_sd, tl.dv_sd, x0, x1);
   }
 }
 
@@ -757,12 +878,12 @@ __global__ __launch_bounds__(256) void sel_bwd_dq_valu_kernel(
   }
 }
 
-template <typename QT, int DQ>
+template <typename QT, int DQ, typename KG>
 __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
-    View4<const QT> q, View4<const QT> dout, View4<const QT> k, View4<const QT> v, View4<QT> dk,
-    View4<QT> dv, const float* __restrict__ lse, const float* __restrict__ delta,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ groups, int M, int N, int H,
-    int D, int G, int MG, int T, int NS, int bs, int nkt, int chunk, bool causal, float scale) {
+    View4<const QT> q, View4<const QT> dout, KG kg, const float* __restrict__ lse,
+    const float* __restrict__ delta, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ groups, int M, int H, int D, int G, int MG, int T, int NS,
+    int nkt, int chunk, bool causal, float scale) {
   constexpr int DP = 4 * DQ;
   __shared__ float Qs[kVQ * DP];
   __shared__ float Ds[kVQ * DP];
@@ -791,9 +912,11 @@ __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
   const int kt = u % nkt; u /= nkt;
   const int h = u % H;
   const int b = u / H;
-  const int t0 = bid * bs + 64 * kt;
-  const int nk = min(min(bs - 64 * kt, 64), N - t0);
-  if (nk <= 0) return;
+  using KT = typename KG::KT;
+  using GT = typename KG::GT;
+  KvTile<KT, GT> tl;
+  if (!kg.tile(b, h, bid, kt, tl)) return;
+  const int t0 = tl.t0, nk = tl.nk;
   const int key = tid >> 2, part = tid & 3, d0 = part * DQ;
   const bool k_ok = key < nk;
 
@@ -802,8 +925,8 @@ __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
   for (int i = 0; i < DQ; ++i) {
     const int d = d0 + i;
     const bool ok = k_ok && d < D;
-    kr[i] = ok ? to_f32<QT>(*k.at(b, t0 + key, h, d)) : 0.0f;
-    vr[i] = ok ? to_f32<QT>(*v.at(b, t0 + key, h, d)) : 0.0f;
+    kr[i] = ok ? to_f32<KT>(tl.k[key * tl.k_sn + d * tl.k_sd]) : 0.0f;
+    vr[i] = ok ? to_f32<KT>(tl.v[key * tl.v_sn + d * tl.v_sd]) : 0.0f;
     acc_k[i] = acc_v[i] = 0.0f;
   }
   const int64_t orow = (static_cast<int64_t>(b) * H + h) * (NS + 1);
@@ -861,8 +984,8 @@ __global__ __launch_bounds__(256) void sel_bwd_dkv_valu_kernel(
     for (int i = 0; i < DQ; ++i) {
       const int d = d0 + i;
       if (d < D) {
-        *dk.at(b, t0 + key, h, d) = from_f32<QT>(acc_k[i]);
-        *dv.at(b, t0 + key, h, d) = from_f32<QT>(acc_v[i]);
+        tl.dk[key * tl.dk_sn + d * tl.dk_sd] = from_f32<GT>(acc_k[i]);
+        tl.dv[key * tl.dv_sn + d * tl.dv_sd] = from_f32<GT>(acc_v[i]);
       }
     }
   }
@@ -874,13 +997,15 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 struct BwdWs {
   size_t delta, nl2, offsets, groups, total;
 };
-inline BwdWs bwd_ws(int64_t B, int64_t M, int64_t H, int64_t MG, int64_t T, int64_t NS) {
+// [delta (dense entry only) | -lse log2 e | CSR offsets | bucket lists (when dK / dV are computed)]
+inline BwdWs bwd_ws(int64_t B, int64_t M, int64_t H, int64_t MG, int64_t T, int64_t NS,
+                    bool with_delta = true, bool with_index = true) {
   BwdWs w;
   w.delta = 0;
-  w.nl2 = align256(static_cast<size_t>(B * H * M) * 4);
+  w.nl2 = with_delta ? align256(static_cast<size_t>(B * H * M) * 4) : 0;
   w.offsets = w.nl2 + align256(static_cast<size_t>(B * H * M) * 4);
-  w.groups = w.offsets + align256(static_cast<size_t>(B * H * (NS + 1)) * 4);
-  w.total = w.groups + align256(static_cast<size_t>(B * H * MG * T) * 4);
+  w.groups = w.offsets + (with_index ? align256(static_cast<size_t>(B * H * (NS + 1)) * 4) : 0);
+  w.total = w.groups + (with_index ? align256(static_cast<size_t>(B * H * MG * T) * 4) : 0);
   return w;
 }
 
@@ -942,7 +1067,7 @@ int sel_bwd_launch(const BwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
   if (rc) return rc;
 
   PairBucket pb{static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
-                ids.stride[2], ids.stride[3], T, NS, bs, ch, G, causal};
+                ids.stride[2], ids.stride[3], T, NS, bs, ch, G, causal, nullptr};
   const int nrange = std::max(1, (NS + kIdxBuckets - 1) / kIdxBuckets);  // NS = 0: offsets[0] = 0
   sel_bwd_index_kernel<<<static_cast<unsigned>(B * H * nrange), kIdxThreads, 0, s>>>(
       pb, H, MG * T, nrange, offsets, groups);
@@ -950,18 +1075,81 @@ int sel_bwd_launch(const BwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
   if (rc) return rc;
 
   if (kv_items == 0) return OMM_OK;
+  const DenseGrad<QT> kg{make_view<const QT>(k), make_view<const QT>(v), make_view<QT>(*a.dk),
+                         make_view<QT>(*a.dv), N, bs};
   if constexpr (DM > 0) {
-    sel_bwd_dkv_kernel<QT, DM><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
-        make_view<const QT>(q), make_view<const QT>(*a.dout), make_view<const QT>(k),
-        make_view<const QT>(v), make_view<QT>(*a.dk), make_view<QT>(*a.dv), nl2, delta, offsets,
-        groups, M, N, H, G, MG, T, NS, bs, nkt, ch, causal, a.scale, nsub);
+    sel_bwd_dkv_kernel<QT, DM, DenseGrad<QT>><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), kg, nl2, delta, offsets, groups, M,
+        H, G, MG, T, NS, nkt, ch, causal, a.scale, nsub);
   } else {
-    sel_bwd_dkv_valu_kernel<QT, DQ><<<static_cast<unsigned>(kv_items), 256, 0, s>>>(
-        make_view<const QT>(q), make_view<const QT>(*a.dout), make_view<const QT>(k),
-        make_view<const QT>(v), make_view<QT>(*a.dk), make_view<QT>(*a.dv), a.lse, delta, offsets,
-        groups, M, N, H, D, G, MG, T, NS, bs, nkt, ch, causal, a.scale);
+    sel_bwd_dkv_valu_kernel<QT, DQ, DenseGrad<QT>><<<static_cast<unsigned>(kv_items), 256, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), kg, a.lse, delta, offsets, groups,
+        M, H, D, G, MG, T, NS, nkt, ch, causal, a.scale);
   }
   return check_launch("selection backward (dk/dv)");
+}
+
+// Pointer-table backward: dQ over the forward's address tables (no chunk mask), then, when dK / dV
+// are asked for, the block -> query-group index over ids bounded per head and dK / dV into the
+// callers' fp32 scratch blocks.  MFMA kernels when DM > 0, else the VALU kernels with DQ dims per
+// lane.  The MFMA dK / dV kernel's item order assumes nothing about which blocks are popular.
+struct PtrBwdArgs {
+  const omm_view4 *q, *out, *dout, *ids, *dq;
+  const float* lse;
+  float* delta;
+  PtrAcc acc;
+  PtrGrad kg;
+  int bs, G, NS;
+  bool dkv;
+  float scale;
+};
+
+template <int DM, int DQ>
+int sel_bwd_ptr_launch(const PtrBwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
+  using QT = bf16_t;
+  const omm_view4 &q = *a.q, &ids = *a.ids;
+  const int B = static_cast<int>(q.size[0]), M = static_cast<int>(q.size[1]);
+  const int H = static_cast<int>(q.size[2]), D = static_cast<int>(q.size[3]);
+  const int MG = static_cast<int>(ids.size[1]), T = static_cast<int>(ids.size[3]);
+  const int G = a.G, NS = a.NS, nsub = (G + 63) / 64;
+  float* nl2 = reinterpret_cast<float*>(ws + L.nl2);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* groups = reinterpret_cast<int32_t*>(ws + L.groups);
+  const int64_t dq_items = static_cast<int64_t>(B) * H * MG * nsub;
+  const int nkt = (a.bs + 63) / 64;
+  const int64_t kv_items = static_cast<int64_t>(B) * H * NS * nkt;
+  OMM_REQUIRE(dq_items <= 2147483647ll && kv_items <= 2147483647ll, OMM_EUNSUPPORTED,
+              "omm_sel_bwd_ptr: grid too large");
+  if constexpr (DM > 0) {
+    sel_bwd_dq_kernel<QT, PtrAcc, DM><<<static_cast<unsigned>(dq_items), kDqThreads, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.out), make_view<const QT>(*a.dout),
+        make_view<QT>(*a.dq), a.lse, a.delta, nl2, a.acc, M, H, G, MG, T, 1, a.scale, nsub);
+  } else {
+    sel_bwd_dq_valu_kernel<QT, PtrAcc, DQ><<<static_cast<unsigned>(dq_items), 256, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.out), make_view<const QT>(*a.dout),
+        make_view<QT>(*a.dq), a.lse, a.delta, nl2, a.acc, M, H, D, G, MG, T, 1, a.scale, nsub,
+        a.kg.s_bd);
+  }
+  int rc = check_launch("pointer selection backward (dq)");
+  if (rc || !a.dkv || kv_items == 0) return rc;
+
+  PairBucket pb{static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
+                ids.stride[2], ids.stride[3], T, NS, a.bs, 1, G, false, a.kg.n_blocks};
+  const int nrange = (NS + kIdxBuckets - 1) / kIdxBuckets;
+  sel_bwd_index_kernel<<<static_cast<unsigned>(B * H * nrange), kIdxThreads, 0, s>>>(
+      pb, H, MG * T, nrange, offsets, groups);
+  rc = check_launch("pointer selection backward (index)");
+  if (rc) return rc;
+  if constexpr (DM > 0) {
+    sel_bwd_dkv_kernel<QT, DM, PtrGrad><<<static_cast<unsigned>(kv_items), kKvThreads, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), a.kg, nl2, a.delta, offsets, groups,
+        M, H, G, MG, T, NS, nkt, 1, false, a.scale, nsub);
+  } else {
+    sel_bwd_dkv_valu_kernel<QT, DQ, PtrGrad><<<static_cast<unsigned>(kv_items), 256, 0, s>>>(
+        make_view<const QT>(q), make_view<const QT>(*a.dout), a.kg, a.lse, a.delta, offsets,
+        groups, M, H, D, G, MG, T, NS, nkt, 1, false, a.scale);
+  }
+  return check_launch("pointer selection backward (dk/dv)");
 }
 
 template <typename QT>
@@ -1043,4 +1231,112 @@ extern "C" int omm_sel_bwd(const omm_view4* q, const omm_view4* k, const omm_vie
     case OMM_F32: return sel_bwd_typed<float>(a, false, ws, L, s);
     default: return set_error(OMM_EINVAL, "omm_sel_bwd: unsupported dtype %d", dtype);
   }
+}
+
+namespace {
+// Block-id range of the dK / dV grid: every id a base table can resolve.
+int64_t ptr_bwd_blocks(int64_t max_base, int32_t blocks_per_chunk) {
+  return blocks_per_chunk > 0 ? max_base * blocks_per_chunk : max_base;
+}
+}  // namespace
+
+extern "C" size_t omm_sel_bwd_ptr_workspace_bytes(int64_t B, int64_t M, int64_t H,
+                                                  int64_t max_base, int32_t blocks_per_chunk,
+                                                  int32_t group_size, int64_t T,
+                                                  int32_t compute_dkv) {
+  if (B <= 0 || M <= 0 || H <= 0 || max_base < 0 || blocks_per_chunk < 0 || group_size < 1 || T < 1)
+    return 0;
+  const int64_t MG = omm::cdiv64(M, group_size);
+  return omm::bwd_ws(B, M, H, MG, T, ptr_bwd_blocks(max_base, blocks_per_chunk), false,
+                     compute_dkv != 0).total;
+}
+
+extern "C" int omm_sel_bwd_ptr(const omm_view4* q, const omm_view4* out, const float* lse,
+                               const omm_view4* dout, const omm_view4* ids, const int64_t* ptr_k,
+                               const int64_t* ptr_v, const int64_t* ptr_stride,
+                               const int64_t* base_k, const int64_t* base_v,
+                               const int64_t* base_dk, const int64_t* base_dv,
+                               const int64_t* base_stride, int64_t max_base,
+                               const int32_t* n_blocks_per_head, int32_t block_size,
+                               int32_t group_size, int64_t batch_stride_kv_bytes,
+                               int64_t batch_stride_dkv_bytes, int64_t stride_bn,
+                               int64_t stride_bd, int64_t stride_dbn, int64_t stride_dbd,
+                               int32_t blocks_per_chunk, int64_t in_chunk_block_bytes_kv,
+                               int64_t in_chunk_block_bytes_dkv, float scale, int32_t compute_dkv,
+                               const omm_view4* dq, float* delta, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(q && out && lse && dout && ids && ptr_k && ptr_v && ptr_stride && dq && delta,
+              OMM_EINVAL, "omm_sel_bwd_ptr: null argument");
+  const int64_t B = q->size[0], M = q->size[1], H = q->size[2], D = q->size[3];
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(out->size[i] == q->size[i] && dout->size[i] == q->size[i] &&
+                    dq->size[i] == q->size[i],
+                OMM_EINVAL, "omm_sel_bwd_ptr: out, d_out and dq must have q's shape");
+  OMM_REQUIRE(group_size >= 1 && block_size >= 1, OMM_EINVAL,
+              "omm_sel_bwd_ptr: group_size and block_size must be >= 1");
+  const int64_t MG = cdiv64(M, group_size);
+  OMM_REQUIRE(ids->size[0] == B && ids->size[1] == MG && ids->size[2] == H && ids->size[3] >= 1,
+              OMM_EINVAL, "omm_sel_bwd_ptr: block_indices must be [%lld,%lld,%lld,T>=1]",
+              (long long)B, (long long)MG, (long long)H);
+  OMM_REQUIRE(stride_bn >= 0 && stride_bd >= 0, OMM_EINVAL, "omm_sel_bwd_ptr: negative stride");
+  OMM_REQUIRE(D >= 1 && D <= 256, OMM_EUNSUPPORTED,
+              "omm_sel_bwd_ptr: head dim must be in [1, 256] (got %lld)", (long long)D);
+  OMM_REQUIRE(__builtin_isfinite(scale), OMM_EINVAL, "omm_sel_bwd_ptr: scale must be finite");
+  const int64_t T = ids->size[3];
+  const bool dkv = compute_dkv != 0;
+  int64_t NS = 0;
+  if (dkv) {
+    OMM_REQUIRE(base_k && base_v && base_dk && base_dv && base_stride && max_base >= 0,
+                OMM_EINVAL, "omm_sel_bwd_ptr: dK / dV need the four [H, max_base] base tables");
+    OMM_REQUIRE(blocks_per_chunk >= 0, OMM_EINVAL, "omm_sel_bwd_ptr: blocks_per_chunk < 0");
+    OMM_REQUIRE(blocks_per_chunk == 0 ||
+                    (in_chunk_block_bytes_kv > 0 && in_chunk_block_bytes_dkv > 0),
+                OMM_EINVAL, "omm_sel_bwd_ptr: chunk-level bases need in_chunk_block_bytes_kv/dkv > 0");
+    OMM_REQUIRE(stride_dbn != 0 || D == 1, OMM_EINVAL,
+                "omm_sel_bwd_ptr: stride_dbn must be the fp32 scratch row stride");
+    NS = ptr_bwd_blocks(max_base, blocks_per_chunk);
+  }
+  OMM_REQUIRE(M <= 2147483647ll && MG * T <= 2147483647ll && B * H * MG * T <= 2147483647ll &&
+                  NS <= 2147483647ll && B * H * (NS + 1) <= 2147483647ll,
+              OMM_EUNSUPPORTED, "omm_sel_bwd_ptr: sizes exceed the int32 index range");
+  if (B == 0 || M == 0 || H == 0) return OMM_OK;
+  const BwdWs L = bwd_ws(B, M, H, MG, T, NS, false, dkv);
+  OMM_REQUIRE(workspace != nullptr && workspace_bytes >= L.total &&
+                  (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+              OMM_EWORKSPACE,
+              "omm_sel_bwd_ptr: workspace of %zu bytes (256-byte aligned) required", L.total);
+  PtrBwdArgs a;
+  a.q = q;
+  a.out = out;
+  a.dout = dout;
+  a.ids = ids;
+  a.dq = dq;
+  a.lse = lse;
+  a.delta = delta;
+  a.acc = PtrAcc{ptr_k, ptr_v, ptr_stride[0], ptr_stride[1], ptr_stride[2], ptr_stride[3],
+                 stride_bn, block_size};
+  a.kg = PtrGrad{base_k, base_v, base_dk, base_dv,
+                 dkv ? base_stride[0] : 0, dkv ? base_stride[1] : 0, max_base, n_blocks_per_head,
+                 batch_stride_kv_bytes, batch_stride_dkv_bytes, in_chunk_block_bytes_kv,
+                 in_chunk_block_bytes_dkv, stride_bn, stride_bd, stride_dbn, stride_dbd,
+                 blocks_per_chunk, block_size};
+  a.bs = block_size;
+  a.G = group_size;
+  a.NS = static_cast<int>(NS);
+  a.dkv = dkv;
+  a.scale = scale;
+  // MFMA kernels: head dim 64 / 128, unit dim stride and 16-byte row strides of the K / V blocks
+  // (a block address itself may be 2-byte aligned), 16-byte q / out / d_out / dq rows and a
+  // non-zero scale; everything else runs the VALU kernels
+  bool rows_ok = true;
+  for (const omm_view4* x : {q, out, dout, dq}) rows_ok = rows_ok && rows16(*x, D);
+  const bool mfma = (D == 64 || D == 128) && stride_bd == 1 && stride_bn % 8 == 0 &&
+                    2 * stride_bn * 64 < (int64_t{1} << 31) && rows_ok && scale != 0.0f;
+  char* ws = static_cast<char*>(workspace);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma) return D == 128 ? sel_bwd_ptr_launch<128, 0>(a, ws, L, s) : sel_bwd_ptr_launch<64, 0>(a, ws, L, s);
+  if (D <= 64) return sel_bwd_ptr_launch<0, 16>(a, ws, L, s);
+  if (D <= 128) return sel_bwd_ptr_launch<0, 32>(a, ws, L, s);
+  return sel_bwd_ptr_launch<0, 64>(a, ws, L, s);
 }

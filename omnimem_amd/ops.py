@@ -4,9 +4,9 @@ The reference registers its CUDA kernels as ``torch.ops.omnimem_nsa.*`` (schemas
 cuda_backend/csrc/bindings.cpp:7-36) and gives each a shape-only fake so ``torch.compile`` can
 trace through them (cuda_backend/ops.py:191-235).  The schemas below are the reference's, so a
 caller of ``torch.ops.omnimem_nsa.topk`` / ``sel_fwd`` / ``sel_bwd`` / ``build_ptr_table`` /
-``sel_fwd_ptr`` runs unchanged.  Two more ops are this build's: ``topk_fused`` (query-group
-pooling, scoring and selection in one call, what ``parallel_nsa_topk`` runs) and ``block_pool``
-(the K block compression), so that the facades trace as a chain of registered ops.
+``sel_fwd_ptr`` / ``sel_bwd_ptr`` runs unchanged.  Two more ops are this build's: ``topk_fused``
+(query-group pooling, scoring and selection in one call, what ``parallel_nsa_topk`` runs) and
+``block_pool`` (the K block compression), so that the facades trace as a chain of registered ops.
 
 The CUDA-key implementations are the C-ABI calls of ``index_topk``, ``selection`` and
 ``padded_ptr`` (ctypes on the current stream, no host synchronisation); they raise
@@ -35,6 +35,15 @@ SCHEMAS = {
     "sel_bwd": "sel_bwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, Tensor out, "
                "Tensor lse, Tensor d_out, int block_size, int chunk_size, float scale, "
                "bool causal, int group_size, bool allow_tf32) -> (Tensor, Tensor, Tensor)",
+    "sel_bwd_ptr": "sel_bwd_ptr(Tensor q, Tensor out, Tensor lse, Tensor d_out, "
+                   "Tensor block_indices, Tensor ptr_k, Tensor ptr_v, Tensor base_k, "
+                   "Tensor base_v, Tensor base_dk, Tensor base_dv, Tensor n_blocks_per_head, "
+                   "int block_size, int group_size, int batch_stride_kv_bytes, "
+                   "int batch_stride_dkv_bytes, int stride_bn, int stride_bd, int stride_dbn, "
+                   "int stride_dbd, int blocks_per_chunk, int in_chunk_block_bytes_kv, "
+                   "int in_chunk_block_bytes_dkv, float scale, str input_precision, "
+                   "bool compute_dkv, Tensor[] owners, Tensor(a!)[] grad_buffers) "
+                   "-> (Tensor, Tensor)",
     # this build's additions
     "topk_fused": "topk_fused(Tensor q, Tensor k, int topk, float scale, int block_size, "
                   "int chunk_size, bool causal, int ex_win, int ex_sink, bool prog_excl, "
@@ -92,6 +101,19 @@ def _sel_fwd_ptr_cuda(q, ptr_k, ptr_v, block_size, group_size, stride_bn, stride
                              scale, input_precision, owners)
 
 
+def _sel_bwd_ptr_cuda(q, out, lse, d_out, block_indices, ptr_k, ptr_v, base_k, base_v, base_dk,
+                      base_dv, n_blocks_per_head, block_size, group_size, batch_stride_kv_bytes,
+                      batch_stride_dkv_bytes, stride_bn, stride_bd, stride_dbn, stride_dbd,
+                      blocks_per_chunk, in_chunk_block_bytes_kv, in_chunk_block_bytes_dkv, scale,
+                      input_precision, compute_dkv, owners, grad_buffers):
+    from .padded_ptr import _sel_bwd_ptr_impl
+    return _sel_bwd_ptr_impl(q, out, lse, d_out, block_indices, ptr_k, ptr_v, base_k, base_v,
+                             base_dk, base_dv, n_blocks_per_head, block_size, group_size,
+                             batch_stride_kv_bytes, batch_stride_dkv_bytes, stride_bn, stride_bd,
+                             stride_dbn, stride_dbd, blocks_per_chunk, in_chunk_block_bytes_kv,
+                             in_chunk_block_bytes_dkv, scale, compute_dkv, grad_buffers)
+
+
 # ---- fakes (shapes only) ------------------------------------------------------------------
 def _topk_fake(q, k, topk, scale, block_size, chunk_size, chunk_size_k, causal, ex_win, ex_sink,
                prog_excl, tf_mask, q_chunk_offset, allow_tf32):
@@ -135,6 +157,16 @@ def _sel_fwd_ptr_fake(q, ptr_k, ptr_v, block_size, group_size, stride_bn, stride
     return torch.empty_like(q), q.new_empty((B, H, M), dtype=torch.float32)
 
 
+def _sel_bwd_ptr_fake(q, out, lse, d_out, block_indices, ptr_k, ptr_v, base_k, base_v, base_dk,
+                      base_dv, n_blocks_per_head, block_size, group_size, batch_stride_kv_bytes,
+                      batch_stride_dkv_bytes, stride_bn, stride_bd, stride_dbn, stride_dbd,
+                      blocks_per_chunk, in_chunk_block_bytes_kv, in_chunk_block_bytes_dkv, scale,
+                      input_precision, compute_dkv, owners, grad_buffers):
+    # dq and delta are fresh contiguous buffers; dK / dV go to grad_buffers in place
+    B, M, H, _ = q.shape
+    return q.new_empty(q.shape), q.new_empty((B, H, M), dtype=torch.float32)
+
+
 _IMPLS = {
     "topk": (_topk_cuda, _topk_fake),
     "topk_fused": (_topk_fused_cuda, _topk_fused_fake),
@@ -143,6 +175,7 @@ _IMPLS = {
     "sel_bwd": (_sel_bwd_cuda, _sel_bwd_fake),
     "build_ptr_table": (_build_ptr_table_cuda, _build_ptr_table_fake),
     "sel_fwd_ptr": (_sel_fwd_ptr_cuda, _sel_fwd_ptr_fake),
+    "sel_bwd_ptr": (_sel_bwd_ptr_cuda, _sel_bwd_ptr_fake),
 }
 
 _LIBRARY = torch.library.Library(NAMESPACE, "DEF")

@@ -11,7 +11,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 
 from omnimem_amd import ops
 
-# The reference's schemas (cuda_backend/csrc/bindings.cpp:8-31), as written there.
+# The reference's schemas (cuda_backend/csrc/bindings.cpp:8-35), as written there.
 REFERENCE_SCHEMAS = {
     "topk": "topk(Tensor q, Tensor k, int topk, float scale, int block_size, int chunk_size, "
             "int chunk_size_k, bool causal, int ex_win, int ex_sink, bool prog_excl, "
@@ -28,6 +28,15 @@ REFERENCE_SCHEMAS = {
     "sel_bwd": "sel_bwd(Tensor q, Tensor k, Tensor v, Tensor block_indices, Tensor out, "
                "Tensor lse, Tensor d_out, int block_size, int chunk_size, float scale, "
                "bool causal, int group_size, bool allow_tf32) -> (Tensor, Tensor, Tensor)",
+    "sel_bwd_ptr": "sel_bwd_ptr(Tensor q, Tensor out, Tensor lse, Tensor d_out, "
+                   "Tensor block_indices, Tensor ptr_k, Tensor ptr_v, Tensor base_k, "
+                   "Tensor base_v, Tensor base_dk, Tensor base_dv, Tensor n_blocks_per_head, "
+                   "int block_size, int group_size, int batch_stride_kv_bytes, "
+                   "int batch_stride_dkv_bytes, int stride_bn, int stride_bd, int stride_dbn, "
+                   "int stride_dbd, int blocks_per_chunk, int in_chunk_block_bytes_kv, "
+                   "int in_chunk_block_bytes_dkv, float scale, str input_precision, "
+                   "bool compute_dkv, Tensor[] owners, Tensor(a!)[] grad_buffers) "
+                   "-> (Tensor, Tensor)",
 }
 
 
@@ -108,3 +117,10 @@ def test_fake_shapes_of_every_op():
         o2, l2 = ops.op("sel_fwd_ptr")(q[:, :256], pk[:, :4], pv[:, :4], 64, 64, 64, 1, 0.125,
                                        "tf32", [])
         assert o2.shape == (2, 256, 3, 64) and l2.shape == (2, 3, 256)
+        scratch = torch.empty((2, 4, 30, 64), dtype=torch.float32, device="cuda")
+        dq2, delta = ops.op("sel_bwd_ptr")(q[:, :256], o2, l2, o2, ids[:, :4], pk[:, :4],
+                                           pv[:, :4], base, base, base, base, nb, 30, 64,
+                                           0, 0, 64, 1, 64, 1, 4, 0, 0, 0.125, "tf32", True, [],
+                                           [scratch])
+        assert dq2.shape == (2, 256, 3, 64) and dq2.dtype == torch.bfloat16
+        assert delta.shape == (2, 3, 256) and delta.dtype == torch.float32
