@@ -66,6 +66,58 @@ __global__ __launch_bounds__(64) void pool_rows_kernel(const T* __restrict__ x, 
       *reinterpret_cast<const uint4*>(res);
 }
 
+// The same pooling with 4 waves per (64 lanes x 16 bytes of the plane, row j), for launches that
+// hold few one-wave workgroups: wave w loads tokens 16 w .. 16 w + 15 of each 64-token run into
+// LDS, then adds 4-byte word w of every staged 16-byte column, element by element in token order,
+// so the sums are those of pool_rows_kernel.  AR chunk q (222 workgroups): 4.4 against 5.9 us.
+constexpr int kPoolRowsWaves = 4;
+
+template <typename T>
+__global__ __launch_bounds__(kPoolRowsWaves * kWave) void pool_rows_wg_kernel(
+    const T* __restrict__ x, int64_t xs0, int64_t xs1, T* __restrict__ out, int64_t os0,
+    int64_t os1, int T_len, int HD, int group) {
+  constexpr int V = Vec16<T>::N;
+  constexpr int E = V / kPoolRowsWaves;       // elements of a 4-byte word
+  constexpr int RW = kWave / kPoolRowsWaves;  // rows per wave per run
+  __shared__ uint4 st[kWave][kWave];          // [token of the run][lane]
+  const int w = static_cast<int>(threadIdx.x) / kWave, lane = lane_id();
+  const int col = (static_cast<int>(blockIdx.x) * kWave + lane) * V;
+  const bool ok = col < HD;
+  const int j = blockIdx.y, b = blockIdx.z;
+  const int t0 = j * group;
+  const int t1 = min(t0 + group, T_len);
+  const T* base = x + b * xs0 + (ok ? col : 0);
+  float acc[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) acc[i] = 0.0f;
+  for (int c0 = t0; c0 < t1; c0 += kWave) {  // workgroup-uniform
+    const int n = min(kWave, t1 - c0);
+    uint4 r[RW];
+#pragma unroll
+    for (int u = 0; u < RW; ++u) {
+      const int row = RW * w + u;
+      r[u] = (ok && row < n) ? *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(c0 + row) * xs1)
+                             : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < RW; ++u) st[RW * w + u][lane] = r[u];
+    __syncthreads();
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&st[0][lane]) + w;
+    for (int row = 0; row < n; ++row) {
+      const uint32_t word = src[row * kWave * 4];
+      const T* e = reinterpret_cast<const T*>(&word);
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[i] += to_f32<T>(e[i]);
+    }
+    __syncthreads();
+  }
+  if (!ok) return;
+  const float cnt = static_cast<float>(t1 - t0);
+  T* dst = out + b * os0 + static_cast<int64_t>(j) * os1 + col + E * w;
+#pragma unroll
+  for (int i = 0; i < E; ++i) dst[i] = from_f32<T>(acc[i] / cnt);
+}
+
 // Any strides: one thread per output element.
 template <typename T>
 __global__ __launch_bounds__(256) void pool_generic_kernel(View4<const T> x, View4<T> out, int B,
@@ -100,9 +152,14 @@ int launch_pool(const omm_view4& x, const omm_view4& out, int group, hipStream_t
   if (rows_ok) {
     const dim3 grid(static_cast<unsigned>(cdiv64(HD, 64 * V)), static_cast<unsigned>(MG),
                     static_cast<unsigned>(B));
-    pool_rows_kernel<T><<<grid, 64, 0, stream>>>(static_cast<const T*>(x.data), x.stride[0],
-                                                 x.stride[1], static_cast<T*>(const_cast<void*>(out.data)),
-                                                 out.stride[0], out.stride[1], T_len, HD, group);
+    const T* xp = static_cast<const T*>(x.data);
+    T* op = static_cast<T*>(const_cast<void*>(out.data));
+    if (static_cast<int64_t>(grid.x) * grid.y * grid.z < 1024)  // fewer than 4 waves per CU
+      pool_rows_wg_kernel<T><<<grid, kPoolRowsWaves * kWave, 0, stream>>>(
+          xp, x.stride[0], x.stride[1], op, out.stride[0], out.stride[1], T_len, HD, group);
+    else
+      pool_rows_kernel<T><<<grid, 64, 0, stream>>>(xp, x.stride[0], x.stride[1], op,
+                                                   out.stride[0], out.stride[1], T_len, HD, group);
   } else {
     const int64_t total = static_cast<int64_t>(B) * MG * H * D;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(cdiv64(total, 256), 65535));

@@ -29,8 +29,12 @@ def _img(t: torch.Tensor) -> np.ndarray:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("T,group", [(256, 64), (70, 64), (4680, 64), (300, 15), (5, 1)])
+@pytest.mark.parametrize("T,group", [(256, 64), (70, 64), (4680, 64), (300, 15), (5, 1),
+                                     (32768, 64), (130, 130)])
 def test_block_pool_bitexact(dtype, T, group):
+    """Small launches run the 4-wave kernel (rows staged in LDS), large ones (32768 tokens:
+    1,024 rows x 1 column slice) the one-wave kernel; group 130 takes two 64-token runs, the
+    second of 2 tokens."""
     from omnimem_amd.index_topk import block_pool
     g = torch.Generator().manual_seed(T * 7 + group)
     x = torch.randn((2, T, 3, 128), generator=g).to(dtype)
