@@ -147,6 +147,9 @@ class WanNSAAR:
         half = hd // 2
         self.inv_freq = 1.0 / (10000 ** (torch.arange(half, device=self.device, dtype=torch.float64) / half))
         self.timers: Optional[Dict[str, List]] = None
+        # set to a dict to record one layer's attention inputs and branch outputs (tests)
+        self.trace: Optional[Dict[str, torch.Tensor]] = None
+        self.trace_layer = 0
         self._rope_tab: Dict = {}
 
     # ------------------------------------------------------------------ pieces
@@ -225,6 +228,9 @@ class WanNSAAR:
         # selection with the branch mix g_cmp*o_cmp + g_slc*o_slc + g_swa*o_swa in its epilogue
         o = cache.select(q, ids, layer, cfg.group_size, gates=g, o_cmp=o_cmp, o_swa=o_swa)
         self._toc(tk)
+        if self.trace is not None and layer == self.trace_layer:
+            self.trace.update(q=q.clone(), g=g.clone(), ids=ids.clone(), o_cmp=o_cmp.clone(),
+                              o_swa=o_swa.clone(), o=o.clone())
         tk = self._tic("linear")
         out = F.linear(o.flatten(2), *blk.o)
         self._toc(tk)

@@ -4,9 +4,18 @@ The selection path must give the same model output whatever the cache residency:
 with identical seeds, one with every unit in HBM and one whose HBM pool forces evictions to the
 host pool (read there directly by the paged kernel), must produce bit-identical latents.  The
 second cache must actually have moved units, and its LRU bookkeeping must balance.
+
+One AR forward's layer is also checked branch by branch against the float64 oracle
+(oracle/nsa_oracle.py): the compressed attention over every pooled row, the window attention,
+the top-k over the pooled history (the MFMA parity check of tests/_topk_checks.py), the
+selection attention over the selected pages and the gated mix of the three
+(causal_wan_nsa_model.py:496-546).
 """
+import numpy as np
 import pytest
 import torch
+
+from oracle import nsa_oracle as O
 
 pytestmark = pytest.mark.gpu
 
@@ -59,3 +68,77 @@ def test_ar_output_independent_of_residency(dtype):
                 assert cb.where(l, h, c) in ("hbm", "host")
     ca.close()
     cb.close()
+
+
+def _close(name, got, want, mx=2e-2, mean=1e-3):
+    g = got.double().cpu().numpy() if isinstance(got, torch.Tensor) else got
+    err = np.abs(g - want)
+    assert err.max() <= mx, f"{name}: max-abs {err.max():.3e}"
+    assert err.mean() <= mean, f"{name}: mean-abs {err.mean():.3e}"
+
+
+def _dense_attn(q, k, v, scale):
+    """float64 softmax attention per head: q [M, H, D], k / v [N, H, D]."""
+    s = np.einsum("mhd,nhd->hmn", q, k) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return np.einsum("hmn,nhd->mhd", p / p.sum(-1, keepdims=True), v)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_ar_layer_branches_match_oracle(dtype):
+    from tests._topk_checks import check_mfma_topk
+    from omnimem_amd.block_cache import PagedKVCache
+    from omnimem_amd.wan_ar import WanNSAAR
+    cfg = _cfg()
+    history = 4
+    cid = history
+    cache = PagedKVCache(cfg.layers, cfg.heads, cfg.head_dim, max_chunks=cid + 2,
+                         chunk_len=cfg.chunk_tokens, page_tokens=cfg.page_tokens, dtype=dtype,
+                         hbm_slots=cfg.layers * cfg.heads * (cid + 2),
+                         window_chunks=cfg.window_chunks, keep_window_kv=(dtype == "fp8"))
+    model = WanNSAAR(cfg, cache, seed=3)
+    model.prefill(history, seed=4, student_t=(dtype == "fp8"))
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn((1, cfg.chunk_tokens, cfg.in_dim * cfg.patch), generator=g,
+                    device="cuda").to(torch.bfloat16)
+    model.trace, model.trace_layer = {}, 1
+    model.forward(x, 500.0, cid)
+    torch.cuda.synchronize()
+    tr = model.trace
+    layer, C, P, G, D = 1, cfg.chunk_tokens, cfg.page_tokens, cfg.group_size, cfg.head_dim
+    scale = D ** -0.5
+    q = tr["q"][0].double().cpu().numpy()
+    # the cache's own K / V (fp8 pages dequantised) and pooled history, as the kernels read them
+    kall = torch.cat([cache._gather_chunk(layer, "k", c) for c in range(cid + 1)], 0)
+    vall = torch.cat([cache._gather_chunk(layer, "v", c) for c in range(cid + 1)], 0)
+    kc, vc = cache.cmp_history(layer)
+    kd, vd = kall.double().cpu().numpy(), vall.double().cpu().numpy()
+    # compressed attention over every pooled row of the history
+    o_cmp = _dense_attn(q, kc[0].double().cpu().numpy(), vc[0].double().cpu().numpy(), scale)
+    _close("o_cmp", tr["o_cmp"][0], o_cmp)
+    # window attention over the last window_chunks chunks (here the current one): the pages of a
+    # bf16 cache, the dense bf16 ring an fp8 cache keeps beside its pages
+    if dtype == "fp8":
+        wk, wv = cache.window_kv(layer)
+        wk, wv = wk[0].double().cpu().numpy(), wv[0].double().cpu().numpy()
+    else:
+        w0 = (cid + 1 - cfg.window_chunks) * C
+        wk, wv = kd[w0:], vd[w0:]
+    o_swa = _dense_attn(q, wk, wv, scale)
+    _close("o_swa", tr["o_swa"][0], o_swa)
+    # top-k: the driver's call, checked on the kernel's own scores plus the fp32 score bound
+    kw = dict(block_size=P, chunk_size=C, causal=False,
+              exclude_window_chunks=cfg.exclude_window_chunks, exclude_sink_chunks=0,
+              progressive_exclude=cfg.progressive_exclude, q_chunk_offset=cid,
+              blocks_per_chunk=cache.ppc)
+    mask = O.Mask(block_size=P, group_size=G, chunk_q=C, chunk_k=C, blocks_per_chunk=cache.ppc,
+                  q_chunk_offset=cid, ex_win=cfg.exclude_window_chunks, causal=0, prog_excl=1)
+    check_mfma_topk(tr["q"], kc, cfg.topk, mask, scale, G, got=tr["ids"].cpu().numpy(), **kw)
+    # selection attention over the selected pages, then the gated mix in float64
+    ids = tr["ids"].cpu().numpy()
+    o_slc, _ = O.selection_attention(q[None], kd[None], vd[None], ids, G, scale,
+                                     O.paged_block_tokens(C, P, cid + 1))
+    gt = tr["g"][0].double().cpu().numpy()
+    mix = gt[..., 0:1] * o_cmp + gt[..., 1:2] * o_slc[0] + gt[..., 2:3] * o_swa
+    _close("mix", tr["o"][0], mix)
+    cache.close()
