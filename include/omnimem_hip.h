@@ -310,9 +310,11 @@ int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_
 /* The same selection with the NSA branch mix fused into its epilogue:
  *   out = g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa
  * per (query, head), in fp32 with one rounding to bf16, where o_slc is the selection output
- * (never written separately) and lse, when given, is the selection's.  gates: bf16 [1, M, H, 3]
- * (the branch gates after their sigmoid), o_cmp / o_swa: bf16 [1, M, H, D] with unit dim
- * stride.  Needs the MFMA path (head dim 64 or 128, 16-byte q / out rows, finite non-zero scale).
+ * and lse, when given, is the selection's.  bf16 caches fuse the mix into the selection kernel's
+ * epilogue (o_slc is never written separately); fp8 caches write o_slc (rounded to bf16) and mix
+ * it in a second pass over out.  gates: bf16 [1, M, H, 3] (the branch gates after their
+ * sigmoid), o_cmp / o_swa: bf16 [1, M, H, D] with unit dim stride and 16-byte aligned rows.
+ * Needs the MFMA path (head dim 64 or 128, 16-byte q / out rows, finite non-zero scale).
  * Reference: the gate combine of causal_wan_nsa_model.py:541-546 after the three branches. */
 int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                             int32_t group_size, float scale, const omm_view4* gates,

@@ -191,7 +191,7 @@ constexpr int kMfmaThreads = 128;
 template <typename QT, typename Acc, int D, bool QK8 = false>
 __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
-    int MG, int T, int chunk, float scale, int nsub, GateArgs gate) {
+    int MG, int T, int chunk, float scale, int nsub) {
   constexpr int KP = D + 8;
   constexpr int KS = 64 * KP, VS = D * kVP;
   constexpr int SD = D / 32;   // k-steps of QK^T
@@ -444,15 +444,6 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
       for (int i = 0; i < ND; ++i) {
         const int d0 = 16 * i + 4 * j4;
         uint2 w2;
-        if constexpr (sizeof(QT) == 2) {
-          if (gate.g != nullptr) {  // launch-uniform
-            const float o4[4] = {o[x][i][0] * inv, o[x][i][1] * inv, o[x][i][2] * inv,
-                                 o[x][i][3] * inv};
-            w2 = gate_mix4(gate, b, my_q[x], h, d0, o4);
-            *reinterpret_cast<uint2*>(op + d0) = w2;
-            continue;
-          }
-        }
         w2.x = Mfma<QT>::pack2(o[x][i][0] * inv, o[x][i][1] * inv);
         w2.y = Mfma<QT>::pack2(o[x][i][2] * inv, o[x][i][3] * inv);
         *reinterpret_cast<uint2*>(op + d0) = w2;
@@ -870,13 +861,67 @@ inline int geom(const omm_view4& q, int64_t MGv, int64_t T, int G, Geom& g) {
   return OMM_OK;
 }
 
+// out = g0 * o_cmp + g1 * out + g2 * o_swa in place, fp32 arithmetic and one rounding: the gated
+// mix after the register-staged kernels, which keep no gate code.  Their epilogue would read
+// o_cmp / o_swa at the end of every workgroup; on the fp8 AR call that cost ~37 us against
+// ~8 us for this pass (and the gate code slowed the ungated kernel too).  One thread per 8 dims
+// of one (b, m, h).
+__global__ __launch_bounds__(256) void branch_mix_kernel(GateArgs ga, View4<bf16_t> out, int M,
+                                                         int H, int C8, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int c = static_cast<int>(i % C8);
+    int64_t r = i / C8;
+    const int h = static_cast<int>(r % H);
+    r /= H;
+    const int m = static_cast<int>(r % M);
+    const int b = static_cast<int>(r / M);
+    const uint16_t* gp =
+        reinterpret_cast<const uint16_t*>(ga.g + b * ga.gs0 + m * ga.gs1 + h * ga.gs2);
+    const float g0 = bf16_bits_to_f32(gp[0]), g1 = bf16_bits_to_f32(gp[ga.gs3]);
+    const float g2 = bf16_bits_to_f32(gp[2 * ga.gs3]);
+    uint4* op = reinterpret_cast<uint4*>(out.at(b, m, h, 8 * c));
+    const uint4 sv = *op;
+    const uint4 cv = *reinterpret_cast<const uint4*>(ga.oc + b * ga.cs0 + m * ga.cs1 + h * ga.cs2 + 8 * c);
+    const uint4 wv = *reinterpret_cast<const uint4*>(ga.ow + b * ga.ws0 + m * ga.ws1 + h * ga.ws2 + 8 * c);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w}, cw[4] = {cv.x, cv.y, cv.z, cv.w};
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t res[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float r2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float cf = __builtin_bit_cast(float, e ? cw[k] & 0xffff0000u : cw[k] << 16);
+        const float sf = __builtin_bit_cast(float, e ? sw[k] & 0xffff0000u : sw[k] << 16);
+        const float wf = __builtin_bit_cast(float, e ? ww[k] & 0xffff0000u : ww[k] << 16);
+        r2[e] = __builtin_fmaf(g2, wf, __builtin_fmaf(g1, sf, g0 * cf));
+      }
+      res[k] = pack_bf16x2(r2[0], r2[1]);
+    }
+    *op = make_uint4(res[0], res[1], res[2], res[3]);
+  }
+}
+
+int launch_mix(const omm_view4& out, const GateArgs& gate, hipStream_t s) {
+  const int B = static_cast<int>(out.size[0]), M = static_cast<int>(out.size[1]);
+  const int H = static_cast<int>(out.size[2]), C8 = static_cast<int>(out.size[3] / 8);
+  const int64_t n = static_cast<int64_t>(B) * M * H * C8;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(cdiv64(n, 256), 4096));
+  branch_mix_kernel<<<blocks, 256, 0, s>>>(gate, make_view<bf16_t>(out), M, H, C8, n);
+  return check_launch("selection attention (branch mix)");
+}
+
 template <typename QT, typename Acc, int D>
 int launch_mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
                 const Acc& acc, int chunk, float scale, hipStream_t s, const GateArgs& gate) {
   sel_fwd_mfma_kernel<QT, Acc, D><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
       make_view<const QT>(q), make_view<QT>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T, chunk,
-      scale, gm.nsub, gate);
-  return check_launch("selection attention (mfma)");
+      scale, gm.nsub);
+  const int rc = check_launch("selection attention (mfma)");
+  if constexpr (sizeof(QT) == 2)
+    if (rc == OMM_OK && gate.g != nullptr) return launch_mix(out, gate, s);
+  return rc;
 }
 
 // fp8 pages with the fp8 QK^T (queries quantised per row), head dim 64 or 128
@@ -885,8 +930,10 @@ int launch_qk8(const Geom& gm, const omm_view4& q, const omm_view4& out, float* 
                const Acc& acc, int chunk, float scale, hipStream_t s, const GateArgs& gate) {
   sel_fwd_mfma_kernel<bf16_t, Acc, D, true><<<static_cast<unsigned>(gm.items), kMfmaThreads, 0, s>>>(
       make_view<const bf16_t>(q), make_view<bf16_t>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
-      chunk, scale, gm.nsub, gate);
-  return check_launch("selection attention (fp8 QK)");
+      chunk, scale, gm.nsub);
+  const int rc = check_launch("selection attention (fp8 QK)");
+  if (rc == OMM_OK && gate.g != nullptr) return launch_mix(out, gate, s);
+  return rc;
 }
 
 template <typename QT, typename Acc, int D>
@@ -1143,11 +1190,11 @@ extern "C" int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids,
     for (int i = 0; i < 4; ++i)
       OMM_REQUIRE(o->size[i] == q->size[i], OMM_EINVAL,
                   "omm_sel_fwd_paged_gated: o_cmp / o_swa must have q's shape");
-    OMM_REQUIRE(o->stride[3] == 1 && o->stride[0] % 4 == 0 && o->stride[1] % 4 == 0 &&
-                    o->stride[2] % 4 == 0 && (reinterpret_cast<uintptr_t>(o->data) & 7u) == 0,
+    OMM_REQUIRE(o->stride[3] == 1 && o->stride[0] % 8 == 0 && o->stride[1] % 8 == 0 &&
+                    o->stride[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(o->data) & 15u) == 0,
                 OMM_EUNSUPPORTED,
-                "omm_sel_fwd_paged_gated: o_cmp / o_swa need unit dim stride and 8-byte "
-                "aligned 4-element groups");
+                "omm_sel_fwd_paged_gated: o_cmp / o_swa need unit dim stride and 16-byte "
+                "aligned rows");
   }
   GateArgs ga;
   ga.g = static_cast<const bf16_t*>(gates->data);

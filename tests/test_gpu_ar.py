@@ -70,10 +70,13 @@ def test_ar_output_independent_of_residency(dtype):
     cb.close()
 
 
-def _close(name, got, want, mx=2e-2, mean=1e-3):
+def _close(name, got, want, mx=2e-2, mean=1e-3, rel=0.0):
+    """max-abs <= mx + rel * max|want| (rel covers bf16 roundings of large values), and mean-abs
+    <= mean."""
     g = got.double().cpu().numpy() if isinstance(got, torch.Tensor) else got
     err = np.abs(g - want)
-    assert err.max() <= mx, f"{name}: max-abs {err.max():.3e}"
+    bound = mx + rel * np.abs(want).max()
+    assert err.max() <= bound, f"{name}: max-abs {err.max():.3e} > {bound:.3e}"
     assert err.mean() <= mean, f"{name}: mean-abs {err.mean():.3e}"
 
 
@@ -140,5 +143,6 @@ def test_ar_layer_branches_match_oracle(dtype):
                                      O.paged_block_tokens(C, P, cid + 1))
     gt = tr["g"][0].double().cpu().numpy()
     mix = gt[..., 0:1] * o_cmp + gt[..., 1:2] * o_slc[0] + gt[..., 2:3] * o_swa
-    _close("mix", tr["o"][0], mix)
+    # an fp8 cache rounds o_slc to bf16 before its mix pass: two roundings of the output scale
+    _close("mix", tr["o"][0], mix, rel=2.0 ** -7 if dtype == "fp8" else 0.0)
     cache.close()
