@@ -79,14 +79,17 @@ ALGO = {
         # bf16 window attention over the window's pages: 4680 queries x 3 chunks of keys
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 4>": (
             "flops", 4 * D * _AR_C * H * _AR_WIN * _AR_C),
+        # gated mix after an fp8 selection: read the compressed, selected and window outputs
+        # and the three gates, write the mixed output (in place over the selected one)
+        "branch_mix_kernel": ("bytes", 4 * _AR_C * H * D * 2 + _AR_C * H * 3 * 2),
     },
 }
 # kernels one call launches together, priced as a whole: the AR top-k (query pooling into the
 # workspace, split scoring + selection, merge) reads the chunk's q and the pooled history
 ALGO_GROUPS = {
     "ar": {
-        "AR top-k call (pool_rows + topk_mfma + merge)": (
-            ["pool_rows_kernel<bf16_t>", "topk_mfma_kernel<bf16_t, 128, false>",
+        "AR top-k call (pool_rows_wg + topk_mfma + merge)": (
+            ["pool_rows_wg_kernel<bf16_t>", "topk_mfma_kernel<bf16_t, 128, false>",
              "topk_merge_kernel"],
             "bytes", _AR_C * H * D * 2 + _AR_HIST * _AR_PPC * H * D * 2
             + _AR_PPC * H * TOPK * 4),
