@@ -623,11 +623,60 @@ def main():
     torch.cuda.synchronize()
     flops = useful_flops(ids, M, N, G, BS, CHUNK, D)
 
+    # Measurement order.  The GPU's clock drops within milliseconds of idling (host work such as
+    # the graph capture below) and takes about 20 ms of load to recover: the first ~20 steps after
+    # an idle period run about 20% slower than the sustained rate.  So the host-side work comes
+    # first, then the backward (about 25 ms of GPU work), the top-k timings, and right after them
+    # the step's warm-up and timed steps, with no idle period in between.
+    #
+    # config 2: top-k alone (pool + score + select).  One call is shorter than its host-side
+    # enqueue, so back-to-back calls would time the host: the calls are captured once in a HIP
+    # graph and the replays timed; the eager per-call time is reported beside it
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g_topk = torch.cuda.CUDAGraph()
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        topk_step()  # allocations of the captured calls come from the graph's pool
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g_topk, stream=s_cap):
+            for _ in range(args.steps):
+                topk_ids = topk_step()
+    torch.cuda.current_stream().wait_stream(s_cap)
+    torch.cuda.synchronize()
+    g_topk.replay()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(topk_ids, topk_step(), rtol=0, atol=0)  # replays are exact
+
+    # selection backward on the same layer (dq, dk, dv from the step's out / lse): useful work is
+    # 2.5x the forward's (S recomputed, dP, dQ, dK, dV: 5 products of the forward's 2)
+    from omnimem_amd.selection import sel_bwd
+    d_out = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
+    for _ in range(2):
+        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record()
+    for _ in range(args.steps):
+        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
+    b1.record()
+    e0.record()
+    g_topk.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    bwd_ms = b0.elapsed_time(b1) / args.steps
+    bwd_tflops = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
+    topk_ms = e0.elapsed_time(e1) / args.steps
+    e0.record()
+    for _ in range(args.steps):
+        topk_step()
+    e1.record()
+    torch.cuda.synchronize()
+    topk_eager_ms = e0.elapsed_time(e1) / args.steps
+    del g_topk, d_out
+
     for _ in range(args.warmup):
         step()
         topk_step()
-    torch.cuda.synchronize()
-
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -647,54 +696,7 @@ def main():
     torch.cuda.synchronize()
     sel_ms = e0.elapsed_time(e1) / args.steps
 
-    # config 2: top-k alone (pool + score + select).  One call is shorter than its host-side
-    # enqueue, so back-to-back calls would time the host: the calls are captured once in a HIP
-    # graph and the replays timed; the eager per-call time is reported beside it
-    g_topk = torch.cuda.CUDAGraph()
-    s_cap = torch.cuda.Stream()
-    s_cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s_cap):
-        topk_step()  # allocations of the captured calls come from the graph's pool
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g_topk, stream=s_cap):
-            for _ in range(args.steps):
-                topk_ids = topk_step()
-    torch.cuda.current_stream().wait_stream(s_cap)
-    torch.cuda.synchronize()
-    g_topk.replay()
-    torch.cuda.synchronize()
-    torch.testing.assert_close(topk_ids, topk_step(), rtol=0, atol=0)  # replays are exact
-    e0.record()
-    g_topk.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    topk_ms = e0.elapsed_time(e1) / args.steps
-    e0.record()
-    for _ in range(args.steps):
-        topk_step()
-    e1.record()
-    torch.cuda.synchronize()
-    topk_eager_ms = e0.elapsed_time(e1) / args.steps
-    del g_topk
-
     sel_tflops = flops / (sel_ms * 1e-3) / 1e12
-
-    # selection backward on the same layer (dq, dk, dv from the step's out / lse): useful work is
-    # 2.5x the forward's (S recomputed, dP, dQ, dK, dV: 5 products of the forward's 2)
-    from omnimem_amd.selection import sel_bwd
-    d_out = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
-    for _ in range(2):
-        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
-    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    b0.record()
-    for _ in range(args.steps):
-        sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
-    b1.record()
-    torch.cuda.synchronize()
-    bwd_ms = b0.elapsed_time(b1) / args.steps
-    bwd_tflops = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
-    del d_out
 
     traffic = measured_traffic(ROOFLINE_KERNEL)
     res = {
