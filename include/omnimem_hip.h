@@ -131,7 +131,8 @@ typedef struct omm_paged_kv {
                                  pages read, e.g. host-link bytes), or NULL */
   int32_t qk_fp8;             /* fp8 caches: 1 = quantise the queries to e4m3 per query row
                                  (scale amax / 448) and compute Q K^T on fp8 MFMA with the K page
-                                 codes (head dim 64 / 128); 0 = dequantise K to bf16 */
+                                 codes (head dim 64 / 128); 0 = K codes widened to bf16
+                                 (bf16 MFMA; the page scales apply to the scores) */
 } omm_paged_kv;
 
 /* ---- library ------------------------------------------------------------------------- */

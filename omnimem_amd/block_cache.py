@@ -108,7 +108,8 @@ class PagedKVCache:
     ``hbm_budget_bytes`` (K + V + scales).  ``host_slots`` defaults to the units the HBM pool
     cannot hold plus one chunk of every layer and head (the slack a flush reserves).
     ``qk_fp8`` (fp8 caches): the selection quantises the queries to e4m3 per query row and runs
-    Q K^T on fp8 MFMA with the K page codes, instead of dequantising K to bf16.
+    Q K^T on fp8 MFMA with the K page codes, instead of widening the K codes to bf16 for the
+    bf16 MFMA (the page scales apply to the scores either way).
     """
 
     def __init__(self, num_layers: int, num_heads: int, head_dim: int, max_chunks: int,

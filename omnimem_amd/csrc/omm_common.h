@@ -81,7 +81,6 @@ __host__ __device__ inline float e4m3_to_f32(uint8_t c) {
 }
 
 // ---- hardware conversions (gfx950) ------------------------------------------------------------
-typedef float omm_f32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 omm_bf16x2;
 
 // Two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even).
@@ -89,11 +88,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const omm_bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, v);
 }
-// Four OCP e4m3fn codes (one word, byte 0 first) -> four floats, exact (v_cvt_pk_f32_fp8).
-__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* f) {
-  const omm_f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-  const omm_f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
-  f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
+// Eight OCP e4m3fn codes (byte 0 first) -> eight bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1:
+// exact; every e4m3 value is a bf16 value).
+__device__ __forceinline__ uint4 e4m3x8_to_bf16(uint2 c) {
+  const omm_bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, false);
+  const omm_bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, true);
+  const omm_bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, false);
+  const omm_bf16x2 e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, true);
+  return make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                    __builtin_bit_cast(uint32_t, d), __builtin_bit_cast(uint32_t, e));
 }
 // Four floats already within [-448, 448] -> four e4m3fn codes, round to nearest even
 // (v_cvt_pk_fp8_f32).

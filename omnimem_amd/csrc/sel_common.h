@@ -316,8 +316,8 @@ template <> __device__ __forceinline__ float kv_elem<f16_t>(const void* p, int64
   return static_cast<float>(static_cast<const _Float16*>(p)[i]);
 }
 template <> __device__ __forceinline__ float kv_elem<uint8_t>(const void* p, int64_t i, float s) {
-  // dequantised value as the MFMA path sees it: code * scale rounded to bf16
-  return bf16_bits_to_f32(f32_to_bf16_bits(e4m3_to_f32(static_cast<const uint8_t*>(p)[i]) * s));
+  // the dequantised value the MFMA path computes with: code * page scale in fp32
+  return e4m3_to_f32(static_cast<const uint8_t*>(p)[i]) * s;
 }
 
 // The same walk for a wave that resolved 64 slots at once: lane i holds the entry of slot

@@ -11,8 +11,9 @@
 //   softmax straight into the PV MFMA with no LDS round trip.
 //   sel_fwd_dma_kernel (16-bit K / V): K / V tiles copied global -> LDS by buffer_load ... lds,
 //   V read as V^T with ds_read_b64_tr_b16 (details at the kernel).
-//   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (dequantised while staging,
-//   x * page scale -> bf16) and for row strides the DMA kernel cannot address.
+//   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (e4m3 codes widened to bf16
+//   while staging, page scales folded into the softmax) and for row strides the DMA kernel
+//   cannot address.
 // fp32 (and any shape the MFMA kernels do not cover) runs a VALU kernel in full fp32.
 #include <type_traits>
 
@@ -29,37 +30,17 @@ namespace {
 // 16 row groups) and the 8-byte PV-operand reads (16 consecutive rows) conflict free.
 constexpr int kVP = 72;
 
-// 8 consecutive elements of a K/V row at byte address p as 8 MFMA-type elements: 16-bit storage
-// loads 16 bytes as is; fp8 pages load 8 bytes and dequantise (code * page scale, rounded).
-template <typename KVT> struct Row8;
-template <> struct Row8<bf16_t> {
-  __device__ __forceinline__ static uint4 load(const char* p, int, float) {
-    return *reinterpret_cast<const uint4*>(p);
-  }
-};
-template <> struct Row8<f16_t> {
-  __device__ __forceinline__ static uint4 load(const char* p, int, float) {
-    return *reinterpret_cast<const uint4*>(p);
-  }
-};
-template <> struct Row8<uint8_t> {
-  __device__ __forceinline__ static uint4 load(const char* p, int, float s) {
-    const uint2 c = *reinterpret_cast<const uint2*>(p);
-    float f[8];
-    e4m3x4_to_f32(c.x, f);
-    e4m3x4_to_f32(c.y, f + 4);
-    return make_uint4(pack_bf16x2(f[0] * s, f[1] * s), pack_bf16x2(f[2] * s, f[3] * s),
-                      pack_bf16x2(f[4] * s, f[5] * s), pack_bf16x2(f[6] * s, f[7] * s));
-  }
-};
 
 // Register staging of one 64-key tile by 128 threads.
 //   K: unit u = tid + 128 j -> key tid / DC + (128 / DC) j, 8-dim slice tid % DC (DC lanes per row)
 //   V: quad q = tid + 128 j -> dims slice tid % DC, keys 4 (tid / DC + (128 / DC) j) + r, r < 4
 // Each thread's byte offset inside a tile is computed once; a tile adds a wave-uniform base, so
 // the loads take the scalar-base + 32-bit-offset form with no per-load address arithmetic.
-// RAWK (fp8 pages): K stays in e4m3 codes (8 bytes per unit) for the fp8 QK^T MFMA; V is
-// dequantised as usual.
+// fp8 pages (F8) keep the e4m3 codes in registers (8 bytes per unit) and widen them to bf16 only
+// when the tile is stored to LDS (exact: every e4m3 value is a bf16 value).  The page scales are
+// not applied here: the kernel folds them into the softmax (K's into the exponent scale, V's into
+// p and the row sum), one per 64-key tile.  RAWK: K stays in codes in LDS too, for the fp8 QK^T
+// MFMA.
 template <typename KVT, int D, bool RAWK = false>
 struct Stager {
   static constexpr int DC = D / 8;                 // 16-byte slices per row
@@ -67,10 +48,12 @@ struct Stager {
   static constexpr int VQ = 16 * DC / 128;         // V quads per thread
   static constexpr int RS = 128 / DC;              // rows between a thread's units
   static constexpr int ES = static_cast<int>(sizeof(KVT));
+  static constexpr bool F8 = ES == 1;
   static constexpr int KP8 = D + 16;               // LDS row pitch of raw K codes (bytes)
-  uint4 k[RAWK ? 1 : KU];
-  uint2 k8[RAWK ? KU : 1];
-  uint4 v[VQ][4];
+  uint4 k[F8 ? 1 : KU];
+  uint2 k8[F8 ? KU : 1];
+  uint4 v[F8 ? 1 : VQ][4];
+  uint2 v8[F8 ? VQ : 1][4];
   uint32_t koff, voff;                             // bytes, within a tile
 
   __device__ __forceinline__ void init(int tid, int64_t sk, int64_t sv) {
@@ -81,13 +64,16 @@ struct Stager {
   __device__ __forceinline__ void zero() {
 #pragma unroll
     for (int j = 0; j < KU; ++j) {
-      if constexpr (RAWK) k8[j] = make_uint2(0, 0);
+      if constexpr (F8) k8[j] = make_uint2(0, 0);
       else k[j] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < VQ; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[j][r] = make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (F8) v8[j][r] = make_uint2(0, 0);
+        else v[j][r] = make_uint4(0, 0, 0, 0);
+      }
   }
 
   // Rows at or past n are not loaded: their registers keep finite values from an earlier tile
@@ -126,9 +112,9 @@ struct Stager {
     for (int j = 0; j < KU; ++j) {
       const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
       if (FULL || row0 + RS * j < n) {
-        if constexpr (RAWK) k8[j] = *reinterpret_cast<const uint2*>(p + koff);
+        if constexpr (F8) k8[j] = *reinterpret_cast<const uint2*>(p + koff);
         else if constexpr (U16) k[j] = load_u16(p + koff);
-        else k[j] = Row8<KVT>::load(p + koff, 0, br.scale_k);
+        else k[j] = *reinterpret_cast<const uint4*>(p + koff);
       }
     }
 #pragma unroll
@@ -137,8 +123,9 @@ struct Stager {
       for (int r = 0; r < 4; ++r) {
         const char* p = vb + static_cast<int64_t>(4 * RS * j + r) * br.sv * ES;
         if (FULL || 4 * (row0 + RS * j) + r < n) {
-          if constexpr (U16) v[j][r] = load_u16(p + voff);
-          else v[j][r] = Row8<KVT>::load(p + voff, 0, br.scale_v);
+          if constexpr (F8) v8[j][r] = *reinterpret_cast<const uint2*>(p + voff);
+          else if constexpr (U16) v[j][r] = load_u16(p + voff);
+          else v[j][r] = *reinterpret_cast<const uint4*>(p + voff);
         }
       }
     }
@@ -152,16 +139,24 @@ struct Stager {
       const int key = tid / DC + RS * j;
       if constexpr (RAWK)
         *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(Ks) + key * KP8 + dc * 8) = k8[j];
+      else if constexpr (F8)
+        *reinterpret_cast<uint4*>(Ks + key * KP + dc * 8) = e4m3x8_to_bf16(k8[j]);
       else
         *reinterpret_cast<uint4*>(Ks + key * KP + dc * 8) = k[j];
     }
 #pragma unroll
     for (int j = 0; j < VQ; ++j) {
       const int kq = tid / DC + RS * j;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[j][0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[j][1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[j][2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[j][3]);
+      uint4 vr4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (F8) vr4[r] = e4m3x8_to_bf16(v8[j][r]);
+        else vr4[r] = v[j][r];
+      }
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vr4[0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vr4[1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vr4[2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vr4[3]);
       // rows 8 dc .. 8 dc + 7 share the swizzle (8 dc) >> 3 = dc
       uint16_t* vrow = Vt + (8 * dc) * kVP + ((kq ^ (dc & 15)) << 2);
 #pragma unroll
@@ -289,8 +284,9 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   }
 
   using KVT = typename Acc::KV;
+  constexpr bool kFp8 = sizeof(KVT) == 1;
   Stager<KVT, D, QK8> st;
-  float sk_next = 1.0f;  // K page scale of the tile being staged (QK8)
+  float sk_next = 1.0f, sv_next = 1.0f;  // page scales of the tile being staged (fp8 pages)
   WaveWalk<Acc> wk;
   wk.start(acc, b, g, h, T, qc);
   st.init(tid, wk.br.sk, wk.br.sv);  // row strides are the same for every block of a call
@@ -299,25 +295,39 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   constexpr bool kMis = Acc::kMayMisalign && sizeof(KVT) == 2;
   if (wk.valid) {
     st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);
-    sk_next = wk.br.scale_k;
+    if constexpr (kFp8) {
+      sk_next = wk.br.scale_k;
+      sv_next = wk.br.scale_v;
+    }
   }
   while (wk.valid) {
     __syncthreads();  // every wave is done reading the previous tile
     st.store(Ks, Vt, tid);
     __syncthreads();
     const int tile_n = wk.n;
-    const float sk_cur = sk_next;
+    const float sk_cur = sk_next, sv_cur = sv_next;
     wk.advance(acc, b, g, h, T, qc);
     if (wk.valid) {
       st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);  // in flight during the MFMAs
-      sk_next = wk.br.scale_k;
+      if constexpr (kFp8) {
+        sk_next = wk.br.scale_k;
+        sv_next = wk.br.scale_v;
+      }
     }
-    // exponent scale per query block: the softmax scale, and for fp8 scores the two
-    // dequantisation scales
+    // exponent scale per query block: the softmax scale, for fp8 pages times the K page scale
+    // (and the query scale of fp8 scores).  V's page scale goes into p as 2^(log2 s_v): p s_v
+    // feeds the PV MFMA and the row sum takes the tile's sum divided by s_v.
     float c2x[2] = {c2, c2};
+    float lv = 0.0f, inv_sv = 1.0f;
     if constexpr (QK8) {
       c2x[0] = c2 * sq[0] * sk_cur;
       c2x[1] = c2 * sq[1] * sk_cur;
+    } else if constexpr (kFp8) {
+      c2x[0] = c2x[1] = c2 * sk_cur;
+    }
+    if constexpr (kFp8) {
+      lv = __builtin_amdgcn_logf(sv_cur);     // log2 (scales are normal floats)
+      inv_sv = __builtin_amdgcn_rcpf(sv_cur);
     }
     if (wave_active) {
       // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16, for both query blocks.  A
@@ -391,16 +401,18 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
           m2[x] = mcand;
         }
         const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+        const float bias = kFp8 ? lv - msafe : -msafe;
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2x[x], -msafe));
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2x[x], bias));
             s4[x][t][r] = pv;
             ps += pv;
           }
-        lsum[x] += ps;
+        if constexpr (kFp8) lsum[x] = __builtin_fmaf(ps, inv_sv, lsum[x]);
+        else lsum[x] += ps;
       }
       // O^T += V^T P^T; k-slot e of lane group j4 is key 32u + 4 j4 + e (e < 4) or
       // 32u + 16 + 4 j4 + (e - 4), for both operands

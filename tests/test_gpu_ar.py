@@ -80,6 +80,24 @@ def _close(name, got, want, mx=2e-2, mean=1e-3, rel=0.0):
     assert err.mean() <= mean, f"{name}: mean-abs {err.mean():.3e}"
 
 
+def _cache_kv(cache, layer, n):
+    """K and V of chunks 0..n-1 as float64 [tokens, H, D], the values the selection kernel
+    computes with: bf16 pages as stored, fp8 pages as code * page scale."""
+    if not cache.fp8:
+        k = torch.cat([cache._gather_chunk(layer, "k", c) for c in range(n)], 0)
+        v = torch.cat([cache._gather_chunk(layer, "v", c) for c in range(n)], 0)
+        return k.double().cpu().numpy(), v.double().cpu().numpy()
+    C, H, D = cache.chunk_len, cache.H, cache.D
+    out = [np.zeros((n * C, H, D)), np.zeros((n * C, H, D))]
+    for c in range(n):
+        for h in range(H):
+            kc, vc, sk, sv = cache.read_unit(layer, h, c)
+            for i, (codes, sc) in enumerate(((kc, sk), (vc, sv))):
+                deq = O.dequantize_pages(codes.numpy(), sc.numpy()[:, None, None])
+                out[i][c * C:(c + 1) * C, h] = deq.reshape(-1, D)[:C]
+    return out[0], out[1]
+
+
 def _dense_attn(q, k, v, scale):
     """float64 softmax attention per head: q [M, H, D], k / v [N, H, D]."""
     s = np.einsum("mhd,nhd->hmn", q, k) * scale
@@ -112,10 +130,8 @@ def test_ar_layer_branches_match_oracle(dtype):
     scale = D ** -0.5
     q = tr["q"][0].double().cpu().numpy()
     # the cache's own K / V (fp8 pages dequantised) and pooled history, as the kernels read them
-    kall = torch.cat([cache._gather_chunk(layer, "k", c) for c in range(cid + 1)], 0)
-    vall = torch.cat([cache._gather_chunk(layer, "v", c) for c in range(cid + 1)], 0)
+    kd, vd = _cache_kv(cache, layer, cid + 1)
     kc, vc = cache.cmp_history(layer)
-    kd, vd = kall.double().cpu().numpy(), vall.double().cpu().numpy()
     # compressed attention over every pooled row of the history
     o_cmp = _dense_attn(q, kc[0].double().cpu().numpy(), vc[0].double().cpu().numpy(), scale)
     _close("o_cmp", tr["o_cmp"][0], o_cmp)

@@ -225,7 +225,8 @@ def test_paged_append_fp8_codes_and_scales_bitexact(H, D, P):
 
 def _paged_oracle_inputs(chunks_k, chunks_v, fp8_cache=None, layer=0):
     """Concatenate chunk tensors [1, C, H, D] into the oracle's [1, n*C, H, D]; for an fp8
-    cache, the dequantised values the kernel sees (code * scale rounded to bf16)."""
+    cache, the dequantised values the kernel computes with (code * page scale in fp32: the kernel
+    widens the codes to bf16 exactly and applies the scales to the scores and to p)."""
     if fp8_cache is None:
         return (torch.cat(chunks_k, 1).float().numpy(), torch.cat(chunks_v, 1).float().numpy())
     c = fp8_cache
@@ -238,7 +239,7 @@ def _paged_oracle_inputs(chunks_k, chunks_v, fp8_cache=None, layer=0):
             kc, vc, sk, sv = c.read_unit(layer, h, cid)
             for codes, sc, dst in ((kc, sk, out_k), (vc, sv, out_v)):
                 deq = O.dequantize_pages(codes.numpy(), sc.numpy()[:, None, None])
-                deq = O.round_to(deq, "bf16").reshape(-1, D)[:C]
+                deq = deq.reshape(-1, D)[:C]
                 dst[0, cid * C:(cid + 1) * C, h] = deq
     return out_k, out_v
 
@@ -302,9 +303,9 @@ def _quantized_rows(q: torch.Tensor) -> np.ndarray:
     return out
 
 
-def _fp8_cache_images(cache, n, round_k: bool):
-    """K and V as the kernels see them: codes * page scale (K rounded to bf16 when the kernel
-    stages it in bf16), V rounded to bf16."""
+def _fp8_cache_images(cache, n):
+    """K and V as the kernels compute with them: codes * page scale in fp32 (the codes are
+    widened exactly and the scales applied to the scores and to p)."""
     H, D, C = cache.H, cache.D, cache.chunk_len
     kk = np.zeros((1, n * C, H, D), np.float32)
     vv = np.zeros_like(kk)
@@ -313,8 +314,8 @@ def _fp8_cache_images(cache, n, round_k: bool):
             kc, vc, sk, sv = cache.read_unit(0, h, cid)
             k = O.dequantize_pages(kc.numpy(), sk.numpy()[:, None, None]).reshape(-1, D)[:C]
             v = O.dequantize_pages(vc.numpy(), sv.numpy()[:, None, None]).reshape(-1, D)[:C]
-            kk[0, cid * C:(cid + 1) * C, h] = O.round_to(k, "bf16") if round_k else k
-            vv[0, cid * C:(cid + 1) * C, h] = O.round_to(v, "bf16")
+            kk[0, cid * C:(cid + 1) * C, h] = k
+            vv[0, cid * C:(cid + 1) * C, h] = v
     return kk, vv
 
 
@@ -322,7 +323,7 @@ def _fp8_cache_images(cache, n, round_k: bool):
 def test_paged_selection_fp8_qk_matches_oracle(D, G, sign):
     """The fp8 Q K^T variant (qk_fp8): queries quantised to e4m3 per query row, K page codes on
     fp8 MFMA.  Checked against the float64 oracle run on the quantised queries and the
-    dequantised K (V dequantised and rounded to bf16, as staged), at the bf16 tolerances; a
+    dequantised K and V, at the bf16 tolerances; a
     negative scale exercises the codes' sign flip."""
     from omnimem_amd.block_cache import PagedKVCache
     g = torch.Generator().manual_seed(int(D + G + (sign < 0)))
@@ -342,7 +343,7 @@ def test_paged_selection_fp8_qk_matches_oracle(D, G, sign):
     ids[0, 2, 1, :5] = -1
     scale = sign * D ** -0.5
     out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, softmax_scale=scale, return_lse=True)
-    kk, vv = _fp8_cache_images(cache, n, round_k=False)
+    kk, vv = _fp8_cache_images(cache, n)
     want_o, want_l = O.selection_attention(_quantized_rows(q), kk, vv, ids.numpy(), G, scale,
                                            O.paged_block_tokens(C, P, n))
     _check_attn(out, lse, want_o, want_l)
@@ -378,7 +379,7 @@ def test_gated_selection_mix_matches_float64(dtype, qk8, G):
     mix, lse = cache.select(qd, idd, 0, G, gates=gates.to(DEV), o_cmp=o_cmp.to(DEV),
                             o_swa=o_swa.to(DEV), return_lse=True)
     if fp8:
-        kk, vv = _fp8_cache_images(cache, n, round_k=not qk8)
+        kk, vv = _fp8_cache_images(cache, n)
         qq = _quantized_rows(q) if qk8 else q.float().numpy()
     else:
         kk, vv = torch.cat(ks, 1).float().numpy(), torch.cat(vs, 1).float().numpy()
