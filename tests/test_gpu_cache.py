@@ -291,6 +291,45 @@ def test_paged_selection_matches_oracle_and_is_residency_invariant(dtype, G):
     assert torch.equal(out, out3)
 
 
+@pytest.mark.parametrize("qk8", [False, True])
+def test_paged_selection_fp8_scale_extremes(qk8):
+    """fp8 pages whose scales span the float range: the kernel folds s_k into the exponent scale
+    and s_v into p as 2^(log2 s_v) with the row sum divided by s_v, so a zero V chunk (scale 1,
+    all codes 0), a tiny chunk (values ~1e-30) and a large one (values ~1e30 in V, K kept
+    moderate so the scores stay finite) must all match the float64 oracle on code * scale."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(91 + int(qk8))
+    torch.manual_seed(91)
+    H, D, C, P, T, n = 2, 128, 4680, 64, 16, 3
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype="fp8",
+                         qk_fp8=qk8, hbm_slots=H * n, host_slots=H * n, window_chunks=0)
+    ks = [_chunk(g, C, H, D, 0.3), _chunk(g, C, H, D, 1e-30), _chunk(g, C, H, D, 0.3)]
+    vs = [torch.zeros((1, C, H, D), dtype=torch.bfloat16), _chunk(g, C, H, D, 1e-30),
+          _chunk(g, C, H, D, 1e30)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    _, _, sk, sv = cache.read_unit(0, 0, 1)
+    assert float(sk.max()) < 1e-29 and float(cache.read_unit(0, 0, 0)[3].min()) == 1.0
+    M, G = 700, 64
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    MG = -(-M // G)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32)
+    out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, return_lse=True)
+    kk, vv = _fp8_cache_images(cache, n)
+    qq = _quantized_rows(q) if qk8 else q.float().numpy()
+    want_o, want_l = O.selection_attention(qq, kk, vv, ids.numpy(), G, D ** -0.5,
+                                           O.paged_block_tokens(C, P, n))
+    # outputs reach 1e30 where large-V pages are selected: compare relative to each row's scale
+    o = out.float().cpu().numpy().astype(np.float64)
+    scale = np.maximum(np.abs(want_o).max(-1, keepdims=True), 1e-300)
+    err = np.abs(o - want_o) / scale
+    assert np.isfinite(o).all()
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.abs(l - want_l).max() <= 1e-3
+
+
 def _quantized_rows(q: torch.Tensor) -> np.ndarray:
     """The e4m3 image of q [1, M, H, D] quantised per (query, head) row with the page rule
     (scale amax / 448, round to nearest even): codes * scale, fp32."""
