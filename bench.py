@@ -332,7 +332,10 @@ def topk_prepooled(q2, k2, want, steps):
     torch.testing.assert_close(out, want, rtol=0, atol=0)
     nbytes = qp.numel() * 2 + k2.numel() * 2 + out.numel() * 4
 
+    keep = (qp, k2, ws, out)  # the captured calls' buffers live as long as the graph is used
+
     def timed():
+        assert all(t is not None for t in keep)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         g.replay()
