@@ -28,7 +28,6 @@ Streams.  Every method enqueues on the current stream of ``device``; use one str
 from __future__ import annotations
 
 import ctypes
-import math
 from typing import Dict, Optional, Tuple
 
 import numpy as np

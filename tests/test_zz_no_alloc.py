@@ -1,8 +1,6 @@
 """The allocation-free top-k entry point (omm_topk_fused_noalloc) against omm_topk_fused, both
 called through the C ABI: identical indices on two calls in a row, the second smaller, so the
 second reuses the per-GPU scratch array the first left filled."""
-import ctypes
-
 import numpy as np
 import pytest
 import torch
