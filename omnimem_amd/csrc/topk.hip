@@ -1625,7 +1625,7 @@ extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, i
                         float scale, const omm_topk_mask* mask, int32_t* out, void* workspace,
                         size_t workspace_bytes, void* stream) {
   using namespace omm;
-  OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL, "omm_topk: null argument");
+  OMM_REQUIRE(q != nullptr && k != nullptr, OMM_EINVAL, "omm_topk: null argument");
   int rc = check_mask(mask);
   if (rc) return rc;
   const int64_t B = q->size[0], MG = q->size[1], H = q->size[2], D = q->size[3], NC = k->size[1];
@@ -1638,7 +1638,8 @@ extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, i
   const int es = esize_of(dtype);
   rc = check_sizes(B, MG, H, NC, topk, static_cast<int>(D), es, false);
   if (rc) return rc;
-  if (B == 0 || MG == 0 || H == 0) return OMM_OK;
+  if (B == 0 || MG == 0 || H == 0) return OMM_OK;  // empty output: out may be null
+  OMM_REQUIRE(out != nullptr, OMM_EINVAL, "omm_topk: null out");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   if (m2_ok(dtype, *q, *k, topk)) {
@@ -1677,8 +1678,7 @@ namespace {
 int topk_fused_impl(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t group_size,
                     int32_t topk, float scale, const omm_topk_mask* mask, int32_t* out,
                     float* dump, void* workspace, size_t workspace_bytes, void* stream) {
-  OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL,
-              "omm_topk_fused: null argument");
+  OMM_REQUIRE(q != nullptr && k != nullptr, OMM_EINVAL, "omm_topk_fused: null argument");
   OMM_REQUIRE(group_size >= 1, OMM_EINVAL, "omm_topk_fused: group_size must be >= 1, got %d",
               group_size);
   int rc = check_mask(mask);
@@ -1698,7 +1698,8 @@ int topk_fused_impl(const omm_view4* q, const omm_view4* k, int32_t dtype, int32
   const int es = esize_of(dtype);
   rc = check_sizes(B, MG, H, NC, topk, static_cast<int>(D), es, false);
   if (rc) return rc;
-  if (B == 0 || MG == 0 || H == 0) return OMM_OK;
+  if (B == 0 || MG == 0 || H == 0) return OMM_OK;  // empty output: out may be null
+  OMM_REQUIRE(out != nullptr, OMM_EINVAL, "omm_topk_fused: null out");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   OMM_REQUIRE(q->data != nullptr && k->data != nullptr, OMM_EINVAL, "omm_topk_fused: null data");
@@ -1790,12 +1791,12 @@ extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, 
                                     int32_t* out, void* workspace, size_t workspace_bytes,
                                     void* stream) {
   using namespace omm;
-  OMM_REQUIRE(out != nullptr, OMM_EINVAL, "omm_topk_from_scores: null output");
   int rc = check_mask(mask);
   if (rc) return rc;
   rc = check_sizes(B, MG, H, NC, topk, 128, 4, true);
   if (rc) return rc;
-  if (B == 0 || MG == 0 || H == 0) return OMM_OK;
+  if (B == 0 || MG == 0 || H == 0) return OMM_OK;  // empty output: out may be null
+  OMM_REQUIRE(out != nullptr, OMM_EINVAL, "omm_topk_from_scores: null output");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   OMM_REQUIRE(scores != nullptr, OMM_EINVAL, "omm_topk_from_scores: null scores");
@@ -1864,8 +1865,7 @@ extern "C" int omm_topk_fused_noalloc(const omm_view4* q, const omm_view4* k, in
                                       int32_t group_size, int32_t topk, float scale,
                                       const omm_topk_mask* mask, int32_t* out, void* stream) {
   using namespace omm;
-  OMM_REQUIRE(q != nullptr && k != nullptr && out != nullptr, OMM_EINVAL,
-              "omm_topk_fused_noalloc: null argument");
+  OMM_REQUIRE(q != nullptr && k != nullptr, OMM_EINVAL, "omm_topk_fused_noalloc: null argument");
   const size_t need = omm_topk_fused_workspace_bytes(q->size[0], q->size[1], q->size[2],
                                                      q->size[3], k->size[1], group_size, topk,
                                                      dtype);

@@ -216,3 +216,32 @@ def test_dense_attention_window_shape_sampled():
                                            groups=groups)
     rows = np.concatenate([np.arange(g * 64, min(M, g * 64 + 64)) for g in groups])
     _check(out, lse, want_o, want_l, torch.bfloat16, rows=rows)
+
+
+def test_empty_shapes():
+    """Degenerate sizes through the facades (the reference's early returns): no queries, no key
+    blocks (every id -1, top-k all -1), and no keys at all (out 0, lse -inf)."""
+    from omnimem_amd.index_topk import block_pool, parallel_nsa_topk
+    from omnimem_amd.selection import sel_fwd
+    H, D = 2, 128
+    g = torch.Generator().manual_seed(5)
+    # no queries: empty ids, empty out / lse
+    q0 = torch.empty((1, 0, H, D), dtype=torch.bfloat16, device=DEV)
+    k = torch.randn((1, 256, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    kc = block_pool(k, 64)
+    ids0 = parallel_nsa_topk(q0, kc, 4, block_size=64, chunk_size=64, causal=False, group_size=64)
+    assert tuple(ids0.shape) == (1, 0, H, 4)
+    out0, lse0 = sel_fwd(q0, k, k, ids0, 64, 1, D ** -0.5, False, 64)
+    assert out0.numel() == 0 and lse0.numel() == 0
+    # pooling of zero tokens
+    assert block_pool(q0, 64).shape[1] == 0
+    # no key blocks: every slot -1
+    q = torch.randn((1, 128, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    kc0 = torch.empty((1, 0, H, D), dtype=torch.bfloat16, device=DEV)
+    ids = parallel_nsa_topk(q, kc0, 4, block_size=64, chunk_size=64, causal=False, group_size=64)
+    assert tuple(ids.shape) == (1, 2, H, 4) and bool((ids == -1).all())
+    # no keys: ids past the end select nothing, so out is 0 and lse -inf
+    k0 = torch.empty((1, 0, H, D), dtype=torch.bfloat16, device=DEV)
+    ids_any = torch.zeros((1, 2, H, 4), dtype=torch.int32, device=DEV)
+    out, lse = sel_fwd(q, k0, k0, ids_any, 64, 1, D ** -0.5, False, 64)
+    assert bool((out == 0).all()) and bool(torch.isneginf(lse).all())
