@@ -40,6 +40,10 @@
  *   omm_sel_fwd_paged       <- selection_attention_padded_ptr_fast
  *                              (nsa/ops/selection/padded_ptr/wrapper.py:458-553) over the paged
  *                              cache, with int32 unit slots instead of raw int64 addresses
+ *   omm_sel_fwd_paged_gated <- the same, with the branch mix of causal_wan_nsa_model.py:541-546
+ *   omm_host_alloc / _free  <- MMCache's pinned offload buffers (models/cache.py:970-1016)
+ *   omm_topk_fused_noalloc, omm_topk_fused_debug: no reference counterpart (callers that cannot
+ *                              allocate; a test hook that also returns the scores)
  */
 #ifndef OMNIMEM_HIP_H_
 #define OMNIMEM_HIP_H_
@@ -140,7 +144,9 @@ const char* omm_last_error(void);
 int omm_abi_version(void); /* 3 */
 
 /* Pinned, device-mapped host memory for the cache's host pool; *dev receives the device
- * address (equal to *host on ROCm with unified addressing, but always use *dev on device). */
+ * address (equal to *host on ROCm with unified addressing, but always use *dev on device).
+ * Reference: the pinned offload buffers of MMCache.preallocate_offload_buffer
+ * (models/cache.py:970-1016) and the pinned tensors of its eviction path (cache.py:853,906). */
 int omm_host_alloc(size_t bytes, void** host, void** dev);
 int omm_host_free(void* host);
 
