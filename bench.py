@@ -594,8 +594,11 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
         "per_chunk": {
             "evicted_bytes": d("evicted_bytes"),
             "promoted_bytes": d("promoted_bytes"),
-            "host_units_touched": d("misses"),
-            "hbm_units_touched": d("hits"),
+            "host_units_touched": d("host_units_touched"),
+            "hbm_units_touched": d("hbm_units_touched"),
+            # per-call unit accesses (the reference's LRU accesses) served by each pool
+            "host_unit_accesses": d("misses"),
+            "hbm_unit_accesses": d("hits"),
             # (layer, head, page) triples read from each pool, each counted once per chunk
             "host_pages_unique": d("host_pages_unique"),
             "hbm_pages_unique": d("hbm_pages_unique"),

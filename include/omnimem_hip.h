@@ -137,11 +137,14 @@ typedef struct omm_paged_kv {
                                  (scale amax / 448) and compute Q K^T on fp8 MFMA with the K page
                                  codes (head dim 64 / 128); 0 = K codes widened to bf16
                                  (bf16 MFMA; the page scales apply to the scores) */
+  int32_t* touches;           /* [num_heads][max_chunks]: += 1 the first time a selection call
+                                 (one epoch) reads the unit, i.e. the reference's per-call LRU
+                                 accesses (models/cache.py:673-699), or NULL; needs kv->stamp */
 } omm_paged_kv;
 
 /* ---- library ------------------------------------------------------------------------- */
 const char* omm_last_error(void);
-int omm_abi_version(void); /* 3 */
+int omm_abi_version(void); /* 4 */
 
 /* Pinned, device-mapped host memory for the cache's host pool; *dev receives the device
  * address (equal to *host on ROCm with unified addressing, but always use *dev on device).
@@ -160,7 +163,13 @@ int omm_block_pool(const omm_view4* x, const omm_view4* out, int32_t dtype, int3
 /* ---- block scoring + top-k (a3, a4) -------------------------------------------------- */
 size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk);
 /* q: pooled queries [B, MG, H, D]; k: compressed keys [B, NC, H, D]; out: int32 contiguous
- * [B, MG, H, topk].  score = (sum_d fmaf(q_d, k_d, acc), d ascending) * scale in fp32.
+ * [B, MG, H, topk].  Scores are fp32, scale * <q, k>, computed one of two ways:
+ *  - MFMA path: bf16 / f16 inputs, head dim 64 or 128, topk <= 16, unit dim strides and 16-byte
+ *    aligned rows.  The products are exact and the fp32 sum runs in the matrix cores' order, so
+ *    a score lies within the fp32 summation bound of the exact dot product (not bit-equal to
+ *    the fmaf chain below); the selection is exact on these scores.
+ *  - VALU path (every other input, fp32 included): score = (sum_d fmaf(q_d, k_d, acc),
+ *    d ascending) * scale, bit-reproducible by a scalar fmaf loop.
  * Valid slots hold block ids in (score desc, id asc) order (+0 == -0); -1 pads rows with fewer
  * than topk visible blocks.  Invisible blocks and scores that are -inf or NaN are never
  * selected.  1 <= topk <= 64, D <= 256.  An empty output (B, MG or H zero) launches nothing and
@@ -311,7 +320,8 @@ int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_v
  * chunks or of units never written are skipped.  With kv->stamp and epoch > 0 every unit read
  * gets stamp = epoch (the LRU touch of the reference's _touch_lru_and_detect_missing,
  * nsa/ops/selection/padded_ptr/wrapper.py:253-291, without its host synchronisation); with
- * kv->reads, reads[h][cid] += 1 for every listed page of the unit. */
+ * kv->reads, reads[h][cid] += 1 for every listed page of the unit; with kv->touches as well,
+ * touches[h][cid] += 1 once per call (the unit's stamp moving to this epoch counts it). */
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
                       int32_t epoch, void* stream);
@@ -323,6 +333,10 @@ int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_
  * it in a second pass over out.  gates: bf16 [1, M, H, 3] (the branch gates after their
  * sigmoid), o_cmp / o_swa: bf16 [1, M, H, D] with unit dim stride and 16-byte aligned rows.
  * Needs the MFMA path (head dim 64 or 128, 16-byte q / out rows, finite non-zero scale).
+ * Aliasing: on a bf16 cache out may be the very view o_cmp or o_swa is (same address and
+ * strides: each element is read before it is written, by the same thread); any other overlap of
+ * out with o_cmp or o_swa, and on an fp8 cache any overlap at all (its first pass writes out
+ * before the mix reads the branches), is rejected with OMM_EINVAL.
  * Reference: the gate combine of causal_wan_nsa_model.py:541-546 after the three branches. */
 int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                             int32_t group_size, float scale, const omm_view4* gates,

@@ -49,6 +49,7 @@ class PagedKV(ctypes.Structure):
         ("n_slots", ctypes.c_int32), ("n_host_slots", ctypes.c_int32),
         ("page_seen", ctypes.c_void_p),
         ("qk_fp8", ctypes.c_int32),
+        ("touches", ctypes.c_void_p),
     ]
 
 

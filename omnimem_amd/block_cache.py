@@ -184,13 +184,17 @@ class PagedKVCache:
         self._stamp_all = torch.zeros((L, H, MC), dtype=torch.int32, device=self.device)
         self._reads_all = torch.zeros((L, H, MC), dtype=torch.int32, device=self.device)
         self._seen_all = torch.zeros((L, H, MC, self.ppc), dtype=torch.uint8, device=self.device)
+        # per-call unit accesses (the reference's LRU access count, models/cache.py:673-699)
+        self._touch_all = torch.zeros((L, H, MC), dtype=torch.int32, device=self.device)
         self.unit_table = list(self._unit_all.unbind(0))
         self.stamp = list(self._stamp_all.unbind(0))
         self.reads = list(self._reads_all.unbind(0))
         self.seen = list(self._seen_all.unbind(0))
+        self.touches = list(self._touch_all.unbind(0))
         self._h_stamp = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._h_reads = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._h_seen = torch.empty((L, H, MC, self.ppc), dtype=torch.uint8).pin_memory()
+        self._h_touch = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._ring = _UploadRing(8, max(L * H * MC, 2 * (self.n_slots + self.n_host)))
         self._d_idx = torch.empty(2 * (self.n_slots + self.n_host), dtype=torch.int32,
                                   device=self.device)
@@ -228,11 +232,16 @@ class PagedKVCache:
         self._stamp_all.zero_()
         self._reads_all.zero_()
         self._seen_all.zero_()
+        self._touch_all.zero_()
         self.n_chunks = [0] * self.L
         self._staged_k.clear()
         self._epoch = 0
         self._flush_epoch = 0
-        self.stats = {"hits": 0, "misses": 0, "evicted_units": 0, "promoted_units": 0,
+        # hits / misses: per-call unit accesses (a selection call reading a unit counts once)
+        # served from HBM / from the host pool, the reference's LRU hit and (non-cold) miss
+        # counts; *_units_touched: distinct units read between two flushes
+        self.stats = {"hits": 0, "misses": 0, "hbm_units_touched": 0, "host_units_touched": 0,
+                      "evicted_units": 0, "promoted_units": 0,
                       "evicted_bytes": 0, "promoted_bytes": 0, "flushes": 0,
                       "hbm_page_reads": 0, "host_page_reads": 0,
                       "hbm_pages_unique": 0, "host_pages_unique": 0}
@@ -262,6 +271,7 @@ class PagedKVCache:
         kv.stamp = self.stamp[layer].data_ptr()
         kv.reads = self.reads[layer].data_ptr()
         kv.page_seen = self.seen[layer].data_ptr()
+        kv.touches = self.touches[layer].data_ptr()
         kv.num_heads, kv.max_chunks, kv.n_chunks = self.H, self.max_chunks, self.n_chunks[layer]
         kv.chunk_len, kv.page_tokens, kv.pages_per_chunk = self.chunk_len, self.P, self.ppc
         kv.head_dim = self.D
@@ -497,6 +507,7 @@ class PagedKVCache:
         kv.stamp = None
         kv.reads = None
         kv.page_seen = None
+        kv.touches = None
         scale = softmax_scale if softmax_scale is not None else D ** -0.5
         _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(ids4), ctypes.byref(kv), G,
                   float(scale), _lib.view4(out), None, 0, _lib.stream_of(q),
@@ -733,17 +744,18 @@ class PagedKVCache:
         return n_ev, n_pr
 
     def _counts(self):
-        """Host copies of every layer's stamps, page-read counts and pages seen (one
-        synchronisation); the arrays are reused by the next call."""
+        """Host copies of every layer's stamps, page-read counts, pages seen and per-call unit
+        accesses (one synchronisation); the arrays are reused by the next call."""
         self._h_stamp.copy_(self._stamp_all, non_blocking=True)
         self._h_reads.copy_(self._reads_all, non_blocking=True)
         self._h_seen.copy_(self._seen_all, non_blocking=True)
+        self._h_touch.copy_(self._touch_all, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         return (self._h_stamp.numpy().astype(np.int64), self._h_reads.numpy(),
-                self._h_seen.numpy())
+                self._h_seen.numpy(), self._h_touch.numpy())
 
     def _make_room(self, need: int):
-        st, rd, _ = self._counts()
+        st, rd, _, _ = self._counts()
         desired = self._plan(st, reserve=need, rd=rd)
         self._apply(desired, st)
         if len(self._free_hbm) < need:
@@ -754,19 +766,25 @@ class PagedKVCache:
         read of the stamps and page counts, then batched evict / promote copies enqueued without
         synchronising.  With ``reserve_next_chunk`` the HBM slots of the next chunk of every
         layer and head are assigned here, so the appends of the next AR step never touch the
-        host.  Returns this flush's counts: units touched in HBM / on the host, page listings
-        (a page read by k selections counts k times) and unique pages read per pool."""
-        st, rd, sn = self._counts()
+        host.  Returns this flush's counts: per-call unit accesses served from HBM (hits) and
+        from the host pool (misses), distinct units touched per pool, page listings (a page read
+        by k selections counts k times) and unique pages read per pool.  Residency changes only
+        here (and in an append that finds no free slot, which a flush's reservation prevents),
+        so the pool a unit sits in now is the pool its accesses since the last flush used."""
+        st, rd, sn, tc = self._counts()
         touched = st > self._flush_epoch
         written = self._table_h != -1
         res, host = self._table_h >= 0, self._table_h <= -2
-        hits = int((touched & res).sum())
-        misses = int((touched & host).sum())
+        hbm_units = int((touched & res).sum())
+        host_units = int((touched & host).sum())
+        hits, misses = int(tc[res].sum()), int(tc[host].sum())
         hbm_reads, host_reads = int(rd[res].sum()), int(rd[host].sum())
         pages = sn.sum(-1, dtype=np.int64)
         hbm_unique, host_unique = int(pages[res].sum()), int(pages[host].sum())
         self.stats["hits"] += hits
         self.stats["misses"] += misses
+        self.stats["hbm_units_touched"] += hbm_units
+        self.stats["host_units_touched"] += host_units
         self.stats["hbm_page_reads"] += hbm_reads
         self.stats["host_page_reads"] += host_reads
         self.stats["hbm_pages_unique"] += hbm_unique
@@ -789,9 +807,11 @@ class PagedKVCache:
                 self._upload_table()
         self._reads_all.zero_()
         self._seen_all.zero_()
+        self._touch_all.zero_()
         self._flush_epoch = self._epoch
         self.stats["flushes"] += 1
-        return {"hits": hits, "misses": misses, "evicted_units": ev, "promoted_units": pr,
+        return {"hits": hits, "misses": misses, "hbm_units_touched": hbm_units,
+                "host_units_touched": host_units, "evicted_units": ev, "promoted_units": pr,
                 "hbm_page_reads": hbm_reads, "host_page_reads": host_reads,
                 "hbm_pages_unique": hbm_unique, "host_pages_unique": host_unique}
 
@@ -811,7 +831,10 @@ class PagedKVCache:
         new epoch, as the selection kernel does for every unit it reads."""
         if name not in ("k_cache", "v_cache"):
             raise BlockKVBackendError(f"unknown cache name {name!r}")
+        if self._table_h[layer_idx, int(head), int(cid)] == -1:
+            return  # never written: nothing to keep (a selection skips such units too)
         self.stamp[layer_idx][int(head), int(cid)] = self.next_epoch()
+        self.touches[layer_idx][int(head), int(cid)] += 1
 
     def get_chunk_metadata(self, layer_idx: int, name: str):
         """MMCache-compatible chunk table (models/cache.py:340-347): (int64 [H, max_chunks] byte
@@ -838,9 +861,23 @@ class PagedKVCache:
         return ptrs, n, strides
 
     def lru_hit_rate_overall(self) -> float:
-        """Fraction of touched units found in HBM (models/cache.py:713)."""
-        tot = self.stats["hits"] + self.stats["misses"]
-        return self.stats["hits"] / tot if tot else 0.0
+        """Hits over accesses since the last ``lru_reset_stats`` (models/cache.py:713-716): an
+        access is one selection call (or ``lru_touch_per_head``) reading a (layer, head, chunk)
+        unit, a hit when the unit is in HBM.  Accesses since the last flush are read from the
+        device counters (one synchronisation).  The reference also counts no access for a
+        chunk that is on the GPU but not yet in its LRU (a "cold miss"); here every HBM-resident
+        unit is in the resident set, so such accesses count as hits."""
+        tc = self._touch_all.cpu().numpy()
+        hits = self.stats["hits"] + int(tc[self._table_h >= 0].sum())
+        tot = hits + self.stats["misses"] + int(tc[self._table_h <= -2].sum())
+        return hits / tot if tot else 0.0
+
+    def lru_reset_stats(self):
+        """Zero the access counts behind ``lru_hit_rate_overall`` (models/cache.py:718-727);
+        residency, stamps and the other statistics are kept."""
+        self.stats["hits"] = 0
+        self.stats["misses"] = 0
+        self._touch_all.zero_()
 
     # ---------------------------------------------------------------- inspection (tests)
     def read_unit(self, layer: int, head: int, cid: int):
@@ -950,6 +987,10 @@ class MMCache(PagedKVCache):
         self.cmp_window = None if cw is None else int(cw)
         self.cmp_sink = int(sink.get("k_cmp_cache") or 0)
         self.config = config
+        # the reference's attribute (models/cache.py:63), which CausalWanNSAModel.forward checks
+        # for the pooled names (causal_wan_nsa_model.py:783-784); every paged cache serves them
+        self.available_type = list(config["cache_type"]) + [
+            t for t in ("k_cmp_cache", "v_cmp_cache") if t not in types]
         self.seq_dim = seq_dim
         self.dtype = dtype
         self.num_heads = H

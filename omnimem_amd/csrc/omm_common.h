@@ -35,6 +35,24 @@ int pool_launch(const omm_view4& x, const omm_view4& out, int32_t dtype, int gro
 
 inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Whether the byte spans of two views of elem-byte elements intersect (empty views never do;
+// negative strides widen the span downwards).
+inline bool views_overlap(const omm_view4& a, const omm_view4& b, int64_t elem) {
+  auto span = [elem](const omm_view4& v, intptr_t& lo, intptr_t& hi) {
+    lo = hi = reinterpret_cast<intptr_t>(v.data);
+    for (int i = 0; i < 4; ++i) {
+      if (v.size[i] <= 0) return false;
+      const int64_t ext = (v.size[i] - 1) * v.stride[i] * elem;
+      (ext < 0 ? lo : hi) += ext;
+    }
+    hi += elem;
+    return true;
+  };
+  intptr_t alo, ahi, blo, bhi;
+  if (!span(a, alo, ahi) || !span(b, blo, bhi)) return false;
+  return alo < bhi && blo < ahi;
+}
+
 // ---- scalar conversions (device + host) -------------------------------------------------
 __host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);

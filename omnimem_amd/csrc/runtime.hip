@@ -44,7 +44,7 @@ extern "C" {
 
 const char* omm_last_error(void) { return omm::g_err; }
 
-int omm_abi_version(void) { return 3; }
+int omm_abi_version(void) { return 4; }
 
 int omm_host_alloc(size_t bytes, void** host, void** dev) {
   OMM_REQUIRE(host != nullptr && dev != nullptr, OMM_EINVAL, "omm_host_alloc: null output");

@@ -198,6 +198,7 @@ struct PagedAcc {
   int32_t* stamp;
   int32_t* reads;
   uint8_t* seen;
+  int32_t* touches;
   int64_t is0, is1, is2, is3;
   int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
   __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
@@ -234,7 +235,8 @@ struct PagedAcc {
   __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.bid; }
   // LRU touch: stamp every readable unit this workgroup's row lists (duplicates store the same
   // epoch, so the races are benign), count its pages read (vector atomics) and mark each listed
-  // page seen (duplicates store the same 1)
+  // page seen (duplicates store the same 1).  With touches, the stamp is exchanged atomically and
+  // the one lane of the whole call that moves it to this epoch counts the unit's access.
   __device__ __forceinline__ void touch(int b, int g, int h, int T) const {
     const bool st = stamp != nullptr && epoch > 0;
     if (!st && reads == nullptr && seen == nullptr) return;
@@ -245,7 +247,11 @@ struct PagedAcc {
       if (cid >= n_chunks || cid >= max_chunks) continue;
       const int64_t u = static_cast<int64_t>(h) * max_chunks + cid;
       if (unit[u] == -1) continue;
-      if (st) stamp[u] = epoch;
+      if (st && touches != nullptr) {
+        if (atomicExch(stamp + u, epoch) != epoch) atomicAdd(touches + u, 1);
+      } else if (st) {
+        stamp[u] = epoch;
+      }
       if (reads != nullptr) atomicAdd(reads + u, 1);
       if (seen != nullptr) seen[u * ppc + (bid - cid * ppc)] = 1;
     }

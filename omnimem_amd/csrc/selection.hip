@@ -1147,7 +1147,8 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
     PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
                          nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
                          static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
-                         idp, kv->stamp, kv->reads, kv->page_seen, ids->stride[0], ids->stride[1], ids->stride[2],
+                         idp, kv->stamp, kv->reads, kv->page_seen, kv->touches, ids->stride[0],
+                         ids->stride[1], ids->stride[2],
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
                          kv->n_slots, kv->n_host_slots};
@@ -1160,7 +1161,7 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
                           kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
                           static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
                           kv->host_scale_v, kv->unit_table, idp, kv->stamp, kv->reads, kv->page_seen,
-                          ids->stride[0],
+                          kv->touches, ids->stride[0],
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
                           kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};
@@ -1207,6 +1208,19 @@ extern "C" int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids,
                 OMM_EUNSUPPORTED,
                 "omm_sel_fwd_paged_gated: o_cmp / o_swa need unit dim stride and 16-byte "
                 "aligned rows");
+  }
+  // out against the branches it mixes: the bf16 epilogue reads each element before the same
+  // thread writes it, so the identical view is safe there; the fp8 cache's first pass writes out
+  // before the mix pass reads the branches
+  OMM_REQUIRE(out != nullptr && kv != nullptr, OMM_EINVAL, "omm_sel_fwd_paged_gated: null argument");
+  for (const omm_view4* o : {o_cmp, o_swa}) {
+    const bool same = o->data == out->data && o->stride[0] == out->stride[0] &&
+                      o->stride[1] == out->stride[1] && o->stride[2] == out->stride[2] &&
+                      o->stride[3] == out->stride[3];
+    if (views_overlap(*o, *out, 2))
+      OMM_REQUIRE(same && kv->dtype == OMM_BF16, OMM_EINVAL,
+                  "omm_sel_fwd_paged_gated: out overlaps o_cmp or o_swa (only a bf16 cache "
+                  "accepts out as the very same view)");
   }
   GateArgs ga;
   ga.g = static_cast<const bf16_t*>(gates->data);

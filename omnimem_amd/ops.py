@@ -12,12 +12,20 @@ The CUDA-key implementations are the C-ABI calls of ``index_topk``, ``selection`
 ``padded_ptr`` (ctypes on the current stream, no host synchronisation); they raise
 ``NSABackendError`` on a bad argument, as the reference's adapters do.  The fakes compute
 output shapes, dtypes and layouts only.  Importing this module registers everything once.
+
+If another library already owns the ``omnimem_nsa`` namespace (the reference's extension loaded
+in the same process, e.g. for a side-by-side parity run), the ops are registered under
+``omnimem_amd_nsa`` instead and ``NAMESPACE`` names it: the reference's ops stay the reference's,
+and the facades of this package call their own through ``op()``.
 """
 from __future__ import annotations
 
+import warnings
+
 import torch
 
-NAMESPACE = "omnimem_nsa"
+REFERENCE_NAMESPACE = "omnimem_nsa"
+FALLBACK_NAMESPACE = "omnimem_amd_nsa"
 
 SCHEMAS = {
     "topk": "topk(Tensor q, Tensor k, int topk, float scale, int block_size, int chunk_size, "
@@ -50,6 +58,10 @@ SCHEMAS = {
                   "bool tf_mask, int q_chunk_offset, int group_size, int blocks_per_chunk) "
                   "-> Tensor",
     "block_pool": "block_pool(Tensor x, int group) -> Tensor",
+    # range check of selection block ids inside a traced graph (an op that mutates its sink is
+    # never dropped as dead code); raises ValueError when run, like the eager facade
+    "check_block_ids": "check_block_ids(Tensor(a!) sink, Tensor block_indices, int num_blocks) "
+                       "-> ()",
 }
 
 
@@ -71,6 +83,24 @@ def _topk_fused_cuda(q, k, topk, scale, block_size, chunk_size, causal, ex_win, 
 def _block_pool_cuda(x, group):
     from .index_topk import _block_pool_impl
     return _block_pool_impl(x, group)
+
+
+def check_block_ids_now(block_indices, num_blocks):
+    """The reference facade's id range check (nsa/ops/selection/__init__.py:36-42): one host
+    synchronisation, ValueError for a valid id >= num_blocks."""
+    valid_mask = block_indices >= 0
+    if valid_mask.any() and torch.any(block_indices[valid_mask] >= num_blocks):
+        raise ValueError(
+            f"top_idx out of range: expected in [-1, {num_blocks - 1}] "
+            f"but got [{block_indices.min()}, {block_indices.max()}]")
+
+
+def _check_block_ids_impl(sink, block_indices, num_blocks):
+    check_block_ids_now(block_indices, num_blocks)
+
+
+def _check_block_ids_fake(sink, block_indices, num_blocks):
+    return None
 
 
 def _sel_fwd_cuda(q, k, v, block_indices, block_size, chunk_size, scale, causal, group_size,
@@ -176,17 +206,39 @@ _IMPLS = {
     "build_ptr_table": (_build_ptr_table_cuda, _build_ptr_table_fake),
     "sel_fwd_ptr": (_sel_fwd_ptr_cuda, _sel_fwd_ptr_fake),
     "sel_bwd_ptr": (_sel_bwd_ptr_cuda, _sel_bwd_ptr_fake),
+    "check_block_ids": (_check_block_ids_impl, _check_block_ids_fake),
 }
+# keys each op is implemented for (the range check also runs on CPU tensors)
+_KEYS = {"check_block_ids": ("CUDA", "CPU")}
 
-_LIBRARY = torch.library.Library(NAMESPACE, "DEF")
+
+def _define_library():
+    """DEF library of the first namespace no other library owns."""
+    for ns in (REFERENCE_NAMESPACE, FALLBACK_NAMESPACE):
+        try:
+            lib = torch.library.Library(ns, "DEF")
+        except RuntimeError:
+            continue
+        if ns != REFERENCE_NAMESPACE:
+            warnings.warn(f"torch.ops.{REFERENCE_NAMESPACE} is owned by another library (the "
+                          f"reference extension?); this package's ops are torch.ops.{ns}.*",
+                          RuntimeWarning, stacklevel=3)
+        return ns, lib
+    from .backend import NSABackendError
+    raise NSABackendError(f"cannot register operators: namespaces {REFERENCE_NAMESPACE} and "
+                          f"{FALLBACK_NAMESPACE} are both owned by other libraries")
+
+
+NAMESPACE, _LIBRARY = _define_library()
 for _name, _schema in SCHEMAS.items():
     _LIBRARY.define(_schema)
     _real, _fake = _IMPLS[_name]
-    _LIBRARY.impl(_name, _real, "CUDA")
+    for _key in _KEYS.get(_name, ("CUDA",)):
+        _LIBRARY.impl(_name, _real, _key)
     torch.library.register_fake(f"{NAMESPACE}::{_name}", _fake, lib=_LIBRARY)
-del _name, _schema, _real, _fake
+del _name, _schema, _real, _fake, _key
 
 
 def op(name: str):
-    """The registered ``torch.ops.omnimem_nsa.<name>`` overload packet."""
+    """The registered ``torch.ops.<NAMESPACE>.<name>`` overload packet."""
     return getattr(getattr(torch.ops, NAMESPACE), name)

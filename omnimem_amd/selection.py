@@ -41,15 +41,13 @@ def _validate_common(q, k, v, block_indices, block_size, chunk_size, group_size,
     if block_indices.shape[-1] == 0:
         raise ValueError("top_idx last dim T must be > 0")
     num_blocks = math.ceil(N / block_size)
+    # One host sync per call, as in the reference; the op-level sel_fwd() skips it.  A traced
+    # graph cannot branch on tensor values, so there the same check runs as an op of the graph
+    # and raises the same ValueError when the graph runs.
     if torch.compiler.is_compiling():
-        # a traced graph cannot branch on tensor values; the kernel skips out-of-range ids
-        return num_blocks
-    # One host sync per call, as in the reference; the op-level sel_fwd() skips it.
-    valid_mask = block_indices >= 0
-    if valid_mask.any() and torch.any(block_indices[valid_mask] >= num_blocks):
-        raise ValueError(
-            f"top_idx out of range: expected in [-1, {num_blocks - 1}] "
-            f"but got [{block_indices.min()}, {block_indices.max()}]")
+        ops.op("check_block_ids")(block_indices.new_empty((1,)), block_indices, num_blocks)
+    else:
+        ops.check_block_ids_now(block_indices, num_blocks)
     return num_blocks
 
 

@@ -18,7 +18,7 @@ def test_header_and_binding_agree():
 
 
 def test_library_exports_every_header_symbol():
-    assert _lib.lib().omm_abi_version() == 3
+    assert _lib.lib().omm_abi_version() == 4
     assert _lib.missing_symbols() == []
 
 

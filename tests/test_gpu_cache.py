@@ -438,6 +438,42 @@ def test_gated_selection_mix_matches_float64(dtype, qk8, G):
     assert torch.equal(plain, via_gate)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_gated_selection_output_aliasing(dtype):
+    """out may be the very view o_cmp is on a bf16 cache (the fused epilogue reads each element
+    before writing it) and gives the same mix; an fp8 cache (two passes) rejects it, and both
+    reject a partial overlap."""
+    from omnimem_amd.backend import BlockKVBackendError
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(5)
+    H, D, C, P, T, n, G, M = 2, 128, 512, 64, 4, 2, 64, 256
+    fp8 = dtype == "fp8"
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         window_chunks=0)
+    for cid in range(n):
+        cache.append(0, _chunk(g, C, H, D, 0.3, fp8).to(DEV), _chunk(g, C, H, D, 1.0, fp8).to(DEV),
+                     cid)
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(M // G * H)])
+    ids = ids.view(1, M // G, H, T).to(torch.int32).to(DEV)
+    gates = torch.sigmoid(torch.randn((1, M, H, 3), generator=g)).to(torch.bfloat16).to(DEV)
+    o_cmp = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    o_swa = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16).to(DEV)
+    want = cache.select(q, ids, 0, G, gates=gates, o_cmp=o_cmp, o_swa=o_swa)
+    if fp8:
+        with pytest.raises(BlockKVBackendError, match="overlaps"):
+            cache.select(q, ids, 0, G, gates=gates, o_cmp=o_cmp, o_swa=o_swa, out=o_cmp)
+    else:
+        alias = o_cmp.clone()
+        got = cache.select(q, ids, 0, G, gates=gates, o_cmp=alias, o_swa=o_swa, out=alias)
+        assert got.data_ptr() == alias.data_ptr() and torch.equal(got, want)
+    buf = torch.zeros((1, M + 1, H, D), dtype=torch.bfloat16, device=DEV)
+    buf[:, :M] = o_swa
+    with pytest.raises(BlockKVBackendError, match="overlaps"):
+        cache.select(q, ids, 0, G, gates=gates, o_cmp=o_cmp, o_swa=buf[:, :M], out=buf[:, 1:])
+    cache.close()
+
+
 def test_fp8_quantisation_error_against_bf16_cache():
     """Config 5's error budget, per variant: selection-attention output over
     Student-t(4) K/V against float64 on the original bf16 values, for the bf16 cache, the fp8

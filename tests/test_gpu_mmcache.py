@@ -144,6 +144,61 @@ def test_reference_ar_sequence_against_mmcache():
     assert cache.block_seqlens["k_cmp_cache"] == S // BS
 
 
+def test_pipeline_chunk_protocol_and_lru_hit_rate():
+    """The pipeline's per-chunk cache protocol (pipeline_wan_causal.py:300-306, 404-406, 420-475)
+    and the model's entry checks (causal_wan_nsa_model.py:783-784) run against ``MMCache``:
+    ``reset``; per chunk ``lru_reset_stats``, then forwards (a denoise and the context forward),
+    each asserting ``available_type`` and running the layer's four ``update_cache`` calls and
+    the selection, then ``flush_offload`` and ``lru_hit_rate_overall``.  The hit rate must be
+    the reference's (models/cache.py:673-716): per selection call, each distinct (head, chunk)
+    unit it reads is one access, a hit when that unit is resident on the GPU; counted here from
+    the call's block ids and the cache's residency at the time of the call."""
+    n_chunks = 7
+    cache = _make_cache(n_chunks)
+    cache.reset()
+    g = torch.Generator().manual_seed(33)
+    ppc = S // BS
+    saw_miss = False
+    for cid in range(n_chunks):
+        cache.lru_reset_stats()
+        assert cache.lru_hit_rate_overall() == 0.0
+        hits = total = 0
+        k = (torch.randn((1, S, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+        v = torch.randn((1, S, H, D), generator=g).to(torch.bfloat16).to(DEV)
+        for fwd in range(2):
+            assert 'k_cmp_cache' in cache.available_type
+            assert 'v_cmp_cache' in cache.available_type
+            q = (torch.randn((1, S, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+            with torch.no_grad():
+                ids = _ar_layer(cache, q, k, v, 0, cid * S, TOPK)[-1]
+            units = {(h, int(b) // ppc) for (_, _, h, _), b in np.ndenumerate(ids.cpu().numpy())
+                     if b >= 0 and int(b) // ppc <= cid}
+            for h, c in units:
+                where = cache.where(0, h, c)
+                assert where in ("hbm", "host")
+                hits += where == "hbm"
+                saw_miss = saw_miss or where == "host"
+            total += len(units)
+            # accesses not yet flushed are already counted
+            want = hits / total if total else 0.0
+            assert abs(cache.lru_hit_rate_overall() - want) < 1e-12
+        cache.flush_offload()
+        want = hits / total if total else 0.0
+        assert abs(cache.lru_hit_rate_overall() - want) < 1e-12, (cid, hits, total)
+    assert saw_miss, "no selection read a host-resident unit"
+    # the model-level checks reject a cache without the pooled names only through the assert;
+    # the adapter adds them even when config['cache_type'] omits them
+    from omnimem_amd.block_cache import MMCache
+    c2 = MMCache(config=dict(cache_type=["k_cache", "v_cache"]), seq_dim=1,
+                 available_shape=dict(k_cache=(1, 480, 2, 128)), device=DEV,
+                 block_seqlen_config=dict(k_cache=240), num_layers=1, num_heads=2,
+                 kv_block_size=30)
+    assert c2.available_type[:2] == ["k_cache", "v_cache"]
+    assert {"k_cmp_cache", "v_cmp_cache"} <= set(c2.available_type)
+    c2.close()
+    cache.close()
+
+
 def test_mmcache_constructor_rejections():
     from omnimem_amd.backend import BlockKVBackendError
     from omnimem_amd.block_cache import MMCache

@@ -124,3 +124,51 @@ def test_fake_shapes_of_every_op():
                                            [scratch])
         assert dq2.shape == (2, 256, 3, 64) and dq2.dtype == torch.bfloat16
         assert delta.shape == (2, 3, 256) and delta.dtype == torch.float32
+
+
+def test_namespace_owned_by_another_library_falls_back():
+    """With ``omnimem_nsa`` already defined by another library (the reference's extension in a
+    side-by-side run), importing this package still works: its ops go to ``omnimem_amd_nsa``,
+    with the same schemas, and the other library's namespace is left alone."""
+    import subprocess
+    import sys
+    code = (
+        "import torch, warnings\n"
+        "other = torch.library.Library('omnimem_nsa', 'DEF')\n"
+        "other.define('topk(Tensor q) -> Tensor')\n"
+        "with warnings.catch_warnings(record=True) as w:\n"
+        "    warnings.simplefilter('always')\n"
+        "    from omnimem_amd import ops\n"
+        "assert ops.NAMESPACE == 'omnimem_amd_nsa', ops.NAMESPACE\n"
+        "assert any('owned by another library' in str(x.message) for x in w)\n"
+        "assert str(torch.ops.omnimem_nsa.topk.default._schema) == 'omnimem_nsa::topk(Tensor q) -> Tensor'\n"
+        "s = str(ops.op('sel_fwd').default._schema)\n"
+        "assert s.startswith('omnimem_amd_nsa::sel_fwd(Tensor q, Tensor k'), s\n"
+        "from omnimem_amd.selection import selection_attention\n"
+        "print('ok')\n")
+    root = __import__("os").path.dirname(__import__("os").path.dirname(__file__))
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr
+
+
+def test_traced_id_check_raises_like_eager():
+    """An out-of-range block id raises the same ValueError whether the facade's checks run
+    eagerly or inside a compiled graph (fullgraph: the check is an op of the graph, not a
+    break), and in-range ids pass both ways."""
+    from omnimem_amd.selection import _validate_common
+    q = torch.zeros((1, 128, 2, 64))
+    k = v = torch.zeros((1, 256, 2, 64))
+
+    def check(ids):
+        return _validate_common(q, k, v, ids, 64, 64, 64, False)
+
+    torch._dynamo.reset()
+    compiled = torch.compile(check, backend="eager", fullgraph=True)
+    good = torch.tensor([0, 3, -1, 2], dtype=torch.int32).view(1, 1, 1, 4).expand(1, 2, 2, 4)
+    bad = good.clone()
+    bad[0, 1, 1, 0] = 4  # 256 keys of 64-token blocks: ids 0..3
+    for fn in (check, compiled):
+        assert fn(good) == 4
+        with pytest.raises(ValueError, match="top_idx out of range"):
+            fn(bad)
