@@ -140,6 +140,16 @@ typedef struct omm_paged_kv {
   int32_t* touches;           /* [num_heads][max_chunks]: += 1 the first time a selection call
                                  (one epoch) reads the unit, i.e. the reference's per-call LRU
                                  accesses (models/cache.py:673-699), or NULL; needs kv->stamp */
+  /* HBM staging of host-resident pages (omm_paged_stage), or stage_map_epoch == NULL: */
+  void* stage_k;              /* [stage_slots][page_tokens][head_dim] pages, cache dtype */
+  void* stage_v;
+  float* stage_scale_k;       /* fp8 only: [stage_slots] */
+  float* stage_scale_v;
+  int32_t* stage_map_epoch;   /* [num_heads][max_chunks][pages_per_chunk]: epoch of the call
+                                 that staged the page last */
+  int32_t* stage_map_slot;    /* same shape: its staging slot, or -1 (pool full: read in place) */
+  int32_t* stage_counter;     /* 1 int32: slots taken by the current call */
+  int32_t stage_slots;
 } omm_paged_kv;
 
 /* ---- library ------------------------------------------------------------------------- */
@@ -325,6 +335,19 @@ int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_v
 int omm_sel_fwd_paged(const omm_view4* q, const omm_view4* ids, const omm_paged_kv* kv,
                       int32_t group_size, float scale, const omm_view4* out, float* lse,
                       int32_t epoch, void* stream);
+/* Stage the host-resident pages that a selection call with these ids will read: each distinct
+ * (head, chunk, page) of a host-pool unit listed in ids is copied once into the staging pool
+ * (K, V and, for fp8, the page scales), and stage_map_epoch / stage_map_slot record where, under
+ * `epoch`.  A later omm_sel_fwd_paged / _gated call with the same epoch and kv reads those pages
+ * from the pool (bit-identical bytes) instead of over the host link page by page; pages that
+ * did not fit (more than stage_slots) are read in place as before.  Enqueue it on a side stream
+ * right after the top-k, ordered before the selection by an event, and the copies overlap the
+ * work in between.  One call in flight per staging pool; epochs must be unique per call.
+ * Reference: the block store's prepare_selection (nsa/ops/selection/padded_ptr/
+ * block_wrapper.py:51-85) over K3 dedup (csrc/block_kv_dedup.cu:134-206) and K1 gather
+ * (csrc/block_kv_gather.cu:14-45), whose per-call gather of missing blocks into a pool this
+ * replaces for the paged cache. */
+int omm_paged_stage(const omm_paged_kv* kv, const omm_view4* ids, int32_t epoch, void* stream);
 /* The same selection with the NSA branch mix fused into its epilogue:
  *   out = g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa
  * per (query, head), in fp32 with one rounding to bf16, where o_slc is the selection output

@@ -50,6 +50,10 @@ class PagedKV(ctypes.Structure):
         ("page_seen", ctypes.c_void_p),
         ("qk_fp8", ctypes.c_int32),
         ("touches", ctypes.c_void_p),
+        ("stage_k", ctypes.c_void_p), ("stage_v", ctypes.c_void_p),
+        ("stage_scale_k", ctypes.c_void_p), ("stage_scale_v", ctypes.c_void_p),
+        ("stage_map_epoch", ctypes.c_void_p), ("stage_map_slot", ctypes.c_void_p),
+        ("stage_counter", ctypes.c_void_p), ("stage_slots", ctypes.c_int32),
     ]
 
 
@@ -67,6 +71,7 @@ PROTOTYPES = {
     "omm_block_pool": (_i32, [_V, _V, _i32, _i32, _vp]),
     "omm_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "omm_topk": (_i32, [_V, _V, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
+    "omm_paged_stage": (_i32, [_P, _V, _i32, _vp]),
     "omm_topk_fused_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32]),
     "omm_topk_fused": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
     "omm_topk_fused_debug": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _vp, _sz, _vp]),

@@ -18,12 +18,17 @@ synchronisation, unlike the reference's ``unique().cpu()`` per call).  At a chun
 ``flush()`` reads stamps and counts once and moves units between the pools in batched copies.
 With ``lru_max_size`` (the reference's count, models/cache.py:673-699) each (layer, head) keeps its
 most recent units by (epoch, chunk id), the order in which the reference's OrderedDict sees
-them.  With a byte budget the policy is cost-based, because a host unit is read in place page by
-page: units are evicted only to make room (coldest first: fewest pages read, then least recent),
-and a host unit is promoted only when its page reads over the last interval exceed the bytes a
-swap would move.  Sink and window chunks always stay in HBM.
+them.  With a byte budget the policy is cost-based, because a host unit is read page by page:
+units are evicted only to make room (coldest first: lowest heat, then least recent), and a host
+unit is promoted only when its heat, a moving average of its page reads per interval, exceeds
+the pages a swap would move.  Sink and window chunks always stay in HBM.
 
-Streams.  Every method enqueues on the current stream of ``device``; use one stream per cache.
+Host pages.  A selection reads a host-resident page over the host link, in place; or, after
+``prefetch(ids, layer)``, from an HBM staging pool that a side stream fills with each distinct
+host page the call lists, once, while the caller's other work runs (``omm_paged_stage``).
+
+Streams.  Every method enqueues on the current stream of ``device`` (``prefetch`` also on the
+cache's side stream, ordered by events); use one stream per cache.
 """
 from __future__ import annotations
 
@@ -117,7 +122,7 @@ class PagedKVCache:
                  host_slots: Optional[int] = None, lru_max_size: int = 0,
                  window_chunks: Optional[int] = 3, sink_chunks: int = 0,
                  keep_window_kv: bool = True, qk_fp8: bool = False,
-                 device="cuda"):
+                 stage_slots: int = 8192, device="cuda"):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise BlockKVBackendError("PagedKVCache lives on a GPU")
@@ -176,6 +181,20 @@ class PagedKVCache:
         self._host_v = _HostPool(self.n_host * self.unit_bytes)
         self._host_sk = _HostPool(self.n_host * self.scale_bytes)
         self._host_sv = _HostPool(self.n_host * self.scale_bytes)
+        # HBM staging of the host-resident pages one selection call reads (``prefetch``)
+        self.stage_slots = int(stage_slots) if self.n_host else 0
+        ns = max(1, self.stage_slots)
+        self._stage_k = torch.empty((ns, self.P, self.D), dtype=store, device=self.device)
+        self._stage_v = torch.empty_like(self._stage_k)
+        self._stage_sk = (torch.empty(ns, dtype=torch.float32, device=self.device)
+                          if self.fp8 else None)
+        self._stage_sv = torch.empty_like(self._stage_sk) if self.fp8 else None
+        self._stage_epoch = torch.zeros((self.H, self.max_chunks, self.ppc), dtype=torch.int32,
+                                        device=self.device)
+        self._stage_slot = torch.full_like(self._stage_epoch, -1)
+        self._stage_counter = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._side = None  # side stream of the staging copies (created on first use)
+        self._stage_pending = None
 
         H, MC, L = self.H, self.max_chunks, self.L
         # one allocation each for every layer (the per-layer lists are views), so that a flush
@@ -228,11 +247,16 @@ class PagedKVCache:
         self._free_hbm = list(range(self.n_slots - 1, -1, -1))
         self._free_host = list(range(self.n_host - 1, -1, -1))
         self._table_h.fill(-1)
+        self._heat = np.zeros(self._table_h.shape, dtype=np.float64)
+        self._heat_init = np.zeros(self._table_h.shape, dtype=bool)
         self._unit_all.fill_(-1)
         self._stamp_all.zero_()
         self._reads_all.zero_()
         self._seen_all.zero_()
         self._touch_all.zero_()
+        # staging-map entries carry the epoch of the call that staged them; epochs restart
+        self._stage_epoch.zero_()
+        self._stage_pending = None
         self.n_chunks = [0] * self.L
         self._staged_k.clear()
         self._epoch = 0
@@ -278,6 +302,15 @@ class PagedKVCache:
         kv.dtype = _lib.OMM_FP8E4M3 if self.fp8 else _lib.OMM_BF16
         kv.n_slots, kv.n_host_slots = self.n_slots, self.n_host
         kv.qk_fp8 = 1 if self.qk_fp8 else 0
+        if self.stage_slots:
+            kv.stage_k, kv.stage_v = self._stage_k.data_ptr(), self._stage_v.data_ptr()
+            if self.fp8:
+                kv.stage_scale_k = self._stage_sk.data_ptr()
+                kv.stage_scale_v = self._stage_sv.data_ptr()
+            kv.stage_map_epoch = self._stage_epoch.data_ptr()
+            kv.stage_map_slot = self._stage_slot.data_ptr()
+            kv.stage_counter = self._stage_counter.data_ptr()
+            kv.stage_slots = self.stage_slots
         return kv
 
     # ---------------------------------------------------------------- append
@@ -508,6 +541,7 @@ class PagedKVCache:
         kv.reads = None
         kv.page_seen = None
         kv.touches = None
+        kv.stage_map_epoch = None
         scale = softmax_scale if softmax_scale is not None else D ** -0.5
         _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(ids4), ctypes.byref(kv), G,
                   float(scale), _lib.view4(out), None, 0, _lib.stream_of(q),
@@ -520,21 +554,67 @@ class PagedKVCache:
         return self.k_cmp[layer][:, :n], self.v_cmp[layer][:, :n]
 
     # ---------------------------------------------------------------- selection
+    def prefetch(self, block_indices: torch.Tensor, layer: int):
+        """Start staging the host-resident pages a ``select`` with these ids will read: one
+        ``omm_paged_stage`` on a side stream (default priority), ordered after the work already
+        enqueued on the current stream (the top-k that produced the ids), copying each distinct
+        host page once into the HBM staging pool.  Returns the handle to pass to ``select``,
+        which then waits for the copies and reads those pages from HBM.  Work enqueued on the
+        current stream in between (the compressed and window branches) overlaps the copies.
+        One prefetch may be outstanding per cache; ids of another layer or call must not be
+        selected with this handle."""
+        if self._stage_pending is not None:
+            raise BlockKVBackendError("a prefetch is already outstanding; select() it first")
+        _lib.require_cuda((block_indices, "block_indices"))
+        if block_indices.dtype != torch.int32:
+            block_indices = block_indices.to(torch.int32)
+        epoch = self.next_epoch()
+        handle = {"epoch": epoch, "layer": layer, "event": None, "ids": block_indices}
+        if self.stage_slots and bool((self._table_h[layer] <= -2).any()):
+            main = torch.cuda.current_stream(self.device)
+            if self._side is None:
+                self._side = torch.cuda.Stream(device=self.device)
+            self._side.wait_stream(main)
+            block_indices.record_stream(self._side)
+            kv = self.layer_view(layer)
+            with torch.cuda.stream(self._side):
+                _lib.call("omm_paged_stage", ctypes.byref(kv), _lib.view4(block_indices),
+                          epoch, _lib.stream_of(block_indices), error=BlockKVBackendError)
+                ev = torch.cuda.Event()
+                ev.record(self._side)
+            handle["event"] = ev
+        self._stage_pending = handle
+        return handle
+
     def select(self, q: torch.Tensor, block_indices: torch.Tensor, layer: int, group_size: int,
                softmax_scale: Optional[float] = None, return_lse: bool = False,
                out: Optional[torch.Tensor] = None, gates: Optional[torch.Tensor] = None,
-               o_cmp: Optional[torch.Tensor] = None, o_swa: Optional[torch.Tensor] = None):
+               o_cmp: Optional[torch.Tensor] = None, o_swa: Optional[torch.Tensor] = None,
+               prefetch: Optional[dict] = None):
         """Selection attention of q (bf16 [1, M, H, D]) over the pages listed in block_indices
         (int32 [1, ceil(M/G), H, T], page id = chunk * pages_per_chunk + page).
 
         With ``gates`` (bf16 [1, M, H, 3], after the sigmoid) and the other two branch outputs
         ``o_cmp`` / ``o_swa`` the kernel writes the NSA branch mix g0*o_cmp + g1*o_slc + g2*o_swa
-        (causal_wan_nsa_model.py:541-546) instead of o_slc, in one fp32 pass."""
+        (causal_wan_nsa_model.py:541-546) instead of o_slc, in one fp32 pass.  ``prefetch``: the
+        handle of ``prefetch(block_indices, layer)``; staged pages are then read from HBM (the
+        result is bit-identical either way)."""
         _lib.require_cuda((q, "q"), (block_indices, "block_indices"))
         if q.dtype != torch.bfloat16:
             raise BlockKVBackendError(f"paged selection needs bf16 queries, got {q.dtype}")
         if block_indices.dtype != torch.int32:
             block_indices = block_indices.to(torch.int32)
+        if prefetch is not None:
+            if prefetch is not self._stage_pending or prefetch["layer"] != layer or \
+                    prefetch["ids"].data_ptr() != block_indices.data_ptr():
+                raise BlockKVBackendError("prefetch handle does not match this select (layer, "
+                                          "ids) or was already used")
+            self._stage_pending = None
+            if prefetch["event"] is not None:
+                torch.cuda.current_stream(self.device).wait_event(prefetch["event"])
+            epoch = prefetch["epoch"]
+        else:
+            epoch = self.next_epoch()
         B, M, H, D = q.shape
         scale = softmax_scale if softmax_scale is not None else D ** -0.5
         if out is None:
@@ -550,12 +630,12 @@ class PagedKVCache:
             _lib.call("omm_sel_fwd_paged_gated", _lib.view4(q), _lib.view4(block_indices),
                       ctypes.byref(kv), int(group_size), float(scale), _lib.view4(gates),
                       _lib.view4(o_cmp), _lib.view4(o_swa), _lib.view4(out),
-                      lse.data_ptr() if lse is not None else None, self.next_epoch(),
+                      lse.data_ptr() if lse is not None else None, epoch,
                       _lib.stream_of(q), error=BlockKVBackendError)
         else:
             _lib.call("omm_sel_fwd_paged", _lib.view4(q), _lib.view4(block_indices),
                       ctypes.byref(kv), int(group_size), float(scale), _lib.view4(out),
-                      lse.data_ptr() if lse is not None else None, self.next_epoch(),
+                      lse.data_ptr() if lse is not None else None, epoch,
                       _lib.stream_of(q), error=BlockKVBackendError)
         return (out, lse) if return_lse else out
 
@@ -608,12 +688,13 @@ class PagedKVCache:
     def _plan_cost(self, st: np.ndarray, rd: np.ndarray, reserve: int):
         """Budget policy: keep what is resident, evict the coldest units only to make room, and
         swap a host unit in when its page reads beat a resident unit's by more than the pages a
-        swap moves (two units each way)."""
+        swap moves (two units each way).  ``rd``: the units' heat, a moving average of page reads
+        per flush interval (``_update_heat``)."""
         written = self._table_h != -1
         prot = (self._protected() & written).reshape(-1)
         res = (self._table_h >= 0).reshape(-1)
         host = (self._table_h <= -2).reshape(-1)
-        reads = rd.reshape(-1).astype(np.int64)
+        reads = rd.reshape(-1).astype(np.float64)
         stamp = st.reshape(-1)
         chunk = np.broadcast_to(np.arange(self.max_chunks), st.shape).reshape(-1)
         desired = res | prot
@@ -754,9 +835,27 @@ class PagedKVCache:
         return (self._h_stamp.numpy().astype(np.int64), self._h_reads.numpy(),
                 self._h_seen.numpy(), self._h_touch.numpy())
 
+    def _update_heat(self, rd: np.ndarray, written: np.ndarray):
+        """Heat of every unit: an exponential moving average (weight HEAT_ALPHA) of its page
+        reads per flush interval, over the intervals in which it could be selected (written and
+        outside the sink / window, which the top-k excludes).  A unit that becomes selectable
+        starts from the mean heat of the others, so leaving the window (zero reads until then)
+        does not make it look cold, and one interval's random fluctuations do not trigger swaps."""
+        eligible = written & ~self._protected()
+        new = eligible & ~self._heat_init
+        if new.any():
+            old = eligible & self._heat_init
+            prior = float(self._heat[old].mean()) if old.any() else float(rd[new].mean())
+            self._heat[new] = prior
+            self._heat_init |= new
+        a = self.HEAT_ALPHA
+        self._heat[eligible] = (1.0 - a) * self._heat[eligible] + a * rd[eligible]
+
+    HEAT_ALPHA = 0.25
+
     def _make_room(self, need: int):
         st, rd, _, _ = self._counts()
-        desired = self._plan(st, reserve=need, rd=rd)
+        desired = self._plan(st, reserve=need, rd=self._heat)
         self._apply(desired, st)
         if len(self._free_hbm) < need:
             raise BlockKVBackendError(f"cannot free {need} HBM slots")
@@ -790,7 +889,8 @@ class PagedKVCache:
         self.stats["hbm_pages_unique"] += hbm_unique
         self.stats["host_pages_unique"] += host_unique
         reserve = self.L * self.H if reserve_next_chunk else 0
-        desired = self._plan(st, reserve=reserve, rd=rd) & written
+        self._update_heat(rd, written)
+        desired = self._plan(st, reserve=reserve, rd=self._heat) & written
         ev, pr = self._apply(desired, st)
         if reserve_next_chunk:
             changed = False

@@ -750,6 +750,162 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
   return check_launch("omm_paged_append");
 }
 
+namespace omm {
+namespace {
+// ---- staging of host-resident pages for one selection call ------------------------------------
+// A grid of kStageWaves one-wave workgroups strides over the (query group, head) rows of ids,
+// one row per wave at a time.  The kernel runs beside the attention kernels of the same layer;
+// 128 waves keep the host link busy while holding few wave slots (one wave per row, 888 rows in
+// the AR shape, stretched the concurrent attention kernels further; the same 128 waves packed
+// into 16 workgroups of 8 staged too slowly).  Lane t takes listing t: a page of a host-pool
+// unit is claimed for this call by moving its map entry to the call's epoch (the lane whose
+// exchange returns another epoch wins, so each distinct page is claimed once per call), gets the
+// next staging slot (or -1 when the pool is full) and publishes it in map_slot.  The wave then
+// copies its claimed pages one after another, all 64 lanes moving 16-byte pieces with 8 loads in
+// flight each.  The selection call that follows reads map_slot only for entries stamped with its
+// own epoch, after this kernel has completed.
+struct StageArgs {
+  const int32_t* ids;
+  int64_t is1, is2, is3;
+  const int32_t* unit;
+  const unsigned char* host_k;
+  const unsigned char* host_v;
+  const float* host_sk;
+  const float* host_sv;
+  unsigned char* stage_k;
+  unsigned char* stage_v;
+  float* stage_sk;
+  float* stage_sv;
+  int32_t* map_epoch;
+  int32_t* map_slot;
+  int32_t* counter;
+  int64_t page_bytes;
+  int H, T, max_chunks, n_chunks, ppc, n_host, slots, epoch;
+};
+
+__device__ __forceinline__ void stage_copy_page(const unsigned char* src, unsigned char* dst,
+                                                int64_t bytes, int lane) {
+  constexpr int kBatch = 8;
+  for (int64_t base = 0; base < bytes; base += static_cast<int64_t>(kBatch) * kWave * 16) {
+    uint4 r[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t off = base + static_cast<int64_t>(j * kWave + lane) * 16;
+      if (off < bytes) r[j] = *reinterpret_cast<const uint4*>(src + off);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t off = base + static_cast<int64_t>(j * kWave + lane) * 16;
+      if (off < bytes) *reinterpret_cast<uint4*>(dst + off) = r[j];
+    }
+  }
+}
+
+constexpr int kStageWaves = 128;
+
+__global__ __launch_bounds__(kWave) void paged_stage_kernel(StageArgs a, int rows) {
+  const int lane = lane_id();
+  for (int row = static_cast<int>(blockIdx.x); row < rows; row += static_cast<int>(gridDim.x)) {
+  const int g = row / a.H, h = row - g * a.H;
+  for (int t0 = 0; t0 < a.T; t0 += kWave) {
+    const int t = t0 + lane;
+    int slot = -1, src_page = 0;
+    if (t < a.T) {
+      const int32_t bid = a.ids[g * a.is1 + h * a.is2 + t * a.is3];
+      if (bid >= 0) {
+        const int cid = bid / a.ppc, p = bid - cid * a.ppc;
+        if (cid < a.n_chunks && cid < a.max_chunks) {
+          const int32_t s = a.unit[static_cast<int64_t>(h) * a.max_chunks + cid];
+          if (s <= -2 && -2 - s < a.n_host) {
+            const int64_t mi = (static_cast<int64_t>(h) * a.max_chunks + cid) * a.ppc + p;
+            if (atomicExch(a.map_epoch + mi, a.epoch) != a.epoch) {
+              const int ss = atomicAdd(a.counter, 1);
+              slot = ss < a.slots ? ss : -1;
+              a.map_slot[mi] = slot;
+              src_page = (-2 - s) * a.ppc + p;
+            }
+          }
+        }
+      }
+    }
+    uint64_t m = __ballot(slot >= 0);
+    while (m != 0ull) {
+      const int l = __builtin_ctzll(m);
+      m &= m - 1ull;
+      const int ss = __builtin_amdgcn_readlane(slot, l);
+      const int sp = __builtin_amdgcn_readlane(src_page, l);
+      const int64_t so = static_cast<int64_t>(sp) * a.page_bytes;
+      const int64_t dof = static_cast<int64_t>(ss) * a.page_bytes;
+      stage_copy_page(a.host_k + so, a.stage_k + dof, a.page_bytes, lane);
+      stage_copy_page(a.host_v + so, a.stage_v + dof, a.page_bytes, lane);
+      if (a.stage_sk != nullptr && lane == 0) {
+        a.stage_sk[ss] = a.host_sk[sp];
+        a.stage_sv[ss] = a.host_sv[sp];
+      }
+    }
+  }
+  }
+}
+}  // namespace
+}  // namespace omm
+
+extern "C" int omm_paged_stage(const omm_paged_kv* kv, const omm_view4* ids, int32_t epoch,
+                               void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(kv != nullptr && ids != nullptr, OMM_EINVAL, "omm_paged_stage: null argument");
+  OMM_REQUIRE(epoch > 0, OMM_EINVAL, "omm_paged_stage: epoch must be positive");
+  OMM_REQUIRE(kv->stage_map_epoch != nullptr && kv->stage_map_slot != nullptr &&
+                  kv->stage_counter != nullptr && kv->stage_k != nullptr &&
+                  kv->stage_v != nullptr && kv->stage_slots >= 0,
+              OMM_EINVAL, "omm_paged_stage: the cache has no staging pool");
+  OMM_REQUIRE(kv->dtype == OMM_BF16 ||
+                  (kv->dtype == OMM_FP8E4M3 && kv->stage_scale_k != nullptr &&
+                   kv->stage_scale_v != nullptr && kv->host_scale_k != nullptr &&
+                   kv->host_scale_v != nullptr),
+              OMM_EINVAL, "omm_paged_stage: cache dtype / scale arrays");
+  OMM_REQUIRE(kv->unit_table != nullptr && kv->page_tokens >= 1 &&
+                  kv->pages_per_chunk == cdiv64(kv->chunk_len, kv->page_tokens) &&
+                  kv->num_heads >= 1 && kv->head_dim >= 1,
+              OMM_EINVAL, "omm_paged_stage: inconsistent cache geometry");
+  OMM_REQUIRE(ids->size[0] == 1 && ids->size[2] == kv->num_heads && ids->size[3] >= 1 &&
+                  ids->size[1] >= 0 && ids->size[1] * kv->num_heads <= 2147483647ll,
+              OMM_EINVAL, "omm_paged_stage: ids must be [1, MG, %d, T]", kv->num_heads);
+  const int64_t elem = kv->dtype == OMM_BF16 ? 2 : 1;
+  const int64_t page_bytes = static_cast<int64_t>(kv->page_tokens) * kv->head_dim * elem;
+  OMM_REQUIRE(page_bytes % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv->host_k) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv->host_v) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv->stage_k) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv->stage_v) & 15u) == 0,
+              OMM_EUNSUPPORTED, "omm_paged_stage: pages must be whole 16-byte pieces, pools "
+              "16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = fill_i32(kv->stage_counter, 1, 0, s);
+  if (rc) return rc;
+  const int64_t rows = ids->size[1] * kv->num_heads;
+  if (rows == 0 || kv->n_host_slots == 0) return OMM_OK;
+  StageArgs a{};
+  a.ids = static_cast<const int32_t*>(ids->data);
+  a.is1 = ids->stride[1]; a.is2 = ids->stride[2]; a.is3 = ids->stride[3];
+  a.unit = kv->unit_table;
+  a.host_k = static_cast<const unsigned char*>(kv->host_k);
+  a.host_v = static_cast<const unsigned char*>(kv->host_v);
+  a.host_sk = kv->host_scale_k; a.host_sv = kv->host_scale_v;
+  a.stage_k = static_cast<unsigned char*>(kv->stage_k);
+  a.stage_v = static_cast<unsigned char*>(kv->stage_v);
+  a.stage_sk = kv->dtype == OMM_BF16 ? nullptr : kv->stage_scale_k;
+  a.stage_sv = kv->dtype == OMM_BF16 ? nullptr : kv->stage_scale_v;
+  a.map_epoch = kv->stage_map_epoch; a.map_slot = kv->stage_map_slot;
+  a.counter = kv->stage_counter;
+  a.page_bytes = page_bytes;
+  a.H = kv->num_heads; a.T = static_cast<int>(ids->size[3]);
+  a.max_chunks = kv->max_chunks; a.n_chunks = kv->n_chunks; a.ppc = kv->pages_per_chunk;
+  a.n_host = kv->n_host_slots; a.slots = kv->stage_slots; a.epoch = epoch;
+  paged_stage_kernel<<<static_cast<unsigned>(std::min<int64_t>(rows, kStageWaves)), kWave, 0, s>>>(
+      a, static_cast<int>(rows));
+  return check_launch("omm_paged_stage");
+}
+
 extern "C" int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
                               const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
                               const int32_t* src_slot, const int32_t* dst_slot, int32_t n,

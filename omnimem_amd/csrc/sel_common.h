@@ -199,8 +199,18 @@ struct PagedAcc {
   int32_t* reads;
   uint8_t* seen;
   int32_t* touches;
+  // staged host pages (omm_paged_stage under this epoch), or smap_epoch == nullptr
+  const KVT* stage_k;
+  const KVT* stage_v;
+  const float* ssc_k;
+  const float* ssc_v;
+  const int32_t* smap_epoch;
+  const int32_t* smap_slot;
   int64_t is0, is1, is2, is3;
   int max_chunks, n_chunks, chunk_len, P, ppc, D, epoch, n_slots, n_host;
+  // Ent::page: >= 0 page of the HBM pool, kStaged | slot a staging-pool slot, < 0 page
+  // -1 - page of the host pool
+  static constexpr int kStaged = 1 << 30;
   __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
     Ent e{};
     const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
@@ -214,18 +224,29 @@ struct PagedAcc {
     e.page = s >= 0 ? page : -1 - page;
     e.n = rem < P ? rem : P;
     e.bid = bid;
+    int ss = -1;
+    if (s < 0 && smap_epoch != nullptr && epoch > 0) {
+      const int64_t mi = (static_cast<int64_t>(h) * max_chunks + cid) * ppc + p;
+      if (smap_epoch[mi] == epoch) ss = smap_slot[mi];
+      if (ss >= 0) e.page = kStaged | ss;
+    }
     if constexpr (sizeof(KVT) == 1) {
-      const float* ck = s >= 0 ? sc_k : hsc_k;
-      const float* cv = s >= 0 ? sc_v : hsc_v;
-      e.sk = ck != nullptr ? ck[page] : 1.0f;
-      e.sv = cv != nullptr ? cv[page] : 1.0f;
+      const float* ck = ss >= 0 ? ssc_k : (s >= 0 ? sc_k : hsc_k);
+      const float* cv = ss >= 0 ? ssc_v : (s >= 0 ? sc_v : hsc_v);
+      const int pi = ss >= 0 ? ss : page;
+      e.sk = ck != nullptr ? ck[pi] : 1.0f;
+      e.sv = cv != nullptr ? cv[pi] : 1.0f;
     }
     return e;
   }
   __device__ __forceinline__ BlockRef ref(int, int, const Ent& e) const {
     const bool hbm = e.page >= 0;
-    const int64_t off = static_cast<int64_t>(hbm ? e.page : -1 - e.page) * P * D;
-    BlockRef r{(hbm ? pool_k : host_k) + off, (hbm ? pool_v : host_v) + off, D, D, e.n, 1.0f, 1.0f};
+    const bool staged = e.page >= kStaged;
+    const int64_t off =
+        static_cast<int64_t>(staged ? e.page - kStaged : (hbm ? e.page : -1 - e.page)) * P * D;
+    const KVT* bk = staged ? stage_k : (hbm ? pool_k : host_k);
+    const KVT* bv = staged ? stage_v : (hbm ? pool_v : host_v);
+    BlockRef r{bk + off, bv + off, D, D, e.n, 1.0f, 1.0f};
     if constexpr (sizeof(KVT) == 1) {
       r.scale_k = e.sk;
       r.scale_v = e.sv;

@@ -1136,6 +1136,12 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
                   kv->pages_per_chunk == cdiv64(kv->chunk_len, kv->page_tokens) &&
                   kv->unit_table != nullptr,
               OMM_EINVAL, "omm_sel_fwd_paged: inconsistent cache geometry");
+  OMM_REQUIRE(kv->stage_map_epoch == nullptr ||
+                  (kv->stage_map_slot != nullptr && kv->stage_k != nullptr &&
+                   kv->stage_v != nullptr &&
+                   (kv->dtype != OMM_FP8E4M3 ||
+                    (kv->stage_scale_k != nullptr && kv->stage_scale_v != nullptr))),
+              OMM_EINVAL, "omm_sel_fwd_paged: incomplete staging pool");
   Geom gm;
   rc = geom(*q, MG, ids->size[3], group_size, gm);
   if (rc) return rc;
@@ -1147,7 +1153,10 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
     PagedAcc<bf16_t> acc{static_cast<const bf16_t*>(kv->pool_k), static_cast<const bf16_t*>(kv->pool_v),
                          nullptr, nullptr, static_cast<const bf16_t*>(kv->host_k),
                          static_cast<const bf16_t*>(kv->host_v), nullptr, nullptr, kv->unit_table,
-                         idp, kv->stamp, kv->reads, kv->page_seen, kv->touches, ids->stride[0],
+                         idp, kv->stamp, kv->reads, kv->page_seen, kv->touches,
+                         static_cast<const bf16_t*>(kv->stage_k),
+                         static_cast<const bf16_t*>(kv->stage_v), nullptr, nullptr,
+                         kv->stage_map_epoch, kv->stage_map_slot, ids->stride[0],
                          ids->stride[1], ids->stride[2],
                          ids->stride[3], kv->max_chunks, kv->n_chunks, kv->chunk_len,
                          kv->page_tokens, kv->pages_per_chunk, kv->head_dim, epoch,
@@ -1161,7 +1170,10 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
                           kv->scale_k, kv->scale_v, static_cast<const uint8_t*>(kv->host_k),
                           static_cast<const uint8_t*>(kv->host_v), kv->host_scale_k,
                           kv->host_scale_v, kv->unit_table, idp, kv->stamp, kv->reads, kv->page_seen,
-                          kv->touches, ids->stride[0],
+                          kv->touches, static_cast<const uint8_t*>(kv->stage_k),
+                          static_cast<const uint8_t*>(kv->stage_v), kv->stage_scale_k,
+                          kv->stage_scale_v, kv->stage_map_epoch, kv->stage_map_slot,
+                          ids->stride[0],
                           ids->stride[1], ids->stride[2], ids->stride[3], kv->max_chunks,
                           kv->n_chunks, kv->chunk_len, kv->page_tokens, kv->pages_per_chunk,
                           kv->head_dim, epoch, kv->n_slots, kv->n_host_slots};

@@ -151,6 +151,8 @@ class WanNSAAR:
         self.trace: Optional[Dict[str, torch.Tensor]] = None
         self.trace_layer = 0
         self._rope_tab: Dict = {}
+        # stage each selection's host-resident pages into HBM on a side stream (prefetch)
+        self.prefetch = True
 
     # ------------------------------------------------------------------ pieces
     def _tic(self, name):
@@ -208,14 +210,10 @@ class WanNSAAR:
         tk = self._tic("cache_append")
         cache.append(layer, k, v, cid)                 # paged K/V + pooled K/V of the chunk
         self._toc(tk)
-        tk = self._tic("attn_cmp")
-        k_cmp, v_cmp = cache.cmp_history(layer)
-        o_cmp = dense_attention(q, k_cmp, v_cmp)       # over the pooled history
-        self._toc(tk)
-        tk = self._tic("attn_swa")
-        o_swa = cache.window_attention(q, layer)        # over the window chunks
-        self._toc(tk)
+        # top-k first, so that the host-resident pages it selects are staged into HBM on a side
+        # stream while the compressed and window branches run
         tk = self._tic("topk")
+        k_cmp, v_cmp = cache.cmp_history(layer)
         ids = parallel_nsa_topk(q, k_cmp, cfg.topk, block_size=cfg.page_tokens,
                                 chunk_size=cfg.chunk_tokens, causal=False,
                                 group_size=cfg.group_size,
@@ -223,10 +221,18 @@ class WanNSAAR:
                                 exclude_sink_chunks=cfg.exclude_sink_chunks,
                                 progressive_exclude=cfg.progressive_exclude,
                                 q_chunk_offset=cid, blocks_per_chunk=cache.ppc)
+        staged = cache.prefetch(ids, layer) if self.prefetch else None
+        self._toc(tk)
+        tk = self._tic("attn_cmp")
+        o_cmp = dense_attention(q, k_cmp, v_cmp)       # over the pooled history
+        self._toc(tk)
+        tk = self._tic("attn_swa")
+        o_swa = cache.window_attention(q, layer)        # over the window chunks
         self._toc(tk)
         tk = self._tic("sel_attn")
         # selection with the branch mix g_cmp*o_cmp + g_slc*o_slc + g_swa*o_swa in its epilogue
-        o = cache.select(q, ids, layer, cfg.group_size, gates=g, o_cmp=o_cmp, o_swa=o_swa)
+        o = cache.select(q, ids, layer, cfg.group_size, gates=g, o_cmp=o_cmp, o_swa=o_swa,
+                         prefetch=staged)
         self._toc(tk)
         if self.trace is not None and layer == self.trace_layer:
             self.trace.update(q=q.clone(), g=g.clone(), ids=ids.clone(), o_cmp=o_cmp.clone(),

@@ -716,3 +716,67 @@ def test_block_store_entry_uses_paged_cache():
     assert torch.equal(a, b)
     with pytest.raises(RuntimeError):
         selection_attention_block_store(q, ids, P, 64, cache, 0)  # grad enabled
+
+
+@pytest.mark.parametrize("dtype,stage_slots", [(torch.bfloat16, 8192), (torch.bfloat16, 5),
+                                               ("fp8", 8192), ("fp8", 5)])
+def test_prefetch_staging_is_bit_identical(dtype, stage_slots):
+    """Selection with the host-resident pages staged into HBM first (prefetch on a side stream,
+    omm_paged_stage) gives exactly the output and LSE of reading them in place over the host
+    link, also when the staging pool holds fewer pages than the call lists (the rest are read in
+    place); both match the float64 oracle.  The map must have staged host pages only, each
+    distinct page once."""
+    from omnimem_amd.backend import BlockKVBackendError
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(91)
+    H, D, C, P, T, n, G, M = 3, 128, 1000, 64, 8, 4, 64, 700
+    fp8 = dtype == "fp8"
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         hbm_slots=H * 2, host_slots=H * n, window_chunks=0,
+                         stage_slots=stage_slots)
+    ks = [_chunk(g, C, H, D, 0.3, fp8) for _ in range(n)]
+    vs = [_chunk(g, C, H, D, 1.0, fp8) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+        cache.flush()
+    host = [(h, c) for h in range(H) for c in range(n) if cache.where(0, h, c) == "host"]
+    assert host, "no unit moved to the host pool"
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+    MG = -(-M // G)
+    ids = torch.stack([torch.randperm(n * cache.ppc, generator=g)[:T] for _ in range(MG * H)])
+    ids = ids.view(1, MG, H, T).to(torch.int32).to(DEV)
+    plain, plain_l = cache.select(q, ids, 0, G, return_lse=True)
+    handle = cache.prefetch(ids, 0)
+    assert handle["event"] is not None
+    staged, staged_l = cache.select(q, ids, 0, G, return_lse=True, prefetch=handle)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, staged) and torch.equal(plain_l, staged_l)
+    # the map: every host page listed is stamped with the call's epoch, once, within the pool
+    ep = cache._stage_epoch.cpu().numpy()
+    sl = cache._stage_slot.cpu().numpy()
+    want = set()
+    for (_, gg, h, t), bid in np.ndenumerate(ids.cpu().numpy()):
+        c, p = divmod(int(bid), cache.ppc)
+        if cache.where(0, h, c) == "host":
+            want.add((h, c, p))
+    got = {tuple(x) for x in np.argwhere(ep == handle["epoch"])}
+    assert got == want
+    slots = sorted(int(sl[x]) for x in got if sl[x] >= 0)
+    assert len(slots) == min(len(want), stage_slots)
+    assert slots == list(range(len(slots)))          # each slot used once
+    assert int(cache._stage_counter.item()) == len(want)
+    # and against the float64 oracle
+    if fp8:
+        kk, vv = _fp8_cache_images(cache, n)
+    else:
+        kk, vv = torch.cat(ks, 1).float().numpy(), torch.cat(vs, 1).float().numpy()
+    want_o, want_l = O.selection_attention(q.float().cpu().numpy(), kk, vv, ids.cpu().numpy(),
+                                           G, D ** -0.5, O.paged_block_tokens(C, P, n))
+    _check_attn(staged, staged_l, want_o, want_l)
+    # one prefetch outstanding at a time, consumed by the matching select only
+    h2 = cache.prefetch(ids, 0)
+    with pytest.raises(BlockKVBackendError):
+        cache.prefetch(ids, 0)
+    with pytest.raises(BlockKVBackendError):
+        cache.select(q, ids.clone(), 0, G, prefetch=h2)
+    cache.close()
