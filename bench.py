@@ -37,6 +37,7 @@ METRIC = "sel-attn TFLOP/s + %MFMA peak; top-k GB/s; ms per AR chunk at 60s cach
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 
 # config 3, one layer
 M = N = 32760
@@ -109,6 +110,10 @@ def parse():
                    help="cached chunks before the timed AR steps (80 chunks = 240 latent frames)")
     p.add_argument("--ar-steps", type=int, default=3, help="timed AR chunks per cache dtype")
     p.add_argument("--no-ar", action="store_true", help="skip the AR (configs 4 and 5) leg")
+    p.add_argument("--no-full", action="store_true",
+                   help="skip the config-3 30-layer forward and the config-1 call")
+    p.add_argument("--full-only", action="store_true",
+                   help="only the config-3 30-layer forward and the config-1 call")
     p.add_argument("--ar-only", action="store_true",
                    help="run only the AR leg (configs 4 and 5) and print its results (profiling "
                         "runs of the cache kernels)")
@@ -351,7 +356,7 @@ def topk_prepooled(q2, k2, want, steps):
     return timed
 
 
-def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
+def useful_flops(ids, M, N, G, BS, chunk, D, g0=0, causal=True):
     """4 * D * sum over queries and heads of the visible tokens of their selected blocks.
 
     ids holds query groups g0, g0+1, ... of a [B, ceil(M/G), H, T] index tensor."""
@@ -359,11 +364,14 @@ def useful_flops(ids, M, N, G, BS, chunk, D, g0=0):
     ids = ids.long()
     B, MG, Hh, T = ids.shape
     g = torch.arange(g0, g0 + MG, device=ids.device).view(1, MG, 1, 1)
-    qc = (g * G) // chunk
     t0 = ids * BS
     n = torch.clamp(N - t0, max=BS)
-    n = torch.minimum(n, (qc + 1) * chunk - t0)
-    ok = (ids >= 0) & (t0 < N) & ((t0 // chunk) <= qc) & (n > 0)
+    if causal:
+        qc = (g * G) // chunk
+        n = torch.minimum(n, (qc + 1) * chunk - t0)
+        ok = (ids >= 0) & (t0 < N) & ((t0 // chunk) <= qc) & (n > 0)
+    else:
+        ok = (ids >= 0) & (t0 < N) & (n > 0)
     n = torch.where(ok, n, torch.zeros_like(n))
     nq = torch.clamp(M - g * G, max=G)
     return int((n.sum(-1, keepdim=True) * nq).sum().item()) * 4 * D
@@ -526,6 +534,86 @@ def cpu_baseline_ar(history: int = 80, q_small: int = 64, q_large: int = 256):
     }
 
 
+def run_config1(steps: int):
+    """Config 1: one fp32 selection call, q [1,1560,12,128], k / v [1,4680,12,128] ~ N(0,1)/sqrt(128),
+    64-token blocks, groups of 64, top-16 over 1560-token frame chunks, the queries read as the
+    last frame (all three frames are candidates).  The attention kernel alone, timed with events
+    over back-to-back launches; useful FLOPs counted from the ids as for config 3."""
+    import torch
+    from omnimem_amd.index_topk import block_pool, parallel_nsa_topk
+    from omnimem_amd.selection import sel_fwd
+    gen = torch.Generator().manual_seed(1)
+    Mq, Nk, Cf = 1560, 4680, 1560
+    q, k, v = (torch.randn((1, L, H, D), generator=gen).div_(D ** 0.5).cuda() for L in (Mq, Nk, Nk))
+    ids = parallel_nsa_topk(q, block_pool(k, BS), TOPK, block_size=BS, chunk_size=Cf,
+                            causal=False, group_size=G)
+    out = torch.empty_like(q)
+    lse = torch.empty((1, H, Mq), dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        sel_fwd(q, k, v, ids, BS, Cf, D ** -0.5, False, G, out=out, lse=lse)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sel_fwd(q, k, v, ids, BS, Cf, D ** -0.5, False, G, out=out, lse=lse)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = useful_flops(ids, Mq, Nk, G, BS, Cf, D, causal=False)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": "config 1: fp32 q [1,1560,12,128], k/v [1,4680,12,128], top-16 of "
+                        "64-token blocks, groups of 64, queries as the last 1560-token frame",
+            "kernel": "sel_fwd_valu_kernel (fp32 arithmetic)", "ms": round(ms, 4),
+            "useful_gflop": round(flops / 1e9, 3), "useful_tflops": round(tf, 3),
+            "peak_fp32_tflops": PEAK_FP32_TFLOPS, "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4),
+            "timing": "--steps back-to-back launches, HIP events"}
+
+
+def run_config3_forward(frames: int = 21):
+    """Config 3: the 30-layer full-sequence Wan2.1-1.3B NSA forward (omnimem_amd/wan_full.py) on
+    seeded latents of one 81-frame 480x832 clip (32760 tokens), random-init weights.  One warm-up
+    forward, then one timed forward with per-category event timers and an event pair around each
+    layer's selection call; selection TFLOP/s = useful FLOPs of the 30 calls / their summed time."""
+    import torch
+    from omnimem_amd.wan_ar import WanARConfig
+    from omnimem_amd.wan_full import WanNSAFull
+    cfg = WanARConfig()
+    t0 = time.perf_counter()
+    model = WanNSAFull(cfg, frames=frames, seed=7)
+    t_init = time.perf_counter() - t0
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn((1, model.tokens, cfg.in_dim * cfg.patch), generator=gen,
+                    device="cuda").to(torch.bfloat16)
+    model.forward(x, 500.0)
+    torch.cuda.synchronize()
+    model.timers, model.sel_events = {}, []
+    t0 = time.perf_counter()
+    model.forward(x, 500.0)
+    torch.cuda.synchronize()
+    fwd_ms = 1e3 * (time.perf_counter() - t0)
+    cats = {k: round(sum(a.elapsed_time(b) for a, b in v), 3) for k, v in sorted(model.timers.items())}
+    sel_ms = sum(a.elapsed_time(b) for a, b in model.sel_events)
+    flops = sum(useful_flops(ids, model.tokens, model.tokens, cfg.group_size, cfg.page_tokens,
+                             cfg.chunk_tokens, cfg.head_dim) for ids in model.sel_ids)
+    tf = flops / (sel_ms * 1e-3) / 1e12
+    res = {"workload": f"config 3: {cfg.layers}-layer full-sequence forward, {model.tokens} "
+                       f"tokens ({frames} latent frames), dim {cfg.dim}, {cfg.heads}x"
+                       f"{cfg.head_dim} heads, RMSNorm q/k, top-{cfg.topk} of {cfg.page_tokens}-"
+                       f"token blocks, groups of {cfg.group_size}, causal by {cfg.chunk_tokens}, "
+                       f"window {cfg.window_chunks} chunks",
+           "ms_per_forward": round(fwd_ms, 2),
+           "selection_ms_per_forward": round(sel_ms, 3),
+           "selection_useful_tflop_per_forward": round(flops / 1e12, 3),
+           "selection_useful_tflops": round(tf, 3),
+           "selection_frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+           "breakdown_ms_per_forward": cats,
+           "setup_s": round(t_init, 1),
+           "timing": "one forward after one warm-up; selection events around each sel_fwd"}
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
            keep_window_kv: Optional[bool] = None, qk_fp8: bool = False):
     """Configs 4 / 5: ms per AR chunk with ``history`` chunks cached, 48 GB HBM budget.  The
@@ -652,6 +740,10 @@ def main():
     from omnimem_amd.selection import sel_fwd
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.full_only:
+        print(json.dumps({"config1": run_config1(args.steps),
+                          "config3_forward": run_config3_forward()}), flush=True)
+        return
     if args.ar_only:
         print(json.dumps({"ms_per_ar_chunk": {
             "bf16": run_ar(torch.bfloat16, args.ar_history, args.ar_steps),
@@ -810,9 +902,14 @@ def main():
             "useful_tflops": round(bwd_tflops, 3),
             "frac_bf16_peak": round(bwd_tflops / PEAK_BF16_TFLOPS, 4),
         },
+        "config1": None,
+        "config3_forward": None,
         "ms_per_ar_chunk": None,
         "cpu_baseline": None,
     }
+    if not args.no_full:
+        res["config1"] = run_config1(args.steps)
+        res["config3_forward"] = run_config3_forward()
     if not args.no_ar:
         del q2, k2
         torch.cuda.empty_cache()

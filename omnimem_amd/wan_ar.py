@@ -106,20 +106,15 @@ class _Block:
         self.modulation = (torch.randn((1, 6, d), generator=gen) / math.sqrt(d)).to(device)
 
 
-class WanNSAAR:
-    """AR generation over a ``PagedKVCache`` (bf16 or fp8 pages).
+class WanNSABase:
+    """Random-init Wan2.1-1.3B-shaped DiT weights (seeded) and the pieces every driver shares:
+    patch / text / time embeddings, rotary embedding, the block (adaLN modulation,
+    self-attention, cross-attention, FFN; causal_wan_nsa_model.py:626-700) and a per-category
+    event-timer breakdown (``timers``).  Subclasses supply the self-attention branch."""
 
-    ``step(cid)`` runs one AR chunk (denoise forwards + context forward + flush); ``prefill``
-    fills chunks 0..n-1 of every layer with seeded random keys / values without running the
-    model, so a long-history cache is reached in seconds.  ``timers`` (category -> list of event
-    pairs) collects a per-category time breakdown when set."""
-
-    def __init__(self, cfg: WanARConfig, cache: PagedKVCache, device="cuda", seed: int = 0,
-                 dtype=torch.bfloat16):
-        self.cfg, self.cache = cfg, cache
+    def __init__(self, cfg: WanARConfig, device="cuda", seed: int = 0, dtype=torch.bfloat16):
+        self.cfg = cfg
         self.device, self.dtype = torch.device(device), dtype
-        assert cache.L == cfg.layers and cache.H == cfg.heads and cache.D == cfg.head_dim
-        assert cache.chunk_len == cfg.chunk_tokens and cache.P == cfg.page_tokens
         gen = torch.Generator().manual_seed(seed)
         self.blocks = [_Block(cfg, gen, self.device, dtype) for _ in range(cfg.layers)]
         d = cfg.dim
@@ -151,8 +146,6 @@ class WanNSAAR:
         self.trace: Optional[Dict[str, torch.Tensor]] = None
         self.trace_layer = 0
         self._rope_tab: Dict = {}
-        # stage each selection's host-resident pages into HBM on a side stream (prefetch)
-        self.prefetch = True
 
     # ------------------------------------------------------------------ pieces
     def _tic(self, name):
@@ -193,14 +186,69 @@ class WanNSAAR:
         e0 = F.linear(F.silu(e), *self.time_proj).float().view(1, 6, cfg.dim)
         return e, e0
 
-    def _self_attn(self, blk: _Block, layer: int, x: torch.Tensor, cid: int) -> torch.Tensor:
-        cfg, cache = self.cfg, self.cache
+    def _qkvg(self, blk: _Block, x: torch.Tensor):
+        """q, k, v [1, S, H, hd] (RMSNorm on q and k) and the sigmoid gates [1, S, H, 3]
+        (causal_wan_nsa_model.py:369-386)."""
+        cfg = self.cfg
         S, H, hd = x.shape[1], cfg.heads, cfg.head_dim
-        tk = self._tic("linear")
         q = _rms(F.linear(x, *blk.q), blk.norm_q, cfg.eps).view(1, S, H, hd)
         k = _rms(F.linear(x, *blk.k), blk.norm_k, cfg.eps).view(1, S, H, hd)
         v = F.linear(x, *blk.v).view(1, S, H, hd)
         g = torch.clamp(F.linear(x, *blk.g), -10.0, 10.0).view(1, S, H, 3).sigmoid()
+        return q, k, v, g
+
+    def _embed(self, latents: torch.Tensor, t: float):
+        x = F.linear(latents, *self.patch_in)
+        e, e0 = self._time_embed(t)
+        return x, e, e0
+
+    def _head_out(self, x: torch.Tensor, e: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        m = (self.head_mod + e.float().unsqueeze(1)).unbind(1)
+        return F.linear((_ln(x, cfg.eps).float() * (1 + m[1]) + m[0]).to(x.dtype), *self.head)
+
+    def _block(self, layer: int, x: torch.Tensor, e0: torch.Tensor, ctx) -> torch.Tensor:
+        cfg, blk = self.cfg, self.blocks[layer]
+        e = (blk.modulation + e0).unbind(1)
+        tk = self._tic("norm")
+        h = (_ln(x, cfg.eps).float() * (1 + e[1]) + e[0]).to(x.dtype)
+        self._toc(tk)
+        x = x + (self._self_attn(blk, layer, h, ctx).float() * e[2]).to(x.dtype)
+        tk = self._tic("cross_ffn")
+        S, H, hd = x.shape[1], cfg.heads, cfg.head_dim
+        hq = _ln(x, cfg.eps, blk.norm3_w, blk.norm3_b)
+        cq = _rms(F.linear(hq, *blk.cq), blk.cnorm_q, cfg.eps).view(1, S, H, hd).transpose(1, 2)
+        ck, cv = self.ctx_kv[layer]
+        co = F.scaled_dot_product_attention(cq, ck, cv).transpose(1, 2).flatten(2)
+        x = x + F.linear(co, *blk.co)
+        h = (_ln(x, cfg.eps).float() * (1 + e[4]) + e[3]).to(x.dtype)
+        y = F.linear(F.gelu(F.linear(h, *blk.f1), approximate="tanh"), *blk.f2)
+        x = x + (y.float() * e[5]).to(x.dtype)
+        self._toc(tk)
+        return x
+
+
+class WanNSAAR(WanNSABase):
+    """AR generation over a ``PagedKVCache`` (bf16 or fp8 pages).
+
+    ``step(cid)`` runs one AR chunk (denoise forwards + context forward + flush); ``prefill``
+    fills chunks 0..n-1 of every layer with seeded random keys / values without running the
+    model, so a long-history cache is reached in seconds.  ``timers`` (category -> list of event
+    pairs) collects a per-category time breakdown when set."""
+
+    def __init__(self, cfg: WanARConfig, cache: PagedKVCache, device="cuda", seed: int = 0,
+                 dtype=torch.bfloat16):
+        super().__init__(cfg, device, seed, dtype)
+        self.cache = cache
+        assert cache.L == cfg.layers and cache.H == cfg.heads and cache.D == cfg.head_dim
+        assert cache.chunk_len == cfg.chunk_tokens and cache.P == cfg.page_tokens
+        # stage each selection's host-resident pages into HBM on a side stream (prefetch)
+        self.prefetch = True
+
+    def _self_attn(self, blk: _Block, layer: int, x: torch.Tensor, cid: int) -> torch.Tensor:
+        cfg, cache = self.cfg, self.cache
+        tk = self._tic("linear")
+        q, k, v, g = self._qkvg(blk, x)
         self._toc(tk)
         tk = self._tic("rope")
         start = cid * cfg.chunk_tokens
@@ -242,39 +290,17 @@ class WanNSAAR:
         self._toc(tk)
         return out
 
-    def _block(self, layer: int, x: torch.Tensor, e0: torch.Tensor, cid: int) -> torch.Tensor:
-        cfg, blk = self.cfg, self.blocks[layer]
-        e = (blk.modulation + e0).unbind(1)
-        tk = self._tic("norm")
-        h = (_ln(x, cfg.eps).float() * (1 + e[1]) + e[0]).to(x.dtype)
-        self._toc(tk)
-        x = x + (self._self_attn(blk, layer, h, cid).float() * e[2]).to(x.dtype)
-        tk = self._tic("cross_ffn")
-        S, H, hd = x.shape[1], cfg.heads, cfg.head_dim
-        hq = _ln(x, cfg.eps, blk.norm3_w, blk.norm3_b)
-        cq = _rms(F.linear(hq, *blk.cq), blk.cnorm_q, cfg.eps).view(1, S, H, hd).transpose(1, 2)
-        ck, cv = self.ctx_kv[layer]
-        co = F.scaled_dot_product_attention(cq, ck, cv).transpose(1, 2).flatten(2)
-        x = x + F.linear(co, *blk.co)
-        h = (_ln(x, cfg.eps).float() * (1 + e[4]) + e[3]).to(x.dtype)
-        y = F.linear(F.gelu(F.linear(h, *blk.f1), approximate="tanh"), *blk.f2)
-        x = x + (y.float() * e[5]).to(x.dtype)
-        self._toc(tk)
-        return x
-
     @torch.no_grad()
     def forward(self, latents: torch.Tensor, t: float, cid: int) -> torch.Tensor:
         """latents: [1, chunk_tokens, in_dim * patch] patchified latents of chunk ``cid``."""
         cfg = self.cfg
-        x = F.linear(latents, *self.patch_in)
-        e, e0 = self._time_embed(t)
+        x, e, e0 = self._embed(latents, t)
         # fused attention kernels only: an unsupported shape raises instead of taking the
         # batched-matmul math path
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             for layer in range(cfg.layers):
                 x = self._block(layer, x, e0, cid)
-        m = (self.head_mod + e.float().unsqueeze(1)).unbind(1)
-        return F.linear((_ln(x, cfg.eps).float() * (1 + m[1]) + m[0]).to(x.dtype), *self.head)
+        return self._head_out(x, e)
 
     @torch.no_grad()
     def step(self, cid: int, noise: torch.Tensor) -> dict:
