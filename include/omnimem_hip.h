@@ -182,7 +182,7 @@ size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC, in
  *    d ascending) * scale, bit-reproducible by a scalar fmaf loop.
  * Valid slots hold block ids in (score desc, id asc) order (+0 == -0); -1 pads rows with fewer
  * than topk visible blocks.  Invisible blocks and scores that are -inf or NaN are never
- * selected.  1 <= topk <= 64, D <= 256.  An empty output (B, MG or H zero) launches nothing and
+ * selected.  1 <= topk <= 128 (the reference's path A range), D <= 256.  An empty output (B, MG or H zero) launches nothing and
  * out may be NULL; NC = 0 fills out with -1. */
 int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t topk, float scale,
              const omm_topk_mask* mask, int32_t* out, void* workspace, size_t workspace_bytes,

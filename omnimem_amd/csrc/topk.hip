@@ -37,6 +37,7 @@ constexpr int kTileC = 64;              // key columns per LDS tile
 constexpr int kSurvCap = 256;           // survivor slots per wave
 constexpr int kSpanCap = 1024;          // columns per workgroup
 constexpr int kMaxSplit = 64;
+constexpr int kMaxTopk = 128;           // the reference's path A bound (topk.cu:584, 648-660)
 constexpr size_t kLdsBudget = 80 * 1024;  // two workgroups per CU
 constexpr int kStageRegs = 8;           // 16-byte staging registers per thread (K tile)
 
@@ -173,23 +174,61 @@ __device__ __forceinline__ uint32_t lane_max_threshold(uint32_t v, int topk, uin
   return theta;
 }
 
+// The same threshold from the two largest values of every lane (v1 >= v2), for 64 < topk <= 128:
+// the topk-th largest of the 128 values.  Every key whose high word is below it has at least
+// topk larger keys, and at least topk keys reach it whenever topk lane values are non-zero.
+// scratch: 128 words of wave-private LDS.
+__device__ __forceinline__ uint32_t lane_max2_threshold(uint32_t v1, uint32_t v2, int topk,
+                                                        uint32_t* scratch) {
+  const int lane = lane_id();
+  scratch[lane] = v1;
+  scratch[kWave + lane] = v2;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int c1 = 0, c2 = 0;
+#pragma unroll 8
+  for (int j = 0; j < 2 * kWave / 4; ++j) {
+    const uint4 w = reinterpret_cast<const uint4*>(scratch)[j];
+    c1 += (w.x >= v1 ? 1 : 0) + (w.y >= v1 ? 1 : 0) + (w.z >= v1 ? 1 : 0) + (w.w >= v1 ? 1 : 0);
+    c2 += (w.x >= v2 ? 1 : 0) + (w.y >= v2 ? 1 : 0) + (w.z >= v2 ? 1 : 0) + (w.w >= v2 ? 1 : 0);
+  }
+  const uint32_t t1 = c1 >= topk ? v1 : 0u, t2 = c2 >= topk ? v2 : 0u;
+  const uint32_t theta = wave_max_u32(t1 > t2 ? t1 : t2);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return theta;
+}
+
+__device__ __forceinline__ void track_top2(uint32_t hi, uint32_t& m1, uint32_t& m2) {
+  if (hi > m1) {
+    m2 = m1;
+    m1 = hi;
+  } else if (hi > m2) {
+    m2 = hi;
+  }
+}
+
 template <int PER, typename KeyF, typename EmitF, typename PadF>
 __device__ __forceinline__ void wave_select_impl(int n, int topk, KeyF key, EmitF emit, PadF pad,
                                                  uint64_t* sv) {
   const int lane = lane_id();
   // keys of slots j * 64 + lane; slots past n read candidate n - 1 (in bounds) and count as 0
   uint64_t kv[PER];
-  uint32_t lmax = 0;  // high word of the lane's largest key
+  uint32_t lmax = 0, lmax2 = 0;  // high words of the lane's two largest keys
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = j * kWave + lane;
     const uint64_t k = key(i < n ? i : n - 1);
     kv[j] = i < n ? k : 0ull;
-    const uint32_t hi = static_cast<uint32_t>(kv[j] >> 32);
-    lmax = hi > lmax ? hi : lmax;
+    track_top2(static_cast<uint32_t>(kv[j] >> 32), lmax, lmax2);
   }
-  // theta: the topk-th largest lane maximum (0 if fewer than topk lanes hold candidates)
-  const uint32_t theta = lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv));
+  // theta: the topk-th largest lane maximum (0 if fewer than topk lanes hold candidates); past
+  // 64, the topk-th largest of the lanes' two largest
+  const uint32_t theta = topk <= kWave
+      ? lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv))
+      : lane_max2_threshold(lmax, lmax2, topk, reinterpret_cast<uint32_t*>(sv));
 
   int ns = 0;
 #pragma unroll
@@ -264,15 +303,14 @@ __device__ __forceinline__ void wave_select_stream(int n, int topk, KeyF key, Em
                                                    PadF pad, uint64_t* sv) {
   const int lane = lane_id();
   const int per = (n + kWave - 1) / kWave;
-  uint32_t lmax = 0;
+  uint32_t lmax = 0, lmax2 = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
-    if (i < n) {
-      const uint32_t hi = static_cast<uint32_t>(key(i) >> 32);
-      lmax = hi > lmax ? hi : lmax;
-    }
+    if (i < n) track_top2(static_cast<uint32_t>(key(i) >> 32), lmax, lmax2);
   }
-  const uint32_t theta = lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv));
+  const uint32_t theta = topk <= kWave
+      ? lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv))
+      : lane_max2_threshold(lmax, lmax2, topk, reinterpret_cast<uint32_t*>(sv));
   int ns = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
@@ -1473,8 +1511,8 @@ int esize_of(int32_t dtype) { return dtype == OMM_F32 ? 4 : 2; }
 int check_sizes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk, int D, int esize,
                 bool scores) {
   OMM_REQUIRE(B >= 0 && MG >= 0 && H >= 0 && NC >= 0, OMM_EINVAL, "top-k: negative size");
-  OMM_REQUIRE(topk >= 1 && topk <= 64, OMM_EUNSUPPORTED, "top-k: topk must be in [1, 64], got %d",
-              topk);
+  OMM_REQUIRE(topk >= 1 && topk <= kMaxTopk, OMM_EUNSUPPORTED,
+              "top-k: topk must be in [1, %d], got %d", kMaxTopk, topk);
   OMM_REQUIRE(B * H <= 65535 && cdiv64(MG, kRG) <= 2147483647ll && MG <= 2147483647ll,
               OMM_EUNSUPPORTED, "top-k: B*H must be <= 65535");
   const int64_t cap = static_cast<int64_t>(span_cap(D, esize, scores)) * kMaxSplit;
@@ -1610,7 +1648,7 @@ M2Args m2_args(const omm_view4& q, const omm_view4& k, int64_t MG, int64_t H, in
 
 extern "C" size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC,
                                            int32_t topk) {
-  if (B <= 0 || MG <= 0 || H <= 0 || NC <= 0 || topk < 1 || topk > 64) return 0;
+  if (B <= 0 || MG <= 0 || H <= 0 || NC <= 0 || topk < 1 || topk > omm::kMaxTopk) return 0;
   // the split plan does not depend on the head dim beyond the LDS cap; use the smallest cap
   // (fp32, D = 256) so the answer covers every dtype and head dim
   size_t ws = 0;
@@ -1665,7 +1703,8 @@ extern "C" size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H
                                                  int64_t NC, int32_t group_size, int32_t topk,
                                                  int32_t dtype) {
   using namespace omm;
-  if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || NC <= 0 || group_size < 1 || topk < 1 || topk > 64)
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || NC <= 0 || group_size < 1 || topk < 1 ||
+      topk > omm::kMaxTopk)
     return 0;
   const int64_t MG = cdiv64(T, group_size);
   const int es = esize_of(dtype);

@@ -77,9 +77,12 @@ MASKS = {
 
 
 @pytest.mark.parametrize("mask", list(MASKS))
-@pytest.mark.parametrize("topk", [1, 16, 64])
+@pytest.mark.parametrize("topk", [1, 16, 64, 65, 100, 128])
 @pytest.mark.parametrize("NC", [37, 512, 5850])
 def test_topk_from_scores_bitexact(mask, topk, NC):
+    """topk up to 128 (the reference's path A range, topk.cu:584, 648-660): past 64 the
+    survivor threshold comes from every lane's two largest keys; rows with fewer visible blocks
+    than topk pad with -1."""
     from omnimem_amd.index_topk import topk_from_scores
     mk = MASKS[mask]
     B, MG, H = 1, 74, 3
@@ -97,6 +100,43 @@ def test_topk_from_scores_bitexact(mask, topk, NC):
         om.group_size = 1
     want = O.topk_select(s, topk, om)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("topk", [96, 128])
+def test_parallel_nsa_topk_fused_large_topk_bitexact(dtype, topk):
+    """Fused pooling + scoring + top-k with 64 < topk <= 128: off the MFMA path (topk > 16), so
+    the scores are the fmaf chain and the indices are bit-exact against the oracle's scores;
+    the AR mask over 80 cached chunks (split spans and the merge) and a causal case."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(topk)
+    B, H, D = 1, 2, 128
+    for T, NC, chunk, causal, qoff, exw in ((4680, 5920, 4680, False, 80, 3),
+                                            (2048, 128, 512, True, 0, 0)):
+        q = torch.randn((B, T, H, D), generator=g).to(dtype)
+        k = torch.randn((B, NC, H, D), generator=g).to(dtype)
+        bpc = 74 if not causal else 0
+        got = parallel_nsa_topk(q.to(DEV), k.to(DEV), topk, block_size=64, chunk_size=chunk,
+                                causal=causal, exclude_window_chunks=exw,
+                                progressive_exclude=not causal, q_chunk_offset=qoff,
+                                blocks_per_chunk=bpc, group_size=64).cpu().numpy()
+        mask = O.Mask(block_size=64, group_size=64, chunk_q=chunk, chunk_k=chunk,
+                      blocks_per_chunk=bpc, q_chunk_offset=qoff, ex_win=exw,
+                      causal=int(causal), prog_excl=int(not causal))
+        dt = "bf16" if dtype == torch.bfloat16 else "f32"
+        want = O.topk(O.pool_mean(_img(q), 64, dt), _img(k), topk, D ** -0.5, mask)
+        np.testing.assert_array_equal(got, want)
+        if causal:
+            assert (got[:, :8] == -1).any()  # early rows see fewer than topk blocks
+
+
+def test_topk_above_128_rejected():
+    from omnimem_amd.backend import NSABackendError
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    q = torch.zeros((1, 128, 1, 64), device=DEV)
+    k = torch.zeros((1, 300, 1, 64), device=DEV)
+    with pytest.raises(NSABackendError, match="128"):
+        parallel_nsa_topk(q, k, 129, block_size=64, chunk_size=64, causal=False, group_size=64)
 
 
 def test_topk_tf_mask_bitexact():
