@@ -257,6 +257,7 @@ class PagedKVCache:
         # staging-map entries carry the epoch of the call that staged them; epochs restart
         self._stage_epoch.zero_()
         self._stage_pending = None
+        self._snaps = []
         self.n_chunks = [0] * self.L
         self._staged_k.clear()
         self._epoch = 0
@@ -338,6 +339,12 @@ class PagedKVCache:
         if v.stride(3) != 1 or v.stride(1) % 8 or v.stride(2) % 8 or v.data_ptr() % 16:
             v = v.contiguous()
         row = self._table_h[layer, :, cid]
+        for sn in self._snaps:  # a snapshot keeps the version it saw: write to a new slot
+            for h in range(self.H):
+                u = (layer, h, cid)
+                if u in sn["units"] and sn["units"][u] is None and row[h] != -1:
+                    sn["units"][u] = int(row[h])
+                    row[h] = -1
         if (row < 0).any():
             need = int((row < 0).sum())
             if len(self._free_hbm) < need:
@@ -651,12 +658,19 @@ class PagedKVCache:
             mask[l, :, :] = prot[None, :]
         return mask
 
+    def _cap(self, reserve: int) -> int:
+        """HBM slots the residency plan may fill: all of them but the reserve and those held by
+        snapshots (``snapshot_chunks``) for units rewritten since."""
+        held = sum(1 for sn in self._snaps for st in sn["units"].values()
+                   if st is not None and st >= 0)
+        return self.n_slots - reserve - held
+
     def head_capacity(self, reserve: int = 0) -> int:
         """HBM units each (layer, head) may keep: ``lru_max_size`` (the reference's count), or an
         equal share of the budget left after ``reserve`` slots (the next chunk's)."""
         if self.lru_max_size > 0:
             return self.lru_max_size
-        return max(1, (self.n_slots - reserve) // (self.L * self.H))
+        return max(1, self._cap(reserve) // (self.L * self.H))
 
     def _plan(self, st: np.ndarray, reserve: int, rd: Optional[np.ndarray] = None):
         if self.lru_max_size > 0 or rd is None:
@@ -679,9 +693,9 @@ class PagedKVCache:
             self.L, 0).repeat(self.H, 1), axis=-1)
         desired = prot | ((key >= 0) & (rank < room[..., None]))
         total = int(desired.sum())
-        if total > self.n_slots - reserve:
+        if total > self._cap(reserve):
             raise BlockKVBackendError(
-                f"{total} units wanted in HBM exceed the {self.n_slots - reserve} slots left after "
+                f"{total} units wanted in HBM exceed the {self._cap(reserve)} slots left after "
                 f"reserving {reserve} for the next chunk (lower lru_max_size or raise the budget)")
         return desired
 
@@ -698,7 +712,7 @@ class PagedKVCache:
         stamp = st.reshape(-1)
         chunk = np.broadcast_to(np.arange(self.max_chunks), st.shape).reshape(-1)
         desired = res | prot
-        cap = self.n_slots - reserve
+        cap = self._cap(reserve)
         # coldest first: fewest pages read, then oldest touch, then oldest chunk
         cold = lambda idx: idx[np.lexsort((chunk[idx], stamp[idx], reads[idx]))]
         movable = cold(np.flatnonzero(desired & ~prot))
@@ -978,6 +992,84 @@ class PagedKVCache:
         self.stats["hits"] = 0
         self.stats["misses"] = 0
         self._touch_all.zero_()
+
+    # ---------------------------------------------------------------- snapshots
+    def snapshot_chunks(self, chunk_start: int, chunk_end: int) -> dict:
+        """Keep chunks [chunk_start, chunk_end) of every layer as they are now, for
+        ``restore_chunks``: the pipeline's prompt switch re-encodes the last chunks with the new
+        prompt and then puts the older ones back (``_snapshot_chunks`` / ``_restore_chunks``,
+        pipelines/pipeline_wan_causal.py:33-57, 369-396).  Copy-on-write per unit: nothing is
+        copied now; the first rewrite of a snapshotted unit goes to a new slot and the snapshot
+        holds the old one (which no flush moves) until it is restored or discarded.  The pooled
+        rows of the range (and, for an fp8 cache, its chunks in the dense window ring) are
+        cloned.  A rewrite needs a free HBM slot per snapshotted unit, and the slots a snapshot
+        holds are unavailable to residency until it is restored or discarded: size the pools
+        (``hbm_slots`` / ``host_slots``) with that room."""
+        a, b = max(0, int(chunk_start)), min(self.max_chunks, int(chunk_end))
+        for sn in self._snaps:
+            if sn["range"][0] < b and a < sn["range"][1]:
+                raise BlockKVBackendError(f"chunks [{a}, {b}) overlap an active snapshot of "
+                                          f"{list(sn['range'])}")
+        units = {}
+        for l in range(self.L):
+            for c in range(a, b):
+                for h in range(self.H):
+                    if self._table_h[l, h, c] != -1:
+                        units[(l, h, c)] = None  # shared with the table until rewritten
+        rows = slice(a * self.ppc, b * self.ppc)
+        snap = {"range": (a, b), "units": units,
+                "k_cmp": [t[:, rows].clone() for t in self.k_cmp],
+                "v_cmp": [t[:, rows].clone() for t in self.v_cmp], "ring": {}}
+        if self.keep_window_kv:
+            for l in range(self.L):
+                n = self.n_chunks[l]
+                for c in range(max(a, n - self.window), min(b, n)):
+                    w = c % self.window
+                    snap["ring"][(l, c)] = (self.win_k[l][w].clone(), self.win_v[l][w].clone())
+        self._snaps.append(snap)
+        return snap
+
+    def _release_slot(self, s: int):
+        if s >= 0:
+            self._free_hbm.append(s)
+        elif s <= -2:
+            self._free_host.append(-2 - s)
+
+    def restore_chunks(self, snapshot: dict, chunk_start: Optional[int] = None):
+        """Put the snapshotted chunks back: units rewritten since the snapshot get their old
+        slot again (the newer version's slot is freed), untouched units stay as they are, and
+        the pooled rows (and ring entries) are copied back.  ``chunk_start`` must be the
+        snapshot's first chunk when given (the reference helper's argument)."""
+        self._active_snapshot(snapshot)
+        a, b = snapshot["range"]
+        if chunk_start is not None and int(chunk_start) != a:
+            raise BlockKVBackendError(f"snapshot starts at chunk {a}, not {chunk_start}")
+        for (l, h, c), old in snapshot["units"].items():
+            if old is None:
+                continue
+            self._release_slot(int(self._table_h[l, h, c]))
+            self._table_h[l, h, c] = old
+        self._snaps = [sn for sn in self._snaps if sn is not snapshot]
+        rows = slice(a * self.ppc, b * self.ppc)
+        for l in range(self.L):
+            self.k_cmp[l][:, rows].copy_(snapshot["k_cmp"][l])
+            self.v_cmp[l][:, rows].copy_(snapshot["v_cmp"][l])
+        for (l, c), (wk, wv) in snapshot["ring"].items():
+            self.win_k[l][c % self.window].copy_(wk)
+            self.win_v[l][c % self.window].copy_(wv)
+        self._upload_table()
+
+    def discard_snapshot(self, snapshot: dict):
+        """Drop a snapshot without restoring it; the slots it held are freed."""
+        self._active_snapshot(snapshot)
+        for old in snapshot["units"].values():
+            if old is not None:
+                self._release_slot(old)
+        self._snaps = [sn for sn in self._snaps if sn is not snapshot]
+
+    def _active_snapshot(self, snapshot: dict):
+        if not any(sn is snapshot for sn in self._snaps):
+            raise BlockKVBackendError("snapshot already restored or discarded")
 
     # ---------------------------------------------------------------- inspection (tests)
     def read_unit(self, layer: int, head: int, cid: int):

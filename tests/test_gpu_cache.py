@@ -780,3 +780,110 @@ def test_prefetch_staging_is_bit_identical(dtype, stage_slots):
     with pytest.raises(BlockKVBackendError):
         cache.select(q, ids.clone(), 0, G, prefetch=h2)
     cache.close()
+
+
+def _slots_balance(cache):
+    """Every HBM / host slot is in the table, held by a snapshot, or free, exactly once."""
+    held = [s for sn in cache._snaps for s in sn["units"].values() if s is not None]
+    t = cache._table_h
+    hbm = sorted(t[t >= 0].tolist() + [s for s in held if s >= 0] + list(cache._free_hbm))
+    host = sorted((-2 - t[t <= -2]).tolist() + [-2 - s for s in held if s <= -2]
+                  + list(cache._free_host))
+    assert hbm == list(range(cache.n_slots))
+    assert host == list(range(cache.n_host))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_snapshot_restore_chunks(dtype):
+    """Prompt-switch snapshots (pipeline_wan_causal.py:33-57, 369-396): chunks [1, 3) are
+    snapshotted, a flush may move them, they are rewritten (new slots, copy on write) and read
+    back as the new data; restore_chunks brings back every byte, scale and pooled row of the old
+    version while later chunks keep their new data; discard_snapshot keeps the new data; slots
+    stay balanced throughout, overlapping snapshots are refused, and the restored cache's
+    selection matches the float64 oracle on the old values."""
+    from omnimem_amd.backend import BlockKVBackendError
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(61)
+    L, H, D, C, P, n = 2, 2, 128, 500, 64, 6
+    fp8 = dtype == "fp8"
+    # the host pool has room for every unit: slots a snapshot holds are spare capacity
+    cache = PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         hbm_slots=L * H * 3, host_slots=L * H * n, window_chunks=1,
+                         keep_window_kv=fp8)
+    data = {}
+    def write(l, c, tag):
+        k = _chunk(g, C, H, D, 0.3, fp8)
+        v = _chunk(g, C, H, D, 1.0, fp8)
+        data[(l, c, tag)] = (k, v)
+        cache.append(l, k.to(DEV), v.to(DEV), c)
+    for c in range(5):
+        for l in range(L):
+            write(l, c, "old")
+        cache.flush()
+    assert any(cache.where(l, h, c) == "host" for l in range(L) for h in range(H) for c in range(5))
+    units = lambda lo, hi: {(l, h, c): cache.read_unit(l, h, c) for l in range(L)
+                            for h in range(H) for c in range(lo, hi)}
+    same = lambda a, b: all(torch.equal(x, y) for x, y in zip(a, b))
+    before = units(0, 5)
+    pooled = [(cache.k_cmp[l].clone(), cache.v_cmp[l].clone()) for l in range(L)]
+    snap = cache.snapshot_chunks(1, 3)
+    with pytest.raises(BlockKVBackendError, match="overlap"):
+        cache.snapshot_chunks(2, 4)
+    cache.flush()                      # may move the snapshotted units before their rewrite
+    _slots_balance(cache)
+    for c in (1, 2):
+        for l in range(L):
+            write(l, c, "new")
+    for l in range(L):
+        write(l, 5, "new")
+    cache.flush()
+    _slots_balance(cache)
+    after = units(0, 6)
+    for (l, h, c), parts in after.items():
+        if c in (1, 2):
+            assert not same(parts, before[(l, h, c)]), "rewrite did not take effect"
+        elif c < 5:
+            assert same(parts, before[(l, h, c)])
+    cache.restore_chunks(snap, 1)
+    _slots_balance(cache)
+    with pytest.raises(BlockKVBackendError):
+        cache.restore_chunks(snap, 1)
+    restored = units(0, 6)
+    for (l, h, c), parts in restored.items():
+        assert same(parts, before[(l, h, c)] if c < 5 else after[(l, h, c)]), (l, h, c)
+    for l in range(L):
+        rows = slice(0, 5 * cache.ppc)
+        assert torch.equal(cache.k_cmp[l][:, rows], pooled[l][0][:, rows])
+        assert torch.equal(cache.v_cmp[l][:, rows], pooled[l][1][:, rows])
+    # selection over the restored layer 0 against float64 on the old values of chunks 0..4
+    M, G, T = 300, 64, 6
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(5 * cache.ppc, generator=g)[:T]
+                       for _ in range(-(-M // G) * H)]).view(1, -1, H, T).to(torch.int32)
+    got, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, return_lse=True)
+    if fp8:
+        kk = np.zeros((1, 5 * C, H, D), np.float32)
+        vv = np.zeros_like(kk)
+        for c in range(5):
+            for h in range(H):
+                kc, vc, sk, sv = restored[(0, h, c)]
+                kk[0, c * C:(c + 1) * C, h] = O.dequantize_pages(
+                    kc.numpy(), sk.numpy()[:, None, None]).reshape(-1, D)[:C]
+                vv[0, c * C:(c + 1) * C, h] = O.dequantize_pages(
+                    vc.numpy(), sv.numpy()[:, None, None]).reshape(-1, D)[:C]
+    else:
+        kk = torch.cat([data[(0, c, "old")][0] for c in range(5)], 1).float().numpy()
+        vv = torch.cat([data[(0, c, "old")][1] for c in range(5)], 1).float().numpy()
+    want_o, want_l = O.selection_attention(q.float().numpy(), kk, vv, ids.numpy(), G, D ** -0.5,
+                                           O.paged_block_tokens(C, P, 5))
+    _check_attn(got, lse, want_o, want_l)
+    # discard: the rewrite stays, the old slots are freed
+    snap2 = cache.snapshot_chunks(3, 5)
+    for l in range(L):
+        write(l, 3, "newer")
+    cache.discard_snapshot(snap2)
+    _slots_balance(cache)
+    for l in range(L):
+        for h in range(H):
+            assert not same(cache.read_unit(l, h, 3), before[(l, h, 3)])
+    cache.close()
