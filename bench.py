@@ -563,7 +563,7 @@ def run_config1(steps: int):
     tf = flops / (ms * 1e-3) / 1e12
     return {"workload": "config 1: fp32 q [1,1560,12,128], k/v [1,4680,12,128], top-16 of "
                         "64-token blocks, groups of 64, queries as the last 1560-token frame",
-            "kernel": "sel_fwd_valu_kernel (fp32 arithmetic)", "ms": round(ms, 4),
+            "kernel": "sel_fwd_f32mfma_kernel (fp32 MFMA, v_mfma_f32_16x16x4_f32)", "ms": round(ms, 4),
             "useful_gflop": round(flops / 1e9, 3), "useful_tflops": round(tf, 3),
             "peak_fp32_tflops": PEAK_FP32_TFLOPS, "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4),
             "timing": "--steps back-to-back launches, HIP events"}

@@ -758,6 +758,235 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
   }
 }
 
+// ---- fp32 MFMA kernel (fp32 q / k / v, head dim 64 or 128) ---------------------------------------
+// One workgroup = one query group of up to 64 queries, 4 waves x 16 queries (the fp32 MFMA is
+// 32 cycles long, so one operand read per MFMA costs little, and 16-query waves give config 1's
+// 300 (group, head) items four times the waves).  K / V tiles of TK = 8 KiB / (4 D) keys go
+// global -> LDS by buffer_load ... lds, double-buffered, every wave reading the same tile.
+// S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x4_f32 with fp32 operands and fp32 P (P is
+// not rounded, so the result stays within the fp32 bar).  The dims of a QK^T k-step are permuted
+// (k-step 4 u + e takes dims 16 u + 4 j + e from lane group j), so a lane fetches the K
+// operands of four k-steps with one 16-byte read; the keys of PV k-step (t, r) are 16 t + 4 j + r,
+// so P^T is the lane's own S^T registers.
+// LDS layout: copy instruction j (RPI rows of ROWB bytes) lands at j * PITCH, PITCH = 1024 +
+// 16 RPI, so the PV operand rows 4 j + r of the 4 lane groups fall on 4 different bank ranges;
+// K's 16-byte chunk c of row r is stored at chunk c ^ (r % 16) (through the copy's source
+// offsets), which spreads the 16-row b128 reads.
+constexpr int kF32Waves = 4;
+
+template <int D>
+struct F32Geom {
+  static constexpr int ROWB = 4 * D;       // bytes per K / V row
+  static constexpr int CPR = D / 4;        // 16-byte chunks per row
+  static constexpr int TK = 8192 / ROWB;   // keys per tile (16 for D = 128, 32 for D = 64)
+  static constexpr int RPI = 1024 / ROWB;  // rows per copy instruction
+  static constexpr int PITCH = 1024 + 16 * RPI;
+  static constexpr int NT = TK / 16;       // 16-key blocks per tile
+  static constexpr int DU = D / 16;        // QK^T groups of 4 k-steps; PV d-tiles
+  __device__ static int swz_k(int r) { return r & (CPR < 16 ? CPR - 1 : 15); }
+  // byte offset of (row, 16-byte chunk slot) in a tile buffer
+  __device__ static int at(int row, int slot) {
+    return (row / RPI) * PITCH + (row % RPI) * ROWB + (slot << 4);
+  }
+};
+
+// This wave's NI copy instructions of one fp32 tile: instruction j = NI w + jj lands at
+// dst + j * PITCH (the M0 base steps by PITCH).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int PITCH>
+__device__ __forceinline__ void dma_pitch2(const void* base, int rsb, int nrows, char* dst, int w,
+                                           const int (&off)[2]) {
+  const i32x4 r = buffer_desc(base, nrows * rsb);
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + PITCH * 2u * w)));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds"
+      :
+      : "s"(m0), "v"(off[0]), "v"(off[1]), "s"(r), "i"(PITCH)
+      : "memory", "m0", "scc");
+}
+#pragma clang diagnostic pop
+
+template <typename Acc, int D>
+__global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
+    View4<const float> q, View4<float> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale) {
+  using FG = F32Geom<D>;
+  constexpr int ROWB = FG::ROWB, CPR = FG::CPR, TK = FG::TK, RPI = FG::RPI, NT = FG::NT;
+  constexpr int DU = FG::DU, PITCH = FG::PITCH;
+  constexpr int NI = 8 / kF32Waves;  // copy instructions per wave per K or V tile
+  static_assert(NI == 2, "two copy instructions per wave");
+  constexpr int BUF = 8 * PITCH;
+  __shared__ __align__(16) char lds[4 * BUF];  // K buffers 0, 1; V buffers 2, 3
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int l16 = lane & 15, j4 = lane >> 4;
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+  const int m_end = min(g * G + G, M);
+  const int qc = (g * G) / chunk;
+  const int mq = g * G + 16 * w + l16;  // this lane's query (column l16 of the wave's block)
+  const bool q_ok = 16 * w + l16 < G && mq < m_end;
+  // Q^T operands: group u holds dims 16 u + 4 j4 + e, e < 4 (the k-steps 4 u + e)
+  float4 qf[DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u)
+    qf[u] = q_ok ? *reinterpret_cast<const float4*>(q.at(b, mq, h, 16 * u + 4 * j4))
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  float c2 = scale * kLog2e;
+  if (c2 < 0.0f) {  // the softmax works on s * c2 with c2 > 0: negate Q instead (exact)
+    c2 = -c2;
+#pragma unroll
+    for (int u = 0; u < DU; ++u) qf[u] = make_float4(-qf[u].x, -qf[u].y, -qf[u].z, -qf[u].w);
+  }
+  // LDS read offsets (tile block t adds 16 rows: 16 / RPI instructions, a compile-time offset)
+  int koff[DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u) koff[u] = FG::at(l16, (4 * u + j4) ^ FG::swz_k(l16));
+  int voff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) voff[r] = FG::at(4 * j4 + r, 0) + 4 * l16;
+  f32x4 o[DU];
+#pragma unroll
+  for (int i = 0; i < DU; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m2 = kNegInf, nms = 0.0f, thr = kNegInf, lsum = 0.0f;
+
+  WaveWalk<Acc, TK> wk;
+  wk.start(acc, b, g, h, T, qc);
+  int n_cur = 0;
+  int kdo[NI], vdo[NI];
+  int rsk = 0, rsv = 0;
+  if (wk.valid) {
+    rsk = static_cast<int>(wk.br.sk) * 4;
+    rsv = static_cast<int>(wk.br.sv) * 4;
+#pragma unroll
+    for (int jj = 0; jj < NI; ++jj) {
+      const int row = (NI * w + jj) * RPI + lane / CPR, c = lane % CPR;
+      kdo[jj] = row * rsk + ((c ^ FG::swz_k(row)) << 4);
+      vdo[jj] = row * rsv + (c << 4);
+    }
+    dma_pitch2<PITCH>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk,
+                      rsk, wk.n, lds, w, kdo);
+    dma_pitch2<PITCH>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv,
+                      rsv, wk.n, lds + 2 * BUF, w, vdo);
+    n_cur = wk.n;
+    wk.advance(acc, b, g, h, T, qc);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+
+  auto step = [&](auto BIc) -> bool {
+    constexpr int BI = decltype(BIc)::value;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int n_nx = 0;
+    if (wk.valid) {
+      dma_pitch2<PITCH>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk,
+                        rsk, wk.n, lds + (BI ^ 1) * BUF, w, kdo);
+      dma_pitch2<PITCH>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv,
+                        rsv, wk.n, lds + (2 + (BI ^ 1)) * BUF, w, vdo);
+      n_nx = wk.n;
+      wk.advance(acc, b, g, h, T, qc);
+    }
+    const char* Kt = lds + BI * BUF;
+    const char* Vt = lds + (2 + BI) * BUF;
+    // S^T = K Q^T: lane holds keys 16 t + 4 j4 + r of query l16
+    f32x4 s4[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      s4[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < DU; ++u) {
+        const float4 a =
+            *reinterpret_cast<const float4*>(Kt + koff[u] + t * (16 / RPI) * PITCH);
+        s4[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[u].x, s4[t], 0, 0, 0);
+        s4[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[u].y, s4[t], 0, 0, 0);
+        s4[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[u].z, s4[t], 0, 0, 0);
+        s4[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[u].w, s4[t], 0, 0, 0);
+      }
+    }
+    if (n_cur < TK) {  // keys past n_cur are not visible (their rows read as 0)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * t + 4 * j4 + r >= n_cur) s4[t][r] = kNegInf;
+    }
+    // online softmax in the log2 domain (the 16-bit kernels' scheme): e = s c2 - m, with m
+    // raised only when some e exceeds 8
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_fmaf(s4[t][r], c2, nms);
+        s4[t][r] = e;
+        mx = fmaxf(mx, e);
+      }
+    if (__ballot(mx > thr) != 0ull) {
+      const float msafe = m2 == kNegInf ? 0.0f : m2;
+      float v = mx;
+      v = fmaxf(v, __shfl_xor(v, 16, kWave));
+      v = fmaxf(v, __shfl_xor(v, 32, kWave));
+      const float mcand = fmaxf(m2, v + msafe);
+      const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
+      const float alpha = __builtin_amdgcn_exp2f(m2 - msafe_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int i = 0; i < DU; ++i) o[i] *= alpha;
+      m2 = mcand;
+      nms = -msafe_new;
+      thr = mcand == kNegInf ? kNegInf : 8.0f;
+      const float shift = msafe - msafe_new;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s4[t][r] += shift;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = __builtin_amdgcn_exp2f(s4[t][r]);
+        s4[t][r] = p;
+        lsum += p;
+      }
+    // O^T += V^T P^T: k-step (t, r) takes keys 16 t + 4 j + r, P^T from the lane's registers
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < DU; ++i) {
+          const float a = *reinterpret_cast<const float*>(Vt + voff[r] + t * (16 / RPI) * PITCH +
+                                                          64 * i);
+          o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s4[t][r], o[i], 0, 0, 0);
+        }
+    n_cur = n_nx;
+    return n_cur > 0;
+  };
+  if (n_cur > 0)
+    while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+    }
+
+  float ls = lsum;
+  ls += __shfl_xor(ls, 16, kWave);
+  ls += __shfl_xor(ls, 32, kWave);
+  if (q_ok) {
+    const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
+    float* op = out.at(b, mq, h, 0);
+#pragma unroll
+    for (int i = 0; i < DU; ++i)
+      *reinterpret_cast<float4*>(op + 16 * i + 4 * j4) =
+          make_float4(o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv);
+    if (lse != nullptr && j4 == 0)
+      lse[(static_cast<int64_t>(b) * H + h) * M + mq] =
+          ls > 0.0f ? (m2 + __builtin_log2f(ls)) * kLn2 : kNegInf;
+  }
+}
+
 // ---- VALU kernel (fp32 arithmetic, any head dim <= 256, any strides) -------------------------
 constexpr int kValuKeys = 32;
 
@@ -964,6 +1193,21 @@ int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* 
   return check_launch("selection attention (dma)");
 }
 
+template <typename Acc>
+int launch_f32mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
+                   const Acc& acc, int chunk, float scale, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(gm.items);
+  if (gm.D == 128)
+    sel_fwd_f32mfma_kernel<Acc, 128><<<grid, kF32Waves * kWave, 0, s>>>(
+        make_view<const float>(q), make_view<float>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
+        chunk, scale);
+  else
+    sel_fwd_f32mfma_kernel<Acc, 64><<<grid, kF32Waves * kWave, 0, s>>>(
+        make_view<const float>(q), make_view<float>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG, gm.T,
+        chunk, scale);
+  return check_launch("selection attention (fp32 mfma)");
+}
+
 template <typename QT, typename Acc>
 int launch_valu(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
                 const Acc& acc, int chunk, float scale, int64_t kv_sd, hipStream_t s) {
@@ -1043,6 +1287,19 @@ int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, co
                      k.stride[2] % 8 == 0 && v.stride[0] % 8 == 0 && v.stride[1] % 8 == 0 &&
                      v.stride[2] % 8 == 0;
   const bool mfma = sizeof(QT) == 2 && kv_ok && qo_mfma_ok(q, out);
+  if constexpr (sizeof(QT) == 4) {
+    // fp32 on MFMA: 16-byte rows of unit dim stride, groups of at most 64 queries, head dim 64 or
+    // 128, a finite non-zero scale (the masking uses -inf scores), 32-bit tile offsets
+    auto rows16 = [](const omm_view4& x) {
+      return x.stride[3] == 1 && aligned16(x.data) && x.stride[0] % 4 == 0 &&
+             x.stride[1] % 4 == 0 && x.stride[2] % 4 == 0;
+    };
+    const int64_t rb = 4 * (k.stride[1] > v.stride[1] ? k.stride[1] : v.stride[1]);
+    if (rows16(q) && rows16(out) && rows16(k) && rows16(v) && G <= 64 &&
+        (gm.D == 64 || gm.D == 128) && scale != 0.0f && __builtin_isfinite(scale) &&
+        rb >= 4 * gm.D && rb * 32 < (int64_t{1} << 31))
+      return launch_f32mfma(gm, q, out, lse, acc, causal ? chunk : 1, scale, s);
+  }
   // the VALU kernel reads K and V with K's dim stride
   OMM_REQUIRE(mfma || k.stride[3] == v.stride[3], OMM_EUNSUPPORTED,
               "selection attention: k and v need the same dim stride");

@@ -82,22 +82,23 @@ def test_sel_fwd_matches_oracle(dtype, case):
     _check(out, lse, want_o, want_l, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("scale", [-0.09, 0.0, 8.0])
-def test_sel_fwd_scale_values(scale):
-    """A negative scale (the MFMA path negates Q), a zero scale (uniform weights over the visible
-    tokens, VALU path) and a large one (the running max is raised on later tiles), with a partial
-    last block so masked keys are present."""
+def test_sel_fwd_scale_values(scale, dtype):
+    """A negative scale (the MFMA paths negate Q), a zero scale (uniform weights over the
+    visible tokens, VALU path) and a large one (the running max is raised on later tiles), with a
+    partial last block so masked keys are present; bf16 and fp32 (the fp32 MFMA kernel)."""
     from omnimem_amd.selection import sel_fwd
     M, N, H, D, G, BS, T = 130, 300, 2, 128, 64, 64, 5
     gen = torch.Generator().manual_seed(11)
-    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
-    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(torch.bfloat16)
-    v = torch.randn((1, N, H, D), generator=gen).to(torch.bfloat16)
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(dtype)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(dtype)
+    v = torch.randn((1, N, H, D), generator=gen).to(dtype)
     ids = _ids(gen, 1, -(-M // G), H, T, 5)
     out, lse = sel_fwd(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), BS, 1, scale, False, G)
     want_o, want_l = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
                                            ids.numpy(), G, scale, O.dense_block_tokens(N, BS, 1, False))
-    _check(out, lse, want_o, want_l, torch.bfloat16)
+    _check(out, lse, want_o, want_l, dtype)
 
 
 def test_sel_fwd_strided_views():
