@@ -648,23 +648,25 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
     s0 = dict(cache.stats)
     times = []
     cats = {}
-    # the timed chunks carry the per-category event timers themselves, so the breakdown and the
-    # mean describe the same chunks
-    for _ in range(steps):
-        x = noise()
-        torch.cuda.synchronize()
-        model.timers = {}
-        t0 = time.perf_counter()
+    # the timed chunks run back to back, as in an AR loop (a flush's copies on the move stream
+    # overlap the next chunk), between two synchronisations of every stream, so the mean
+    # includes the last flush's copies too; the chunks carry the per-category event timers
+    # themselves, so the breakdown and the mean describe the same chunks
+    xs = [noise() for _ in range(steps)]
+    model.timers = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for x in xs:
         model.step(cid, x)
-        torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-        for name, pairs in model.timers.items():
-            cats[name] = cats.get(name, 0.0) + sum(a.elapsed_time(b) for a, b in pairs)
         cid += 1
+    torch.cuda.synchronize()
+    times.append(time.perf_counter() - t0)
+    for name, pairs in model.timers.items():
+        cats[name] = cats.get(name, 0.0) + sum(a.elapsed_time(b) for a, b in pairs)
     model.timers = None
     s1 = dict(cache.stats)
     breakdown = {k: round(v / steps, 3) for k, v in sorted(cats.items())}
-    ms_chunk = 1e3 * sum(times) / len(times)
+    ms_chunk = 1e3 * sum(times) / steps
     moved = (s1["evicted_bytes"] - s0["evicted_bytes"]) + (s1["promoted_bytes"] - s0["promoted_bytes"])
     page_bytes = 2 * cfg.page_tokens * cfg.head_dim * cache.elem  # one K page + one V page
     d = lambda key: (s1[key] - s0[key]) // steps
@@ -679,6 +681,8 @@ def run_ar(dtype, history: int, steps: int, budget_bytes: float = 48e9,
         "hbm_budget_bytes": cache.hbm_budget_bytes,
         "hbm_unit_slots": cache.n_slots,
         "host_unit_slots": cache.n_host,
+        # async: a flush's copies run on the cache's move stream, committed by the next flush
+        "flush_copies": "async" if cache._async_ok() else "on the compute stream",
         "per_chunk": {
             "evicted_bytes": d("evicted_bytes"),
             "promoted_bytes": d("promoted_bytes"),

@@ -375,6 +375,16 @@ int omm_copy_units(const void* src_k, void* dst_k, const void* src_v, void* dst_
                    const int32_t* src_slot, const int32_t* dst_slot, int32_t n,
                    int32_t n_src_slots, int32_t n_dst_slots, int64_t unit_bytes,
                    int64_t scale_bytes, void* stream);
+/* The same moves with the slot lists in host memory, each unit (K, V and, when given, the two
+ * scale arrays) one hipMemcpyAsync on `stream`: the copy engines move the bytes, no kernel runs,
+ * so a side stream's moves do not occupy compute units beside the attention kernels.  Runs of
+ * units consecutive in both pools are merged into one copy.  Reference: the same flush_offload
+ * D2H (models/cache.py:1086-1117), whose pinned-buffer copies are non_blocking. */
+int omm_copy_units_async(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
+                         const void* src_sk, void* dst_sk, const void* src_sv, void* dst_sv,
+                         const int32_t* src_slot_host, const int32_t* dst_slot_host, int32_t n,
+                         int32_t n_src_slots, int32_t n_dst_slots, int64_t unit_bytes,
+                         int64_t scale_bytes, void* stream);
 
 /* ---- reference block-store kernels (K1 / K2 / K3) ------------------------------------ */
 /* K1 (cuda_backend/csrc/block_kv_ops.h:12-16, block_kv_gather.cu:14-45): desc is int64

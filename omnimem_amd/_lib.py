@@ -72,6 +72,7 @@ PROTOTYPES = {
     "omm_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "omm_topk": (_i32, [_V, _V, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
     "omm_paged_stage": (_i32, [_P, _V, _i32, _vp]),
+    "omm_copy_units_async": (_i32, [_vp] * 8 + [_vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp]),
     "omm_topk_fused_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32]),
     "omm_topk_fused": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _sz, _vp]),
     "omm_topk_fused_debug": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp, _vp, _sz, _vp]),

@@ -21,14 +21,17 @@ most recent units by (epoch, chunk id), the order in which the reference's Order
 them.  With a byte budget the policy is cost-based, because a host unit is read page by page:
 units are evicted only to make room (coldest first: lowest heat, then least recent), and a host
 unit is promoted only when its heat, a moving average of its page reads per interval, exceeds
-the pages a swap would move.  Sink and window chunks always stay in HBM.
+the pages a swap would move.  Sink and window chunks always stay in HBM.  Under the byte budget
+a flush only enqueues its copies, on a stream of their own (the copy engines), and the next
+flush commits them; until then a moving unit is read from its source slot.
 
 Host pages.  A selection reads a host-resident page over the host link, in place; or, after
 ``prefetch(ids, layer)``, from an HBM staging pool that a side stream fills with each distinct
 host page the call lists, once, while the caller's other work runs (``omm_paged_stage``).
 
-Streams.  Every method enqueues on the current stream of ``device`` (``prefetch`` also on the
-cache's side stream, ordered by events); use one stream per cache.
+Streams.  Every method enqueues on the current stream of ``device`` (``prefetch`` and an
+asynchronous ``flush`` also on the cache's side streams, ordered by events); use one stream per
+cache.
 """
 from __future__ import annotations
 
@@ -114,6 +117,12 @@ class PagedKVCache:
     ``qk_fp8`` (fp8 caches): the selection quantises the queries to e4m3 per query row and runs
     Q K^T on fp8 MFMA with the K page codes, instead of widening the K codes to bf16 for the
     bf16 MFMA (the page scales apply to the scores either way).
+    ``async_flush`` (byte-budget policy only): a flush enqueues its evictions and promotions on
+    a stream of their own (copy engines) and returns; the moves are committed -- the unit table switched
+    and the source slots freed -- at the next flush, or earlier when an operation needs them.
+    Until then every moving unit is read from its source slot, which nothing rewrites.  The
+    plan then keeps two chunks of slots free instead of one (the next chunk's, and the one the
+    pending evictions release).
     """
 
     def __init__(self, num_layers: int, num_heads: int, head_dim: int, max_chunks: int,
@@ -122,7 +131,7 @@ class PagedKVCache:
                  host_slots: Optional[int] = None, lru_max_size: int = 0,
                  window_chunks: Optional[int] = 3, sink_chunks: int = 0,
                  keep_window_kv: bool = True, qk_fp8: bool = False,
-                 stage_slots: int = 8192, device="cuda"):
+                 stage_slots: int = 8192, async_flush: bool = True, device="cuda"):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise BlockKVBackendError("PagedKVCache lives on a GPU")
@@ -159,8 +168,9 @@ class PagedKVCache:
                 # (the reference preallocates a pinned slot per chunk, models/cache.py:970-1016)
                 host_slots = total_units
             else:
-                # every unit the HBM pool cannot hold, plus the chunk reserved at a flush
-                host_slots = min(total_units, total_units - self.n_slots + self.L * self.H)
+                # every unit the HBM pool cannot hold, plus the chunk reserved at a flush and the
+                # chunk of slots an asynchronous flush keeps free for its evictions to land in
+                host_slots = min(total_units, total_units - self.n_slots + 2 * self.L * self.H)
         self.n_host = int(host_slots)
         self.hbm_budget_bytes = self.n_slots * per_slot
         # window None: the sink + window view is every chunk, and no chunk is protected from
@@ -193,8 +203,13 @@ class PagedKVCache:
                                         device=self.device)
         self._stage_slot = torch.full_like(self._stage_epoch, -1)
         self._stage_counter = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self._side = None  # side stream of the staging copies (created on first use)
+        self._side = None  # side stream of the staging and flush copies (created on first use)
         self._stage_pending = None
+        # byte-budget policy: a flush enqueues its moves on the side stream and commits them
+        # (table switch, source slots freed) at the next flush or whenever the host needs them
+        self.async_flush = bool(async_flush) and self.lru_max_size == 0
+        self._moves = None
+        self._mover = None
 
         H, MC, L = self.H, self.max_chunks, self.L
         # one allocation each for every layer (the per-layer lists are views), so that a flush
@@ -244,6 +259,9 @@ class PagedKVCache:
     # ---------------------------------------------------------------- bookkeeping
     def reset(self):
         """Forget every chunk (pools keep their memory), as MMCache.reset (models/cache.py:771)."""
+        if getattr(self, "_moves", None) is not None:
+            self._moves[0].synchronize()  # copies in flight must land before slots are reused
+        self._moves = None
         self._free_hbm = list(range(self.n_slots - 1, -1, -1))
         self._free_host = list(range(self.n_host - 1, -1, -1))
         self._table_h.fill(-1)
@@ -338,6 +356,8 @@ class PagedKVCache:
             k = k.contiguous()
         if v.stride(3) != 1 or v.stride(1) % 8 or v.stride(2) % 8 or v.data_ptr() % 16:
             v = v.contiguous()
+        if self._pending_in(layer, cid):
+            self._commit()  # a unit of this chunk is moving: its copy must read the old data
         row = self._table_h[layer, :, cid]
         for sn in self._snaps:  # a snapshot keeps the version it saw: write to a new slot
             for h in range(self.H):
@@ -838,6 +858,99 @@ class PagedKVCache:
         self.stats["promoted_bytes"] += n_pr * unit
         return n_ev, n_pr
 
+    def _move_stream(self) -> torch.cuda.Stream:
+        """Stream of an asynchronous flush's copies (default priority), apart from the staging
+        stream so that a prefetch never queues behind a flush's evictions."""
+        if self._mover is None:
+            self._mover = torch.cuda.Stream(device=self.device)
+        return self._mover
+
+    def _pick_moves(self, desired: np.ndarray, st: np.ndarray, keep_free: int):
+        """The moves an asynchronous flush makes towards ``desired``: evictions, least recent
+        first, as many as there are free host slots; promotions, most recent first, into the
+        free HBM slots beyond the ``keep_free`` the caller reserves next.  A move that finds no
+        free slot waits for a later flush (a pending move frees its source only when
+        committed).  Returns (evict, promote) as [n, 3] (layer, head, chunk) arrays."""
+        evict = np.argwhere((self._table_h >= 0) & ~desired)
+        promote = np.argwhere((self._table_h <= -2) & desired)
+        key = lambda u: st[u[:, 0], u[:, 1], u[:, 2]] * (1 << 20) + u[:, 2]
+        evict = evict[np.argsort(key(evict), kind="stable")][:len(self._free_host)]
+        room = max(0, len(self._free_hbm) - keep_free)
+        promote = promote[np.argsort(-key(promote), kind="stable")][:room]
+        return evict, promote
+
+    def _apply_async(self, evict: np.ndarray, promote: np.ndarray):
+        """Enqueue the moves of ``_pick_moves`` on the move stream and leave them pending
+        (``_commit``).  Within a batch the units are paired with destination slots in
+        source-slot order, so that units adjacent in both pools go in one copy."""
+        if len(evict) == 0 and len(promote) == 0:
+            return 0, 0
+        moves = []
+        main = torch.cuda.current_stream(self.device)
+        side = self._move_stream()
+        side.wait_stream(main)  # the units' last writes (appends) come first
+        hk, hv = self._host_k.host.value, self._host_v.host.value
+        pk, pv = self.pool_k.data_ptr(), self.pool_v.data_ptr()
+        if self.fp8:
+            hsk, hsv = self._host_sk.host.value, self._host_sv.host.value
+            psk, psv = self.scale_k.data_ptr(), self.scale_v.data_ptr()
+        else:
+            hsk = hsv = psk = psv = None
+        for units, to_host in ((evict, True), (promote, False)):
+            if len(units) == 0:
+                continue
+            src = self._table_h[units[:, 0], units[:, 1], units[:, 2]].astype(np.int64)
+            if not to_host:
+                src = -2 - src
+            order = np.argsort(src, kind="stable")
+            units, src = units[order], src[order]
+            free = self._free_host if to_host else self._free_hbm
+            free.sort(reverse=True)  # pops ascend: consecutive destinations where possible
+            dst = np.array([free.pop() for _ in range(len(units))], dtype=np.int64)
+            for (l, h, c), a, b in zip(units.tolist(), src.tolist(), dst.tolist()):
+                # (unit, table entry once committed, slot released then)
+                moves.append(((l, h, c), -2 - b if to_host else b, a if to_host else -2 - a))
+            if to_host:
+                args = (pk, hk, pv, hv, psk, hsk, psv, hsv)
+                limits = (self.n_slots, self.n_host)
+            else:
+                args = (hk, pk, hv, pv, hsk, psk, hsv, psv)
+                limits = (self.n_host, self.n_slots)
+            s32, d32 = src.astype(np.int32), dst.astype(np.int32)
+            _lib.call("omm_copy_units_async", *args, s32.ctypes.data, d32.ctypes.data,
+                      len(units), *limits, self.unit_bytes, self.scale_bytes, side.cuda_stream,
+                      error=BlockKVBackendError)
+        ev = torch.cuda.Event()
+        ev.record(side)
+        self._moves = (ev, moves, {(l, c) for (l, _, c), _, _ in moves})
+        n_ev, n_pr = len(evict), len(promote)
+        unit = 2 * (self.unit_bytes + self.scale_bytes)
+        self.stats["evicted_units"] += n_ev
+        self.stats["promoted_units"] += n_pr
+        self.stats["evicted_bytes"] += n_ev * unit
+        self.stats["promoted_bytes"] += n_pr * unit
+        return n_ev, n_pr
+
+    def _commit(self, upload: bool = True) -> bool:
+        """Commit the pending moves of an asynchronous flush: the current stream waits for
+        their copies, the unit table switches to the destination slots and the source slots
+        return to the free lists (work enqueued from now on may reuse them).  Returns whether
+        the table changed (uploaded unless ``upload`` is false)."""
+        if self._moves is None:
+            return False
+        ev, moves, _ = self._moves
+        self._moves = None
+        torch.cuda.current_stream(self.device).wait_event(ev)
+        for (l, h, c), entry, old in moves:
+            self._table_h[l, h, c] = entry
+            self._release_slot(old)
+        if upload:
+            self._upload_table()
+        return True
+
+    def _pending_in(self, layer: int, cid: int) -> bool:
+        return self._moves is not None and (layer, cid) in self._moves[2]
+
     def _counts(self):
         """Host copies of every layer's stamps, page-read counts, pages seen and per-call unit
         accesses (one synchronisation); the arrays are reused by the next call."""
@@ -867,7 +980,17 @@ class PagedKVCache:
 
     HEAT_ALPHA = 0.25
 
+    def _async_ok(self) -> bool:
+        """Asynchronous flushes apply when some unit may have to leave HBM (the pool is smaller
+        than every chunk of every layer and head) and there is room for the protected (sink +
+        window) units besides the two chunks of slots they keep free."""
+        if not self.async_flush or self.n_slots >= self.L * self.H * self.max_chunks:
+            return False
+        prot = (0 if self.window is None else self.window) + self.sink
+        return self.n_slots >= (prot + 3) * self.L * self.H
+
     def _make_room(self, need: int):
+        self._commit()
         st, rd, _, _ = self._counts()
         desired = self._plan(st, reserve=need, rd=self._heat)
         self._apply(desired, st)
@@ -877,13 +1000,15 @@ class PagedKVCache:
     def flush(self, reserve_next_chunk: bool = True) -> dict:
         """Chunk-boundary residency update (MMCache.flush_offload, models/cache.py:1032): one
         read of the stamps and page counts, then batched evict / promote copies enqueued without
-        synchronising.  With ``reserve_next_chunk`` the HBM slots of the next chunk of every
+        synchronising: on the current stream, or (``async_flush``) on the cache's move stream,
+        committed by the next flush.  With ``reserve_next_chunk`` the HBM slots of the next chunk of every
         layer and head are assigned here, so the appends of the next AR step never touch the
         host.  Returns this flush's counts: per-call unit accesses served from HBM (hits) and
         from the host pool (misses), distinct units touched per pool, page listings (a page read
-        by k selections counts k times) and unique pages read per pool.  Residency changes only
-        here (and in an append that finds no free slot, which a flush's reservation prevents),
-        so the pool a unit sits in now is the pool its accesses since the last flush used."""
+        by k selections counts k times) and unique pages read per pool.  The pool serving a
+        unit's reads changes only here (and in an append that finds no free slot, which a
+        flush's reservation prevents, or one that rewrites a moving unit), so the pool a unit
+        sits in now is the pool its accesses since the last flush used."""
         st, rd, sn, tc = self._counts()
         touched = st > self._flush_epoch
         written = self._table_h != -1
@@ -902,26 +1027,41 @@ class PagedKVCache:
         self.stats["host_page_reads"] += host_reads
         self.stats["hbm_pages_unique"] += hbm_unique
         self.stats["host_pages_unique"] += host_unique
-        reserve = self.L * self.H if reserve_next_chunk else 0
+        # the previous flush's moves: their units were read from the source slots until now
+        changed = self._commit(upload=False)
+        LH = self.L * self.H
+        asyn = self._async_ok() and reserve_next_chunk
+        reserve = (2 * LH if asyn else LH) if reserve_next_chunk else 0
         self._update_heat(rd, written)
         desired = self._plan(st, reserve=reserve, rd=self._heat) & written
-        ev, pr = self._apply(desired, st)
+        if asyn:
+            moves = self._pick_moves(desired, st, keep_free=LH)
+        else:
+            if changed:
+                self._upload_table()
+                changed = False
+            ev, pr = self._apply(desired, st)
         if reserve_next_chunk:
-            changed = False
             for l in range(self.L):
                 c = self.n_chunks[l]
                 if c >= self.max_chunks:
                     continue
                 row = self._table_h[l, :, c]
-                free = np.nonzero(row == -1)[0]
-                for h in free:
+                # slots short (snapshots holding some): the append makes room itself
+                for h in np.nonzero(row == -1)[0]:
+                    if not self._free_hbm:
+                        break
                     row[h] = self._free_hbm.pop()
                     changed = True
-            if changed:
-                self._upload_table()
+        if changed:
+            self._upload_table()
         self._reads_all.zero_()
         self._seen_all.zero_()
         self._touch_all.zero_()
+        if asyn:
+            # last: a copy engine busy with the moves would hold up copies enqueued after them
+            # on the current stream (the table uploads above)
+            ev, pr = self._apply_async(*moves)
         self._flush_epoch = self._epoch
         self.stats["flushes"] += 1
         return {"hits": hits, "misses": misses, "hbm_units_touched": hbm_units,
@@ -1005,6 +1145,7 @@ class PagedKVCache:
         cloned.  A rewrite needs a free HBM slot per snapshotted unit, and the slots a snapshot
         holds are unavailable to residency until it is restored or discarded: size the pools
         (``hbm_slots`` / ``host_slots``) with that room."""
+        self._commit()
         a, b = max(0, int(chunk_start)), min(self.max_chunks, int(chunk_end))
         for sn in self._snaps:
             if sn["range"][0] < b and a < sn["range"][1]:
@@ -1041,6 +1182,7 @@ class PagedKVCache:
         the pooled rows (and ring entries) are copied back.  ``chunk_start`` must be the
         snapshot's first chunk when given (the reference helper's argument)."""
         self._active_snapshot(snapshot)
+        self._commit()  # a pending move of a rewritten unit would re-point it after the restore
         a, b = snapshot["range"]
         if chunk_start is not None and int(chunk_start) != a:
             raise BlockKVBackendError(f"snapshot starts at chunk {a}, not {chunk_start}")
@@ -1062,6 +1204,7 @@ class PagedKVCache:
     def discard_snapshot(self, snapshot: dict):
         """Drop a snapshot without restoring it; the slots it held are freed."""
         self._active_snapshot(snapshot)
+        self._commit()
         for old in snapshot["units"].values():
             if old is not None:
                 self._release_slot(old)
@@ -1073,7 +1216,8 @@ class PagedKVCache:
 
     # ---------------------------------------------------------------- inspection (tests)
     def read_unit(self, layer: int, head: int, cid: int):
-        """(K, V[, scale_k, scale_v]) of one unit as CPU tensors, from whichever pool holds it."""
+        """(K, V[, scale_k, scale_v]) of one unit as CPU tensors, from the pool that serves its
+        reads now (``where``)."""
         s = int(self._table_h[layer, head, cid])
         if s == -1:
             raise BlockKVBackendError("unit never written")
@@ -1096,15 +1240,21 @@ class PagedKVCache:
         return (k, v) + tuple(sc)
 
     def where(self, layer: int, head: int, cid: int) -> str:
+        """Pool that serves the unit's reads now: a unit an asynchronous flush is moving is
+        read from its source slot until the move is committed."""
         s = int(self._table_h[layer, head, cid])
         return "none" if s == -1 else ("hbm" if s >= 0 else "host")
 
     def evict_all(self):
         """Move every unit to the host pool (failure-injection / parity tests)."""
+        self._commit()
         desired = np.zeros_like(self._table_h, dtype=bool)
         self._apply(desired)
 
     def close(self):
+        if self._moves is not None:
+            self._moves[0].synchronize()
+            self._moves = None
         for p in (self._host_k, self._host_v, self._host_sk, self._host_sv):
             p.free()
 

@@ -1098,6 +1098,49 @@ extern "C" int omm_copy_units(const void* src_k, void* dst_k, const void* src_v,
   return check_launch("omm_copy_units");
 }
 
+extern "C" int omm_copy_units_async(const void* src_k, void* dst_k, const void* src_v,
+                                    void* dst_v, const void* src_sk, void* dst_sk,
+                                    const void* src_sv, void* dst_sv,
+                                    const int32_t* src_slot_host, const int32_t* dst_slot_host,
+                                    int32_t n, int32_t n_src_slots, int32_t n_dst_slots,
+                                    int64_t unit_bytes, int64_t scale_bytes, void* stream) {
+  using namespace omm;
+  OMM_REQUIRE(n >= 0 && unit_bytes > 0 && scale_bytes >= 0, OMM_EINVAL,
+              "omm_copy_units_async: n >= 0 and unit_bytes > 0 required");
+  if (n == 0) return OMM_OK;
+  OMM_REQUIRE(src_k && dst_k && src_slot_host && dst_slot_host, OMM_EINVAL,
+              "omm_copy_units_async: null pointer");
+  OMM_REQUIRE((src_v == nullptr) == (dst_v == nullptr) && (src_sk == nullptr) == (dst_sk == nullptr) &&
+                  (src_sv == nullptr) == (dst_sv == nullptr),
+              OMM_EINVAL, "omm_copy_units_async: source and destination pairs must both be given");
+  for (int32_t i = 0; i < n; ++i)
+    OMM_REQUIRE(src_slot_host[i] >= 0 && src_slot_host[i] < n_src_slots &&
+                    dst_slot_host[i] >= 0 && dst_slot_host[i] < n_dst_slots,
+                OMM_EINVAL, "omm_copy_units_async: slot pair %d (%d -> %d) out of range", i,
+                src_slot_host[i], dst_slot_host[i]);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto copy = [&](const void* src, void* dst, int64_t bytes, int64_t a, int64_t b, int64_t cnt) {
+    if (src == nullptr || bytes == 0) return hipSuccess;
+    return hipMemcpyAsync(static_cast<unsigned char*>(dst) + b * bytes,
+                          static_cast<const unsigned char*>(src) + a * bytes, cnt * bytes,
+                          hipMemcpyDefault, s);
+  };
+  for (int32_t i = 0; i < n;) {
+    int32_t j = i + 1;  // a run of units consecutive in both pools
+    while (j < n && src_slot_host[j] == src_slot_host[j - 1] + 1 &&
+           dst_slot_host[j] == dst_slot_host[j - 1] + 1)
+      ++j;
+    const int64_t a = src_slot_host[i], b = dst_slot_host[i], cnt = j - i;
+    for (hipError_t e : {copy(src_k, dst_k, unit_bytes, a, b, cnt),
+                         copy(src_v, dst_v, unit_bytes, a, b, cnt),
+                         copy(src_sk, dst_sk, scale_bytes, a, b, cnt),
+                         copy(src_sv, dst_sv, scale_bytes, a, b, cnt)})
+      OMM_REQUIRE(e == hipSuccess, OMM_EHIP, "omm_copy_units_async: %s", hipGetErrorString(e));
+    i = j;
+  }
+  return OMM_OK;
+}
+
 extern "C" int omm_gather_publish_clear(const int64_t* desc, int64_t n_fetch, int64_t n_clear,
                                         int64_t block_bytes, int64_t* ctas, void* stream) {
   using namespace omm;

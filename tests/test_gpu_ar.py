@@ -55,19 +55,23 @@ def test_ar_output_independent_of_residency(dtype):
     cfg = _cfg()
     full = cfg.layers * cfg.heads * 8
     a, ca = _run(full, dtype)
-    b, cb = _run(cfg.layers * cfg.heads * 3, dtype)   # room for 3 chunks per (layer, head)
-    assert cb.stats["evicted_units"] > 0 and ca.stats["evicted_units"] == 0
-    assert cb.stats["misses"] > 0
-    for x, y in zip(a, b):
-        assert torch.isfinite(x.float()).all()
-        assert torch.equal(x, y)
-    # every written unit is in exactly one pool
-    for l in range(cfg.layers):
-        for h in range(cfg.heads):
-            for c in range(cb.n_chunks[l]):
-                assert cb.where(l, h, c) in ("hbm", "host")
+    assert ca.stats["evicted_units"] == 0
+    # room for 3 chunks per (layer, head): synchronous flushes; for 5: asynchronous ones
+    for per_head, asyn in ((3, False), (5, True)):
+        b, cb = _run(cfg.layers * cfg.heads * per_head, dtype)
+        assert cb._async_ok() == asyn
+        assert cb.stats["evicted_units"] > 0
+        assert cb.stats["misses"] > 0
+        for x, y in zip(a, b):
+            assert torch.isfinite(x.float()).all()
+            assert torch.equal(x, y), per_head
+        # every written unit is in exactly one pool
+        for l in range(cfg.layers):
+            for h in range(cfg.heads):
+                for c in range(cb.n_chunks[l]):
+                    assert cb.where(l, h, c) in ("hbm", "host")
+        cb.close()
     ca.close()
-    cb.close()
 
 
 def _close(name, got, want, mx=2e-2, mean=1e-3, rel=0.0):

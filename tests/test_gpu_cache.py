@@ -887,3 +887,69 @@ def test_snapshot_restore_chunks(dtype):
         for h in range(H):
             assert not same(cache.read_unit(l, h, 3), before[(l, h, 3)])
     cache.close()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+def test_async_flush_matches_resident_cache(dtype):
+    """Asynchronous flush (byte budget): a flush enqueues its moves on the move stream and the
+    next flush commits them.  Selections before and after each commit return exactly what an
+    all-HBM cache returns, ``read_unit`` reads the pool serving the unit, slots balance once
+    committed, and an append that rewrites a chunk still moving commits first and lands."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(71)
+    L, H, D, C, P, n, W, G, T, M = 2, 2, 128, 500, 64, 9, 1, 64, 6, 200
+    fp8 = dtype == "fp8"
+    mk = lambda slots: PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P,
+                                    dtype=dtype, hbm_slots=slots, window_chunks=W,
+                                    keep_window_kv=False)
+    full, small = mk(L * H * n), mk(L * H * 5)
+    assert small._async_ok()
+    rng = np.random.default_rng(7)
+
+    def write(l, c):
+        k, v = _chunk(g, C, H, D, 0.3, fp8).to(DEV), _chunk(g, C, H, D, 1.0, fp8).to(DEV)
+        full.append(l, k, v, c)
+        small.append(l, k, v, c)
+
+    def compare(cid):
+        for l in range(L):
+            q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+            ids = rng.integers(0, (cid + 1) * small.ppc, size=(1, -(-M // G), H, T))
+            ids = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+            a, la = full.select(q, ids, l, G, return_lse=True)
+            b, lb = small.select(q, ids, l, G, return_lse=True)
+            torch.cuda.synchronize()
+            assert torch.equal(a, b) and torch.equal(la, lb), (cid, l)
+
+    pending = 0
+    for cid in range(n - 1):
+        for l in range(L):
+            write(l, cid)
+        compare(cid)
+        full.flush()
+        st = small.flush()
+        if st["evicted_units"] or st["promoted_units"]:
+            assert small._moves is not None
+            pending += 1
+            moving = sorted(u for u, _, _ in small._moves[1])
+            for (l, h, c) in moving[:2]:    # served by the source slot until committed
+                same = zip(full.read_unit(l, h, c), small.read_unit(l, h, c))
+                assert all(torch.equal(x, y) for x, y in same), (l, h, c)
+        compare(cid)
+    assert pending > 0 and small.stats["evicted_units"] > 0
+    assert any(small.where(l, h, c) == "host" for l in range(L) for h in range(H)
+               for c in range(n))
+    # rewrite a chunk whose units are still moving: the append commits the moves first
+    assert small._moves is not None
+    (l, _, c), _, _ = small._moves[1][0]
+    k, v = _chunk(g, C, H, D, 0.3, fp8).to(DEV), _chunk(g, C, H, D, 1.0, fp8).to(DEV)
+    full.append(l, k, v, c)
+    small.append(l, k, v, c)
+    assert small._moves is None
+    compare(n - 2)
+    _slots_balance(small)
+    for l, h, c in [(a, b, x) for a in range(L) for b in range(H) for x in range(n - 1)]:
+        same = zip(full.read_unit(l, h, c), small.read_unit(l, h, c))
+        assert all(torch.equal(x, y) for x, y in same), (l, h, c)
+    full.close()
+    small.close()
