@@ -40,8 +40,8 @@ constexpr int kVP = 72;
 // when the tile is stored to LDS (exact: every e4m3 value is a bf16 value).  The page scales are
 // not applied here: the kernel folds them into the softmax (K's into the exponent scale, V's into
 // p and the row sum), one per 64-key tile.  RAWK: K stays in codes in LDS too, for the fp8 QK^T
-// MFMA.
-template <typename KVT, int D, bool RAWK = false>
+// MFMA.  NOK: K is not staged at all (the kernel copies it global -> LDS by DMA); only V is.
+template <typename KVT, int D, bool RAWK = false, bool NOK = false>
 struct Stager {
   static constexpr int DC = D / 8;                 // 16-byte slices per row
   static constexpr int KU = 64 * DC / 128;         // K units per thread
@@ -50,8 +50,8 @@ struct Stager {
   static constexpr int ES = static_cast<int>(sizeof(KVT));
   static constexpr bool F8 = ES == 1;
   static constexpr int KP8 = D + 16;               // LDS row pitch of raw K codes (bytes)
-  uint4 k[F8 ? 1 : KU];
-  uint2 k8[F8 ? KU : 1];
+  uint4 k[F8 || NOK ? 1 : KU];
+  uint2 k8[F8 && !NOK ? KU : 1];
   uint4 v[F8 ? 1 : VQ][4];
   uint2 v8[F8 ? VQ : 1][4];
   uint32_t koff, voff;                             // bytes, within a tile
@@ -63,7 +63,7 @@ struct Stager {
 
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int j = 0; j < KU; ++j) {
+    for (int j = 0; j < (NOK ? 0 : KU); ++j) {
       if constexpr (F8) k8[j] = make_uint2(0, 0);
       else k[j] = make_uint4(0, 0, 0, 0);
     }
@@ -109,7 +109,7 @@ struct Stager {
     const char* vb = static_cast<const char*>(br.v) + static_cast<int64_t>(tok0) * br.sv * ES;
     const int row0 = tid / DC;
 #pragma unroll
-    for (int j = 0; j < KU; ++j) {
+    for (int j = 0; j < (NOK ? 0 : KU); ++j) {
       const char* p = kb + static_cast<int64_t>(RS * j) * br.sk * ES;
       if (FULL || row0 + RS * j < n) {
         if constexpr (F8) k8[j] = *reinterpret_cast<const uint2*>(p + koff);
@@ -135,7 +135,7 @@ struct Stager {
     constexpr int KP = D + 8;
     const int dc = tid % DC;
 #pragma unroll
-    for (int j = 0; j < KU; ++j) {
+    for (int j = 0; j < (NOK ? 0 : KU); ++j) {
       const int key = tid / DC + RS * j;
       if constexpr (RAWK)
         *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(Ks) + key * KP8 + dc * 8) = k8[j];
@@ -183,6 +183,14 @@ constexpr int kMfmaThreads = 128;
 // stays in its page codes, S = (Qc Kc^T) * s_q * s_k on v_mfma_f32_16x16x32_fp8_fp8 (products
 // of e4m3 codes are exact in fp32), the K page scale s_k is one per 64-key tile and s_q one per
 // query column, both folded into the softmax's exponent scale.  PV stays bf16.
+// At D = 128 the K codes need no widening, so they skip the registers: each tile's 64 rows of 128
+// bytes go global -> LDS by buffer_load ... lds (4 instructions per wave) into one of two 8 KiB
+// buffers, issued a tile ahead like the register loads of V.  16-byte chunk c of row r sits at
+// slot c ^ kSwz8(r), which keeps the b128 operand reads conflict free whether a read cycle
+// serves 8 lanes (32 banks) or 16 (64 banks).  One b128 read feeds two fp8 k-steps: k-step s of
+// lane group j4 covers head dims 64 (s >> 1) + 16 j4 + 8 (s & 1) .. +7 for K and for Q alike.
+__device__ __forceinline__ int kSwz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 template <typename QT, typename Acc, int D, bool QK8 = false>
 __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     View4<const QT> q, View4<QT> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
@@ -192,6 +200,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   constexpr int SD = D / 32;   // k-steps of QK^T
   constexpr int ND = D / 16;   // d-tiles of PV
   static_assert(!QK8 || sizeof(typename Acc::KV) == 1, "fp8 QK^T needs fp8 pages");
+  constexpr bool DMAK = QK8 && D == 128;  // K codes by LDS DMA (two 8 KiB buffers in Ks)
+  static_assert(!DMAK || 2 * 8192 <= KS * 2, "K DMA buffers fit the K region");
   __shared__ __align__(16) uint16_t lds[KS + VS];
   uint16_t* Ks = lds;
   uint16_t* Vt = lds + KS;
@@ -219,9 +229,11 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     my_q[x] = m0 + 32 * w + 16 * x + l16;
     q_ok[x] = my_q[x] < m_end;
 #pragma unroll
-    for (int s = 0; s < SD; ++s)
-      qb[x][s] = q_ok[x] ? *reinterpret_cast<const uint4*>(q.at(b, my_q[x], h, 32 * s + 8 * j4))
+    for (int s = 0; s < SD; ++s) {
+      const int d0 = DMAK ? 64 * (s >> 1) + 16 * j4 + 8 * (s & 1) : 32 * s + 8 * j4;
+      qb[x][s] = q_ok[x] ? *reinterpret_cast<const uint4*>(q.at(b, my_q[x], h, d0))
                          : make_uint4(0, 0, 0, 0);
+    }
   }
   // fp8 queries: per-row amax over the 4 lane groups holding the row's dims, scale amax / 448,
   // codes by round-to-nearest-even (v_cvt_pk_fp8_f32)
@@ -285,7 +297,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 
   using KVT = typename Acc::KV;
   constexpr bool kFp8 = sizeof(KVT) == 1;
-  Stager<KVT, D, QK8> st;
+  Stager<KVT, D, QK8, DMAK> st;
   float sk_next = 1.0f, sv_next = 1.0f;  // page scales of the tile being staged (fp8 pages)
   WaveWalk<Acc> wk;
   wk.start(acc, b, g, h, T, qc);
@@ -293,7 +305,26 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
   st.zero();
   // raw pointer tables may hold blocks that are not 16-byte aligned (2-byte loads for those)
   constexpr bool kMis = Acc::kMayMisalign && sizeof(KVT) == 2;
+  // DMAK: this lane's source offsets for the wave's 4 copy instructions (rows 32 w .. 32 w + 31)
+  // and its operand read offsets (row l16, chunk 4 p + j4; the 16 t rows are an immediate)
+  int kdo[4] = {0, 0, 0, 0}, k8off[2] = {0, 0};
+  int rsk = 0, kbi = 0;
+  char* const kbuf = reinterpret_cast<char*>(Ks);
+  if constexpr (DMAK) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) k8off[p] = l16 * D + (((4 * p + j4) ^ kSwz8(l16)) << 4);
+  }
   if (wk.valid) {
+    if constexpr (DMAK) {
+      rsk = static_cast<int>(wk.br.sk);  // bytes: one code per element
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int row = (4 * w + jj) * 8 + lane / 8, c = lane % 8;
+        kdo[jj] = row * rsk + ((c ^ kSwz8(row)) << 4);
+      }
+      dma_part<4>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+                  wk.n, kbuf, w, kdo);
+    }
     st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);
     if constexpr (kFp8) {
       sk_next = wk.br.scale_k;
@@ -301,13 +332,20 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
     }
   }
   while (wk.valid) {
-    __syncthreads();  // every wave is done reading the previous tile
+    // this wave's K copy of the tile has landed (DMAK); after the barrier every wave's has, and
+    // every wave is done reading the previous tile
+    if constexpr (DMAK) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     st.store(Ks, Vt, tid);
     __syncthreads();
     const int tile_n = wk.n;
     const float sk_cur = sk_next, sv_cur = sv_next;
+    const char* const kcur = kbuf + 8192 * kbi;
     wk.advance(acc, b, g, h, T, qc);
     if (wk.valid) {
+      if constexpr (DMAK)  // into the other buffer, which every wave finished reading last tile
+        dma_part<4>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+                    wk.n, kbuf + 8192 * (kbi ^ 1), w, kdo);
       st.template load<kMis>(wk.br, wk.tok0, wk.n, tid);  // in flight during the MFMAs
       if constexpr (kFp8) {
         sk_next = wk.br.scale_k;
@@ -338,6 +376,16 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
         for (int t = 0; t < 4; ++t) {
           s4[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
           s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (DMAK) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const uint4 a = *reinterpret_cast<const uint4*>(kcur + k8off[p] + 16 * D * t);
+              s4[0][t] = mfma_fp8(make_uint2(a.x, a.y), qb8[0][2 * p], s4[0][t]);
+              s4[1][t] = mfma_fp8(make_uint2(a.x, a.y), qb8[1][2 * p], s4[1][t]);
+              s4[0][t] = mfma_fp8(make_uint2(a.z, a.w), qb8[0][2 * p + 1], s4[0][t]);
+              s4[1][t] = mfma_fp8(make_uint2(a.z, a.w), qb8[1][2 * p + 1], s4[1][t]);
+            }
+          } else
 #pragma unroll
           for (int s = 0; s < SD; ++s) {
             if constexpr (QK8) {
@@ -362,6 +410,16 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
                            lim > 2 ? 0.f : kNegInf, lim > 3 ? 0.f : kNegInf};
           s4[0][t] = bias;
           s4[1][t] = bias;
+          if constexpr (DMAK) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const uint4 a = *reinterpret_cast<const uint4*>(kcur + k8off[p] + 16 * D * t);
+              s4[0][t] = mfma_fp8(make_uint2(a.x, a.y), qb8[0][2 * p], s4[0][t]);
+              s4[1][t] = mfma_fp8(make_uint2(a.x, a.y), qb8[1][2 * p], s4[1][t]);
+              s4[0][t] = mfma_fp8(make_uint2(a.z, a.w), qb8[0][2 * p + 1], s4[0][t]);
+              s4[1][t] = mfma_fp8(make_uint2(a.z, a.w), qb8[1][2 * p + 1], s4[1][t]);
+            }
+          } else
 #pragma unroll
           for (int s = 0; s < SD; ++s) {
             if constexpr (QK8) {
@@ -441,6 +499,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
         }
       }
     }
+    kbi ^= 1;
   }
 
   // epilogue: reduce the lane-partial sums of each query over its 4 lane groups
