@@ -68,6 +68,13 @@ ALGO = {
         "paged_append_wg_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2
                                          + 2 * _AR_PPC * BS * H * D + 2 * _AR_PPC * H * 4
                                          + 2 * _AR_PPC * H * D * 2),
+        # the per-(page, head) append kernel that serves head dims 64 / 128: the same bytes
+        "paged_append_head_kernel<false>": ("bytes", 2 * _AR_C * H * D * 2
+                                            + 2 * _AR_PPC * BS * H * D * 2
+                                            + 2 * _AR_PPC * H * D * 2),
+        "paged_append_head_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2
+                                           + 2 * _AR_PPC * BS * H * D + 2 * _AR_PPC * H * 4
+                                           + 2 * _AR_PPC * H * D * 2),
         # selection over the history (cache.select): 4680 queries x 12 heads x 16 pages x 64
         # tokens, 4 D FLOPs each (bf16 pages, some host-resident; fp8 pages)
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 2>": (
@@ -85,6 +92,9 @@ ALGO = {
         "branch_mix_kernel": ("bytes", 4 * _AR_C * H * D * 2 + _AR_C * H * 3 * 2),
     },
 }
+# config 1 (bench.py --c1-only): useful FLOPs of the seeded fp32 call, counted from its ids by
+# useful_flops (the queries as the last frame: every selected block visible)
+ALGO["c1"] = {"sel_fwd_f32mfma_kernel<DenseAcc<float>, 128>": ("flops_fp32", 9602498560)}
 # kernels one call launches together, priced as a whole: the AR top-k (query pooling into the
 # workspace, split scoring + selection, merge) reads the chunk's q and the pooled history
 ALGO_GROUPS = {
@@ -114,6 +124,8 @@ def parse():
                    help="skip the config-3 30-layer forward and the config-1 call")
     p.add_argument("--full-only", action="store_true",
                    help="only the config-3 30-layer forward and the config-1 call")
+    p.add_argument("--c1-only", action="store_true",
+                   help="only the config-1 fp32 selection call (its rocprof profile)")
     p.add_argument("--ar-only", action="store_true",
                    help="run only the AR leg (configs 4 and 5) and print its results (profiling "
                         "runs of the cache kernels)")
@@ -205,6 +217,10 @@ def rocprof_summary(out: str, d: str, command: str, workload: str = "c3"):
                 k["algorithmic_bytes"] = amount
                 k["algorithmic_GBps"] = round(amount / avg_ns, 1)
                 k["frac_hbm_8TBps"] = round(amount / avg_ns / PEAK_HBM_GBS, 4)
+            elif unit == "flops_fp32":
+                k["useful_flops"] = amount
+                k["useful_TFLOPs"] = round(amount / avg_ns / 1e3, 1)
+                k["frac_fp32_peak"] = round(amount / avg_ns / 1e3 / PEAK_FP32_TFLOPS, 4)
             else:
                 k["useful_flops"] = amount
                 k["useful_TFLOPs"] = round(amount / avg_ns / 1e3, 1)
@@ -274,7 +290,7 @@ def summary_md(res: dict, path: str):
         ach = (f"{k['algorithmic_GBps']} GB/s" if "algorithmic_bytes" in k else
                f"{k['useful_TFLOPs']} TFLOP/s" if "useful_flops" in k else "")
         frac = k.get("frac_hbm_8TBps", k.get("frac_mixed_fp8_bf16_peak",
-                                              k.get("frac_bf16_peak", "")))
+                                              k.get("frac_bf16_peak", k.get("frac_fp32_peak", ""))))
         shown = name if len(name) <= 72 else name[:69] + "..."
         lines.append(f"| `{shown}` | {k['calls']} | {k['avg_us']} | "
                      f"{k.get('hbm_bytes_scaled', ''):,} | {k.get('hbm_GBps', '')} | {alg} | "
@@ -564,7 +580,7 @@ def run_config1(steps: int):
     return {"workload": "config 1: fp32 q [1,1560,12,128], k/v [1,4680,12,128], top-16 of "
                         "64-token blocks, groups of 64, queries as the last 1560-token frame",
             "kernel": "sel_fwd_f32mfma_kernel (fp32 MFMA, v_mfma_f32_16x16x4_f32)", "ms": round(ms, 4),
-            "useful_gflop": round(flops / 1e9, 3), "useful_tflops": round(tf, 3),
+            "useful_flops": int(flops), "useful_gflop": round(flops / 1e9, 3), "useful_tflops": round(tf, 3),
             "peak_fp32_tflops": PEAK_FP32_TFLOPS, "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4),
             "timing": "--steps back-to-back launches, HIP events"}
 
@@ -744,6 +760,9 @@ def main():
     from omnimem_amd.selection import sel_fwd
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.c1_only:
+        print(json.dumps({"config1": run_config1(args.steps)}), flush=True)
+        return
     if args.full_only:
         print(json.dumps({"config1": run_config1(args.steps),
                           "config3_forward": run_config3_forward()}), flush=True)
