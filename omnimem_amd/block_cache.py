@@ -733,8 +733,11 @@ class PagedKVCache:
         chunk = np.broadcast_to(np.arange(self.max_chunks), st.shape).reshape(-1)
         desired = res | prot
         cap = self._cap(reserve)
-        # coldest first: fewest pages read, then oldest touch, then oldest chunk
-        cold = lambda idx: idx[np.lexsort((chunk[idx], stamp[idx], reads[idx]))]
+        # coldest first: fewest pages read, then oldest touch, then oldest chunk (two stable
+        # sorts: by the packed (touch, chunk) key, then by reads)
+        def cold(idx):
+            idx = idx[np.argsort(stamp[idx] * (1 << 20) + chunk[idx], kind="stable")]
+            return idx[np.argsort(reads[idx], kind="stable")]
         movable = cold(np.flatnonzero(desired & ~prot))
         over = int(desired.sum()) - cap
         if over > 0:
@@ -747,18 +750,17 @@ class PagedKVCache:
         hot = np.flatnonzero(host & ~desired & (reads > 0))
         hot = hot[np.argsort(-reads[hot], kind="stable")]
         unit_pages = self.ppc
+        # free slots first, hottest first, for units read more than a promotion moves
         free = cap - int(desired.sum())
-        i = 0
-        while i < hot.size and free > 0 and reads[hot[i]] > unit_pages:
-            desired[hot[i]] = True
-            free -= 1
-            i += 1
-        j = 0
-        while i < hot.size and j < movable.size and reads[hot[i]] > reads[movable[j]] + 2 * unit_pages:
-            desired[hot[i]] = True
-            desired[movable[j]] = False
-            i += 1
-            j += 1
+        i = min(max(0, free), int(np.argmin(np.append(reads[hot] > unit_pages, False))))
+        desired[hot[:i]] = True
+        # then swaps, hottest host unit against coldest resident one, while the reads gained
+        # beat the pages moved (both lists sorted, so the swaps that pay are a prefix)
+        k = min(hot.size - i, movable.size)
+        pays = reads[hot[i:i + k]] > reads[movable[:k]] + 2 * unit_pages
+        j = int(np.argmin(np.append(pays, False)))
+        desired[hot[i:i + j]] = True
+        desired[movable[:j]] = False
         return desired.reshape(self._table_h.shape)
 
     def _take_slots(self, layer_units, to_host: bool):
