@@ -227,7 +227,7 @@ class PagedKVCache:
         self.touches = list(self._touch_all.unbind(0))
         self._h_stamp = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._h_reads = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
-        self._h_seen = torch.empty((L, H, MC, self.ppc), dtype=torch.uint8).pin_memory()
+        self._h_pages = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._h_touch = torch.empty((L, H, MC), dtype=torch.int32).pin_memory()
         self._ring = _UploadRing(8, max(L * H * MC, 2 * (self.n_slots + self.n_host)))
         self._d_idx = torch.empty(2 * (self.n_slots + self.n_host), dtype=torch.int32,
@@ -954,15 +954,16 @@ class PagedKVCache:
         return self._moves is not None and (layer, cid) in self._moves[2]
 
     def _counts(self):
-        """Host copies of every layer's stamps, page-read counts, pages seen and per-call unit
-        accesses (one synchronisation); the arrays are reused by the next call."""
+        """Host copies of every layer's stamps, page-read counts, distinct pages read per unit
+        (summed on the device) and per-call unit accesses (one synchronisation); the arrays are
+        reused by the next call."""
         self._h_stamp.copy_(self._stamp_all, non_blocking=True)
         self._h_reads.copy_(self._reads_all, non_blocking=True)
-        self._h_seen.copy_(self._seen_all, non_blocking=True)
+        self._h_pages.copy_(self._seen_all.sum(-1, dtype=torch.int32), non_blocking=True)
         self._h_touch.copy_(self._touch_all, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         return (self._h_stamp.numpy().astype(np.int64), self._h_reads.numpy(),
-                self._h_seen.numpy(), self._h_touch.numpy())
+                self._h_pages.numpy(), self._h_touch.numpy())
 
     def _update_heat(self, rd: np.ndarray, written: np.ndarray):
         """Heat of every unit: an exponential moving average (weight HEAT_ALPHA) of its page
@@ -1011,7 +1012,7 @@ class PagedKVCache:
         unit's reads changes only here (and in an append that finds no free slot, which a
         flush's reservation prevents, or one that rewrites a moving unit), so the pool a unit
         sits in now is the pool its accesses since the last flush used."""
-        st, rd, sn, tc = self._counts()
+        st, rd, pages, tc = self._counts()
         touched = st > self._flush_epoch
         written = self._table_h != -1
         res, host = self._table_h >= 0, self._table_h <= -2
@@ -1019,7 +1020,6 @@ class PagedKVCache:
         host_units = int((touched & host).sum())
         hits, misses = int(tc[res].sum()), int(tc[host].sum())
         hbm_reads, host_reads = int(rd[res].sum()), int(rd[host].sum())
-        pages = sn.sum(-1, dtype=np.int64)
         hbm_unique, host_unique = int(pages[res].sum()), int(pages[host].sum())
         self.stats["hits"] += hits
         self.stats["misses"] += misses
@@ -1035,7 +1035,13 @@ class PagedKVCache:
         asyn = self._async_ok() and reserve_next_chunk
         reserve = (2 * LH if asyn else LH) if reserve_next_chunk else 0
         self._update_heat(rd, written)
-        desired = self._plan(st, reserve=reserve, rd=self._heat) & written
+        if (self.lru_max_size == 0 and not bool((self._table_h <= -2).any())
+                and int((self._table_h >= 0).sum()) <= self._cap(reserve)):
+            # byte budget, nothing on the host and room for everything: the cost plan keeps
+            # exactly the resident set
+            desired = self._table_h >= 0
+        else:
+            desired = self._plan(st, reserve=reserve, rd=self._heat) & written
         if asyn:
             moves = self._pick_moves(desired, st, keep_free=LH)
         else:
