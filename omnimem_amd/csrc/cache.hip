@@ -392,152 +392,119 @@ __global__ __launch_bounds__(kAppendThreads) void paged_append_wg_kernel(AppendA
     a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
 }
 
-// The same append with one workgroup of 4 waves per (page, head), for pages of at most 64 tokens
-// and head dims of 64 or 128 (kAppHeadThreads threads; the AR chunk: 74 x 12 = 888 workgroups,
-// several per CU).  Lane (tl, dc): a wave's load covers TPI = 64 / lph consecutive token rows of
-// the head, 16 bytes per lane; the thread's rows are TPI (w + 4 j) + tl.  bf16 pages are written
-// from registers.  fp8 takes the page's amax over the whole wave (one head) and the 4 waves
-// through LDS, so the one barrier that holds the stores spans 4 waves instead of the 16 of
-// paged_append_wg_kernel; that barrier also publishes the LDS-staged rows, from which one thread
-// per element pair adds the pooled row in token order.  AR chunk, graph replay: bf16 11.1 us
-// (11.7 with the 16-wave kernel), fp8 10.3 us (12.1).  Measured and not kept: one thread per
-// pooled element (10.2 / 11.2 us), 8 waves per workgroup (10.8 / 11.4), and persistent
-// workgroups that load the next (page, head) while storing the current one (256 / 512 / 1024
-// workgroups: 16.3 / 12.2 / 11.5 us fp8): the chunk's loads all in flight at once is fastest.
+// The same append with one workgroup of 4 waves per (page, head, K or V), for pages of at most
+// 64 tokens and head dims of 64 or 128 (kAppHeadThreads threads; blockIdx.z = 0 for K, 1 for V;
+// the AR chunk: 74 x 12 x 2 = 1,776 workgroups, several per CU).  Lane (tl, dc): a wave's load
+// covers TPI = 64 / lph consecutive token rows of the head, 16 bytes per lane; the thread's rows
+// are TPI (w + 4 j) + tl.  bf16 pages are written from registers.  fp8 takes the page's amax
+// over the whole wave (one head) and the 4 waves through LDS, so the one barrier that holds the
+// stores spans 4 waves and one tensor; that barrier also publishes the LDS-staged rows, from
+// which one thread per element pair adds the pooled row in token order.  AR chunk, graph replay:
+// bf16 11.0 us, fp8 9.7-9.9 us, against 11.3 / 10.5-10.7 with K and V of a (page, head) in one
+// workgroup and 11.7 / 12.1 with 16-wave (page, 4 heads) workgroups.  Measured and not kept: 2 or
+// 8 waves per workgroup (fp8 10.4 / 10.5 us), one thread per pooled element, and persistent
+// workgroups that load the next item while storing the current one (11.5-16.3 us fp8): the
+// chunk's loads all in flight at once is fastest.
 constexpr int kAppHeadThreads = 256;
 constexpr int kAppHeadWaves = kAppHeadThreads / kWave;
 
 template <bool FP8>
-__global__ __launch_bounds__(kAppHeadThreads) void paged_append_head_kernel(AppendArgs a) {
-  __shared__ __align__(16) uint4 stage[2][kAppendMaxP][16];  // [K / V][token row][16-byte column]
-  __shared__ float amx[2][kAppHeadWaves];
+__global__ __launch_bounds__(kAppHeadThreads) void paged_append_kv_kernel(AppendArgs a) {
+  __shared__ __align__(16) uint4 stage[kAppendMaxP][16];  // [token row][16-byte column]
+  __shared__ float amx[kAppHeadWaves];
   const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
   const int lph = a.lph, TPI = kWave / lph;
   const int tl = lane / lph, dc = lane - tl * lph;
   const int p = blockIdx.x, h = blockIdx.y;
+  const bool isv = blockIdx.z != 0;
   const int32_t slot = a.unit_table[static_cast<int64_t>(h) * a.max_chunks + a.cid];
   if (slot < 0 || slot >= a.n_slots) return;  // whole workgroup
   const int P = a.P;
   const int t_first = p * P;
   const int nvalid = max(0, min(P, a.tokens - t_first));
   const int64_t page = static_cast<int64_t>(slot) * a.ppc + p;
-  const bf16_t* ksrc = a.k + static_cast<int64_t>(h) * a.ks2 + dc * 8;
-  const bf16_t* vsrc = a.v + static_cast<int64_t>(h) * a.vs2 + dc * 8;
-  constexpr int NR = kAppendMaxP / (kAppHeadWaves * 4);  // rows per thread at TPI = 4 (D = 128)
-  uint4 kr[NR], vr[NR];
+  const bf16_t* src = (isv ? a.v + static_cast<int64_t>(h) * a.vs2 : a.k + static_cast<int64_t>(h) * a.ks2) + dc * 8;
+  const int64_t s1 = isv ? a.vs1 : a.ks1;
+  constexpr int NR = kAppendMaxP / (kAppHeadWaves * 4);
+  uint4 xr[NR];
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     const int r = TPI * (w + kAppHeadWaves * j) + tl;
-    kr[j] = vr[j] = make_uint4(0, 0, 0, 0);
-    if (r < nvalid) {
-      kr[j] = *reinterpret_cast<const uint4*>(ksrc + static_cast<int64_t>(t_first + r) * a.ks1);
-      vr[j] = *reinterpret_cast<const uint4*>(vsrc + static_cast<int64_t>(t_first + r) * a.vs1);
-    }
+    xr[j] = make_uint4(0, 0, 0, 0);
+    if (r < nvalid) xr[j] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(t_first + r) * s1);
   }
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     const int r = TPI * (w + kAppHeadWaves * j) + tl;
-    if (r < nvalid) {
-      stage[0][r][dc] = kr[j];
-      stage[1][r][dc] = vr[j];
-    }
+    if (r < nvalid) stage[r][dc] = xr[j];
   }
-  const int64_t row = a.D / 8;  // 16-byte (bf16) or 8-byte (fp8) pieces per page row
+  const int64_t row = a.D / 8;
   if constexpr (!FP8) {
-    uint4* kd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_k) + page * P * a.D + dc * 8);
-    uint4* vd = reinterpret_cast<uint4*>(static_cast<bf16_t*>(a.pool_v) + page * P * a.D + dc * 8);
+    uint4* d = reinterpret_cast<uint4*>(static_cast<bf16_t*>(isv ? a.pool_v : a.pool_k) + page * P * a.D + dc * 8);
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
       const int r = TPI * (w + kAppHeadWaves * j) + tl;
-      if (r < P) {
-        kd[r * row] = kr[j];
-        vd[r * row] = vr[j];
-      }
+      if (r < P) d[r * row] = xr[j];
     }
     __syncthreads();
   } else {
-    float mk = 0.0f, mv = 0.0f;
+    float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
-      float fk[8], fv[8];
-      unpack_bf16x8(kr[j], fk);
-      unpack_bf16x8(vr[j], fv);
+      float f[8];
+      unpack_bf16x8(xr[j], f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        mk = fmaxf(mk, fabsf(fk[i]));
-        mv = fmaxf(mv, fabsf(fv[i]));
-      }
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(f[i]));
     }
-    // the whole wave holds one head's rows: max over it (exact, order-free), then the 4 waves
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) {
-      mk = fmaxf(mk, __shfl_xor(mk, m, kWave));
-      mv = fmaxf(mv, __shfl_xor(mv, m, kWave));
-    }
-    if (lane == 0) {
-      amx[0][w] = mk;
-      amx[1][w] = mv;
-    }
+    for (int mm = 1; mm < kWave; mm <<= 1) m = fmaxf(m, __shfl_xor(m, mm, kWave));
+    if (lane == 0) amx[w] = m;
     __syncthreads();
 #pragma unroll
-    for (int ww = 0; ww < kAppHeadWaves; ++ww) {
-      mk = fmaxf(mk, amx[0][ww]);
-      mv = fmaxf(mv, amx[1][ww]);
-    }
-    const float ik = mk > 0.0f ? 448.0f / mk : 1.0f;
-    const float iv = mv > 0.0f ? 448.0f / mv : 1.0f;
-    uint2* kd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_k) + page * P * a.D + dc * 8);
-    uint2* vd = reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.pool_v) + page * P * a.D + dc * 8);
+    for (int ww = 0; ww < kAppHeadWaves; ++ww) m = fmaxf(m, amx[ww]);
+    const float im = m > 0.0f ? 448.0f / m : 1.0f;
+    uint2* d = reinterpret_cast<uint2*>(static_cast<uint8_t*>(isv ? a.pool_v : a.pool_k) + page * P * a.D + dc * 8);
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
       const int r = TPI * (w + kAppHeadWaves * j) + tl;
       if (r < P) {
-        uint2 kq = make_uint2(0, 0), vq = make_uint2(0, 0);
+        uint2 qv = make_uint2(0, 0);
         if (r < nvalid) {
-          float fk[8], fv[8];
-          unpack_bf16x8(kr[j], fk);
-          unpack_bf16x8(vr[j], fv);
-          kq = quant8(fk, ik);
-          vq = quant8(fv, iv);
+          float f[8];
+          unpack_bf16x8(xr[j], f);
+          qv = quant8(f, im);
         }
-        kd[r * row] = kq;
-        vd[r * row] = vq;
+        d[r * row] = qv;
       }
     }
-    if (tid == 0) {
-      a.scale_k[page] = mk > 0.0f ? mk / 448.0f : 1.0f;
-      a.scale_v[page] = mv > 0.0f ? mv / 448.0f : 1.0f;
-    }
+    if (tid == 0) (isv ? a.scale_v : a.scale_k)[page] = m > 0.0f ? m / 448.0f : 1.0f;
   }
-  // pooled rows: thread t < D takes element pair t % (D / 2) of K (t < D / 2) or V, adding the
-  // staged rows in token order (the omm_block_pool sum)
-  if (tid < a.D) {
-    const int half = a.D / 2;
-    const bool isv = tid >= half;
-    const int e = isv ? tid - half : tid;
+  // pooled row: thread t < D / 2 takes element pair t, adding the staged rows in token order
+  if (tid < a.D / 2) {
+    const int e = tid;
     const int col = e >> 2, e2 = e & 3;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(&stage[isv ? 1 : 0][0][col]) + e2;
-    constexpr int RS = 16 * 4;  // 32-bit words per staged row
-    float s0 = 0.0f, s1 = 0.0f;
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(&stage[0][col]) + e2;
+    constexpr int RS = 16 * 4;
+    float s0 = 0.0f, s1f = 0.0f;
     int r = 0;
     for (; r + 16 <= nvalid; r += 16) {
       uint32_t x[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) x[u] = src[(r + u) * RS];
+      for (int u = 0; u < 16; ++u) x[u] = sp[(r + u) * RS];
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         s0 += bf16_bits_to_f32(static_cast<uint16_t>(x[u]));
-        s1 += bf16_bits_to_f32(static_cast<uint16_t>(x[u] >> 16));
+        s1f += bf16_bits_to_f32(static_cast<uint16_t>(x[u] >> 16));
       }
     }
     for (; r < nvalid; ++r) {
-      const uint32_t x = src[r * RS];
+      const uint32_t x = sp[r * RS];
       s0 += bf16_bits_to_f32(static_cast<uint16_t>(x));
-      s1 += bf16_bits_to_f32(static_cast<uint16_t>(x >> 16));
+      s1f += bf16_bits_to_f32(static_cast<uint16_t>(x >> 16));
     }
     const float cnt = static_cast<float>(nvalid);
     const uint16_t lo = nvalid > 0 ? f32_to_bf16_bits(s0 / cnt) : 0;
-    const uint16_t hi = nvalid > 0 ? f32_to_bf16_bits(s1 / cnt) : 0;
+    const uint16_t hi = nvalid > 0 ? f32_to_bf16_bits(s1f / cnt) : 0;
     const uint32_t packed = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
     const int64_t crow = static_cast<int64_t>(a.cid) * a.ppc + p;
     bf16_t* dst = isv ? a.v_cmp : a.k_cmp;
@@ -546,9 +513,10 @@ __global__ __launch_bounds__(kAppHeadThreads) void paged_append_head_kernel(Appe
       *reinterpret_cast<uint32_t*>(dst + off + 2 * e) = packed;
     }
   }
-  if (p == 0 && tid == 0 && a.stamp != nullptr && a.epoch > 0)
+  if (!isv && p == 0 && tid == 0 && a.stamp != nullptr && a.epoch > 0)
     a.stamp[static_cast<int64_t>(h) * a.max_chunks + a.cid] = a.epoch;
 }
+
 
 // ---- batched unit copies (evict to the host pool, promote to HBM) ---------------------------
 constexpr int64_t kCopyPart = 64 * 1024;  // bytes per workgroup
@@ -885,11 +853,11 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
   const dim3 grid(static_cast<unsigned>(ppc), static_cast<unsigned>(cdiv64(H, kWave / a.lph)));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (P <= kAppendMaxP && (D == 64 || D == 128)) {
-    const dim3 hgrid(static_cast<unsigned>(ppc), static_cast<unsigned>(H));
+    const dim3 hgrid(static_cast<unsigned>(ppc), static_cast<unsigned>(H), 2u);
     if (kv->dtype == OMM_BF16)
-      paged_append_head_kernel<false><<<hgrid, kAppHeadThreads, 0, s>>>(a);
+      paged_append_kv_kernel<false><<<hgrid, kAppHeadThreads, 0, s>>>(a);
     else
-      paged_append_head_kernel<true><<<hgrid, kAppHeadThreads, 0, s>>>(a);
+      paged_append_kv_kernel<true><<<hgrid, kAppHeadThreads, 0, s>>>(a);
     return check_launch("omm_paged_append");
   }
   if (P <= kAppendMaxP) {

@@ -322,7 +322,8 @@ class WanNSAAR(WanNSABase):
     @torch.no_grad()
     def prefill(self, n_chunks: int, seed: int = 1, student_t: bool = False):
         """Chunks 0..n_chunks-1 of every layer from seeded random K/V (N(0,1), or Student-t with
-        4 degrees of freedom), flushing after each chunk like the AR loop."""
+        4 degrees of freedom), flushing after each chunk like the AR loop and waiting for each
+        flush's copies before the next chunk's appends."""
         cfg, cache = self.cfg, self.cache
         g = torch.Generator(device=self.device).manual_seed(seed)
         shape = (1, cfg.chunk_tokens, cfg.heads, cfg.head_dim)
@@ -338,3 +339,6 @@ class WanNSAAR(WanNSABase):
                     kv = torch.randn((2,) + shape, generator=g, device=self.device).to(self.dtype)
                 cache.append(layer, kv[0], kv[1], cid)
             cache.flush()
+            # a flush's copies run beside the next chunk's work; here that is only the next
+            # chunk's appends, so let them land first
+            torch.cuda.synchronize(self.device)
