@@ -953,3 +953,67 @@ def test_async_flush_matches_resident_cache(dtype):
         assert all(torch.equal(x, y) for x, y in same), (l, h, c)
     full.close()
     small.close()
+
+
+def test_async_flush_pending_moves_with_snapshots_reset_and_evict_all():
+    """Operations that meet an asynchronous flush's pending moves commit them first: a snapshot
+    taken while units are moving, its restore after further flushes, evict_all, and reset; the
+    bytes read back stay those written, and slots balance after each step."""
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(83)
+    L, H, D, C, P, n, W = 2, 2, 128, 500, 64, 9, 1
+    cache = PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P, hbm_slots=L * H * 5,
+                         host_slots=L * H * n, window_chunks=W, keep_window_kv=False)
+    assert cache._async_ok()
+    data = {}
+
+    def write(l, c):
+        k, v = _chunk(g, C, H, D, 0.3), _chunk(g, C, H, D, 1.0)
+        data[(l, c)] = (k, v)
+        cache.append(l, k.to(DEV), v.to(DEV), c)
+
+    def check(upto):
+        for l in range(L):
+            for c in range(upto):
+                k, v = data[(l, c)]
+                for h in range(H):
+                    uk, uv = cache.read_unit(l, h, c)[:2]
+                    want_k = _pages(k[0, :, h].float().numpy(), C, P)
+                    want_v = _pages(v[0, :, h].float().numpy(), C, P)
+                    assert np.array_equal(uk.float().numpy().reshape(want_k.shape), want_k), (l, h, c)
+                    assert np.array_equal(uv.float().numpy().reshape(want_v.shape), want_v), (l, h, c)
+
+    for c in range(6):
+        for l in range(L):
+            write(l, c)
+        cache.flush()
+    assert cache._moves is not None            # this flush's evictions are still pending
+    snap = cache.snapshot_chunks(1, 3)         # commits them first
+    assert cache._moves is None
+    _slots_balance(cache)
+    old = {key: data[key] for key in data if key[1] in (1, 2)}
+    for c in (1, 2):                           # rewrite the snapshotted chunks
+        for l in range(L):
+            write(l, c)
+    for l in range(L):
+        write(l, 6)
+    cache.flush()
+    assert cache._moves is not None
+    cache.restore_chunks(snap, 1)              # commits, then restores
+    assert cache._moves is None
+    data.update(old)
+    _slots_balance(cache)
+    check(7)
+    cache.flush()
+    cache.evict_all()                          # commits, then moves everything to the host
+    assert cache._moves is None
+    assert all(cache.where(l, h, c) == "host" for l in range(L) for h in range(H) for c in range(7))
+    _slots_balance(cache)
+    check(7)
+    for l in range(L):
+        write(l, 7)
+    cache.flush()
+    cache.reset()                              # waits for any copies in flight, forgets all
+    assert cache._moves is None and all(nc == 0 for nc in cache.n_chunks)
+    _slots_balance(cache)
+    cache.close()
