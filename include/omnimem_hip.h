@@ -41,6 +41,12 @@
  *                              (nsa/ops/selection/padded_ptr/wrapper.py:458-553) over the paged
  *                              cache, with int32 unit slots instead of raw int64 addresses
  *   omm_sel_fwd_paged_gated <- the same, with the branch mix of causal_wan_nsa_model.py:541-546
+ *   omm_sel_fwd_gated       <- sel_fwd with that branch mix, for the full-sequence branch
+ *                              (causal_wan_nsa_model.py:391-458, 541-546)
+ *   omm_paged_stage         <- the reload of missing blocks before a selection
+ *                              (padded_ptr/wrapper.py:268-361), per page on a side stream
+ *   omm_copy_units_async    <- flush_offload's D2H copies (models/cache.py:1086-1117) on the
+ *                              copy engines
  *   omm_host_alloc / _free  <- MMCache's pinned offload buffers (models/cache.py:970-1016)
  *   omm_topk_fused_noalloc, omm_topk_fused_debug: no reference counterpart (callers that cannot
  *                              allocate; a test hook that also returns the scores)
@@ -233,6 +239,18 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 const omm_view4* ids, int32_t dtype, int32_t block_size, int32_t chunk_size,
                 int32_t causal, int32_t group_size, float scale, const omm_view4* out,
                 float* lse, void* stream);
+/* The same selection (bf16 only) with the NSA branch mix of causal_wan_nsa_model.py:541-546 in
+ * its epilogue, for the full-sequence branch (:391-458):
+ *   out = g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa
+ * in fp32 from the unrounded o_slc, one rounding to bf16.  gates: bf16 [B, M, H, 3] (after the
+ * clamp and sigmoid); o_cmp, o_swa: bf16 of q's shape, unit dim stride, 16-byte aligned rows;
+ * out must not overlap them.  lse stays that of the selection alone.  Needs the MFMA path (head
+ * dim 64 or 128, 16-byte q / out rows, a finite non-zero scale), else OMM_EUNSUPPORTED. */
+int omm_sel_fwd_gated(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                      const omm_view4* ids, int32_t block_size, int32_t chunk_size,
+                      int32_t causal, int32_t group_size, float scale, const omm_view4* gates,
+                      const omm_view4* o_cmp, const omm_view4* o_swa, const omm_view4* out,
+                      float* lse, void* stream);
 /* ---- selection attention backward, dense K/V -------------------------------------------- */
 /* Reference: torch.ops.omnimem_nsa.sel_bwd (bindings.cpp:25-28, ops.h:38-43,
  * selection_bwd.cu:1329-1407) and the inverted index it builds (inverted_index.cu:103-177).

@@ -1333,7 +1333,7 @@ int check_q_out(const char* op, const omm_view4* q, const omm_view4* out) {
 template <typename QT>
 int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, const omm_view4& ids,
                   int bs, int chunk, bool causal, int G, float scale, const omm_view4& out,
-                  float* lse, hipStream_t s) {
+                  float* lse, hipStream_t s, const GateArgs& gate = GateArgs{}) {
   Geom gm;
   int rc = geom(q, ids.size[1], ids.size[3], G, gm);
   if (rc) return rc;
@@ -1364,7 +1364,40 @@ int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, co
               "selection attention: k and v need the same dim stride");
   const int64_t row_bytes = 2 * (k.stride[1] > v.stride[1] ? k.stride[1] : v.stride[1]);
   return dispatch<QT>(gm, q, out, lse, acc, causal ? chunk : 1, scale, mfma, k.stride[3],
-                      row_bytes, s);
+                      row_bytes, s, gate);
+}
+
+// The gate views of a gated call against q and out: gates [B, M, H, 3] bf16, o_cmp / o_swa of q's
+// shape with unit dim stride and 16-byte rows; out may not overlap o_cmp or o_swa unless it is
+// the very same view and `same_ok` (an epilogue that reads each element before writing it).
+int gate_args(const char* op, const omm_view4* q, const omm_view4* gates, const omm_view4* o_cmp,
+              const omm_view4* o_swa, const omm_view4* out, bool same_ok, GateArgs& ga) {
+  OMM_REQUIRE(q != nullptr && out != nullptr && gates != nullptr && o_cmp != nullptr &&
+                  o_swa != nullptr, OMM_EINVAL, "%s: null argument", op);
+  OMM_REQUIRE(gates->size[0] == q->size[0] && gates->size[1] == q->size[1] &&
+                  gates->size[2] == q->size[2] && gates->size[3] == 3,
+              OMM_EINVAL, "%s: gates must be [B, M, H, 3]", op);
+  for (const omm_view4* o : {o_cmp, o_swa}) {
+    for (int i = 0; i < 4; ++i)
+      OMM_REQUIRE(o->size[i] == q->size[i], OMM_EINVAL, "%s: o_cmp / o_swa must have q's shape", op);
+    OMM_REQUIRE(o->stride[3] == 1 && o->stride[0] % 8 == 0 && o->stride[1] % 8 == 0 &&
+                    o->stride[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(o->data) & 15u) == 0,
+                OMM_EUNSUPPORTED,
+                "%s: o_cmp / o_swa need unit dim stride and 16-byte aligned rows", op);
+    const bool same = o->data == out->data && o->stride[0] == out->stride[0] &&
+                      o->stride[1] == out->stride[1] && o->stride[2] == out->stride[2] &&
+                      o->stride[3] == out->stride[3];
+    if (views_overlap(*o, *out, 2))
+      OMM_REQUIRE(same && same_ok, OMM_EINVAL, "%s: out overlaps o_cmp or o_swa", op);
+  }
+  ga.g = static_cast<const bf16_t*>(gates->data);
+  ga.gs0 = gates->stride[0]; ga.gs1 = gates->stride[1]; ga.gs2 = gates->stride[2];
+  ga.gs3 = gates->stride[3];
+  ga.oc = static_cast<const bf16_t*>(o_cmp->data);
+  ga.cs0 = o_cmp->stride[0]; ga.cs1 = o_cmp->stride[1]; ga.cs2 = o_cmp->stride[2];
+  ga.ow = static_cast<const bf16_t*>(o_swa->data);
+  ga.ws0 = o_swa->stride[0]; ga.ws1 = o_swa->stride[1]; ga.ws2 = o_swa->stride[2];
+  return OMM_OK;
 }
 
 }  // namespace
@@ -1404,6 +1437,40 @@ extern "C" int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_vie
                                   scale, *out, lse, s);
     default: return set_error(OMM_EINVAL, "omm_sel_fwd: unsupported dtype %d", dtype);
   }
+}
+
+extern "C" int omm_sel_fwd_gated(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                                 const omm_view4* ids, int32_t block_size, int32_t chunk_size,
+                                 int32_t causal, int32_t group_size, float scale,
+                                 const omm_view4* gates, const omm_view4* o_cmp,
+                                 const omm_view4* o_swa, const omm_view4* out, float* lse,
+                                 void* stream) {
+  using namespace omm;
+  int rc = check_q_out("omm_sel_fwd_gated", q, out);
+  if (rc) return rc;
+  GateArgs ga;
+  // the register-staged fallback mixes in a second pass after writing out: no overlap at all
+  rc = gate_args("omm_sel_fwd_gated", q, gates, o_cmp, o_swa, out, false, ga);
+  if (rc) return rc;
+  OMM_REQUIRE(k != nullptr && v != nullptr && ids != nullptr, OMM_EINVAL,
+              "omm_sel_fwd_gated: null view");
+  const int64_t B = q->size[0], M = q->size[1], H = q->size[2], D = q->size[3];
+  for (int i = 0; i < 4; ++i)
+    OMM_REQUIRE(k->size[i] == v->size[i], OMM_EINVAL,
+                "omm_sel_fwd_gated: k and v must have the same shape");
+  OMM_REQUIRE(k->size[0] == B && k->size[2] == H && k->size[3] == D, OMM_EINVAL,
+              "omm_sel_fwd_gated: expected k/v [B,N,H,D] compatible with q");
+  OMM_REQUIRE(group_size >= 1 && block_size >= 1 && chunk_size >= 1, OMM_EINVAL,
+              "omm_sel_fwd_gated: group_size, block_size and chunk_size must be >= 1");
+  const int64_t MG = cdiv64(M, group_size);
+  OMM_REQUIRE(ids->size[0] == B && ids->size[1] == MG && ids->size[2] == H && ids->size[3] >= 1,
+              OMM_EINVAL, "omm_sel_fwd_gated: block_indices must be [%lld,%lld,%lld,T>=1]",
+              (long long)B, (long long)MG, (long long)H);
+  OMM_REQUIRE(k->size[1] <= 2147483647ll && M <= 2147483647ll, OMM_EUNSUPPORTED,
+              "omm_sel_fwd_gated: too long");
+  if (B == 0 || M == 0 || H == 0) return OMM_OK;
+  return sel_fwd_typed<bf16_t>(*q, *k, *v, *ids, block_size, chunk_size, causal != 0, group_size,
+                               scale, *out, lse, static_cast<hipStream_t>(stream), ga);
 }
 
 extern "C" int omm_sel_fwd_ptr(const omm_view4* q, const int64_t* ptr_k, const int64_t* ptr_v,
@@ -1522,41 +1589,12 @@ extern "C" int omm_sel_fwd_paged_gated(const omm_view4* q, const omm_view4* ids,
                                        const omm_view4* o_swa, const omm_view4* out, float* lse,
                                        int32_t epoch, void* stream) {
   using namespace omm;
-  OMM_REQUIRE(q != nullptr && gates != nullptr && o_cmp != nullptr && o_swa != nullptr,
-              OMM_EINVAL, "omm_sel_fwd_paged_gated: null argument");
-  OMM_REQUIRE(gates->size[0] == q->size[0] && gates->size[1] == q->size[1] &&
-                  gates->size[2] == q->size[2] && gates->size[3] == 3,
-              OMM_EINVAL, "omm_sel_fwd_paged_gated: gates must be [B, M, H, 3]");
-  for (const omm_view4* o : {o_cmp, o_swa}) {
-    for (int i = 0; i < 4; ++i)
-      OMM_REQUIRE(o->size[i] == q->size[i], OMM_EINVAL,
-                  "omm_sel_fwd_paged_gated: o_cmp / o_swa must have q's shape");
-    OMM_REQUIRE(o->stride[3] == 1 && o->stride[0] % 8 == 0 && o->stride[1] % 8 == 0 &&
-                    o->stride[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(o->data) & 15u) == 0,
-                OMM_EUNSUPPORTED,
-                "omm_sel_fwd_paged_gated: o_cmp / o_swa need unit dim stride and 16-byte "
-                "aligned rows");
-  }
-  // out against the branches it mixes: the bf16 epilogue reads each element before the same
-  // thread writes it, so the identical view is safe there; the fp8 cache's first pass writes out
-  // before the mix pass reads the branches
-  OMM_REQUIRE(out != nullptr && kv != nullptr, OMM_EINVAL, "omm_sel_fwd_paged_gated: null argument");
-  for (const omm_view4* o : {o_cmp, o_swa}) {
-    const bool same = o->data == out->data && o->stride[0] == out->stride[0] &&
-                      o->stride[1] == out->stride[1] && o->stride[2] == out->stride[2] &&
-                      o->stride[3] == out->stride[3];
-    if (views_overlap(*o, *out, 2))
-      OMM_REQUIRE(same && kv->dtype == OMM_BF16, OMM_EINVAL,
-                  "omm_sel_fwd_paged_gated: out overlaps o_cmp or o_swa (only a bf16 cache "
-                  "accepts out as the very same view)");
-  }
+  OMM_REQUIRE(kv != nullptr, OMM_EINVAL, "omm_sel_fwd_paged_gated: null argument");
+  // the bf16 epilogue reads each element before the same thread writes it, so the identical view
+  // is safe there; the fp8 cache's first pass writes out before the mix pass reads the branches
   GateArgs ga;
-  ga.g = static_cast<const bf16_t*>(gates->data);
-  ga.gs0 = gates->stride[0]; ga.gs1 = gates->stride[1]; ga.gs2 = gates->stride[2];
-  ga.gs3 = gates->stride[3];
-  ga.oc = static_cast<const bf16_t*>(o_cmp->data);
-  ga.cs0 = o_cmp->stride[0]; ga.cs1 = o_cmp->stride[1]; ga.cs2 = o_cmp->stride[2];
-  ga.ow = static_cast<const bf16_t*>(o_swa->data);
-  ga.ws0 = o_swa->stride[0]; ga.ws1 = o_swa->stride[1]; ga.ws2 = o_swa->stride[2];
+  const int rc = gate_args("omm_sel_fwd_paged_gated", q, gates, o_cmp, o_swa, out,
+                           kv->dtype == OMM_BF16, ga);
+  if (rc) return rc;
   return sel_fwd_paged_impl(q, ids, kv, group_size, scale, out, lse, epoch, stream, ga);
 }

@@ -18,7 +18,7 @@ import torch
 from . import _lib, ops
 from .backend import NSABackendError, get_backend
 
-__all__ = ["selection_attention", "sel_fwd", "sel_bwd", "dense_attention"]
+__all__ = ["selection_attention", "sel_fwd", "sel_fwd_gated", "sel_bwd", "dense_attention"]
 
 
 def _debug_checks_enabled() -> bool:
@@ -105,6 +105,32 @@ def _sel_fwd_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indic
               int(group_size), float(scale), _lib.view4(out), lse.data_ptr() if lse.numel() else None,
               _lib.stream_of(q))
     return out, lse
+
+
+def sel_fwd_gated(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                  block_size: int, chunk_size: int, scale: float, causal: bool, group_size: int,
+                  gates: torch.Tensor, o_cmp: torch.Tensor, o_swa: torch.Tensor,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``sel_fwd`` with the NSA branch mix in the kernel's epilogue (bf16): returns
+    ``g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa`` computed in fp32 from the
+    unrounded selection output o_slc and rounded once, as the full-sequence branch of
+    causal_wan_nsa_model.py:391-458 combines them (:541-546).  gates: bf16 [B, M, H, 3] after the
+    clamp and sigmoid; o_cmp / o_swa: bf16 like q; ``out`` must not overlap them."""
+    _lib.require_cuda((q, "q"), (k, "k"), (v, "v"), (block_indices, "block_indices"),
+                      (gates, "gates"), (o_cmp, "o_cmp"), (o_swa, "o_swa"))
+    for name, t in (("q", q), ("k", k), ("v", v), ("gates", gates), ("o_cmp", o_cmp),
+                    ("o_swa", o_swa)):
+        if t.dtype != torch.bfloat16:
+            raise NSABackendError(f"sel_fwd_gated: {name} must be bf16, got {t.dtype}")
+    if block_indices.dtype != torch.int32:
+        block_indices = block_indices.to(torch.int32)
+    if out is None:
+        out = torch.empty_like(q)
+    _lib.call("omm_sel_fwd_gated", _lib.view4(q), _lib.view4(k), _lib.view4(v),
+              _lib.view4(block_indices), int(block_size), int(chunk_size), int(bool(causal)),
+              int(group_size), float(scale), _lib.view4(gates), _lib.view4(o_cmp),
+              _lib.view4(o_swa), _lib.view4(out), None, _lib.stream_of(q))
+    return out
 
 
 def sel_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,

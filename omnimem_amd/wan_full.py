@@ -17,12 +17,14 @@ with the full-sequence branch of the reference's NSA self-attention
 * sliding-window attention o_swa over the chunks c - window + 1 .. c (block-causal by chunk, the
   window block mask), one dense call per chunk;
 * top-k selection with the causal chunk mask (``parallel_nsa_topk``, groups of 64 queries) and
-  selection attention (``sel_fwd``, causal by chunk) -- the config-3 hot path;
-* the sigmoid-gated mix g_cmp o_cmp + g_slc o_slc + g_swa o_swa and the output projection.
+  selection attention causal by chunk -- the config-3 hot path -- with the sigmoid-gated mix
+  g_cmp o_cmp + g_slc o_slc + g_swa o_swa in its epilogue (``sel_fwd_gated``);
+* the output projection.
 
 ``forward(latents, t)`` returns the head output; ``timers`` (as in ``WanNSAAR``) break the time
-down by category, and ``sel_events`` collects one event pair per selection call so that the
-selection kernel's own time can be summed over the 30 layers.
+down by category, and ``sel_events`` collects one event pair per selection call (the gated one:
+the mix is part of its epilogue) so that the selection kernel's own time can be summed over the
+30 layers.
 """
 from __future__ import annotations
 
@@ -33,7 +35,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .index_topk import block_pool, parallel_nsa_topk
-from .selection import dense_attention, sel_fwd
+from .selection import dense_attention, sel_fwd, sel_fwd_gated
 from .wan_ar import WanARConfig, WanNSABase, _Block
 
 __all__ = ["WanNSAFull"]
@@ -76,17 +78,6 @@ class WanNSAFull(WanNSABase):
         ids = parallel_nsa_topk(q, k_cmp, cfg.topk, block_size=BS, chunk_size=C, causal=True,
                                 group_size=G)
         self._toc(tk)
-        tk = self._tic("sel_attn")
-        ev = None
-        if self.sel_events is not None:
-            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            ev[0].record()
-        o_slc, _ = sel_fwd(q, k, v, ids, BS, C, scale, True, G)
-        if ev is not None:
-            ev[1].record()
-            self.sel_events.append(ev)
-            self.sel_ids.append(ids)
-        self._toc(tk)
         tk = self._tic("attn_cmp")
         o_cmp = torch.empty_like(q)
         n_cmp = k_cmp.shape[1]
@@ -102,15 +93,23 @@ class WanNSAFull(WanNSABase):
             lo = max(0, c - W + 1) * C
             dense_attention(q[:, a:b], k[:, lo:b], v[:, lo:b], scale=scale, out=o_swa[:, a:b])
         self._toc(tk)
-        tk = self._tic("mix")
-        gf = g.float()
-        o = (gf[..., 0:1] * o_cmp.float() + gf[..., 1:2] * o_slc.float()
-             + gf[..., 2:3] * o_swa.float()).to(q.dtype)
+        tk = self._tic("sel_attn")
+        ev = None
+        if self.sel_events is not None:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+        # selection with the branch mix in its epilogue
+        o = sel_fwd_gated(q, k, v, ids, BS, C, scale, True, G, g, o_cmp, o_swa)
+        if ev is not None:
+            ev[1].record()
+            self.sel_events.append(ev)
+            self.sel_ids.append(ids)
         self._toc(tk)
         if self.trace is not None and layer == self.trace_layer:
+            o_slc, _ = sel_fwd(q, k, v, ids, BS, C, scale, True, G)  # the branch alone
             self.trace.update(q=q.clone(), k=k.clone(), v=v.clone(), g=g.clone(),
                               ids=ids.clone(), o_cmp=o_cmp.clone(), o_swa=o_swa.clone(),
-                              o_slc=o_slc.clone(), o=o.clone())
+                              o_slc=o_slc, o=o.clone())
         tk = self._tic("linear")
         out = F.linear(o.flatten(2), *blk.o)
         self._toc(tk)

@@ -246,3 +246,67 @@ def test_empty_shapes():
     ids_any = torch.zeros((1, 2, H, 4), dtype=torch.int32, device=DEV)
     out, lse = sel_fwd(q, k0, k0, ids_any, 64, 1, D ** -0.5, False, 64)
     assert bool((out == 0).all()) and bool(torch.isneginf(lse).all())
+
+
+@pytest.mark.parametrize("case", [
+    # M, N, H, D, G, BS, T, causal, chunk
+    (300, 700, 3, 128, 64, 64, 6, True, 256),   # 2-wave DMA kernel, ragged last group
+    (400, 512, 2, 128, 192, 64, 5, True, 256),  # 4-wave DMA kernel (two subgroups)
+    (130, 256, 2, 64, 64, 32, 5, False, 1),     # head dim 64
+])
+def test_sel_fwd_gated_mix_matches_float64(case):
+    """Dense selection with the NSA branch mix in its epilogue (causal_wan_nsa_model.py:541-546):
+    out = g0 o_cmp + g1 o_slc + g2 o_swa against float64 from the oracle's o_slc, at the bf16
+    tolerances."""
+    from omnimem_amd.selection import sel_fwd_gated
+    M, N, H, D, G, BS, T, causal, chunk = case
+    gen = torch.Generator().manual_seed(M + 7 * N)
+    dt = torch.bfloat16
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(dt)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(dt)
+    v = torch.randn((1, N, H, D), generator=gen).to(dt)
+    oc = torch.randn((1, M, H, D), generator=gen).to(dt)
+    ow = torch.randn((1, M, H, D), generator=gen).to(dt)
+    g = torch.sigmoid(torch.randn((1, M, H, 3), generator=gen)).to(dt)
+    ids = _ids(gen, 1, -(-M // G), H, T, -(-N // BS))
+    out = sel_fwd_gated(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), BS, chunk, D ** -0.5, causal,
+                        G, g.to(DEV), oc.to(DEV), ow.to(DEV))
+    want_slc, _ = O.selection_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                        ids.numpy(), G, D ** -0.5,
+                                        O.dense_block_tokens(N, BS, chunk, causal),
+                                        chunk_size=chunk, causal=causal)
+    gg = g.double().numpy()
+    want = (gg[..., 0:1] * oc.double().numpy() + gg[..., 1:2] * want_slc
+            + gg[..., 2:3] * ow.double().numpy())
+    err = np.abs(out.double().cpu().numpy() - want)
+    assert err.max() <= 2e-2, f"max-abs {err.max():.3e}"
+    assert err.mean() <= 1e-3, f"mean-abs {err.mean():.3e}"
+
+
+def test_sel_fwd_gated_rejects_overlap_and_bad_inputs():
+    """out may not be or overlap o_cmp / o_swa (the fallback kernel mixes in a second pass after
+    writing out); the gated call is bf16 only, with gates [B, M, H, 3]."""
+    from omnimem_amd.backend import NSABackendError
+    from omnimem_amd.selection import sel_fwd_gated
+    M, N, H, D, G, BS = 128, 256, 2, 128, 64, 64
+    dt = torch.bfloat16
+    q = torch.randn((1, M, H, D), device=DEV).to(dt)
+    k = torch.randn((1, N, H, D), device=DEV).to(dt)
+    oc, ow = torch.randn_like(q), torch.randn_like(q)
+    g = torch.rand((1, M, H, 3), device=DEV).to(dt)
+    ids = torch.zeros((1, 2, H, 2), dtype=torch.int32, device=DEV)
+    ids[..., 1] = 1
+
+    def call(q_=q, g_=g, oc_=oc, ow_=ow, out=None):
+        return sel_fwd_gated(q_, k.to(q_.dtype), k.to(q_.dtype), ids, BS, 1, D ** -0.5, False, G,
+                             g_, oc_, ow_, out=out)
+
+    buf = torch.empty((1, M + 1, H, D), dtype=dt, device=DEV)
+    for kw in ({"out": oc}, {"out": ow}, {"oc_": buf[:, :M], "out": buf[:, 1:]}):
+        with pytest.raises(NSABackendError, match="overlap"):
+            call(**kw)
+    with pytest.raises(NSABackendError, match="bf16"):
+        call(q_=q.float())
+    with pytest.raises(NSABackendError, match="gates"):
+        call(g_=torch.rand((1, M, H, 2), device=DEV).to(dt))
+    assert torch.isfinite(call().float()).all()
