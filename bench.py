@@ -590,7 +590,8 @@ def run_config3_forward(frames: int = 21):
     """Config 3: the 30-layer full-sequence Wan2.1-1.3B NSA forward (omnimem_amd/wan_full.py) on
     seeded latents of one 81-frame 480x832 clip (32760 tokens), random-init weights.  One warm-up
     forward, then one timed forward with per-category event timers and an event pair around each
-    layer's selection call; selection TFLOP/s = useful FLOPs of the 30 calls / their summed time."""
+    layer's selection call (with the branch mix in its epilogue); selection TFLOP/s = useful
+    selection FLOPs of the 30 calls / their summed time."""
     import torch
     from omnimem_amd.wan_ar import WanARConfig
     from omnimem_amd.wan_full import WanNSAFull
@@ -625,7 +626,10 @@ def run_config3_forward(frames: int = 21):
            "selection_frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
            "breakdown_ms_per_forward": cats,
            "setup_s": round(t_init, 1),
-           "timing": "one forward after one warm-up; selection events around each sel_fwd"}
+           "timing": "one forward after one warm-up; selection events around each layer's "
+                     "sel_fwd_gated call, whose epilogue also mixes the three branches (the "
+                     "mix's reads of o_cmp, o_swa and the gates are inside the selection time; "
+                     "the selection alone is the top-level roofline)"}
     del model
     torch.cuda.empty_cache()
     return res
