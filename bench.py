@@ -95,7 +95,8 @@ ALGO = {
 }
 # config 1 (bench.py --c1-only): useful FLOPs of the seeded fp32 call, counted from its ids by
 # useful_flops (the queries as the last frame: every selected block visible)
-ALGO["c1"] = {"sel_fwd_f32mfma_kernel<DenseAcc<float>, 128>": ("flops_fp32", 9602498560)}
+ALGO["c1"] = {"sel_fwd_f32mfma_kernel<DenseAcc<float>, 128>": ("flops_fp32", 9602498560),
+             "sel_fwd_f32split_kernel<DenseAcc<float>, 128>": ("flops_fp32", 9602498560)}
 # kernels one call launches together, priced as a whole: the AR top-k (query pooling into the
 # workspace, split scoring + selection, merge) reads the chunk's q and the pooled history
 ALGO_GROUPS = {
@@ -105,6 +106,13 @@ ALGO_GROUPS = {
              "topk_merge_kernel"],
             "bytes", _AR_C * H * D * 2 + _AR_HIST * _AR_PPC * H * D * 2
             + _AR_PPC * H * TOPK * 4),
+    },
+    # the split fp32 call: equal runs of selected blocks per workgroup, then the merge of the
+    # split items' records
+    "c1": {
+        "config-1 call (f32split + f32merge)": (
+            ["sel_fwd_f32split_kernel<DenseAcc<float>, 128>", "sel_fwd_f32merge_kernel<128>"],
+            "flops_fp32", 9602498560),
     },
 }
 
@@ -262,6 +270,12 @@ def rocprof_summary(out: str, d: str, command: str, workload: str = "c3"):
     for gname, (members, unit, amount) in ALGO_GROUPS.get(workload, {}).items():
         if all(m in kernels for m in members):
             us = sum(kernels[m]["avg_us"] for m in members)
+            if unit == "flops_fp32":
+                groups[gname] = {"avg_us_sum": round(us, 2), "useful_flops": amount,
+                                 "useful_TFLOPs": round(amount / (us * 1e6), 1),
+                                 "frac_fp32_peak": round(amount / (us * 1e6) / PEAK_FP32_TFLOPS,
+                                                         4)}
+                continue
             groups[gname] = {"avg_us_sum": round(us, 2), "algorithmic_bytes": amount,
                              "algorithmic_GBps": round(amount / (us * 1e3), 1),
                              "frac_hbm_8TBps": round(amount / (us * 1e3) / PEAK_HBM_GBS, 4)}
@@ -298,6 +312,10 @@ def summary_md(res: dict, path: str):
                      f"{ach} | {frac} |" if "hbm_bytes_scaled" in k else
                      f"| `{shown}` | {k['calls']} | {k['avg_us']} |  |  | {alg} | {ach} | {frac} |")
     for gname, g in groups.items():
+        if "useful_flops" in g:
+            lines.append(f"| {gname} | | {g['avg_us_sum']} | | | {g['useful_flops']:,} FLOP | "
+                         f"{g['useful_TFLOPs']} TFLOP/s | {g['frac_fp32_peak']} |")
+            continue
         lines.append(f"| {gname} | | {g['avg_us_sum']} | | | {g['algorithmic_bytes']:,} B | "
                      f"{g['algorithmic_GBps']} GB/s | {g['frac_hbm_8TBps']} |")
     derived = ("mfma_bf16_executed_TFLOPs", "mfma_bf16_executed_frac_peak", "mfma_busy_share",
@@ -554,8 +572,9 @@ def cpu_baseline_ar(history: int = 80, q_small: int = 64, q_large: int = 256):
 def run_config1(steps: int):
     """Config 1: one fp32 selection call, q [1,1560,12,128], k / v [1,4680,12,128] ~ N(0,1)/sqrt(128),
     64-token blocks, groups of 64, top-16 over 1560-token frame chunks, the queries read as the
-    last frame (all three frames are candidates).  The attention kernel alone, timed with events
-    over back-to-back launches; useful FLOPs counted from the ids as for config 3."""
+    last frame (all three frames are candidates).  The attention call alone (its split and
+    merge kernels), timed with events over back-to-back calls; useful FLOPs counted from the ids
+    as for config 3."""
     import torch
     from omnimem_amd.index_topk import block_pool, parallel_nsa_topk
     from omnimem_amd.selection import sel_fwd
@@ -580,7 +599,10 @@ def run_config1(steps: int):
     tf = flops / (ms * 1e-3) / 1e12
     return {"workload": "config 1: fp32 q [1,1560,12,128], k/v [1,4680,12,128], top-16 of "
                         "64-token blocks, groups of 64, queries as the last 1560-token frame",
-            "kernel": "sel_fwd_f32mfma_kernel (fp32 MFMA, v_mfma_f32_16x16x4_f32)", "ms": round(ms, 4),
+            "kernel": "sel_fwd_f32split_kernel + sel_fwd_f32merge_kernel (fp32 MFMA, "
+                      "v_mfma_f32_16x16x4_f32; the 300 (group, head) items' selected blocks cut "
+                      "into 2 equal runs per CU, split items merged in a second pass)",
+            "ms": round(ms, 4),
             "useful_flops": int(flops), "useful_gflop": round(flops / 1e9, 3), "useful_tflops": round(tf, 3),
             "peak_fp32_tflops": PEAK_FP32_TFLOPS, "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4),
             "timing": "--steps back-to-back launches, HIP events"}

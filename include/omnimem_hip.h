@@ -20,6 +20,8 @@
  *                              in, indices out, so bit-exactness is testable on identical scores
  *   omm_sel_fwd             <- torch.ops.omnimem_nsa.sel_fwd (bindings.cpp:16-19, ops.h:25-29,
  *                              selection_fwd.cu:934-966)
+ *   omm_sel_fwd_ws          <- the same op with a workspace for the split fp32 path (the
+ *                              reference's fp32 kernel takes none: selection_fwd.cu:820-932)
  *   omm_sel_bwd             <- torch.ops.omnimem_nsa.sel_bwd (bindings.cpp:25-28, ops.h:38-43,
  *                              selection_bwd.cu:1329-1407) with its inverted index
  *                              (inverted_index.cu:103-177)
@@ -239,6 +241,21 @@ int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 const omm_view4* ids, int32_t dtype, int32_t block_size, int32_t chunk_size,
                 int32_t causal, int32_t group_size, float scale, const omm_view4* out,
                 float* lse, void* stream);
+/* omm_sel_fwd with a device workspace (same reference op; the workspace is this library's own).
+ * An f32 call with few (b, query group, head) items for the current device's CUs splits its
+ * selected blocks into equal runs, one per workgroup, and merges the split items' partial
+ * results in a second pass through the workspace: all CUs get the same work (config 1:
+ * 300 items on 256 CUs).  omm_sel_fwd_workspace_bytes gives the size for a call (ids [B, MG, H,
+ * T]); 0 means no split, and so does a NULL or smaller workspace: then the call is
+ * omm_sel_fwd.  The workspace is 16-byte aligned, must not overlap the other arguments, and is
+ * in use until the call's work on the stream ends; nothing in it needs to start at zero.
+ * Results agree with omm_sel_fwd's within fp32 rounding (the sums run in another order). */
+size_t omm_sel_fwd_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t D, int64_t T,
+                                   int32_t dtype, int32_t group_size);
+int omm_sel_fwd_ws(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                   const omm_view4* ids, int32_t dtype, int32_t block_size, int32_t chunk_size,
+                   int32_t causal, int32_t group_size, float scale, const omm_view4* out,
+                   float* lse, void* workspace, size_t workspace_bytes, void* stream);
 /* The same selection (bf16 only) with the NSA branch mix of causal_wan_nsa_model.py:541-546 in
  * its epilogue, for the full-sequence branch (:391-458):
  *   out = g[..., 0] * o_cmp + g[..., 1] * o_slc + g[..., 2] * o_swa

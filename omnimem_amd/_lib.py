@@ -80,6 +80,9 @@ PROTOTYPES = {
     "omm_topk_fused_noalloc": (_i32, [_V, _V, _i32, _i32, _i32, _f32, _M, _vp, _vp]),
     "omm_topk_from_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _M, _vp, _vp, _sz, _vp]),
     "omm_sel_fwd": (_i32, [_V, _V, _V, _V, _i32, _i32, _i32, _i32, _i32, _f32, _V, _vp, _vp]),
+    "omm_sel_fwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
+    "omm_sel_fwd_ws": (_i32, [_V, _V, _V, _V, _i32, _i32, _i32, _i32, _i32, _f32, _V, _vp, _vp, _sz,
+                              _vp]),
     "omm_sel_fwd_gated": (_i32, [_V, _V, _V, _V, _i32, _i32, _i32, _i32, _f32, _V, _V, _V, _V, _vp,
                                  _vp]),
     "omm_sel_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32, _i64]),

@@ -424,11 +424,16 @@ struct WaveWalk {
     }
   }
   __device__ __forceinline__ void start(const Acc& acc, int b, int g, int h, int T, int qc) {
-    base = 0;
+    start_at(acc, b, g, h, 0, T, qc);
+  }
+  // walk only the slots [lo, hi) of the row (advance() then takes hi as its T)
+  __device__ __forceinline__ void start_at(const Acc& acc, int b, int g, int h, int lo, int hi,
+                                           int qc) {
+    base = lo;
     valid = false;
-    if (T <= 0) return;
-    fill(acc, b, g, h, T, qc);
-    next_block(acc, b, g, h, T, qc);
+    if (hi <= lo) return;
+    fill(acc, b, g, h, hi, qc);
+    next_block(acc, b, g, h, hi, qc);
   }
   __device__ __forceinline__ void advance(const Acc& acc, int b, int g, int h, int T, int qc) {
     if (tok0 + TK < br.nvalid) {

@@ -14,7 +14,10 @@
 //   sel_fwd_mfma_kernel: register-staged variant for fp8 pages (e4m3 codes widened to bf16
 //   while staging, page scales folded into the softmax) and for row strides the DMA kernel
 //   cannot address.
-// fp32 (and any shape the MFMA kernels do not cover) runs a VALU kernel in full fp32.
+// fp32 with 16-byte rows and head dim 64 or 128 runs sel_fwd_f32mfma_kernel (fp32 MFMA, split
+// into equal runs per CU when the call has few items); any other shape a VALU kernel in full
+// fp32.
+#include <atomic>
 #include <type_traits>
 
 #include "sel_common.h"
@@ -868,23 +871,40 @@ __device__ __forceinline__ void dma_pitch2(const void* base, int rsb, int nrows,
 }
 #pragma clang diagnostic pop
 
+// Split fp32 calls: the B * H * MG items' T slots each, laid end to end (item-major, query group
+// fastest, then head, then batch), are cut into `ranges` equal runs, one per workgroup, so that
+// every CU gets the same number of selected blocks however few items the call has.  A workgroup
+// walks the items its run touches; an item it covers whole is written out directly, a piece of
+// an item is written as a record: per query row the unnormalised o (fp32, relative to m), the
+// log2-domain reference m (-inf when the piece saw no key) and the sum l of its exponentials.  The
+// first piece of run r goes to record 2 r, a later (its last) piece to record 2 r + 1, and
+// sel_fwd_f32merge_kernel combines the records of every split item.
+struct F32Split {
+  float* rec;
+  int64_t units;  // items * T
+  int ranges;     // workgroups, <= units
+};
+
+template <int D>
+constexpr int f32_rec_floats() {  // o [64][D], then (m, l) for 64 rows
+  return 64 * D + 128;
+}
+
+// The item (b, query group g, head h) over its slots [lo, hi): writes out / lse when rec is
+// null, else the piece's record at rec.
 template <typename Acc, int D>
-__global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
-    View4<const float> q, View4<float> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
-    int MG, int T, int chunk, float scale) {
+__device__ __forceinline__ void f32_piece(View4<const float> q, View4<float> out,
+                                          float* __restrict__ lse, const Acc& acc, int M, int H,
+                                          int G, int T, int chunk, float scale, int b, int g, int h,
+                                          int lo, int hi, float* __restrict__ rec, char* lds) {
   using FG = F32Geom<D>;
-  constexpr int ROWB = FG::ROWB, CPR = FG::CPR, TK = FG::TK, RPI = FG::RPI, NT = FG::NT;
+  constexpr int CPR = FG::CPR, TK = FG::TK, RPI = FG::RPI, NT = FG::NT;
   constexpr int DU = FG::DU, PITCH = FG::PITCH;
   constexpr int NI = 8 / kF32Waves;  // copy instructions per wave per K or V tile
   static_assert(NI == 2, "two copy instructions per wave");
-  constexpr int BUF = 8 * PITCH;
-  __shared__ __align__(16) char lds[4 * BUF];  // K buffers 0, 1; V buffers 2, 3
+  constexpr int BUF = 8 * PITCH;  // lds: K buffers 0, 1; V buffers 2, 3
   const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
   const int l16 = lane & 15, j4 = lane >> 4;
-  int wi = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
-  const int g = wi % MG; wi /= MG;
-  const int h = wi % H;
-  const int b = wi / H;
   const int m_end = min(g * G + G, M);
   const int qc = (g * G) / chunk;
   const int mq = g * G + 16 * w + l16;  // this lane's query (column l16 of the wave's block)
@@ -914,7 +934,7 @@ __global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
   float m2 = kNegInf, nms = 0.0f, thr = kNegInf, lsum = 0.0f;
 
   WaveWalk<Acc, TK> wk;
-  wk.start(acc, b, g, h, T, qc);
+  wk.start_at(acc, b, g, h, lo, hi, qc);
   int n_cur = 0;
   int kdo[NI], vdo[NI];
   int rsk = 0, rsv = 0;
@@ -932,7 +952,7 @@ __global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
     dma_pitch2<PITCH>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv,
                       rsv, wk.n, lds + 2 * BUF, w, vdo);
     n_cur = wk.n;
-    wk.advance(acc, b, g, h, T, qc);
+    wk.advance(acc, b, g, h, hi, qc);
   }
   __builtin_amdgcn_s_waitcnt(0);
 
@@ -947,7 +967,7 @@ __global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
       dma_pitch2<PITCH>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv,
                         rsv, wk.n, lds + (2 + (BI ^ 1)) * BUF, w, vdo);
       n_nx = wk.n;
-      wk.advance(acc, b, g, h, T, qc);
+      wk.advance(acc, b, g, h, hi, qc);
     }
     const char* Kt = lds + BI * BUF;
     const char* Vt = lds + (2 + BI) * BUF;
@@ -1033,6 +1053,16 @@ __global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
   float ls = lsum;
   ls += __shfl_xor(ls, 16, kWave);
   ls += __shfl_xor(ls, 32, kWave);
+  if (rec != nullptr) {  // a piece: every row of the record, unnormalised
+    const int row = 16 * w + l16;
+    float* ro = rec + row * D;
+#pragma unroll
+    for (int i = 0; i < DU; ++i)
+      *reinterpret_cast<float4*>(ro + 16 * i + 4 * j4) =
+          make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+    if (j4 == 0) *reinterpret_cast<float2*>(rec + 64 * D + 2 * row) = make_float2(m2, ls);
+    return;
+  }
   if (q_ok) {
     const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
     float* op = out.at(b, mq, h, 0);
@@ -1044,6 +1074,95 @@ __global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
       lse[(static_cast<int64_t>(b) * H + h) * M + mq] =
           ls > 0.0f ? (m2 + __builtin_log2f(ls)) * kLn2 : kNegInf;
   }
+}
+
+// One workgroup per (b, query group, head), launch order remapped so that an XCD's workgroups
+// take consecutive groups of one head.
+template <typename Acc, int D>
+__global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32mfma_kernel(
+    View4<const float> q, View4<float> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale) {
+  __shared__ __align__(16) char lds[4 * 8 * F32Geom<D>::PITCH];
+  int wi = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int g = wi % MG; wi /= MG;
+  const int h = wi % H;
+  const int b = wi / H;
+  f32_piece<Acc, D>(q, out, lse, acc, M, H, G, T, chunk, scale, b, g, h, 0, T, nullptr, lds);
+}
+
+// One workgroup per run of sp.units / sp.ranges slots (see F32Split); consecutive runs on one XCD.
+template <typename Acc, int D>
+__global__ __launch_bounds__(kF32Waves * kWave, 2) void sel_fwd_f32split_kernel(
+    View4<const float> q, View4<float> out, float* __restrict__ lse, Acc acc, int M, int H, int G,
+    int MG, int T, int chunk, float scale, F32Split sp) {
+  __shared__ __align__(16) char lds[4 * 8 * F32Geom<D>::PITCH];
+  const int r = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int64_t u0 = static_cast<int64_t>(r) * sp.units / sp.ranges;
+  const int64_t u1 = static_cast<int64_t>(r + 1) * sp.units / sp.ranges;
+  bool first = true;
+  for (int64_t i = u0 / T; i * T < u1; ++i) {
+    const int lo = static_cast<int>(u0 > i * T ? u0 - i * T : 0);
+    const int hi = static_cast<int>(u1 - i * T < T ? u1 - i * T : T);
+    float* rec = nullptr;
+    if (lo > 0 || hi < T)
+      rec = sp.rec + (2 * static_cast<int64_t>(r) + (first ? 0 : 1)) * f32_rec_floats<D>();
+    if (!first) __syncthreads();  // the previous piece's last tile reads are done everywhere
+    const int g = static_cast<int>(i % MG);
+    const int h = static_cast<int>((i / MG) % H);
+    const int b = static_cast<int>(i / (static_cast<int64_t>(MG) * H));
+    f32_piece<Acc, D>(q, out, lse, acc, M, H, G, T, chunk, scale, b, g, h, lo, hi, rec, lds);
+    first = false;
+  }
+}
+
+// The split items (those whose slots span two or more runs): out = sum_r 2^(m_r - m) o_r /
+// sum_r 2^(m_r - m) l_r over the records r of the item, m = the largest m_r with l_r > 0, and
+// lse = (m + log2 of that sum) ln 2 (0 and -inf when no piece saw a key).  One thread per 4 dims
+// of a query row; workgroup x covers rows RPW (x % (64 / RPW)) .. of item x / (64 / RPW).
+template <int D>
+__global__ __launch_bounds__(256) void sel_fwd_f32merge_kernel(View4<float> out,
+                                                               float* __restrict__ lse, int M,
+                                                               int H, int G, int MG, int T,
+                                                               F32Split sp) {
+  constexpr int REC = f32_rec_floats<D>(), TPR = D / 4, RPW = 256 / TPR, WPI = 64 / RPW;
+  const int64_t i = blockIdx.x / WPI;
+  const int64_t s0 = i * T;
+  auto run_of = [&](int64_t s) {  // r with floor(r U / R) <= s < floor((r + 1) U / R)
+    return ((s + 1) * sp.ranges + sp.units - 1) / sp.units - 1;
+  };
+  const int64_t ra = run_of(s0), rb = run_of(s0 + T - 1);
+  if (ra == rb) return;  // written whole by its run
+  const bool ra_first = ra * sp.units / sp.ranges == s0;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int row = static_cast<int>(blockIdx.x % WPI) * RPW + tid / TPR, c4 = tid % TPR;
+  const int g = static_cast<int>(i % MG);
+  const int h = static_cast<int>((i / MG) % H);
+  const int b = static_cast<int>(i / (static_cast<int64_t>(MG) * H));
+  const int mq = g * G + row;
+  if (row >= G || mq >= M) return;
+  const float* rp = sp.rec + (2 * ra + (ra_first ? 0 : 1)) * REC;
+  float mx = kNegInf, l = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t r = ra; r <= rb; ++r, rp = sp.rec + 2 * r * REC) {
+    const float2 ml = *reinterpret_cast<const float2*>(rp + 64 * D + 2 * row);
+    const float4 x = *reinterpret_cast<const float4*>(rp + row * D + 4 * c4);
+    if (!(ml.y > 0.0f)) continue;
+    if (ml.x > mx) {  // a new reference: rescale what is summed so far
+      const float f = __builtin_amdgcn_exp2f(mx - ml.x);
+      l *= f;
+      acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
+      mx = ml.x;
+    }
+    const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);
+    l += wgt * ml.y;
+    acc.x += wgt * x.x; acc.y += wgt * x.y; acc.z += wgt * x.z; acc.w += wgt * x.w;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  *reinterpret_cast<float4*>(out.at(b, mq, h, 4 * c4)) =
+      make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+  if (lse != nullptr && c4 == 0)
+    lse[(static_cast<int64_t>(b) * H + h) * M + mq] =
+        l > 0.0f ? (mx + __builtin_log2f(l)) * kLn2 : kNegInf;
 }
 
 // ---- VALU kernel (fp32 arithmetic, any head dim <= 256, any strides) -------------------------
@@ -1252,9 +1371,59 @@ int launch_dma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* 
   return check_launch("selection attention (dma)");
 }
 
+// Compute units of the current device (0 when the runtime cannot say), cached per device.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// A split fp32 call runs kF32RunsPerCu equal runs per CU when it has fewer than kF32SplitBelow
+// items per CU (one item per workgroup leaves CUs idle or doubly loaded there: config 1's 300
+// items take as long as 500 on 256 CUs).  0: no split.
+constexpr int kF32RunsPerCu = 2;
+constexpr int kF32SplitBelow = 4;
+
+inline int f32_split_runs(int64_t items, int64_t T) {
+  const int cus = device_cus();
+  if (cus <= 0 || items <= 0 || T <= 0 || items >= int64_t{kF32SplitBelow} * cus) return 0;
+  const int64_t units = items * T;
+  const int64_t runs = int64_t{kF32RunsPerCu} * cus;
+  return static_cast<int>(runs < units ? runs : units);
+}
+
+inline size_t f32_split_bytes(int runs, int64_t D) {
+  return static_cast<size_t>(2) * runs * static_cast<size_t>(64 * D + 128) * sizeof(float);
+}
+
 template <typename Acc>
 int launch_f32mfma(const Geom& gm, const omm_view4& q, const omm_view4& out, float* lse,
-                   const Acc& acc, int chunk, float scale, hipStream_t s) {
+                   const Acc& acc, int chunk, float scale, hipStream_t s, const F32Split* sp) {
+  if (sp != nullptr) {
+    const unsigned runs = static_cast<unsigned>(sp->ranges);
+    const unsigned items = static_cast<unsigned>(gm.items);
+    if (gm.D == 128) {
+      sel_fwd_f32split_kernel<Acc, 128><<<runs, kF32Waves * kWave, 0, s>>>(
+          make_view<const float>(q), make_view<float>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG,
+          gm.T, chunk, scale, *sp);
+      sel_fwd_f32merge_kernel<128><<<items * 8, 256, 0, s>>>(make_view<float>(out), lse, gm.M,
+                                                            gm.H, gm.G, gm.MG, gm.T, *sp);
+    } else {
+      sel_fwd_f32split_kernel<Acc, 64><<<runs, kF32Waves * kWave, 0, s>>>(
+          make_view<const float>(q), make_view<float>(out), lse, acc, gm.M, gm.H, gm.G, gm.MG,
+          gm.T, chunk, scale, *sp);
+      sel_fwd_f32merge_kernel<64><<<items * 4, 256, 0, s>>>(make_view<float>(out), lse, gm.M,
+                                                           gm.H, gm.G, gm.MG, gm.T, *sp);
+    }
+    return check_launch("selection attention (fp32 mfma, split)");
+  }
   const unsigned grid = static_cast<unsigned>(gm.items);
   if (gm.D == 128)
     sel_fwd_f32mfma_kernel<Acc, 128><<<grid, kF32Waves * kWave, 0, s>>>(
@@ -1333,7 +1502,8 @@ int check_q_out(const char* op, const omm_view4* q, const omm_view4* out) {
 template <typename QT>
 int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, const omm_view4& ids,
                   int bs, int chunk, bool causal, int G, float scale, const omm_view4& out,
-                  float* lse, hipStream_t s, const GateArgs& gate = GateArgs{}) {
+                  float* lse, hipStream_t s, const GateArgs& gate = GateArgs{},
+                  void* ws = nullptr, size_t ws_bytes = 0) {
   Geom gm;
   int rc = geom(q, ids.size[1], ids.size[3], G, gm);
   if (rc) return rc;
@@ -1356,8 +1526,16 @@ int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, co
     const int64_t rb = 4 * (k.stride[1] > v.stride[1] ? k.stride[1] : v.stride[1]);
     if (rows16(q) && rows16(out) && rows16(k) && rows16(v) && G <= 64 &&
         (gm.D == 64 || gm.D == 128) && scale != 0.0f && __builtin_isfinite(scale) &&
-        rb >= 4 * gm.D && rb * 32 < (int64_t{1} << 31))
-      return launch_f32mfma(gm, q, out, lse, acc, causal ? chunk : 1, scale, s);
+        rb >= 4 * gm.D && rb * 32 < (int64_t{1} << 31)) {
+      // the split needs the caller's workspace (omm_sel_fwd_workspace_bytes) and one item per
+      // 64-query group
+      const int runs = ws != nullptr && gm.nsub == 1 ? f32_split_runs(gm.items, gm.T) : 0;
+      if (runs > 0 && ws_bytes >= f32_split_bytes(runs, gm.D)) {
+        const F32Split sp{static_cast<float*>(ws), gm.items * gm.T, runs};
+        return launch_f32mfma(gm, q, out, lse, acc, causal ? chunk : 1, scale, s, &sp);
+      }
+      return launch_f32mfma(gm, q, out, lse, acc, causal ? chunk : 1, scale, s, nullptr);
+    }
   }
   // the VALU kernel reads K and V with K's dim stride
   OMM_REQUIRE(mfma || k.stride[3] == v.stride[3], OMM_EUNSUPPORTED,
@@ -1403,11 +1581,32 @@ int gate_args(const char* op, const omm_view4* q, const omm_view4* gates, const 
 }  // namespace
 }  // namespace omm
 
+extern "C" size_t omm_sel_fwd_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t D,
+                                               int64_t T, int32_t dtype, int32_t group_size) {
+  using namespace omm;
+  if (dtype != OMM_F32 || (D != 64 && D != 128) || group_size < 1 || group_size > 64 || B <= 0 ||
+      M <= 0 || H <= 0 || T <= 0)
+    return 0;
+  const int runs = f32_split_runs(B * H * cdiv64(M, group_size), T);
+  return runs > 0 ? f32_split_bytes(runs, D) : 0;
+}
+
 extern "C" int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                            const omm_view4* ids, int32_t dtype, int32_t block_size,
                            int32_t chunk_size, int32_t causal, int32_t group_size, float scale,
                            const omm_view4* out, float* lse, void* stream) {
+  return omm_sel_fwd_ws(q, k, v, ids, dtype, block_size, chunk_size, causal, group_size, scale,
+                        out, lse, nullptr, 0, stream);
+}
+
+extern "C" int omm_sel_fwd_ws(const omm_view4* q, const omm_view4* k, const omm_view4* v,
+                              const omm_view4* ids, int32_t dtype, int32_t block_size,
+                              int32_t chunk_size, int32_t causal, int32_t group_size, float scale,
+                              const omm_view4* out, float* lse, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   using namespace omm;
+  OMM_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, OMM_EINVAL,
+              "omm_sel_fwd: workspace must be 16-byte aligned");
   int rc = check_q_out("omm_sel_fwd", q, out);
   if (rc) return rc;
   OMM_REQUIRE(k != nullptr && v != nullptr && ids != nullptr, OMM_EINVAL, "omm_sel_fwd: null view");
@@ -1434,7 +1633,7 @@ extern "C" int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_vie
                                   scale, *out, lse, s);
     case OMM_F32:
       return sel_fwd_typed<float>(*q, *k, *v, *ids, block_size, chunk_size, causal != 0, group_size,
-                                  scale, *out, lse, s);
+                                  scale, *out, lse, s, GateArgs{}, workspace, workspace_bytes);
     default: return set_error(OMM_EINVAL, "omm_sel_fwd: unsupported dtype %d", dtype);
   }
 }

@@ -100,10 +100,15 @@ def _sel_fwd_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indic
         out = torch.empty_like(q)
     if lse is None:
         lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device)
-    _lib.call("omm_sel_fwd", _lib.view4(q), _lib.view4(k), _lib.view4(v), _lib.view4(block_indices),
-              _lib.dtype_code(q), int(block_size), int(chunk_size), int(bool(causal)),
-              int(group_size), float(scale), _lib.view4(out), lse.data_ptr() if lse.numel() else None,
-              _lib.stream_of(q))
+    # fp32 calls with few items per CU split into equal runs and merge through a workspace
+    ws_bytes = _lib.lib().omm_sel_fwd_workspace_bytes(
+        B, M, H, D, block_indices.shape[-1], _lib.dtype_code(q), int(group_size))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device) if ws_bytes else None
+    _lib.call("omm_sel_fwd_ws", _lib.view4(q), _lib.view4(k), _lib.view4(v),
+              _lib.view4(block_indices), _lib.dtype_code(q), int(block_size), int(chunk_size),
+              int(bool(causal)), int(group_size), float(scale), _lib.view4(out),
+              lse.data_ptr() if lse.numel() else None,
+              ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_of(q))
     return out, lse
 
 

@@ -101,6 +101,95 @@ def test_sel_fwd_scale_values(scale, dtype):
     _check(out, lse, want_o, want_l, dtype)
 
 
+SPLIT_CASES = [
+    # M, N, H, D, G, BS, T, causal, chunk, minus, dup
+    (1560, 4680, 12, 128, 64, 64, 16, False, 1560, 0.0, False),  # config 1 shape, 300 items
+    (64, 512, 1, 128, 64, 64, 3, False, 1, 0.0, False),    # one item: 3 runs of one slot each
+    (64, 512, 1, 128, 64, 64, 7, True, 256, 0.5, True),    # runs with no live slot, duplicates
+    (300, 700, 3, 128, 15, 30, 8, True, 600, 0.1, False),  # reference geometry, ragged groups
+    (130, 256, 2, 64, 48, 32, 5, False, 1, 0.2, True),     # head dim 64, groups of 48
+    (128, 64, 1, 128, 64, 64, 5, False, 1, 1.0, False),    # every id -1 across the runs
+    (2000, 2048, 4, 128, 64, 64, 9, True, 512, 0.0, False),  # 128 items over 512 runs
+]
+
+
+def _sel_fwd_raw(q, k, v, ids, BS, chunk, scale, causal, G, ws):
+    """omm_sel_fwd (ws None) or omm_sel_fwd_ws through the C-ABI; returns (out, lse)."""
+    from omnimem_amd import _lib
+    B, M, H, D = q.shape
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=q.device)
+    args = [_lib.view4(q), _lib.view4(k), _lib.view4(v), _lib.view4(ids), _lib.dtype_code(q), BS,
+            chunk, int(causal), G, scale, _lib.view4(out), lse.data_ptr()]
+    if ws is None:
+        _lib.call("omm_sel_fwd", *args, _lib.stream_of(q))
+    else:
+        _lib.call("omm_sel_fwd_ws", *args, ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+    return out, lse
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_sel_fwd_f32_split_matches_oracle_and_unsplit(case):
+    """fp32 calls with few items per CU split their selected blocks into equal runs (one per
+    workgroup) and merge the split items' records in a second pass.  Both the split call (its
+    workspace filled with NaN first: nothing in it may be read before it is written) and the
+    unsplit omm_sel_fwd are checked against the float64 oracle at the fp32 bar, and against each
+    other (same arithmetic per piece, merged in another order)."""
+    from omnimem_amd import _lib
+    M, N, H, D, G, BS, T, causal, chunk, minus, dup = case
+    gen = torch.Generator().manual_seed(M + 7 * N + T)
+    q = torch.randn((1, M, H, D), generator=gen) * D ** -0.25
+    k = torch.randn((1, N, H, D), generator=gen) * D ** -0.25
+    v = torch.randn((1, N, H, D), generator=gen)
+    MG = -(-M // G)
+    ids = _ids(gen, 1, MG, H, T, -(-N // BS) + 1, minus, dup)
+    nbytes = _lib.lib().omm_sel_fwd_workspace_bytes(1, M, H, D, T, _lib.OMM_F32, G)
+    assert nbytes > 0, "few items per CU: the call must split"
+    ws = torch.full((nbytes // 4,), float("nan"), device=DEV)
+    qd, kd, vd, idd = q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV)
+    o_s, l_s = _sel_fwd_raw(qd, kd, vd, idd, BS, chunk, D ** -0.5, causal, G, ws)
+    o_p, l_p = _sel_fwd_raw(qd, kd, vd, idd, BS, chunk, D ** -0.5, causal, G, None)
+    want_o, want_l = O.selection_attention(q.numpy(), k.numpy(), v.numpy(), ids.numpy(), G,
+                                           D ** -0.5, O.dense_block_tokens(N, BS, chunk, causal),
+                                           chunk_size=chunk, causal=causal)
+    _check(o_s, l_s, want_o, want_l, torch.float32)
+    _check(o_p, l_p, want_o, want_l, torch.float32)
+    assert (o_s - o_p).abs().max().item() <= 1e-5
+    fin = torch.isfinite(l_p)
+    assert torch.equal(fin, torch.isfinite(l_s))
+    assert (l_s[fin] - l_p[fin]).abs().max().item() <= 1e-5 if fin.any() else True
+    # a second call reuses the workspace as the first left it
+    o_2, l_2 = _sel_fwd_raw(qd, kd, vd, idd, BS, chunk, D ** -0.5, causal, G, ws)
+    assert torch.equal(o_2, o_s) and torch.equal(l_2, l_s)
+
+
+def test_sel_fwd_f32_split_policy():
+    """The split needs fp32, head dim 64 / 128, groups of at most 64 and fewer than 4 items per
+    CU; a workspace that is too small (or none) runs the unsplit kernel."""
+    from omnimem_amd import _lib
+    L = _lib.lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert L.omm_sel_fwd_workspace_bytes(1, 1560, 12, 128, 16, _lib.OMM_F32, 64) > 0
+    assert L.omm_sel_fwd_workspace_bytes(1, 1560, 12, 128, 16, _lib.OMM_BF16, 64) == 0
+    assert L.omm_sel_fwd_workspace_bytes(1, 1560, 12, 96, 16, _lib.OMM_F32, 64) == 0
+    assert L.omm_sel_fwd_workspace_bytes(1, 1560, 12, 128, 16, _lib.OMM_F32, 128) == 0
+    assert L.omm_sel_fwd_workspace_bytes(1, 64 * 4 * cus, 1, 128, 16, _lib.OMM_F32, 64) == 0
+    assert L.omm_sel_fwd_workspace_bytes(1, 64 * (4 * cus - 1), 1, 128, 16, _lib.OMM_F32, 64) > 0
+    # too small a workspace: the unsplit path, same result as omm_sel_fwd bit for bit
+    gen = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn((1, L_, 2, 128), generator=gen).div_(128 ** 0.5).to(DEV)
+               for L_ in (256, 512, 512))
+    ids = _ids(gen, 1, 4, 2, 4, 8).to(DEV)
+    small = torch.empty((1024,), dtype=torch.uint8, device=DEV)
+    o_a, l_a = _sel_fwd_raw(q, k, v, ids, 64, 1, 128 ** -0.5, False, 64, small)
+    o_b, l_b = _sel_fwd_raw(q, k, v, ids, 64, 1, 128 ** -0.5, False, 64, None)
+    assert torch.equal(o_a, o_b) and torch.equal(l_a, l_b)
+    with pytest.raises(Exception, match="16-byte aligned"):
+        _lib.call("omm_sel_fwd_ws", _lib.view4(q), _lib.view4(k), _lib.view4(v), _lib.view4(ids),
+                  _lib.OMM_F32, 64, 1, 0, 64, 128 ** -0.5, _lib.view4(o_a), l_a.data_ptr(),
+                  small.data_ptr() + 4, 1020, _lib.stream_of(q))
+
+
 def test_sel_fwd_strided_views():
     from omnimem_amd.selection import sel_fwd
     gen = torch.Generator().manual_seed(9)
