@@ -69,13 +69,14 @@ ALGO = {
                                          + 2 * _AR_PPC * BS * H * D + 2 * _AR_PPC * H * 4
                                          + 2 * _AR_PPC * H * D * 2),
         # the per-(page, head, K or V) append kernel that serves head dims 64 / 128: the same
-        # bytes per dispatch
+        # bytes per dispatch; the fp8 caches also write the chunk's bf16 K / V into the window
+        # ring from the kernel's registers
         "paged_append_kv_kernel<false>": ("bytes", 2 * _AR_C * H * D * 2
                                           + 2 * _AR_PPC * BS * H * D * 2
                                           + 2 * _AR_PPC * H * D * 2),
         "paged_append_kv_kernel<true>": ("bytes", 2 * _AR_C * H * D * 2
                                          + 2 * _AR_PPC * BS * H * D + 2 * _AR_PPC * H * 4
-                                         + 2 * _AR_PPC * H * D * 2),
+                                         + 2 * _AR_PPC * H * D * 2 + 2 * _AR_C * H * D * 2),
         # selection over the history (cache.select): 4680 queries x 12 heads x 16 pages x 64
         # tokens, 4 D FLOPs each (bf16 pages, some host-resident; fp8 pages)
         "sel_fwd_dma_kernel<bf16_t, PagedAcc<bf16_t>, 128, 2>": (

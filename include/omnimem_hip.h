@@ -35,6 +35,7 @@
  *   omm_paged_append        <- MMCache.update_cache chunk_per_head branch (models/cache.py:478-502)
  *                              fused with the K / V block compression
  *                              (causal_wan_nsa_model.py:479-490)
+ *   omm_paged_append_ring   <- the same, also writing the chunk into a bf16 window ring slot
  *   omm_copy_units          <- flush_offload D2H (models/cache.py:1086-1117) and the reload H2D
  *                              (nsa/ops/selection/padded_ptr/wrapper.py:342-361)
  *   omm_gather_publish_clear, omm_block_range, omm_dedup_run
@@ -359,6 +360,16 @@ int omm_sel_bwd_ptr(const omm_view4* q, const omm_view4* out, const float* lse,
 int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new, const omm_view4* v_new,
                      int32_t cid, int32_t chunk_tokens, const omm_view4* k_cmp,
                      const omm_view4* v_cmp, int32_t epoch, void* stream);
+/* omm_paged_append that also copies k_new / v_new bit for bit into ring_k / ring_v (bf16
+ * [1, chunk_tokens, H, D], unit dim stride, 16-byte aligned rows, apart from k_new / v_new; each
+ * optional): the slot of a bf16 window ring that an fp8 cache keeps for the window branch
+ * (MMCache.update_cache also returns the window K/V it stores, models/cache.py:478-502,
+ * 576-588).  With head dim 64 / 128 and pages of <= 64 tokens the append kernel writes the
+ * copies from its registers, so the chunk is read once. */
+int omm_paged_append_ring(const omm_paged_kv* kv, const omm_view4* k_new,
+                          const omm_view4* v_new, int32_t cid, int32_t chunk_tokens,
+                          const omm_view4* k_cmp, const omm_view4* v_cmp, const omm_view4* ring_k,
+                          const omm_view4* ring_v, int32_t epoch, void* stream);
 /* Selection attention over the cache, non-causal.  q: bf16 [1, M, H, D]; ids: int32
  * [1, MG, H, T] of chunk-aligned page ids (page p of chunk c is id c*pages_per_chunk + p,
  * with min(page_tokens, chunk_len - p*page_tokens) valid tokens); ids outside the readable

@@ -97,6 +97,7 @@ PROTOTYPES = {
                                _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
                                _i64, _f32, _i32, _V, _vp, _vp, _sz, _vp]),
     "omm_paged_append": (_i32, [_P, _V, _V, _i32, _i32, _V, _V, _i32, _vp]),
+    "omm_paged_append_ring": (_i32, [_P, _V, _V, _i32, _i32, _V, _V, _V, _V, _i32, _vp]),
     "omm_sel_fwd_paged": (_i32, [_V, _V, _P, _i32, _f32, _V, _vp, _i32, _vp]),
     "omm_sel_fwd_paged_gated": (_i32, [_V, _V, _P, _i32, _f32, _V, _V, _V, _V, _vp, _i32, _vp]),
     "omm_copy_units": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,

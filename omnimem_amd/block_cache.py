@@ -382,13 +382,14 @@ class PagedKVCache:
         pool_k = pool_v = None
         if not self._pooled_by_caller:
             pool_k, pool_v = _lib.view4(self.k_cmp[layer]), _lib.view4(self.v_cmp[layer])
-        _lib.call("omm_paged_append", ctypes.byref(kv), _lib.view4(k), _lib.view4(v), int(cid),
-                  int(S), pool_k, pool_v, self.next_epoch(), _lib.stream_of(k),
-                  error=BlockKVBackendError)
-        if self.keep_window_kv:
+        ring_k = ring_v = None
+        if self.keep_window_kv:  # the window ring's slot, written by the append kernel
             w = cid % self.window
-            self.win_k[layer][w, :S].copy_(k[0])
-            self.win_v[layer][w, :S].copy_(v[0])
+            ring_k = _lib.view4(self.win_k[layer][w:w + 1, :S])
+            ring_v = _lib.view4(self.win_v[layer][w:w + 1, :S])
+        _lib.call("omm_paged_append_ring", ctypes.byref(kv), _lib.view4(k), _lib.view4(v),
+                  int(cid), int(S), pool_k, pool_v, ring_k, ring_v, self.next_epoch(),
+                  _lib.stream_of(k), error=BlockKVBackendError)
 
     @staticmethod
     def _window_chunks(n_valid: int, window: Optional[int], sink: int):

@@ -60,6 +60,10 @@ struct AppendArgs {
   int64_t cs1, cs2;
   bf16_t* v_cmp;       // optional pooled values, same layout
   int64_t vcs1, vcs2;
+  bf16_t* ring_k;      // optional bf16 copy of the chunk's keys [1, S, H, D] (a window ring slot)
+  int64_t rks1, rks2;
+  bf16_t* ring_v;      // optional copy of the values, same layout
+  int64_t rvs1, rvs2;
   int H, D, P, ppc, max_chunks, cid, tokens, lph, epoch, n_slots;
 };
 
@@ -418,7 +422,9 @@ __global__ __launch_bounds__(kAppHeadThreads) void paged_append_kv_kernel(Append
   const int p = blockIdx.x, h = blockIdx.y;
   const bool isv = blockIdx.z != 0;
   const int32_t slot = a.unit_table[static_cast<int64_t>(h) * a.max_chunks + a.cid];
-  if (slot < 0 || slot >= a.n_slots) return;  // whole workgroup
+  const bool pages = slot >= 0 && slot < a.n_slots;  // no unit slot: only the ring is written
+  bf16_t* ring = isv ? a.ring_v : a.ring_k;
+  if (!pages && ring == nullptr) return;  // whole workgroup
   const int P = a.P;
   const int t_first = p * P;
   const int nvalid = max(0, min(P, a.tokens - t_first));
@@ -433,6 +439,16 @@ __global__ __launch_bounds__(kAppHeadThreads) void paged_append_kv_kernel(Append
     xr[j] = make_uint4(0, 0, 0, 0);
     if (r < nvalid) xr[j] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(t_first + r) * s1);
   }
+  if (ring != nullptr) {  // the chunk's bf16 rows, copied from registers
+    const int64_t rs1 = isv ? a.rvs1 : a.rks1;
+    ring += static_cast<int64_t>(h) * (isv ? a.rvs2 : a.rks2) + dc * 8;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const int r = TPI * (w + kAppHeadWaves * j) + tl;
+      if (r < nvalid) *reinterpret_cast<uint4*>(ring + static_cast<int64_t>(t_first + r) * rs1) = xr[j];
+    }
+  }
+  if (!pages) return;  // whole workgroup
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     const int r = TPI * (w + kAppHeadWaves * j) + tl;
@@ -784,6 +800,24 @@ int check_cmp(const omm_view4* c, int64_t rows, int H, int D, const char* what) 
               what, (long long)rows, H, D);
   return OMM_OK;
 }
+
+// The bf16 ring copy for the append kernels that do not write it themselves: one 16-byte piece
+// of one (token, head) row per thread.
+__global__ __launch_bounds__(256) void ring_copy_kernel(const bf16_t* __restrict__ src,
+                                                        int64_t ss1, int64_t ss2,
+                                                        bf16_t* __restrict__ dst, int64_t ds1,
+                                                        int64_t ds2, int S, int H, int D8) {
+  const int64_t n = static_cast<int64_t>(S) * H * D8;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int c = static_cast<int>(i % D8);
+    const int64_t r = i / D8;
+    const int h = static_cast<int>(r % H);
+    const int64_t t = r / H;
+    *reinterpret_cast<uint4*>(dst + t * ds1 + h * ds2 + 8 * c) =
+        *reinterpret_cast<const uint4*>(src + t * ss1 + h * ss2 + 8 * c);
+  }
+}
 }  // namespace
 }  // namespace omm
 
@@ -791,6 +825,15 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
                                 const omm_view4* v_new, int32_t cid, int32_t chunk_tokens,
                                 const omm_view4* k_cmp, const omm_view4* v_cmp, int32_t epoch,
                                 void* stream) {
+  return omm_paged_append_ring(kv, k_new, v_new, cid, chunk_tokens, k_cmp, v_cmp, nullptr,
+                               nullptr, epoch, stream);
+}
+
+extern "C" int omm_paged_append_ring(const omm_paged_kv* kv, const omm_view4* k_new,
+                                     const omm_view4* v_new, int32_t cid, int32_t chunk_tokens,
+                                     const omm_view4* k_cmp, const omm_view4* v_cmp,
+                                     const omm_view4* ring_k, const omm_view4* ring_v,
+                                     int32_t epoch, void* stream) {
   using namespace omm;
   OMM_REQUIRE(kv != nullptr && k_new != nullptr && v_new != nullptr, OMM_EINVAL,
               "omm_paged_append: null argument");
@@ -843,6 +886,27 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
     a.v_cmp = static_cast<bf16_t*>(const_cast<void*>(v_cmp->data));
     a.vcs1 = v_cmp->stride[1]; a.vcs2 = v_cmp->stride[2];
   }
+  // ring copies: [1, chunk_tokens, H, D] bf16 views with unit dim stride and 16-byte rows, apart
+  // from the inputs (the copy is written while they are read)
+  for (const omm_view4* r : {ring_k, ring_v}) {
+    if (r == nullptr || r->data == nullptr) continue;
+    OMM_REQUIRE(r->size[0] == 1 && r->size[1] == chunk_tokens && r->size[2] == H &&
+                    r->size[3] == D && r->stride[3] == 1 && r->stride[1] % 8 == 0 &&
+                    r->stride[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(r->data) & 15u) == 0,
+                OMM_EINVAL,
+                "omm_paged_append: ring_k / ring_v must be 16-byte aligned [1, %d, %d, %d] bf16 "
+                "views with unit dim stride", chunk_tokens, H, D);
+    OMM_REQUIRE(!views_overlap(*r, *k_new, 2) && !views_overlap(*r, *v_new, 2), OMM_EINVAL,
+                "omm_paged_append: a ring view overlaps k_new / v_new");
+  }
+  if (ring_k != nullptr && ring_k->data != nullptr) {
+    a.ring_k = static_cast<bf16_t*>(const_cast<void*>(ring_k->data));
+    a.rks1 = ring_k->stride[1]; a.rks2 = ring_k->stride[2];
+  }
+  if (ring_v != nullptr && ring_v->data != nullptr) {
+    a.ring_v = static_cast<bf16_t*>(const_cast<void*>(ring_v->data));
+    a.rvs1 = ring_v->stride[1]; a.rvs2 = ring_v->stride[2];
+  }
   a.H = H; a.D = D; a.P = P; a.ppc = ppc; a.max_chunks = kv->max_chunks; a.cid = cid;
   a.tokens = chunk_tokens;
   a.n_slots = kv->n_slots;
@@ -859,6 +923,17 @@ extern "C" int omm_paged_append(const omm_paged_kv* kv, const omm_view4* k_new,
     else
       paged_append_kv_kernel<true><<<hgrid, kAppHeadThreads, 0, s>>>(a);
     return check_launch("omm_paged_append");
+  }
+  // the other append kernels leave the ring copies to ring_copy_kernel
+  for (int t = 0; t < 2; ++t) {
+    bf16_t* ring = t == 0 ? a.ring_k : a.ring_v;
+    if (ring == nullptr) continue;
+    const int64_t n = static_cast<int64_t>(chunk_tokens) * H * (D / 8);
+    const unsigned blocks = static_cast<unsigned>(n / 256 + 1 < 4096 ? n / 256 + 1 : 4096);
+    ring_copy_kernel<<<blocks, 256, 0, s>>>(t == 0 ? a.k : a.v, t == 0 ? a.ks1 : a.vs1,
+                                            t == 0 ? a.ks2 : a.vs2, ring,
+                                            t == 0 ? a.rks1 : a.rvs1, t == 0 ? a.rks2 : a.rvs2,
+                                            chunk_tokens, H, D / 8);
   }
   if (P <= kAppendMaxP) {
     const size_t lds = static_cast<size_t>(2) * P * kWave * sizeof(uint4);

@@ -223,6 +223,58 @@ def test_paged_append_fp8_codes_and_scales_bitexact(H, D, P):
                 assert np.float32(sc[p].item()) == want_s, (h, p)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, "fp8"])
+@pytest.mark.parametrize("H,D,P", [(3, 128, 64), (2, 64, 30), (2, 128, 80)])
+def test_paged_append_ring_copy(dtype, H, D, P):
+    """The window ring slot an fp8 cache keeps (written by the append kernel from its registers
+    for head dim 64 / 128 and pages of <= 64 tokens, by a copy kernel otherwise) holds k / v bit
+    for bit, and the pages, scales and pooled rows equal those of a cache without the ring."""
+    from omnimem_amd.block_cache import PagedKVCache
+    torch.manual_seed(11 + P)
+    C, W = 4680, 2
+    kw = dict(max_chunks=4, chunk_len=C, page_tokens=P, dtype=dtype, hbm_slots=4 * H,
+              window_chunks=W)
+    ring = PagedKVCache(1, H, D, keep_window_kv=True, **kw)
+    plain = PagedKVCache(1, H, D, keep_window_kv=False, **kw)
+    for cid in range(3):
+        k, v = _chunk(None, C, H, D, 2.0, True).to(DEV), _chunk(None, C, H, D, 1.5, True).to(DEV)
+        ring.append(0, k, v, cid)
+        plain.append(0, k, v, cid)
+        assert torch.equal(ring.win_k[0][cid % W], k[0]) and torch.equal(ring.win_v[0][cid % W], v[0])
+    for cid in range(3):
+        for h in range(H):
+            for a, b in zip(ring.read_unit(0, h, cid), plain.read_unit(0, h, cid)):
+                assert torch.equal(a, b), (cid, h)
+    for a, b in zip(ring.cmp_history(0), plain.cmp_history(0)):
+        assert torch.equal(a, b)
+
+
+def test_paged_append_ring_without_unit_slots():
+    """Heads whose unit slot is not allocated (table entry -1) skip their pages but still get
+    the ring copy; a ring view overlapping the input is rejected."""
+    import ctypes
+    from omnimem_amd import _lib
+    from omnimem_amd.backend import BlockKVBackendError
+    from omnimem_amd.block_cache import PagedKVCache
+    g = torch.Generator().manual_seed(12)
+    H, D, C, P = 2, 128, 4680, 64
+    cache = PagedKVCache(1, H, D, max_chunks=2, chunk_len=C, page_tokens=P, dtype="fp8",
+                         hbm_slots=2, window_chunks=1, keep_window_kv=True)
+    k, v = _chunk(g, C, H, D).to(DEV), _chunk(g, C, H, D).to(DEV)
+    rk, rv = torch.zeros_like(k), torch.zeros_like(v)
+    pool_before = cache.pool_k.clone()
+    kv = cache.layer_view(0)  # nothing written: every unit slot is -1
+    _lib.call("omm_paged_append_ring", ctypes.byref(kv), _lib.view4(k), _lib.view4(v), 0, C,
+              None, None, _lib.view4(rk), _lib.view4(rv), 0, _lib.stream_of(k),
+              error=BlockKVBackendError)
+    torch.cuda.synchronize()
+    assert torch.equal(rk, k) and torch.equal(rv, v)
+    assert torch.equal(cache.pool_k, pool_before)
+    with pytest.raises(BlockKVBackendError, match="overlaps"):
+        _lib.call("omm_paged_append_ring", ctypes.byref(kv), _lib.view4(k), _lib.view4(v), 0, C,
+                  None, None, _lib.view4(k), None, 0, _lib.stream_of(k), error=BlockKVBackendError)
+
+
 def _paged_oracle_inputs(chunks_k, chunks_v, fp8_cache=None, layer=0):
     """Concatenate chunk tensors [1, C, H, D] into the oracle's [1, n*C, H, D]; for an fp8
     cache, the dequantised values the kernel computes with (code * page scale in fp32: the kernel
