@@ -621,9 +621,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
 #pragma unroll
     for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m2[2] = {kNegInf, kNegInf};
-  // -max(m2, 0 if none finite) and the raise threshold (8, or -inf while m2 = -inf)
-  float nms[2] = {0.0f, 0.0f}, thr[2] = {kNegInf, kNegInf};
+  float nms[2] = {0.0f, 0.0f};  // -max(m2, 0 if none finite)
   float lsum[2] = {0.0f, 0.0f};  // fp32 row sums of the unrounded p (lane partials)
+  bool started = false;          // every row of the wave has seen a visible key
 
   WaveWalk<Acc, TK> wk;
   wk.start(acc, b, g, h, T, qc);
@@ -713,26 +713,21 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
           if (16 * t + 4 * j4 + r >= n_cur) s4[0][t][r] = s4[1][t][r] = kNegInf;
     }
 
-    // online softmax in the log2 domain: e = s c2 - m with m a running max of s c2 per query
-    // (0 while none is finite), p = 2^e.  m is raised only when some e exceeds 8 (p stays
-    // <= 256, exact enough in fp32 and in the 16-bit P operand), so the common path needs no
-    // cross-lane max.
-    bool raise = false;
+    // online softmax in the log2 domain: e = s c2 - msafe per query, p = 2^e, msafe = m2 (0
+    // while m2 = -inf).  m2 (the largest s c2 seen when it last moved) moves before a row's first
+    // visible key and when some lane's sum of the tile's p for the row passes 256, so the common
+    // path takes no max at all.  The bound keeps p small, and a move makes the new largest key's
+    // p exactly 1: with a bound of 2^60 instead, peaked rows (scale 8) lost accuracy to the
+    // rounding of their dominant p to 16 bits (simulated mean error 1.12e-3 against 0.99e-3).
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       const float msafe = -nms[x];
-      float mx = kNegInf;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = __builtin_fmaf(s4[x][t][r], c2, -msafe);
-          s4[x][t][r] = e;
-          mx = fmaxf(mx, e);
-        }
-      raise = raise || (mx > thr[x]);
+        for (int r = 0; r < 4; ++r) s4[x][t][r] = __builtin_fmaf(s4[x][t][r], c2, -msafe);
     }
-    if (__ballot(raise) != 0ull) {
+    auto move_max = [&]() {
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
@@ -751,35 +746,51 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
         for (int i2 = 0; i2 < ND; ++i2) o[x][i2] *= alpha;
         m2[x] = mcand;
         nms[x] = -msafe_new;
-        thr[x] = mcand == kNegInf ? kNegInf : 8.0f;
         const float shift = msafe - msafe_new;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) s4[x][t][r] += shift;
       }
+    };
+    if (!started) {  // wave-uniform: some row has not seen a visible key yet
+      move_max();
+      started = __ballot(m2[0] == kNegInf || m2[1] == kNegInf) == 0ull;
     }
-
-    // O^T += V^T P^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
-    // 32 u + 16 + 4 j4 + (e - 4), for both operands
+    // p = 2^e packed as the P^T operands (k-slot e of lane group j4 is key 32 u + 4 j4 + e,
+    // e < 4, or 32 u + 16 + 4 j4 + (e - 4)), and the lane's sum of the tile's p per row
+    uint4 pb[NU][2];
+    float ps[2];
+    auto exps = [&]() {
+      ps[0] = ps[1] = 0.0f;
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      uint4 pb[2];
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        float pv[8];
+        for (int x = 0; x < 2; ++x) {
+          float pv[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(s4[x][2 * u + (e >> 2)][e & 3]);
-        lsum[x] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-        pb[x] = make_uint4(Mfma<QT>::pack2(pv[0], pv[1]), Mfma<QT>::pack2(pv[2], pv[3]),
-                           Mfma<QT>::pack2(pv[4], pv[5]), Mfma<QT>::pack2(pv[6], pv[7]));
-      }
+          for (int e = 0; e < 8; ++e)
+            pv[e] = __builtin_amdgcn_exp2f(s4[x][2 * u + (e >> 2)][e & 3]);
+          ps[x] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+          pb[u][x] = make_uint4(Mfma<QT>::pack2(pv[0], pv[1]), Mfma<QT>::pack2(pv[2], pv[3]),
+                                Mfma<QT>::pack2(pv[4], pv[5]), Mfma<QT>::pack2(pv[6], pv[7]));
+        }
+    };
+    exps();
+    if (__ballot(ps[0] > 256.0f || ps[1] > 256.0f) != 0ull) {
+      move_max();
+      exps();
+    }
+    lsum[0] += ps[0];
+    lsum[1] += ps[1];
+    // O^T += V^T P^T
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int i2 = 0; i2 < ND; ++i2) {
-        o[0][i2] = Mfma<QT>::run(va[u][i2], pb[0], o[0][i2]);
-        o[1][i2] = Mfma<QT>::run(va[u][i2], pb[1], o[1][i2]);
+        o[0][i2] = Mfma<QT>::run(va[u][i2], pb[u][0], o[0][i2]);
+        o[1][i2] = Mfma<QT>::run(va[u][i2], pb[u][1], o[1][i2]);
       }
-    }
     n_cur = n_nx;
     return n_cur > 0;
   };
