@@ -102,8 +102,9 @@ def test_sel_fwd_scale_values(scale, dtype):
 
 
 SPLIT_CASES = [
-    # M, N, H, D, G, BS, T, causal, chunk, minus, dup
+    # M, N, H, D, G, BS, T, causal, chunk, minus, dup[, B]
     (1560, 4680, 12, 128, 64, 64, 16, False, 1560, 0.0, False),  # config 1 shape, 300 items
+    (500, 1000, 3, 128, 64, 64, 6, True, 250, 0.1, False, 2),  # two batches: item order b, h, g
     (64, 512, 1, 128, 64, 64, 3, False, 1, 0.0, False),    # one item: 3 runs of one slot each
     (64, 512, 1, 128, 64, 64, 7, True, 256, 0.5, True),    # runs with no live slot, duplicates
     (300, 700, 3, 128, 15, 30, 8, True, 600, 0.1, False),  # reference geometry, ragged groups
@@ -136,14 +137,15 @@ def test_sel_fwd_f32_split_matches_oracle_and_unsplit(case):
     unsplit omm_sel_fwd are checked against the float64 oracle at the fp32 bar, and against each
     other (same arithmetic per piece, merged in another order)."""
     from omnimem_amd import _lib
-    M, N, H, D, G, BS, T, causal, chunk, minus, dup = case
+    M, N, H, D, G, BS, T, causal, chunk, minus, dup = case[:11]
+    B = case[11] if len(case) > 11 else 1
     gen = torch.Generator().manual_seed(M + 7 * N + T)
-    q = torch.randn((1, M, H, D), generator=gen) * D ** -0.25
-    k = torch.randn((1, N, H, D), generator=gen) * D ** -0.25
-    v = torch.randn((1, N, H, D), generator=gen)
+    q = torch.randn((B, M, H, D), generator=gen) * D ** -0.25
+    k = torch.randn((B, N, H, D), generator=gen) * D ** -0.25
+    v = torch.randn((B, N, H, D), generator=gen)
     MG = -(-M // G)
-    ids = _ids(gen, 1, MG, H, T, -(-N // BS) + 1, minus, dup)
-    nbytes = _lib.lib().omm_sel_fwd_workspace_bytes(1, M, H, D, T, _lib.OMM_F32, G)
+    ids = _ids(gen, B, MG, H, T, -(-N // BS) + 1, minus, dup)
+    nbytes = _lib.lib().omm_sel_fwd_workspace_bytes(B, M, H, D, T, _lib.OMM_F32, G)
     assert nbytes > 0, "few items per CU: the call must split"
     ws = torch.full((nbytes // 4,), float("nan"), device=DEV)
     qd, kd, vd, idd = q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV)
