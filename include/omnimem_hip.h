@@ -237,7 +237,9 @@ int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H, 
  * Query m (group g = m / group_size) attends to the tokens of its listed blocks (0 <= id,
  * id*block_size < N; causal: (id*block_size)/chunk_size <= q_chunk and token/chunk_size <=
  * q_chunk with q_chunk = (g*group_size)/chunk_size).  No visible token: out 0, lse -inf.
- * bf16/f16 run on MFMA with bf16/f16 P; f32 runs full fp32 arithmetic. */
+ * bf16/f16 run on MFMA with bf16/f16 P; f32 runs full fp32 arithmetic.  Offsets are 32-bit
+ * where they can be: ids must span fewer than 2^31 elements and each (b, h) slice of k / v
+ * fewer than 2^32 (OMM_EUNSUPPORTED otherwise). */
 int omm_sel_fwd(const omm_view4* q, const omm_view4* k, const omm_view4* v,
                 const omm_view4* ids, int32_t dtype, int32_t block_size, int32_t chunk_size,
                 int32_t causal, int32_t group_size, float scale, const omm_view4* out,
@@ -371,7 +373,7 @@ int omm_paged_append_ring(const omm_paged_kv* kv, const omm_view4* k_new,
                           const omm_view4* k_cmp, const omm_view4* v_cmp, const omm_view4* ring_k,
                           const omm_view4* ring_v, int32_t epoch, void* stream);
 /* Selection attention over the cache, non-causal.  q: bf16 [1, M, H, D]; ids: int32
- * [1, MG, H, T] of chunk-aligned page ids (page p of chunk c is id c*pages_per_chunk + p,
+ * [1, MG, H, T] (spanning fewer than 2^31 elements) of chunk-aligned page ids (page p of chunk c is id c*pages_per_chunk + p,
  * with min(page_tokens, chunk_len - p*page_tokens) valid tokens); ids outside the readable
  * chunks or of units never written are skipped.  With kv->stamp and epoch > 0 every unit read
  * gets stamp = epoch (the LRU touch of the reference's _touch_lru_and_detect_missing,

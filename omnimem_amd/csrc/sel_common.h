@@ -101,6 +101,33 @@ struct BlockRef {
 // slots at once, one per lane; ref() -> the block's addresses from a wave-uniform entry.
 // order_key() orders the blocks of a row by position in memory (the walk visits them in that
 // order, so concurrent rows that share blocks tend to read them at the same time).
+// Slot t of row (b, g, h) of an ids view, as a 32-bit element offset: the (b, g, h) part is
+// wave-uniform (scalar arithmetic), the lane's t part one 32-bit multiply.  The host checks
+// ids_offsets_fit32 before it builds an accessor that uses this.
+__device__ __forceinline__ int ids_off32(int64_t is0, int64_t is1, int64_t is2, int64_t is3,
+                                         int b, int g, int h, int t) {
+  return static_cast<int32_t>(b * is0 + g * is1 + h * is2) + t * static_cast<int32_t>(is3);
+}
+
+inline bool ids_offsets_fit32(const omm_view4& ids) {
+  int64_t last = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (ids.stride[i] < 0 || ids.stride[i] > 2147483647ll) return false;
+    if (ids.size[i] > 0) last += (ids.size[i] - 1) * ids.stride[i];
+  }
+  return last < 2147483647ll;
+}
+
+// DenseAcc::ref forms token offsets in 32 bits: (N - 1) * the token stride of k and v below 2^32
+// elements, strides non-negative.
+inline bool kv_offsets_fit32(const omm_view4& k, const omm_view4& v) {
+  for (const omm_view4* x : {&k, &v}) {
+    if (x->stride[1] < 0) return false;
+    if (x->size[1] > 0 && (x->size[1] - 1) * x->stride[1] >= (int64_t{1} << 32)) return false;
+  }
+  return true;
+}
+
 template <typename T>
 struct DenseAcc {
   static constexpr bool kMayMisalign = false;  // 16-byte rows checked on the host
@@ -115,7 +142,7 @@ struct DenseAcc {
   bool causal;
   __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int q_chunk) const {
     Ent e{0, 0};
-    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    const int32_t bid = ids[ids_off32(is0, is1, is2, is3, b, g, h, t)];
     if (bid < 0) return e;
     const int64_t t0 = static_cast<int64_t>(bid) * bs;
     if (t0 >= N) return e;
@@ -130,8 +157,14 @@ struct DenseAcc {
     e.n = static_cast<int>(n);
     return e;
   }
+  // the (b, h) slice's base in 64 bits, the token offset in 32 (the host keeps every slice's
+  // token extent under 2^32 elements: kv_offsets_fit32), so no 64-bit multiply per block
   __device__ __forceinline__ BlockRef ref(int b, int h, const Ent& e) const {
-    return BlockRef{k.at(b, e.t0, h, 0), v.at(b, e.t0, h, 0), k.s1, v.s1, e.n, 1.0f, 1.0f};
+    const T* kb = k.p + (static_cast<int64_t>(b) * k.s0 + static_cast<int64_t>(h) * k.s2);
+    const T* vb = v.p + (static_cast<int64_t>(b) * v.s0 + static_cast<int64_t>(h) * v.s2);
+    const uint32_t ko = static_cast<uint32_t>(e.t0) * static_cast<uint32_t>(k.s1);
+    const uint32_t vo = static_cast<uint32_t>(e.t0) * static_cast<uint32_t>(v.s1);
+    return BlockRef{kb + ko, vb + vo, k.s1, v.s1, e.n, 1.0f, 1.0f};
   }
   __device__ __forceinline__ static int64_t order_key(const Ent& e) { return e.t0; }
   __device__ __forceinline__ void touch(int, int, int, int) const {}
@@ -213,7 +246,7 @@ struct PagedAcc {
   static constexpr int kStaged = 1 << 30;
   __device__ __forceinline__ Ent resolve(int b, int g, int h, int t, int) const {
     Ent e{};
-    const int32_t bid = ids[b * is0 + g * is1 + h * is2 + t * is3];
+    const int32_t bid = ids[ids_off32(is0, is1, is2, is3, b, g, h, t)];
     if (bid < 0) return e;
     const int cid = bid / ppc, p = bid - cid * ppc;
     if (cid >= n_chunks || cid >= max_chunks) return e;

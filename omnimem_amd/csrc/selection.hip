@@ -663,9 +663,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
     __syncthreads();
     int n_nx = 0;
     if (wk.valid) {
-      copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(wk.tok0) * rsk, rsk,
+      const int tok = __builtin_amdgcn_readfirstlane(wk.tok0);  // uniform: scalar arithmetic
+      copy_part<Acc>(static_cast<const char*>(wk.br.k) + static_cast<int64_t>(tok) * rsk, rsk,
                wk.n, lds[BI ^ 1], w, kdo);
-      copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(wk.tok0) * rsv, rsv,
+      copy_part<Acc>(static_cast<const char*>(wk.br.v) + static_cast<int64_t>(tok) * rsv, rsv,
                wk.n, lds[2 + (BI ^ 1)], w, vdo);
       n_nx = wk.n;
       wk.advance(acc, b, g, h, T, qc);
@@ -762,7 +763,6 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
     uint4 pb[NU][2];
     float ps[2];
     auto exps = [&]() {
-      ps[0] = ps[1] = 0.0f;
 #pragma unroll
       for (int u = 0; u < NU; ++u)
 #pragma unroll
@@ -771,7 +771,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void sel_fwd_dma_kernel(
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             pv[e] = __builtin_amdgcn_exp2f(s4[x][2 * u + (e >> 2)][e & 3]);
-          ps[x] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+          // the first group's sum starts ps (0 + x is not folded: it would turn -0 into +0)
+          const float s8 =
+              ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+          ps[x] = u == 0 ? s8 : ps[x] + s8;
           pb[u][x] = make_uint4(Mfma<QT>::pack2(pv[0], pv[1]), Mfma<QT>::pack2(pv[2], pv[3]),
                                 Mfma<QT>::pack2(pv[4], pv[5]), Mfma<QT>::pack2(pv[6], pv[7]));
         }
@@ -1518,6 +1521,11 @@ int sel_fwd_typed(const omm_view4& q, const omm_view4& k, const omm_view4& v, co
   Geom gm;
   int rc = geom(q, ids.size[1], ids.size[3], G, gm);
   if (rc) return rc;
+  OMM_REQUIRE(ids_offsets_fit32(ids), OMM_EUNSUPPORTED,
+              "selection attention: block_indices must span fewer than 2^31 elements");
+  OMM_REQUIRE(kv_offsets_fit32(k, v), OMM_EUNSUPPORTED,
+              "selection attention: a (batch, head) slice of k / v must span fewer than 2^32 "
+              "elements");
   DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
                    static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
                    ids.stride[2], ids.stride[3], static_cast<int>(k.size[1]), bs,
@@ -1739,6 +1747,8 @@ int sel_fwd_paged_impl(const omm_view4* q, const omm_view4* ids, const omm_paged
   rc = geom(*q, MG, ids->size[3], group_size, gm);
   if (rc) return rc;
   if (gm.items == 0) return OMM_OK;
+  OMM_REQUIRE(ids_offsets_fit32(*ids), OMM_EUNSUPPORTED,
+              "omm_sel_fwd_paged: ids must span fewer than 2^31 elements");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool mfma = qo_mfma_ok(*q, *out) && kv->head_dim % 64 == 0;
   const int32_t* idp = static_cast<const int32_t*>(ids->data);

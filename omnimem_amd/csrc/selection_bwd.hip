@@ -1045,6 +1045,10 @@ int sel_bwd_launch(const BwdArgs& a, char* ws, const BwdWs& L, hipStream_t s) {
   int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
   int32_t* groups = reinterpret_cast<int32_t*>(ws + L.groups);
 
+  OMM_REQUIRE(ids_offsets_fit32(ids), OMM_EUNSUPPORTED,
+              "omm_sel_bwd: block_indices must span fewer than 2^31 elements");
+  OMM_REQUIRE(kv_offsets_fit32(k, v), OMM_EUNSUPPORTED,
+              "omm_sel_bwd: a (batch, head) slice of k / v must span fewer than 2^32 elements");
   DenseAcc<QT> acc{make_view<const QT>(k), make_view<const QT>(v),
                    static_cast<const int32_t*>(ids.data), ids.stride[0], ids.stride[1],
                    ids.stride[2], ids.stride[3], N, bs, ch, causal};
