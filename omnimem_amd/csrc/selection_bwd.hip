@@ -27,6 +27,8 @@
 //                        dV += P^T dO and dK += dS^T Q with P^T / dS^T from the accumulator
 //                        layout and dO / Q from transposed LDS reads.  Every token of every block
 //                        is written (0 when no group selected it).
+#include <type_traits>
+
 #include "sel_common.h"
 
 namespace omm {
@@ -166,7 +168,10 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
   }
   __builtin_amdgcn_s_waitcnt(0);
 
-  auto step = [&](int BI) -> bool {
+  // one key tile in LDS buffers BI, a compile-time constant so that LDS addresses are a lane
+  // offset plus an immediate
+  auto step = [&](auto BIc) -> bool {
+    constexpr int BI = decltype(BIc)::value;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int n_nx = 0;
@@ -197,15 +202,22 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
       }
     }
     // dS / scale = P (dP - delta), P = 2^(s c2 - lse log2 e); keys past n_cur are not visible
-    // (the scale multiplies the dQ sums once at the end)
+    // (the scale multiplies the dQ sums once at the end).  The mask is a wave-uniform branch
+    // taken by partial tiles only, so full tiles pay nothing for it.
+    if (n_cur < TK) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * t + 4 * j4 + r >= n_cur) s4[0][t][r] = s4[1][t][r] = kNegInf;
+    }
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
-          if (n_cur < TK && 16 * t + 4 * j4 + r >= n_cur) p = 0.0f;
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
           s4[x][t][r] = p * (p4[x][t][r] - dl[x]);
         }
     // dQ^T += K^T dS^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     return n_cur > 0;
   };
   if (n_cur > 0)
-    for (int it = 0; step(it & 1); ++it) {
+    while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
     }
 
   // lane holds dQ[query l16][dims 16 i + 4 j4 + r]
