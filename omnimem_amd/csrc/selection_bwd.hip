@@ -123,6 +123,18 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     }
   }
   const float c2 = scale * kLog2e;
+  // dO^T negated (sign bits, exact) and delta as the accumulator input: the dP^T MFMAs then
+  // give delta - dP directly, and dS = -P (delta - dP) costs one multiply per score
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int s = 0; s < SD; ++s) {
+      db[x][s].x ^= 0x80008000u;
+      db[x][s].y ^= 0x80008000u;
+      db[x][s].z ^= 0x80008000u;
+      db[x][s].w ^= 0x80008000u;
+    }
+  const f32x4 dlv[2] = {f32x4{dl[0], dl[0], dl[0], dl[0]}, f32x4{dl[1], dl[1], dl[1], dl[1]}};
 
   // LDS read offsets inside a tile buffer; K and V rows are swizzled by swz_v (K is read both as
   // rows and transposed; measured on gfx950 swz_v serves both read kinds best).  K / V row
@@ -190,7 +202,9 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
     f32x4 s4[2][NT], p4[2][NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      s4[0][t] = s4[1][t] = p4[0][t] = p4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s4[0][t] = s4[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      p4[0][t] = dlv[0];
+      p4[1][t] = dlv[1];
 #pragma unroll
       for (int s = 0; s < SD; ++s) {
         const uint4 a = *reinterpret_cast<const uint4*>(Kt + koff[s] + 16 * t * ROWB);
@@ -218,7 +232,7 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
-          s4[x][t][r] = p * (p4[x][t][r] - dl[x]);
+          s4[x][t][r] = -(p * p4[x][t][r]);
         }
     // dQ^T += K^T dS^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
     // 32 u + 16 + 4 j4 + (e - 4), for both operands
