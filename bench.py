@@ -829,8 +829,9 @@ def main():
     # Measurement order.  The GPU's clock drops within milliseconds of idling (host work such as
     # the graph capture below) and takes about 20 ms of load to recover: the first ~20 steps after
     # an idle period run about 20% slower than the sustained rate.  So the host-side work comes
-    # first, then the backward (about 25 ms of GPU work), the top-k timings, and right after them
-    # the step's warm-up and timed steps, with no idle period in between.
+    # first, then the backward (about 30 ms of untimed calls, then the timed ones), the top-k
+    # timings, and right after them the step's warm-up and timed steps, with no idle period in
+    # between.
     #
     # config 2: top-k alone (pool + score + select).  One call is shorter than its host-side
     # enqueue, so back-to-back calls would time the host: the calls are captured once in a HIP
@@ -855,7 +856,9 @@ def main():
     # 2.5x the forward's (S recomputed, dP, dQ, dK, dV: 5 products of the forward's 2)
     from omnimem_amd.selection import sel_bwd
     d_out = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
-    for _ in range(2):
+    # about 30 ms of untimed backward calls: the clock recovers from the graph capture's idle
+    # period before the timed calls start
+    for _ in range(30):
         sel_bwd(q, k, v, ids, out, lse, d_out, BS, CHUNK, scale, True, G)
     b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     b0.record()
