@@ -280,6 +280,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < ND; ++i) o[x][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m2[2] = {kNegInf, kNegInf}, lsum[2] = {0.0f, 0.0f};
+  bool started = false;  // every row of the wave has seen a visible key (kLazyMax)
   // the softmax works on s * c2 with c2 > 0; a negative scale negates Q instead, which is exact
   // (the host routes a zero or non-finite scale to the VALU kernel)
   float c2 = scale * kLog2e;
@@ -300,6 +301,9 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
 
   using KVT = typename Acc::KV;
   constexpr bool kFp8 = sizeof(KVT) == 1;
+  // fp8 pages at D = 128 take the running max only when it must move (below); the other
+  // instances keep a per-tile max test, which needs fewer registers
+  constexpr bool kLazyMax = kFp8 && D == 128;
   Stager<KVT, D, QK8, DMAK> st;
   float sk_next = 1.0f, sv_next = 1.0f;  // page scales of the tile being staged (fp8 pages)
   WaveWalk<Acc> wk;
@@ -440,53 +444,135 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // online softmax in the log2 domain: p = 2^(s * c2 - m), m a running max of s * c2 shared
-      // by the 4 lane groups of a query.  m is raised only when some lane's tile max exceeds it
-      // by more than 2^8 (p then stays <= 256, exact enough in fp32 and in the bf16 P operand),
-      // so after the first tiles the cross-lane max reduction is rarely needed.
+      // P^T operands (k-slot e of lane group j4 is key 32 u + 4 j4 + e, e < 4, or 32 u + 16 +
+      // 4 j4 + (e - 4))
+      uint4 pb[2][2];
+      if constexpr (kLazyMax) {
+        // online softmax in the log2 domain: e = s c2x - msafe (plus log2 s_v for fp8 pages),
+        // p = 2^e, msafe = m2 (0 while m2 = -inf), shared by the 4 lane groups of a query.  m2
+        // (the largest s c2x seen when it last moved) moves before a row's first visible key
+        // and when some lane's sum of the tile's p / s_v for the row passes 256; a move
+        // recomputes the tile's p.  So the common path takes no max, p stays small, and a move
+        // gives the new largest key p = 1.
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        float mt = kNegInf;
+        for (int x = 0; x < 2; ++x) {
+          const float bias = (kFp8 ? lv : 0.0f) - (m2[x] == kNegInf ? 0.0f : m2[x]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          mt = fmaxf(mt, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
-        if (__ballot(mt * c2x[x] > m2[x] + 8.0f) != 0ull) {
-          mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-          mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-          const float mcand = fmaxf(m2[x], mt * c2x[x]);
-          const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
-          const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
-          lsum[x] *= alpha;
+          for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < ND; ++i) o[x][i] *= alpha;
-          m2[x] = mcand;
+            for (int r = 0; r < 4; ++r) s4[x][t][r] = __builtin_fmaf(s4[x][t][r], c2x[x], bias);
         }
-        const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
-        const float bias = kFp8 ? lv - msafe : -msafe;
-        float ps = 0.0f;
+        auto move_max = [&]() {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+          for (int x = 0; x < 2; ++x) {
+            const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+            float v = kNegInf;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2x[x], bias));
-            s4[x][t][r] = pv;
-            ps += pv;
+            for (int t = 0; t < 4; ++t)
+              v = fmaxf(v, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
+            v = fmaxf(v, __shfl_xor(v, 16, kWave));
+            v = fmaxf(v, __shfl_xor(v, 32, kWave));
+            // v: the query's largest e of this tile, relative to msafe (and log2 s_v)
+            const float mcand = fmaxf(m2[x], (kFp8 ? v - lv : v) + msafe);
+            const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
+            const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
+            lsum[x] *= alpha;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) o[x][i] *= alpha;
+            m2[x] = mcand;
+            const float shift = msafe - msafe_new;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) s4[x][t][r] += shift;
           }
-        if constexpr (kFp8) lsum[x] = __builtin_fmaf(ps, inv_sv, lsum[x]);
-        else lsum[x] += ps;
+        };
+        if (!started) {  // wave-uniform: some row has not seen a visible key yet
+          move_max();
+          started = __ballot(m2[0] == kNegInf || m2[1] == kNegInf) == 0ull;
+        }
+        float ps[2];  // the lane's sum of the tile's p per row (times s_v for fp8 pages)
+        auto exps = [&]() {
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            float pv[4][4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) pv[t][r] = __builtin_amdgcn_exp2f(s4[x][t][r]);
+            // the first group's sum starts ps (0 + x is not folded: it would turn -0 into +0)
+            float sum = (pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3]);
+#pragma unroll
+            for (int t = 1; t < 4; ++t) sum += (pv[t][0] + pv[t][1]) + (pv[t][2] + pv[t][3]);
+            ps[x] = sum;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+              pb[u][x] = make_uint4(Mfma<QT>::pack2(pv[2 * u][0], pv[2 * u][1]),
+                                    Mfma<QT>::pack2(pv[2 * u][2], pv[2 * u][3]),
+                                    Mfma<QT>::pack2(pv[2 * u + 1][0], pv[2 * u + 1][1]),
+                                    Mfma<QT>::pack2(pv[2 * u + 1][2], pv[2 * u + 1][3]));
+          }
+        };
+        exps();
+        const float bound = kFp8 ? 256.0f * sv_cur : 256.0f;  // 256 for p / s_v
+        if (__ballot(ps[0] > bound || ps[1] > bound) != 0ull) {
+          move_max();
+          exps();
+        }
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          if constexpr (kFp8) lsum[x] = __builtin_fmaf(ps[x], inv_sv, lsum[x]);
+          else lsum[x] += ps[x];
+        }
+      } else {
+        // online softmax in the log2 domain: p = 2^(s * c2 - m), m a running max of s * c2 shared
+        // by the 4 lane groups of a query.  m is raised only when some lane's tile max exceeds it
+        // by more than 2^8 (p then stays <= 256, exact enough in fp32 and in the bf16 P operand),
+        // so after the first tiles the cross-lane max reduction is rarely needed.
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          float mt = kNegInf;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            mt = fmaxf(mt, fmaxf(fmaxf(s4[x][t][0], s4[x][t][1]), fmaxf(s4[x][t][2], s4[x][t][3])));
+          if (__ballot(mt * c2x[x] > m2[x] + 8.0f) != 0ull) {
+            mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+            const float mcand = fmaxf(m2[x], mt * c2x[x]);
+            const float msafe_new = mcand == kNegInf ? 0.0f : mcand;
+            const float alpha = __builtin_amdgcn_exp2f(m2[x] - msafe_new);
+            lsum[x] *= alpha;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) o[x][i] *= alpha;
+            m2[x] = mcand;
+          }
+          const float msafe = m2[x] == kNegInf ? 0.0f : m2[x];
+          const float bias = kFp8 ? lv - msafe : -msafe;
+          float ps = 0.0f;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2x[x], bias));
+              s4[x][t][r] = pv;
+              ps += pv;
+            }
+          if constexpr (kFp8) lsum[x] = __builtin_fmaf(ps, inv_sv, lsum[x]);
+          else lsum[x] += ps;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+            pb[u][x] = make_uint4(Mfma<QT>::pack2(s4[x][2 * u][0], s4[x][2 * u][1]),
+                                  Mfma<QT>::pack2(s4[x][2 * u][2], s4[x][2 * u][3]),
+                                  Mfma<QT>::pack2(s4[x][2 * u + 1][0], s4[x][2 * u + 1][1]),
+                                  Mfma<QT>::pack2(s4[x][2 * u + 1][2], s4[x][2 * u + 1][3]));
       }
       // O^T += V^T P^T; k-slot e of lane group j4 is key 32u + 4 j4 + e (e < 4) or
       // 32u + 16 + 4 j4 + (e - 4), for both operands
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        uint4 pb[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          pb[x].x = Mfma<QT>::pack2(s4[x][2 * u][0], s4[x][2 * u][1]);
-          pb[x].y = Mfma<QT>::pack2(s4[x][2 * u][2], s4[x][2 * u][3]);
-          pb[x].z = Mfma<QT>::pack2(s4[x][2 * u + 1][0], s4[x][2 * u + 1][1]);
-          pb[x].w = Mfma<QT>::pack2(s4[x][2 * u + 1][2], s4[x][2 * u + 1][3]);
-        }
 #pragma unroll
         for (int i = 0; i < ND; ++i) {
           // row d = 16i + l16, chunk c = 8u + 4h + j4 stored at c ^ (2i + (l16 >> 3)): the
@@ -496,8 +582,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void sel_fwd_mfma_kernel(
           const uint2 lo = *reinterpret_cast<const uint2*>(vr + 16 * i1);
           const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16 * (1 - i1));
           const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          o[0][i] = Mfma<QT>::run(a, pb[0], o[0][i]);
-          o[1][i] = Mfma<QT>::run(a, pb[1], o[1][i]);
+          o[0][i] = Mfma<QT>::run(a, pb[u][0], o[0][i]);
+          o[1][i] = Mfma<QT>::run(a, pb[u][1], o[1][i]);
           if ((i & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
       }
