@@ -189,10 +189,15 @@ size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC, in
  *    the fmaf chain below); the selection is exact on these scores.
  *  - VALU path (every other input, fp32 included): score = (sum_d fmaf(q_d, k_d, acc),
  *    d ascending) * scale, bit-reproducible by a scalar fmaf loop.
- * Valid slots hold block ids in (score desc, id asc) order (+0 == -0); -1 pads rows with fewer
- * than topk visible blocks.  Invisible blocks and scores that are -inf or NaN are never
- * selected.  1 <= topk <= 128 (the reference's path A range), D <= 256.  An empty output (B, MG or H zero) launches nothing and
- * out may be NULL; NC = 0 fills out with -1. */
+ * For topk <= 128 (the reference's path A, topk.cu:584, 648-660) valid slots hold block ids in
+ * (score desc, id asc) order (+0 == -0); -1 pads rows with fewer than topk visible blocks;
+ * invisible blocks and scores that are -inf or NaN are never selected.  For 128 < topk <= 4096
+ * the reference's path B rule applies (topk.cu:741-807): each visible block is ranked by the
+ * raw order code of its score (+0 above -0; -inf and NaN ranked too, a NaN with the sign bit
+ * clear first), hidden blocks come last as -1, ties by id ascending, -1 past NC.  That path
+ * writes every row's scores to the workspace (omm_topk_workspace_bytes) and selects per row.
+ * D <= 256.  An empty output (B, MG or H zero) launches nothing and out may be NULL; NC = 0
+ * fills out with -1. */
 int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, int32_t topk, float scale,
              const omm_topk_mask* mask, int32_t* out, void* workspace, size_t workspace_bytes,
              void* stream);
@@ -226,7 +231,8 @@ size_t omm_topk_fused_noalloc_max_bytes(void);
 int omm_topk_fused_noalloc(const omm_view4* q, const omm_view4* k, int32_t dtype,
                            int32_t group_size, int32_t topk, float scale,
                            const omm_topk_mask* mask, int32_t* out, void* stream);
-/* scores: fp32 contiguous [B, MG, H, NC], already scaled; same selection and output as above. */
+/* scores: fp32 contiguous [B, MG, H, NC], already scaled; same selection and output as above
+ * (topk > 128 needs no workspace here). */
 int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, int64_t H, int64_t NC,
                          int32_t topk, const omm_topk_mask* mask, int32_t* out, void* workspace,
                          size_t workspace_bytes, void* stream);

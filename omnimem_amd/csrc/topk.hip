@@ -21,6 +21,8 @@
 //      Column chunk ids are precomputed once per workgroup in LDS.
 //   Rows whose columns are split over several workgroups (long key histories) write packed
 //   keys and a merge kernel selects again over the per-span winners.
+// topk > 128 (the reference's path B): the same scoring writes every row's scores to the
+// workspace and topk_large_kernel selects per row (radix select, then an LDS bitonic sort).
 #include "omm_common.h"
 
 #include <mutex>
@@ -465,6 +467,7 @@ struct TopkArgs {
   int vec;             // 16-byte loads allowed for q and k
   int32_t* out;
   uint64_t* part;
+  float* dump;         // set: write the scores to [B, MG, H, NC] and select nothing
   uint32_t o_sv, o_kc, o_qs, o_ks;
 };
 
@@ -642,6 +645,15 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
     }
   }
   __syncthreads();
+  if (a.dump != nullptr) {  // scoring only (topk > kMaxTopk): the selection runs per row after
+    for (int i = tid; i < kRG * n; i += kThreads) {
+      const int r = i / n, j = i - r * n, g = row0 + r;
+      if (g < a.MG)
+        a.dump[((static_cast<int64_t>(b) * a.MG + g) * a.H + h) * a.NC + c_begin + j] =
+            sc[r * span + j];
+    }
+    return;
+  }
 
   // ---- 3. selection: wave w owns rows w, w + 4, w + 8 ----
   uint64_t* wsv = sv + wave * kSurvCap;
@@ -688,6 +700,155 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
       nsplit * topk, topk, [&](int i) { return p[i]; },
       [&](int rank, uint64_t kk) { o[rank] = key_id(kk, NC); }, [&](int q) { o[q] = -1; },
       sv + wave * kSurvCap);
+}
+
+// ---- topk > 128: the reference's path B -----------------------------------------------------
+// Past 128 the reference sorts every column of a row (topk.cu:741-807): key f32_to_ord(score)
+// for a visible column and 0 for a hidden one, whose value is -1 (topk.cu:163-166, 549-559);
+// a stable descending segmented radix sort, so equal keys keep ascending column order; then
+// the first topk values, -1 past NC (topk.cu:563-581).  The key is the raw order code, unlike the
+// topk <= 128 rule: +0 ranks above -0, and visible -inf and NaN scores are ranked too (a NaN with
+// the sign bit clear above every number, one with it set level with the hidden columns).
+// One workgroup per row: the topk-th largest code by a 4-pass radix select (256-bin LDS
+// histograms over the row's codes), then the codes above it and the first codes equal to it in
+// column order, sorted in LDS by a bitonic network; their columns are written in that order.
+constexpr int kLargeTopkCap = 4096;
+constexpr int kLargeThreads = 256;
+
+__device__ __forceinline__ uint32_t f32_ord_raw(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// scores: [rows, NC] fp32 with rows = (b, g, h) in [B, MG, H] order (only the visible columns
+// are read); out: [rows, topk].
+__global__ __launch_bounds__(kLargeThreads) void topk_large_kernel(const float* __restrict__ scores,
+                                                                   int MG, int H, int NC,
+                                                                   int topk, MaskDev mk,
+                                                                   int32_t* __restrict__ out) {
+  __shared__ uint64_t keys[kLargeTopkCap];
+  __shared__ uint32_t hist[256];
+  __shared__ int sel[2];  // the chosen bin and the count in the bins above it
+  __shared__ int wcnt[kLargeThreads / kWave];
+  const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), w = tid / kWave;
+  const int64_t row = blockIdx.x;
+  const int g = static_cast<int>((row / H) % MG);
+  const float* srow = scores + row * NC;
+  const RowInfo ri = row_info(mk, g);
+  const bool simple = !mk.tf && mk.ex_sink <= 0 && mk.ex_win <= 0;
+  const int rub = row_ub(mk, ri, NC);
+  auto vis = [&](int c) { return c < rub && (simple || visible(mk, ri, col_cid(mk, c))); };
+  auto code = [&](int c) -> uint32_t { return vis(c) ? f32_ord_raw(srow[c]) : 0u; };
+  const int K = min(topk, NC);
+
+  // radix select, 8 bits a pass from the top: theta = the K-th largest code, `need` = how many
+  // codes equal to theta the first K take
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = K;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0u;  // kLargeThreads == 256 bins
+    __syncthreads();
+    for (int c = tid; c < NC; c += kLargeThreads) {
+      const uint32_t o = code(c);
+      if ((o & pmask) == prefix) atomicAdd(&hist[(o >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (w == 0) {
+      // lane l holds bins 255 - 4 l .. 252 - 4 l; running counts from the top bin down
+      uint32_t hb[4], sum = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hb[j] = hist[255 - 4 * lane - j];
+        sum += hb[j];
+      }
+      uint32_t incl = sum;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d, kWave));
+        if (lane >= d) incl += o;
+      }
+      uint32_t acc = incl - sum;
+      const uint32_t nd = static_cast<uint32_t>(need);
+      if (acc < nd && incl >= nd) {  // exactly one lane: the counts reach need inside its bins
+        for (int j = 0; j < 4; ++j) {
+          if (acc + hb[j] >= nd) {
+            sel[0] = 255 - 4 * lane - j;
+            sel[1] = static_cast<int>(acc);
+            break;
+          }
+          acc += hb[j];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(sel[0]) << shift;
+    pmask |= 255u << shift;
+    need -= sel[1];
+    __syncthreads();  // sel and hist are rewritten by the next pass
+  }
+  const uint32_t theta = prefix;
+  const int n_gt = K - need;  // codes above theta, all taken
+
+  // codes above theta in any order (sorted below), then the first `need` equal to it in column
+  // order; keys are code << 32 | (NC - 1 - column), so a larger key comes first
+  if (tid == 0) sel[0] = 0;
+  __syncthreads();
+  for (int c = tid; c < NC; c += kLargeThreads) {
+    const uint32_t o = code(c);
+    if (o > theta) {
+      const int slot = atomicAdd(&sel[0], 1);
+      keys[slot] = (static_cast<uint64_t>(o) << 32) | static_cast<uint32_t>(NC - 1 - c);
+    }
+  }
+  int base = 0;  // equal codes in earlier rounds (the same in every thread)
+  for (int c0 = 0; c0 < NC && base < need; c0 += kLargeThreads) {
+    const int c = c0 + tid;
+    const bool eq = c < NC && code(c) == theta;
+    const uint64_t m = ballot64(eq);
+    if (lane == 0) wcnt[w] = popc64(m);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int j = 0; j < kLargeThreads / kWave; ++j) {
+      before += j < w ? wcnt[j] : 0;
+      total += wcnt[j];
+    }
+    const int pos = base + before + lanes_below(m);
+    if (eq && pos < need)
+      keys[n_gt + pos] = (static_cast<uint64_t>(theta) << 32) | static_cast<uint32_t>(NC - 1 - c);
+    base += total;
+    __syncthreads();  // wcnt is rewritten by the next round
+  }
+
+  // bitonic sort of the K keys, descending; the padding keys (0) sort last, and a real key 0
+  // equals them bit for bit
+  int P = 1;
+  while (P < K) P <<= 1;
+  for (int i = K + tid; i < P; i += kLargeThreads) keys[i] = 0ull;
+  __syncthreads();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < P / 2; i += kLargeThreads) {
+        const int x = 2 * i - (i & (stride - 1)), y = x + stride;
+        const uint64_t kx = keys[x], ky = keys[y];
+        const bool desc = (x & size) == 0;
+        if (desc ? (kx < ky) : (kx > ky)) {
+          keys[x] = ky;
+          keys[y] = kx;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  int32_t* o = out + row * topk;
+  for (int p = tid; p < topk; p += kLargeThreads) {
+    int v = -1;
+    if (p < K) {
+      const int c = NC - 1 - static_cast<int>(static_cast<uint32_t>(keys[p]));
+      v = vis(c) ? c : -1;
+    }
+    o[p] = v;
+  }
 }
 
 // ---- MFMA scoring path ------------------------------------------------------------------------
@@ -1488,7 +1649,7 @@ int launch_core(TopkArgs a, int64_t B, int64_t MG, int64_t H, const Plan& p, int
                   static_cast<unsigned>(B * H));
   topk_kernel<T, MODE><<<grid, kThreads, l.total, stream>>>(a);
   int rc = check_launch("top-k");
-  if (rc != OMM_OK || p.nsplit == 1) return rc;
+  if (rc != OMM_OK || p.nsplit == 1 || a.dump != nullptr) return rc;
   const int64_t rows = B * MG * H;
   topk_merge_kernel<<<static_cast<unsigned>(cdiv64(rows, kWaves)), kThreads, 0, stream>>>(
       a.part, a.out, rows, p.nsplit, a.topk, a.NC);
@@ -1511,8 +1672,8 @@ int esize_of(int32_t dtype) { return dtype == OMM_F32 ? 4 : 2; }
 int check_sizes(int64_t B, int64_t MG, int64_t H, int64_t NC, int32_t topk, int D, int esize,
                 bool scores) {
   OMM_REQUIRE(B >= 0 && MG >= 0 && H >= 0 && NC >= 0, OMM_EINVAL, "top-k: negative size");
-  OMM_REQUIRE(topk >= 1 && topk <= kMaxTopk, OMM_EUNSUPPORTED,
-              "top-k: topk must be in [1, %d], got %d", kMaxTopk, topk);
+  OMM_REQUIRE(topk >= 1 && topk <= kLargeTopkCap, OMM_EUNSUPPORTED,
+              "top-k: topk must be in [1, %d], got %d", kLargeTopkCap, topk);
   OMM_REQUIRE(B * H <= 65535 && cdiv64(MG, kRG) <= 2147483647ll && MG <= 2147483647ll,
               OMM_EUNSUPPORTED, "top-k: B*H must be <= 65535");
   const int64_t cap = static_cast<int64_t>(span_cap(D, esize, scores)) * kMaxSplit;
@@ -1547,6 +1708,23 @@ void set_k(TopkArgs& a, const omm_view4& k) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// topk > kMaxTopk: every row's scores go to the workspace ([B, MG, H, NC] fp32), then one
+// workgroup per row selects (topk_large_kernel)
+size_t large_ws_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC) {
+  return align256(static_cast<size_t>(B * MG * H) * static_cast<size_t>(NC) * sizeof(float));
+}
+
+int launch_large(const float* scores, int64_t B, int64_t MG, int64_t H, int64_t NC, int topk,
+                 const omm_topk_mask& mask, int32_t* out, hipStream_t s) {
+  const int64_t rows = B * MG * H;
+  OMM_REQUIRE(rows <= 2147483647ll && MG <= 2147483647ll && NC <= 2147483647ll,
+              OMM_EUNSUPPORTED, "top-k: %lld rows exceed the grid", (long long)rows);
+  topk_large_kernel<<<static_cast<unsigned>(rows), kLargeThreads, 0, s>>>(
+      scores, static_cast<int>(MG), static_cast<int>(H), static_cast<int>(NC), topk,
+      to_dev(mask), out);
+  return check_launch("top-k (topk > 128)");
+}
 
 // ---- MFMA path planning ---------------------------------------------------------------------
 inline bool m2_view_ok(const omm_view4& v) {
@@ -1648,7 +1826,8 @@ M2Args m2_args(const omm_view4& q, const omm_view4& k, int64_t MG, int64_t H, in
 
 extern "C" size_t omm_topk_workspace_bytes(int64_t B, int64_t MG, int64_t H, int64_t NC,
                                            int32_t topk) {
-  if (B <= 0 || MG <= 0 || H <= 0 || NC <= 0 || topk < 1 || topk > omm::kMaxTopk) return 0;
+  if (B <= 0 || MG <= 0 || H <= 0 || NC <= 0 || topk < 1 || topk > omm::kLargeTopkCap) return 0;
+  if (topk > omm::kMaxTopk) return omm::large_ws_bytes(B, MG, H, NC);
   // the split plan does not depend on the head dim beyond the LDS cap; use the smallest cap
   // (fp32, D = 256) so the answer covers every dtype and head dim
   size_t ws = 0;
@@ -1688,6 +1867,21 @@ extern "C" int omm_topk(const omm_view4* q, const omm_view4* k, int32_t dtype, i
     const M2Args a = m2_args(*q, *k, MG, H, NC, topk, scale, *mask, out, workspace, nullptr);
     return launch_m2<false>(dtype, static_cast<int>(D), a, B, H, p, s);
   }
+  if (topk > kMaxTopk) {  // scores to the workspace, then the per-row selection
+    const size_t need = large_ws_bytes(B, MG, H, NC);
+    OMM_REQUIRE(workspace != nullptr && need <= workspace_bytes, OMM_EWORKSPACE,
+                "omm_topk: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    float* sc = static_cast<float*>(workspace);
+    const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
+    TopkArgs a = base_args(MG, H, NC, static_cast<int>(D), topk, scale, *mask, out, nullptr);
+    set_q(a, *q);
+    set_k(a, *k);
+    a.vec = vec_ok(*q, es) && vec_ok(*k, es);
+    a.dump = sc;
+    rc = launch_typed<kModePooled>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
+    if (rc) return rc;
+    return launch_large(sc, B, MG, H, NC, topk, *mask, out, s);
+  }
   const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
   OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
               OMM_EWORKSPACE, "omm_topk: workspace of %zu bytes required, got %zu", p.ws_part,
@@ -1704,7 +1898,7 @@ extern "C" size_t omm_topk_fused_workspace_bytes(int64_t B, int64_t T, int64_t H
                                                  int32_t dtype) {
   using namespace omm;
   if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || NC <= 0 || group_size < 1 || topk < 1 ||
-      topk > omm::kMaxTopk)
+      topk > omm::kLargeTopkCap)
     return 0;
   const int64_t MG = cdiv64(T, group_size);
   const int es = esize_of(dtype);
@@ -1773,6 +1967,31 @@ int topk_fused_impl(const omm_view4* q, const omm_view4* k, int32_t dtype, int32
               "omm_topk_fused_debug: the score dump exists on the MFMA path only (bf16 / f16, "
               "head dim 64 or 128, unit dim strides, 16-byte aligned rows)");
 
+  if (topk > kMaxTopk) {  // pool, scores to the workspace, then the per-row selection
+    const size_t pooled_bytes = align256(static_cast<size_t>(B * MG * H * D) * es);
+    const size_t need = pooled_bytes + large_ws_bytes(B, MG, H, NC);
+    OMM_REQUIRE(workspace != nullptr && need <= workspace_bytes, OMM_EWORKSPACE,
+                "omm_topk_fused: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    omm_view4 pooled{};
+    pooled.data = workspace;
+    pooled.size[0] = B; pooled.size[1] = MG; pooled.size[2] = H; pooled.size[3] = D;
+    pooled.stride[3] = 1; pooled.stride[2] = D; pooled.stride[1] = H * D;
+    pooled.stride[0] = MG * H * D;
+    OMM_REQUIRE(MG <= 65535 && B <= 65535, OMM_EUNSUPPORTED, "omm_topk_fused: grid limit");
+    rc = pool_launch(*q, pooled, dtype, group_size, s);
+    if (rc) return rc;
+    float* sc = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + pooled_bytes);
+    const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, false);
+    TopkArgs a = base_args(MG, H, NC, static_cast<int>(D), topk, scale, *mask, out, nullptr);
+    set_q(a, pooled);
+    set_k(a, *k);
+    a.vec = vec_ok(pooled, es) && vec_ok(*k, es);
+    a.dump = sc;
+    rc = launch_typed<kModePooled>(dtype, a, B, MG, H, p, static_cast<int>(D), s);
+    if (rc) return rc;
+    return launch_large(sc, B, MG, H, NC, topk, *mask, out, s);
+  }
+
   const bool vec = vec_ok(*q, es) && vec_ok(*k, es);
   if (vec && fused_ok(B, MG, H, NC, static_cast<int>(D), es)) {
     const Plan p = make_plan(B, MG, H, NC, topk, static_cast<int>(D), es, false, true);
@@ -1839,6 +2058,7 @@ extern "C" int omm_topk_from_scores(const float* scores, int64_t B, int64_t MG, 
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (NC == 0) return fill_i32(out, B * MG * H * topk, -1, s);
   OMM_REQUIRE(scores != nullptr, OMM_EINVAL, "omm_topk_from_scores: null scores");
+  if (topk > kMaxTopk) return launch_large(scores, B, MG, H, NC, topk, *mask, out, s);
   const Plan p = make_plan(B, MG, H, NC, topk, 128, 4, true, false);
   OMM_REQUIRE(p.ws_part <= workspace_bytes && (p.ws_part == 0 || workspace != nullptr),
               OMM_EWORKSPACE, "omm_topk_from_scores: workspace of %zu bytes required, got %zu",

@@ -15,6 +15,8 @@ wuyushuwys/OmniMem):
                               fixed fmaf order of nsa_oracle.c.
 * ``topk_select``          -- visibility (cuda_backend/csrc/topk.cu:36-97) and ordering
                               (topk.cu:3,100-102; ops.h:11-12), in nsa_oracle.c.
+* ``topk_select_large``    -- the rule past topk = 128 (path B, topk.cu:741-807): raw order codes,
+                              hidden columns as key 0 / value -1, a stable descending sort.
 * ``selection_attention``  -- dense selection attention (cuda_backend/csrc/common.cuh:158-190,
                               :327-332; selection_fwd.cu:1-3,218) as a float64 softmax over the
                               gathered token set; duplicated ids count twice, as in the kernel.
@@ -190,6 +192,27 @@ def topk_select(scores: np.ndarray, topk: int, mask: Mask) -> np.ndarray:
     m = mask.c()
     lib().orc_topk(_ptr(s, ctypes.c_float), B, MG, H, NC, topk, ctypes.byref(m),
                    _ptr(out, ctypes.c_int32))
+    return out
+
+
+def topk_select_large(scores: np.ndarray, topk: int, mask: Mask) -> np.ndarray:
+    """The reference's rule past topk = 128 (path B, cuda_backend/csrc/topk.cu:741-807): per row,
+    key f32_to_ord(score) (topk.cu:163-166) for a visible column and 0 for a hidden one, whose
+    value is -1 (:549-559); a stable descending sort of the keys (CUB segmented radix sort, so
+    equal keys keep ascending column order); the first topk values, -1 past NC (:563-581).  The
+    raw order code ranks +0 above -0 and ranks visible -inf and NaN scores as well."""
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    B, MG, H, NC = s.shape
+    vis = visible_matrix(mask, MG, NC)[None, :, None, :]
+    u = s.view(np.uint32)
+    code = np.where((u & np.uint32(0x80000000)) != 0, ~u, u | np.uint32(0x80000000))
+    code = np.where(vis, code, np.uint32(0)).astype(np.int64)
+    val = np.broadcast_to(np.where(vis, np.arange(NC, dtype=np.int32), np.int32(-1)), s.shape)
+    order = np.argsort(-code, axis=-1, kind="stable")
+    ranked = np.take_along_axis(val, order, axis=-1)
+    out = np.full((B, MG, H, topk), -1, dtype=np.int32)
+    n = min(topk, NC)
+    out[..., :n] = ranked[..., :n]
     return out
 
 

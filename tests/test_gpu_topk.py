@@ -130,13 +130,85 @@ def test_parallel_nsa_topk_fused_large_topk_bitexact(dtype, topk):
             assert (got[:, :8] == -1).any()  # early rows see fewer than topk blocks
 
 
-def test_topk_above_128_rejected():
+def test_topk_above_cap_rejected():
     from omnimem_amd.backend import NSABackendError
     from omnimem_amd.index_topk import parallel_nsa_topk
     q = torch.zeros((1, 128, 1, 64), device=DEV)
     k = torch.zeros((1, 300, 1, 64), device=DEV)
-    with pytest.raises(NSABackendError, match="128"):
-        parallel_nsa_topk(q, k, 129, block_size=64, chunk_size=64, causal=False, group_size=64)
+    with pytest.raises(NSABackendError, match="4096"):
+        parallel_nsa_topk(q, k, 4097, block_size=64, chunk_size=64, causal=False, group_size=64)
+
+
+@pytest.mark.parametrize("mask", list(MASKS))
+@pytest.mark.parametrize("topk", [129, 300])
+@pytest.mark.parametrize("NC", [37, 512, 5850])
+def test_topk_from_scores_above_128_bitexact(mask, topk, NC):
+    """topk past 128 follows the reference's path B (topk.cu:741-807): raw order codes, so -0,
+    -inf and NaN scores of visible blocks are ranked; hidden blocks give -1; -1 past NC."""
+    from omnimem_amd.index_topk import topk_from_scores
+    mk = MASKS[mask]
+    B, MG, H = 1, 74, 3
+    s = _scores_case(zlib.crc32(f"large/{mask}/{topk}/{NC}".encode()) & 0xFFFF, B, MG, H, NC)
+    G = mk["group_size"]
+    got = topk_from_scores(torch.from_numpy(s).to(DEV), topk, mk["block_size"], mk["chunk_q"] // G
+                           if mk["chunk_q"] % G == 0 else mk["chunk_q"], mk["chunk_k"],
+                           bool(mk["causal"]), ex_win=mk.get("ex_win", 0),
+                           ex_sink=mk.get("ex_sink", 0), prog_excl=bool(mk.get("prog_excl", 0)),
+                           q_chunk_offset=mk.get("q_chunk_offset", 0), group_size=G
+                           if mk["chunk_q"] % G == 0 else 1,
+                           blocks_per_chunk=mk.get("blocks_per_chunk", 0)).cpu().numpy()
+    om = O.Mask(**mk)
+    if mk["chunk_q"] % G != 0:
+        om.group_size = 1
+    np.testing.assert_array_equal(got, O.topk_select_large(s, topk, om))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("topk", [129, 700])
+def test_parallel_nsa_topk_fused_above_128_bitexact(dtype, topk):
+    """Fused pooling + scoring with topk past 128: the scores of every row go to the workspace
+    (the fmaf chain, across split column spans for the 5920-block AR history) and one
+    workgroup per row selects; bit-exact against the oracle's scores under path B's rule.  On
+    these finite scores the first 128 ids equal the topk = 128 call's."""
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    g = torch.Generator().manual_seed(topk)
+    B, H, D = 1, 2, 128
+    for T, NC, chunk, causal, qoff, exw in ((4680, 5920, 4680, False, 80, 3),
+                                            (2048, 600, 512, True, 0, 0)):
+        q = torch.randn((B, T, H, D), generator=g).to(dtype)
+        k = torch.randn((B, NC, H, D), generator=g).to(dtype)
+        bpc = 74 if not causal else 0
+        kw = dict(block_size=64, chunk_size=chunk, causal=causal, exclude_window_chunks=exw,
+                  progressive_exclude=not causal, q_chunk_offset=qoff, blocks_per_chunk=bpc,
+                  group_size=64)
+        got = parallel_nsa_topk(q.to(DEV), k.to(DEV), topk, **kw).cpu().numpy()
+        mask = O.Mask(block_size=64, group_size=64, chunk_q=chunk, chunk_k=chunk,
+                      blocks_per_chunk=bpc, q_chunk_offset=qoff, ex_win=exw,
+                      causal=int(causal), prog_excl=int(not causal))
+        dt = "bf16" if dtype == torch.bfloat16 else "f32"
+        scores = O.block_scores(O.pool_mean(_img(q), 64, dt), _img(k), D ** -0.5)
+        np.testing.assert_array_equal(got, O.topk_select_large(scores, topk, mask))
+        small = parallel_nsa_topk(q.to(DEV), k.to(DEV), 128, **kw).cpu().numpy()
+        np.testing.assert_array_equal(got[..., :128], small)
+
+
+def test_topk_pooled_op_above_128_bitexact():
+    """The pooled-rows op (omm_topk) with topk past 128: top-200 of 300 visible blocks, and a
+    causal case whose rows see at most 10 blocks and pad with -1."""
+    from omnimem_amd.index_topk import topk as topk_op
+    g = torch.Generator().manual_seed(5)
+    B, MG, H, D, NC = 2, 40, 3, 64, 300
+    q = torch.randn((B, MG, H, D), generator=g)
+    k = torch.randn((B, NC, H, D), generator=g)
+    scores = O.block_scores(_img(q), _img(k), 0.125)
+    for causal, cq, ck in ((False, 64, 64), (True, 8, 128)):
+        got = topk_op(q.to(DEV), k.to(DEV), 200, 0.125, 64, cq, ck, causal).cpu().numpy()
+        mask = O.Mask(block_size=64, group_size=1, chunk_q=cq, chunk_k=ck, causal=int(causal))
+        np.testing.assert_array_equal(got, O.topk_select_large(scores, 200, mask))
+        if causal:
+            assert (got[..., 10:] == -1).all() and (got[..., :2] >= 0).all()
+        else:
+            assert (got >= 0).all()
 
 
 def test_topk_tf_mask_bitexact():

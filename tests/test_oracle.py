@@ -211,6 +211,37 @@ def test_topk_fewer_visible_than_k_pads_minus_one():
     assert sorted(got[0, 0, 0, :3].tolist()) == [0, 1, 2] and (got[0, 0, 0, 3:] == -1).all()
 
 
+def test_topk_select_large_known_answer():
+    """Past topk = 128 the reference ranks raw order codes (topk.cu:163-166) with hidden columns
+    as key 0 / value -1, sorted stably (topk.cu:741-807).  Row 6 of a causal mask with one-column
+    chunks sees columns 0..6; the expected order is read off those rules: +NaN (code 0xffc00000)
+    first, then 2.0, 1.0, +0 above -0, -inf (code 0x007fffff), then the code-0 tie in column
+    order: the visible -NaN 0xffffffff (column 6) and the hidden column 7, which gives -1, then
+    -1 past NC."""
+    m = O.Mask(block_size=1, group_size=1, chunk_q=1, chunk_k=1, causal=1)
+    s = np.zeros((1, 8, 1, 8), np.float32)
+    row = np.array([1.0, 0.0, -np.inf, -0.0, 0.0, 2.0, 0.0, 5.0], np.float32)
+    bits = row.view(np.uint32)
+    bits[1] = 0x7FC00000  # +NaN
+    bits[6] = 0xFFFFFFFF  # -NaN with every mantissa bit set: code 0
+    s[0, 6, 0] = row
+    got = O.topk_select_large(s, 10, m)[0, 6, 0]
+    np.testing.assert_array_equal(got, [1, 5, 0, 4, 3, 2, 6, -1, -1, -1])
+
+
+@pytest.mark.parametrize("topk", [5, 60, 400])
+def test_topk_select_large_agrees_with_the_small_rule_on_finite_scores(topk):
+    """On finite scores without -0 both rules order by (score desc, id asc) over the visible
+    columns: the numpy sort of path B and the C qsort of path A agree wherever the row has at
+    least topk visible columns, and path B pads with -1 (hidden columns) where it has fewer."""
+    rng = np.random.default_rng(20 + topk)
+    B, MG, H, NC = 1, 37, 2, 300
+    s = rng.integers(-6, 6, size=(B, MG, H, NC)).astype(np.float32) * 0.5  # many ties
+    s[s == 0] = 0.25
+    m = O.Mask(block_size=16, group_size=4, chunk_q=64, chunk_k=64, causal=1)
+    np.testing.assert_array_equal(O.topk_select_large(s, topk, m), O.topk_select(s, topk, m))
+
+
 # ---------------------------------------------------------------- attention
 def _sdpa64(q, k, v, mask):
     qt, kt, vt = (torch.from_numpy(np.asarray(a, np.float64)) for a in (q, k, v))
