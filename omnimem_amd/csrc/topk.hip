@@ -16,7 +16,8 @@
 //      owns 4 rows, and every score is fmaf over d ascending from 0, then * scale, so the fp32
 //      score is a fixed function of its inputs (reproduced bit for bit by the C oracle).
 //   3. selection, one wave per row: keys in registers; theta = topk-th largest score word of the
-//      64 per-lane maxima (ranked across lanes); only keys at or above it survive;
+//      64 per-lane maxima (ranked across lanes), past topk 64 the exact topk-th largest score
+//      word (wave radix select); only keys at or above it survive;
 //      each survivor's exact rank among survivors is counted from LDS; rank < topk is written.
 //      Column chunk ids are precomputed once per workgroup in LDS.
 //   Rows whose columns are split over several workgroups (long key histories) write packed
@@ -37,6 +38,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsPerWave = kRG / kWaves;
 constexpr int kTileC = 64;              // key columns per LDS tile
 constexpr int kSurvCap = 256;           // survivor slots per wave
+static_assert(kSurvCap % 64 == 0, "survivors are ranked 8 at a time, a wave's 64 lanes each");
 constexpr int kSpanCap = 1024;          // columns per workgroup
 constexpr int kMaxSplit = 64;
 constexpr int kMaxTopk = 128;           // the reference's path A bound (topk.cu:584, 648-660)
@@ -176,40 +178,72 @@ __device__ __forceinline__ uint32_t lane_max_threshold(uint32_t v, int topk, uin
   return theta;
 }
 
-// The same threshold from the two largest values of every lane (v1 >= v2), for 64 < topk <= 128:
-// the topk-th largest of the 128 values.  Every key whose high word is below it has at least
-// topk larger keys, and at least topk keys reach it whenever topk lane values are non-zero.
-// scratch: 128 words of wave-private LDS.
-__device__ __forceinline__ uint32_t lane_max2_threshold(uint32_t v1, uint32_t v2, int topk,
-                                                        uint32_t* scratch) {
+// For 64 < topk <= 128: the exact topk-th largest high word among the wave's candidates, by a
+// radix select over the 32-bit high words (4 passes of 8 bits, each a 256-bin histogram in the
+// wave's LDS scratch and a scan of the bins from the top), so that about topk keys survive.  1
+// when fewer than topk candidates exist (every candidate passes: candidates have a high word
+// >= 1).  hi(j, ok) gives the high word of the lane's j-th key (j < nper) and whether it is a
+// candidate.  scratch: 256 words of wave-private LDS.
+template <typename HiF>
+__device__ __forceinline__ uint32_t wave_radix_threshold(int nper, int topk, HiF hi,
+                                                         uint32_t* scratch) {
   const int lane = lane_id();
-  scratch[lane] = v1;
-  scratch[kWave + lane] = v2;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int c1 = 0, c2 = 0;
-#pragma unroll 8
-  for (int j = 0; j < 2 * kWave / 4; ++j) {
-    const uint4 w = reinterpret_cast<const uint4*>(scratch)[j];
-    c1 += (w.x >= v1 ? 1 : 0) + (w.y >= v1 ? 1 : 0) + (w.z >= v1 ? 1 : 0) + (w.w >= v1 ? 1 : 0);
-    c2 += (w.x >= v2 ? 1 : 0) + (w.y >= v2 ? 1 : 0) + (w.z >= v2 ? 1 : 0) + (w.w >= v2 ? 1 : 0);
+  uint32_t prefix = 0u, pmask = 0u;
+  uint32_t need = static_cast<uint32_t>(topk);
+  for (int shift = 24; shift >= 0; shift -= 8) {
+#pragma unroll
+    for (int j = 0; j < 256 / kWave; ++j) scratch[lane + kWave * j] = 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int j = 0; j < nper; ++j) {
+      bool ok;
+      const uint32_t h = hi(j, ok);
+      if (ok && (h & pmask) == prefix) atomicAdd(&scratch[(h >> shift) & 255u], 1u);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane l holds bins 255 - 4 l .. 252 - 4 l; running counts from the top bin down
+    uint32_t hb[4], sum = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hb[j] = scratch[255 - 4 * lane - j];
+      sum += hb[j];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d, kWave));
+      if (lane >= d) incl += o;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // scratch is rewritten next
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+    if (shift == 24 && total < need) return 1u;  // wave-uniform
+    uint32_t acc = incl - sum;
+    const bool cross = acc < need && incl >= need;  // exactly one lane
+    int bin = 0;
+    uint32_t above = 0u;
+    if (cross) {
+      for (int j = 0; j < 4; ++j) {
+        if (acc + hb[j] >= need) {
+          bin = 255 - 4 * lane - j;
+          above = acc;
+          break;
+        }
+        acc += hb[j];
+      }
+    }
+    const int cl = __builtin_ctzll(ballot64(cross));
+    bin = __builtin_amdgcn_readlane(bin, cl);
+    above = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(above), cl));
+    prefix |= static_cast<uint32_t>(bin) << shift;
+    pmask |= 255u << shift;
+    need -= above;
   }
-  const uint32_t t1 = c1 >= topk ? v1 : 0u, t2 = c2 >= topk ? v2 : 0u;
-  const uint32_t theta = wave_max_u32(t1 > t2 ? t1 : t2);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  return theta;
-}
-
-__device__ __forceinline__ void track_top2(uint32_t hi, uint32_t& m1, uint32_t& m2) {
-  if (hi > m1) {
-    m2 = m1;
-    m1 = hi;
-  } else if (hi > m2) {
-    m2 = hi;
-  }
+  return prefix;
 }
 
 template <int PER, typename KeyF, typename EmitF, typename PadF>
@@ -218,19 +252,26 @@ __device__ __forceinline__ void wave_select_impl(int n, int topk, KeyF key, Emit
   const int lane = lane_id();
   // keys of slots j * 64 + lane; slots past n read candidate n - 1 (in bounds) and count as 0
   uint64_t kv[PER];
-  uint32_t lmax = 0, lmax2 = 0;  // high words of the lane's two largest keys
+  uint32_t lmax = 0;  // high word of the lane's largest key
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = j * kWave + lane;
     const uint64_t k = key(i < n ? i : n - 1);
     kv[j] = i < n ? k : 0ull;
-    track_top2(static_cast<uint32_t>(kv[j] >> 32), lmax, lmax2);
+    const uint32_t h = static_cast<uint32_t>(kv[j] >> 32);
+    lmax = h > lmax ? h : lmax;
   }
   // theta: the topk-th largest lane maximum (0 if fewer than topk lanes hold candidates); past
-  // 64, the topk-th largest of the lanes' two largest
+  // 64, the exact topk-th largest high word
   const uint32_t theta = topk <= kWave
       ? lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv))
-      : lane_max2_threshold(lmax, lmax2, topk, reinterpret_cast<uint32_t*>(sv));
+      : wave_radix_threshold(
+            PER, topk,
+            [&](int j, bool& ok) {
+              ok = kv[j] != 0ull;
+              return static_cast<uint32_t>(kv[j] >> 32);
+            },
+            reinterpret_cast<uint32_t*>(sv));
 
   int ns = 0;
 #pragma unroll
@@ -263,12 +304,34 @@ __device__ __forceinline__ void wave_select_impl(int n, int topk, KeyF key, Emit
     }
     if (lane < ns && rank < topk) emit(rank, mine);
   } else if (ns <= kSurvCap) {
-    for (int i = lane; i < ns; i += kWave) {
-      const uint64_t k = sv[i];
-      int rank = 0;
-      for (int j = 0; j < ns; ++j) rank += (sv[j] > k) ? 1 : 0;
-      if (rank < topk) emit(rank, k);
+    // lane ranks survivors lane, lane + 64, ... against all of them, 8 broadcast keys a round
+    // for all of its survivors at once; slots from ns up to the next multiple of 8 read as 0
+    constexpr int MS = kSurvCap / kWave;
+    uint64_t mine[MS];
+    int rank[MS];
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+      const int i = lane + kWave * m;
+      mine[m] = i < ns ? sv[i] : 0ull;
+      rank[m] = 0;
     }
+    if (lane < ((ns + 7) & ~7) - ns) sv[ns + lane] = 0ull;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int j = 0; j < ns; j += 8) {
+      ulonglong2 w8[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w8[q] = reinterpret_cast<const ulonglong2*>(sv + j)[q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int m = 0; m < MS; ++m)
+          rank[m] += (w8[q].x > mine[m] ? 1 : 0) + (w8[q].y > mine[m] ? 1 : 0);
+    }
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+      if (lane + kWave * m < ns && rank[m] < topk) emit(rank[m], mine[m]);
   } else {
     // too many survivors for the buffer (massive score ties): extract the maxima one at a
     // time, each a wave-wide max over the keys below the previous one
@@ -305,14 +368,25 @@ __device__ __forceinline__ void wave_select_stream(int n, int topk, KeyF key, Em
                                                    PadF pad, uint64_t* sv) {
   const int lane = lane_id();
   const int per = (n + kWave - 1) / kWave;
-  uint32_t lmax = 0, lmax2 = 0;
+  uint32_t lmax = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
-    if (i < n) track_top2(static_cast<uint32_t>(key(i) >> 32), lmax, lmax2);
+    if (i < n) {
+      const uint32_t h = static_cast<uint32_t>(key(i) >> 32);
+      lmax = h > lmax ? h : lmax;
+    }
   }
   const uint32_t theta = topk <= kWave
       ? lane_max_threshold(lmax, topk, reinterpret_cast<uint32_t*>(sv))
-      : lane_max2_threshold(lmax, lmax2, topk, reinterpret_cast<uint32_t*>(sv));
+      : wave_radix_threshold(
+            per, topk,
+            [&](int j, bool& ok) {
+              const int i = j * kWave + lane;
+              const uint64_t k = i < n ? key(i) : 0ull;
+              ok = k != 0ull;
+              return static_cast<uint32_t>(k >> 32);
+            },
+            reinterpret_cast<uint32_t*>(sv));
   int ns = 0;
   for (int j = 0; j < per; ++j) {
     const int i = j * kWave + lane;
