@@ -215,9 +215,16 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
         p4[1][t] = Mfma<QT>::run(av, db[1][s], p4[1][t]);
       }
     }
-    // dS / scale = P (dP - delta), P = 2^(s c2 - lse log2 e); keys past n_cur are not visible
-    // (the scale multiplies the dQ sums once at the end).  The mask is a wave-uniform branch
-    // taken by partial tiles only, so full tiles pay nothing for it.
+    // dS / scale = P (dP - delta), P = 2^e, e = s c2 - lse log2 e (the scale multiplies the dQ
+    // sums once at the end).  Keys past n_cur are not visible: a wave-uniform branch taken by
+    // partial tiles only sets their e to -inf, so P = 0 whatever the sign of c2 (a negative
+    // scale makes c2 negative: -inf in s would give e = +inf).
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s4[x][t][r] = __builtin_fmaf(s4[x][t][r], c2, nl2[x]);
     if (n_cur < TK) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -230,10 +237,8 @@ __global__ __launch_bounds__(kDqThreads, 2) void sel_bwd_dq_kernel(
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[x][t][r], c2, nl2[x]));
-          s4[x][t][r] = -(p * p4[x][t][r]);
-        }
+        for (int r = 0; r < 4; ++r)
+          s4[x][t][r] = -(__builtin_amdgcn_exp2f(s4[x][t][r]) * p4[x][t][r]);
     // dQ^T += K^T dS^T; k-slot e of lane group j4 is key 32 u + 4 j4 + e (e < 4) or
     // 32 u + 16 + 4 j4 + (e - 4), for both operands
 #pragma unroll

@@ -199,6 +199,31 @@ def test_sel_bwd_negative_scale_and_determinism():
         assert torch.equal(a, b2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_sel_bwd_negative_scale_partial_blocks(dtype, D):
+    """A negative scale with a partial last block (N = 343: block 5 holds 23 tokens) and a
+    causal chunk that ends inside a block: the dQ kernel's masked keys must get P = 0 whichever
+    sign the scale has (regression: masking the scores with -inf before the negative scale
+    turned them into +inf)."""
+    M, N, H, G, BS, T = 207, 343, 2, 64, 64, 5
+    gen = torch.Generator().manual_seed(D + 3)
+    q, k, v = (torch.randn((1, L, H, D), generator=gen).to(dtype) for L in (M, N, N))
+    ids = _ids(gen, 1, -(-M // G), H, T, -(-N // BS), 0.1)
+    for causal, chunk in ((False, 1), (True, 150)):
+        out, lse, do, dq, dk, dv, scale = _run(q, k, v, ids, G, BS, causal, chunk, dtype,
+                                               scale=-D ** -0.5)
+        want = O.selection_attention_bwd(q.double().numpy(), k.double().numpy(),
+                                         v.double().numpy(), ids.numpy(),
+                                         out.double().cpu().numpy(), lse.double().cpu().numpy(),
+                                         do.double().numpy(), G, scale,
+                                         O.dense_block_tokens(N, BS, chunk, causal),
+                                         chunk_size=chunk, causal=causal)
+        for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
+            assert torch.isfinite(got).all(), name
+            _close(name, got, w)
+
+
 def test_selection_attention_autograd_matches_exact_gradient():
     """Facade with requires_grad: loss.backward() through the autograd function, against the
     oracle's gradient of its own exact forward."""

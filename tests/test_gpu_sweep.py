@@ -1,0 +1,132 @@
+"""Seeded random sweep over the selection path's argument space, each case against the oracle.
+
+Every case draws its shape and options from its own seed, so a failure names a reproducible
+configuration: the selection forward (dtypes, head dims 64 / 96 / 128, group sizes up to 192,
+block sizes 16..100, ragged tails, chunk-causal masks, -1 / out-of-range / duplicate ids,
+negative scales) against the float64 oracle at the BASELINE tolerances; its backward against the
+oracle's exact gradient; and the top-k selection from given scores (ties, -0, -inf, NaN) for
+topk 1..600 against the oracle's rule (path A to 128, path B past it).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import nsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FWD_TOL = {torch.bfloat16: (2e-2, 1e-3), torch.float16: (2e-2, 1e-3), torch.float32: (1e-4, 1e-5)}
+BWD_TOL = {torch.bfloat16: (2e-2, 5e-3), torch.float16: (2e-2, 5e-3), torch.float32: (1e-4, 1e-5)}
+DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _case(seed, max_m, max_n, max_t):
+    r = np.random.default_rng(seed)
+    dtype = DTYPES[r.integers(0, 3)]
+    D = int(r.choice([64, 128, 128, 64, 96]))
+    H = int(r.integers(1, 4))
+    G = int(r.choice([16, 30, 64, 64, 100, 128, 192]))
+    BS = int(r.choice([16, 32, 64, 64, 100]))
+    M = int(r.integers(1, max_m + 1))
+    N = int(r.integers(BS // 2 + 1, max_n + 1))
+    nb = -(-N // BS)
+    T = int(r.integers(1, min(max_t, nb + 2) + 1))
+    causal = bool(r.integers(0, 2))
+    chunk = int(r.integers(BS, max(BS + 1, N))) if causal else 1
+    minus = float(r.choice([0.0, 0.1, 0.3]))
+    dup = bool(r.integers(0, 2))
+    sgn = float(r.choice([1.0, 1.0, -1.0]))
+    return dict(dtype=dtype, D=D, H=H, G=G, BS=BS, M=M, N=N, nb=nb, T=T, causal=causal,
+                chunk=chunk, minus=minus, dup=dup, scale=sgn * D ** -0.5)
+
+
+def _inputs(c, seed):
+    gen = torch.Generator().manual_seed(seed)
+    M, N, H, D, dt = c["M"], c["N"], c["H"], c["D"], c["dtype"]
+    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(dt)
+    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(dt)
+    v = torch.randn((1, N, H, D), generator=gen).to(dt)
+    MG = -(-M // c["G"])
+    ids = torch.randint(-1, c["nb"], (1, MG, H, c["T"]), generator=gen, dtype=torch.int32)
+    ids[torch.rand(ids.shape, generator=gen) < c["minus"]] = -1
+    if c["dup"] and c["T"] > 1:
+        ids[..., 1] = ids[..., 0]
+    return q, k, v, ids
+
+
+def _desc(c):
+    return ", ".join(f"{k}={v}" for k, v in c.items())
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_sel_fwd_sweep(seed):
+    from omnimem_amd.selection import sel_fwd
+    c = _case(7000 + seed, 400, 1500, 12)
+    q, k, v, ids = _inputs(c, seed)
+    out, lse = sel_fwd(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), c["BS"], c["chunk"],
+                       c["scale"], c["causal"], c["G"])
+    want_o, want_l = O.selection_attention(
+        q.float().numpy(), k.float().numpy(), v.float().numpy(), ids.numpy(), c["G"], c["scale"],
+        O.dense_block_tokens(c["N"], c["BS"], c["chunk"], c["causal"]), chunk_size=c["chunk"],
+        causal=c["causal"])
+    o = out.float().cpu().numpy().astype(np.float64)
+    l = lse.cpu().numpy().astype(np.float64)
+    mx, mean = FWD_TOL[c["dtype"]]
+    err = np.abs(o - want_o)
+    assert err.max() <= mx and err.mean() <= mean, (
+        f"{_desc(c)}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
+    assert np.array_equal(np.isneginf(l), np.isneginf(want_l)), _desc(c)
+    fin = ~np.isneginf(want_l)
+    if fin.any():
+        assert np.abs(l[fin] - want_l[fin]).max() <= 1e-3, _desc(c)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_sel_bwd_sweep(seed):
+    from omnimem_amd.selection import sel_bwd, sel_fwd
+    c = _case(8000 + seed, 256, 800, 8)
+    q, k, v, ids = _inputs(c, seed)
+    qd, kd, vd, idd = (x.to(DEV) for x in (q, k, v, ids))
+    out, lse = sel_fwd(qd, kd, vd, idd, c["BS"], c["chunk"], c["scale"], c["causal"], c["G"])
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(seed + 1)).to(c["dtype"])
+    dq, dk, dv = sel_bwd(qd, kd, vd, idd, out, lse, do.to(DEV), c["BS"], c["chunk"], c["scale"],
+                         c["causal"], c["G"])
+    want = O.selection_attention_bwd(
+        q.double().numpy(), k.double().numpy(), v.double().numpy(), ids.numpy(),
+        out.double().cpu().numpy(), lse.double().cpu().numpy(), do.double().numpy(), c["G"],
+        c["scale"], O.dense_block_tokens(c["N"], c["BS"], c["chunk"], c["causal"]),
+        chunk_size=c["chunk"], causal=c["causal"])
+    mx, mean = BWD_TOL[c["dtype"]]
+    for name, got, w in (("dq", dq, want[0]), ("dk", dk, want[1]), ("dv", dv, want[2])):
+        g = got.float().cpu().numpy().astype(np.float64)
+        if not np.abs(w).max() > 0:
+            assert not np.abs(g).max() > 0, f"{name}: {_desc(c)}"
+            continue
+        err = np.abs(g - w)
+        assert err.max() <= mx * np.abs(w).max(), f"{name} max-abs {err.max():.3e}: {_desc(c)}"
+        assert err.mean() <= mean * np.abs(w).mean(), f"{name} mean-abs {err.mean():.3e}: {_desc(c)}"
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_topk_from_scores_sweep(seed):
+    from omnimem_amd.index_topk import topk_from_scores
+    r = np.random.default_rng(9000 + seed)
+    MG, H, NC = int(r.integers(1, 101)), int(r.integers(1, 4)), int(r.integers(1, 3001))
+    topk = int(r.choice([int(r.integers(1, 17)), int(r.integers(17, 65)),
+                         int(r.integers(65, 129)), int(r.integers(129, 601))]))
+    bs = int(r.choice([16, 30, 64]))
+    chunk = int(bs * r.integers(1, 6))
+    causal = bool(r.integers(0, 2))
+    ex_win = int(r.integers(0, 3)) if not causal else 0
+    mk = dict(block_size=bs, group_size=1, chunk_q=chunk, chunk_k=chunk, causal=int(causal),
+              ex_win=ex_win, prog_excl=int(ex_win > 0), q_chunk_offset=int(r.integers(0, 3)) if ex_win else 0)
+    s = r.integers(-20, 20, size=(1, MG, H, NC)).astype(np.float32) * 0.125
+    s[r.random(s.shape) < 0.02] = -0.0
+    s[r.random(s.shape) < 0.01] = -np.inf
+    s[r.random(s.shape) < 0.005] = np.nan
+    got = topk_from_scores(torch.from_numpy(s).to(DEV), topk, bs, chunk, chunk, causal,
+                           ex_win=ex_win, prog_excl=bool(mk["prog_excl"]),
+                           q_chunk_offset=mk["q_chunk_offset"]).cpu().numpy()
+    om = O.Mask(**mk)
+    want = O.topk_select(s, topk, om) if topk <= 128 else O.topk_select_large(s, topk, om)
+    np.testing.assert_array_equal(got, want, err_msg=f"MG={MG} H={H} NC={NC} topk={topk} {mk}")
