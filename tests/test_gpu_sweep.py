@@ -4,8 +4,10 @@ Every case draws its shape and options from its own seed, so a failure names a r
 configuration: the selection forward (dtypes, head dims 64 / 96 / 128, group sizes up to 192,
 block sizes 16..100, ragged tails, chunk-causal masks, -1 / out-of-range / duplicate ids,
 negative scales) against the float64 oracle at the BASELINE tolerances; its backward against the
-oracle's exact gradient; and the top-k selection from given scores (ties, -0, -inf, NaN) for
-topk 1..600 against the oracle's rule (path A to 128, path B past it).
+oracle's exact gradient; the paged cache's selection (bf16 / fp8 pages, host-resident units);
+the top-k selection from given scores (ties, -0, -inf, NaN) for topk 1..600 against the oracle's
+rule (path A to 128, path B past it); and the fused pool + score + top-k call (MFMA and fmaf
+paths, causal and AR window masks).
 """
 import numpy as np
 import pytest
@@ -130,3 +132,99 @@ def test_topk_from_scores_sweep(seed):
     om = O.Mask(**mk)
     want = O.topk_select(s, topk, om) if topk <= 128 else O.topk_select_large(s, topk, om)
     np.testing.assert_array_equal(got, want, err_msg=f"MG={MG} H={H} NC={NC} topk={topk} {mk}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_paged_selection_sweep(seed):
+    """The paged cache (bf16 or fp8 pages, 16..64-token pages, ragged chunk tails, head dims 64 /
+    128, groups up to 128, some units on the host) against the float64 oracle on the values the
+    kernel computes with (fp8: codes times page scales)."""
+    from omnimem_amd.block_cache import PagedKVCache
+    r = np.random.default_rng(9500 + seed)
+    dtype = [torch.bfloat16, "fp8"][int(r.integers(0, 2))]
+    H, D = int(r.integers(1, 4)), int(r.choice([64, 128]))
+    P = int(r.choice([16, 32, 64]))
+    C = int(r.integers(P, 701))
+    n = int(r.integers(1, 5))
+    G = int(r.choice([16, 64, 128]))
+    M = int(r.integers(1, 401))
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         hbm_slots=H * n, host_slots=H * n, window_chunks=0)
+    fp8 = dtype == "fp8"
+    g = torch.Generator().manual_seed(seed)
+    ks = [(torch.randn((1, C, H, D), generator=g) * 0.3).to(torch.bfloat16) for _ in range(n)]
+    vs = [torch.randn((1, C, H, D), generator=g).to(torch.bfloat16) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    if r.integers(0, 2):
+        cache.evict_all()  # every unit read from the host pool
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    MG, npages = -(-M // G), n * cache.ppc
+    T = int(r.integers(1, min(20, npages) + 1))
+    ids = torch.randint(-1, npages, (1, MG, H, T), generator=g, dtype=torch.int32)
+    out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, return_lse=True)
+    if fp8:
+        kk = np.zeros((1, n * C, H, D), np.float32)
+        vv = np.zeros_like(kk)
+        for cid in range(n):
+            for h in range(H):
+                kc, vc, sk, sv = cache.read_unit(0, h, cid)
+                for codes, sc, dst in ((kc, sk, kk), (vc, sv, vv)):
+                    deq = O.dequantize_pages(codes.numpy(), sc.numpy()[:, None, None])
+                    dst[0, cid * C:(cid + 1) * C, h] = deq.reshape(-1, D)[:C]
+    else:
+        kk = torch.cat(ks, 1).float().numpy()
+        vv = torch.cat(vs, 1).float().numpy()
+    want_o, want_l = O.selection_attention(q.float().numpy(), kk, vv, ids.numpy(), G, D ** -0.5,
+                                           O.paged_block_tokens(C, P, n))
+    desc = f"dtype={dtype} H={H} D={D} P={P} C={C} n={n} G={G} M={M} T={T}"
+    o = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(o - want_o)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3, (
+        f"{desc}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.array_equal(np.isneginf(l), np.isneginf(want_l)), desc
+    fin = ~np.isneginf(want_l)
+    if fin.any():
+        assert np.abs(l[fin] - want_l[fin]).max() <= 1e-3, desc
+    cache.close()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_fused_topk_sweep(seed):
+    """parallel_nsa_topk on random shapes: bf16 / f16 at head dims 64 / 128 with topk <= 16 (the
+    MFMA path: indices equal the oracle's rule on the kernel's own scores, scores within the fp32
+    summation bound) and fp32 or topk up to 200 (the fmaf chain: bit-exact against the oracle's
+    scores, path A to 128, path B past it); causal chunks, the AR window exclusion, ragged tails."""
+    from _topk_checks import check_mfma_topk
+    from omnimem_amd.index_topk import parallel_nsa_topk
+    r = np.random.default_rng(9700 + seed)
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(r.integers(0, 3))]
+    D = int(r.choice([64, 128]))
+    H = int(r.integers(1, 4))
+    G = int(r.choice([16, 32, 64]))
+    T = int(r.integers(1, 3001))
+    NC = int(r.integers(1, 1201))
+    topk = int(r.choice([int(r.integers(1, 17)), int(r.integers(1, 17)), int(r.integers(17, 201))]))
+    chunk = int(G * r.integers(1, 8))
+    causal = bool(r.integers(0, 2))
+    exw = 0 if causal else int(r.integers(0, 3))
+    qoff = int(r.integers(0, 4)) if exw else 0
+    bpc = int(r.integers(1, 40)) if exw else 0
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((1, T, H, D), generator=g).to(dtype)
+    k = torch.randn((1, NC, H, D), generator=g).to(dtype)
+    kw = dict(block_size=64, chunk_size=chunk, causal=causal, exclude_window_chunks=exw,
+              progressive_exclude=exw > 0, q_chunk_offset=qoff, blocks_per_chunk=bpc)
+    mask = O.Mask(block_size=64, group_size=G, chunk_q=chunk, chunk_k=chunk, blocks_per_chunk=bpc,
+                  q_chunk_offset=qoff, ex_win=exw, causal=int(causal), prog_excl=int(exw > 0))
+    got = parallel_nsa_topk(q.to(DEV), k.to(DEV), topk, group_size=G, **kw).cpu().numpy()
+    desc = f"dtype={dtype} D={D} H={H} G={G} T={T} NC={NC} topk={topk} {kw}"
+    if dtype != torch.float32 and topk <= 16:
+        check_mfma_topk(q.to(DEV), k.to(DEV), topk, mask, D ** -0.5, G, got=got, **kw)
+        return
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dtype]
+    scores = O.block_scores(O.pool_mean(q.float().numpy(), G, dt), k.float().numpy(), D ** -0.5)
+    want = (O.topk_select(scores, topk, mask) if topk <= 128
+            else O.topk_select_large(scores, topk, mask))
+    np.testing.assert_array_equal(got, want, err_msg=desc)
