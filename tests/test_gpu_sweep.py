@@ -134,35 +134,59 @@ def test_topk_from_scores_sweep(seed):
     np.testing.assert_array_equal(got, want, err_msg=f"MG={MG} H={H} NC={NC} topk={topk} {mk}")
 
 
-@pytest.mark.parametrize("seed", range(16))
+def _e4m3_rows(q: torch.Tensor) -> np.ndarray:
+    """q [1, M, H, D] quantised to e4m3 per (query, head) row with the page rule (scale amax /
+    448, round to nearest even), as codes * scale: what the fp8 Q K^T kernel multiplies."""
+    x = q.float().numpy()
+    out = np.empty_like(x)
+    for m in range(x.shape[1]):
+        for h in range(x.shape[2]):
+            c, sc = O.quantize_pages(x[0, m, h][None, :], 1)
+            out[0, m, h] = O.dequantize_pages(c, sc)[0]
+    return out
+
+
+@pytest.mark.parametrize("seed", range(24))
 def test_paged_selection_sweep(seed):
-    """The paged cache (bf16 or fp8 pages, 16..64-token pages, ragged chunk tails, head dims 64 /
-    128, groups up to 128, some units on the host) against the float64 oracle on the values the
-    kernel computes with (fp8: codes times page scales)."""
+    """The paged cache (bf16 or fp8 pages, fp8 Q K^T, 16..64-token pages, ragged chunk tails,
+    head dims 64 / 128, groups up to 128, negative scales, some units on the host, with or
+    without the gated branch mix) against the float64 oracle on the values the kernel computes
+    with (fp8: codes times page scales; fp8 Q K^T: the queries' e4m3 image too)."""
     from omnimem_amd.block_cache import PagedKVCache
     r = np.random.default_rng(9500 + seed)
     dtype = [torch.bfloat16, "fp8"][int(r.integers(0, 2))]
     H, D = int(r.integers(1, 4)), int(r.choice([64, 128]))
+    fp8 = dtype == "fp8"
+    qk8 = fp8 and bool(r.integers(0, 2))
     P = int(r.choice([16, 32, 64]))
     C = int(r.integers(P, 701))
     n = int(r.integers(1, 5))
     G = int(r.choice([16, 64, 128]))
     M = int(r.integers(1, 401))
+    scale = float(r.choice([1.0, 1.0, -1.0])) * D ** -0.5
+    gated = bool(r.integers(0, 2))
+    host = bool(r.integers(0, 2))
     cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
-                         hbm_slots=H * n, host_slots=H * n, window_chunks=0)
-    fp8 = dtype == "fp8"
+                         qk_fp8=qk8, hbm_slots=H * n, host_slots=H * n, window_chunks=0)
     g = torch.Generator().manual_seed(seed)
     ks = [(torch.randn((1, C, H, D), generator=g) * 0.3).to(torch.bfloat16) for _ in range(n)]
     vs = [torch.randn((1, C, H, D), generator=g).to(torch.bfloat16) for _ in range(n)]
     for cid in range(n):
         cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
-    if r.integers(0, 2):
+    if host:
         cache.evict_all()  # every unit read from the host pool
     q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
     MG, npages = -(-M // G), n * cache.ppc
     T = int(r.integers(1, min(20, npages) + 1))
     ids = torch.randint(-1, npages, (1, MG, H, T), generator=g, dtype=torch.int32)
-    out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, return_lse=True)
+    kw = {}
+    if gated:
+        gates = torch.sigmoid(torch.randn((1, M, H, 3), generator=g) * 2).to(torch.bfloat16)
+        o_cmp = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16)
+        o_swa = torch.randn((1, M, H, D), generator=g).to(torch.bfloat16)
+        kw = dict(gates=gates.to(DEV), o_cmp=o_cmp.to(DEV), o_swa=o_swa.to(DEV))
+    out, lse = cache.select(q.to(DEV), ids.to(DEV), 0, G, softmax_scale=scale, return_lse=True,
+                            **kw)
     if fp8:
         kk = np.zeros((1, n * C, H, D), np.float32)
         vv = np.zeros_like(kk)
@@ -175,12 +199,20 @@ def test_paged_selection_sweep(seed):
     else:
         kk = torch.cat(ks, 1).float().numpy()
         vv = torch.cat(vs, 1).float().numpy()
-    want_o, want_l = O.selection_attention(q.float().numpy(), kk, vv, ids.numpy(), G, D ** -0.5,
+    qq = _e4m3_rows(q) if qk8 else q.float().numpy()
+    want_o, want_l = O.selection_attention(qq, kk, vv, ids.numpy(), G, scale,
                                            O.paged_block_tokens(C, P, n))
-    desc = f"dtype={dtype} H={H} D={D} P={P} C={C} n={n} G={G} M={M} T={T}"
+    mx, mean = 2e-2, 1e-3
+    if gated:  # the mix is O(1): its bf16 rounding alone is about 1e-3 mean-abs
+        gg = gates.float().numpy().astype(np.float64)
+        want_o = (gg[..., 0:1] * o_cmp.float().numpy() + gg[..., 1:2] * want_o
+                  + gg[..., 2:3] * o_swa.float().numpy())
+        mx, mean = 4e-2, 3e-3
+    desc = (f"dtype={dtype} qk8={qk8} H={H} D={D} P={P} C={C} n={n} G={G} M={M} T={T} "
+            f"scale={scale:.4f} gated={gated} host={host}")
     o = out.float().cpu().numpy().astype(np.float64)
     err = np.abs(o - want_o)
-    assert err.max() <= 2e-2 and err.mean() <= 1e-3, (
+    assert err.max() <= mx and err.mean() <= mean, (
         f"{desc}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
     l = lse.cpu().numpy().astype(np.float64)
     assert np.array_equal(np.isneginf(l), np.isneginf(want_l)), desc
