@@ -199,6 +199,35 @@ def test_sel_bwd_ptr_matches_oracle(case):
     _check(s, out, lse, dq, delta)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_sel_bwd_ptr_sweep(seed):
+    """Seeded random geometries for the pointer path, forward and backward: batch 1 or 2, head
+    dims 64 / 96 / 128, groups of 8..150 queries, 16..64-token blocks, ragged chunk counts per
+    head, 2-byte aligned bases, unresolvable chunks, ids past a head's bound, duplicates, chunk-
+    or block-level base tables."""
+    r = np.random.default_rng(4400 + seed)
+    B, H = int(r.integers(1, 3)), int(r.integers(1, 4))
+    D = int(r.choice([64, 128, 128, 96]))
+    G = int(r.choice([8, 15, 32, 64, 150]))
+    BS = int(r.choice([16, 30, 32, 64]))
+    C = BS * int(r.integers(1, 9))
+    n_chunks = tuple(int(x) for x in r.integers(1, 4, size=H))
+    M = G * int(r.integers(1, max(2, 320 // G) + 1))  # the pointer path takes whole groups
+    T = int(r.integers(1, 9))
+    shift, dk_shift = int(r.integers(0, 2)), int(r.integers(0, 2))
+    missing = tuple((h, c) for h in range(H) for c in range(n_chunks[h]) if r.random() < 0.15)
+    dup, blk = bool(r.integers(0, 2)) and T > 1, bool(r.integers(0, 2))
+    case = (seed, B, M, H, D, G, BS, C, T, n_chunks, shift, dk_shift, missing, dup, blk)
+    print(f"sel_bwd_ptr sweep case {case}", flush=True)
+    s = Setup(4400 + seed, B, M, H, D, G, BS, C, T, n_chunks, shift, dk_shift, missing, dup=dup,
+              block_level=blk)
+    bases = s.bases()
+    nb = s.nblk.to(DEV)
+    pk, pv, out, lse = _forward(s, bases[0], bases[1], nb)
+    dq, delta = _backward(s, pk, pv, out, lse, bases, nb)
+    _check(s, out, lse, dq, delta)
+
+
 def test_sel_bwd_ptr_dq_only_and_unbounded():
     """compute_dkv=False gives the same dq and writes no scratch; an empty n_blocks_per_head
     drops the per-head bound of the dK / dV index (every id below the table's width reaches its
