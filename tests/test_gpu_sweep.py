@@ -6,8 +6,9 @@ block sizes 16..100, ragged tails, chunk-causal masks, -1 / out-of-range / dupli
 negative scales) against the float64 oracle at the BASELINE tolerances; its backward against the
 oracle's exact gradient; the paged cache's selection (bf16 / fp8 pages, host-resident units);
 the top-k selection from given scores (ties, -0, -inf, NaN) for topk 1..600 against the oracle's
-rule (path A to 128, path B past it); and the fused pool + score + top-k call (MFMA and fmaf
-paths, causal and AR window masks).
+rule (path A to 128, path B past it); the fused pool + score + top-k call (MFMA and fmaf
+paths, causal and AR window masks); and the cache appends, bit-exact (pages, fp8 codes and
+scales, pooled rows, the window ring).
 """
 import numpy as np
 import pytest
@@ -260,3 +261,55 @@ def test_fused_topk_sweep(seed):
     want = (O.topk_select(scores, topk, mask) if topk <= 128
             else O.topk_select_large(scores, topk, mask))
     np.testing.assert_array_equal(got, want, err_msg=desc)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_paged_append_sweep(seed):
+    """Cache appends over random geometries (heads, head dims 64 / 96 / 128, pages of 16..100
+    tokens, chunk lengths with ragged last pages, bf16 or fp8 pages, a window ring or none),
+    bit-exact: page bytes (bf16) or e4m3 codes and per-page scales (fp8), the pooled K / V rows
+    of each page, and the ring slot's copy of the chunk."""
+    from omnimem_amd.block_cache import PagedKVCache
+    r = np.random.default_rng(9900 + seed)
+    dtype = [torch.bfloat16, "fp8"][int(r.integers(0, 2))]
+    H, D = int(r.integers(1, 5)), int(r.choice([64, 96, 128]))
+    P = int(r.choice([16, 30, 64, 64, 100]))
+    C = int(r.integers(P, 1201))
+    n = int(r.integers(1, 4))
+    ring = bool(r.integers(0, 2))
+    fp8 = dtype == "fp8"
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         hbm_slots=H * n, host_slots=H * n, window_chunks=n if ring else 0,
+                         keep_window_kv=ring)
+    g = torch.Generator().manual_seed(seed)
+    ppc = cache.ppc
+    desc = f"dtype={dtype} H={H} D={D} P={P} C={C} n={n} ring={ring}"
+    for cid in range(n):
+        k = (torch.randn((1, C, H, D), generator=g) * 2.0).to(torch.bfloat16)
+        v = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16)
+        cache.append(0, k.to(DEV), v.to(DEV), cid)
+        kc_all, vc_all = cache.cmp_history(0)
+        for x, pooled in ((k, kc_all), (v, vc_all)):
+            want = O.pool_mean(x.float().numpy(), P, "bf16")
+            got = pooled[:, cid * ppc:(cid + 1) * ppc].float().cpu().numpy()
+            np.testing.assert_array_equal(got, want, err_msg=f"pooled, {desc}")
+        for h in range(H):
+            unit = cache.read_unit(0, h, cid)
+            for j, x in enumerate((k, v)):
+                rows = np.zeros((ppc * P, D), np.float32)
+                rows[:C] = x[0, :, h].float().numpy()
+                pages = rows.reshape(ppc, P, D)
+                if not fp8:
+                    np.testing.assert_array_equal(unit[j].float().numpy(), pages,
+                                                  err_msg=f"pages h{h}, {desc}")
+                    continue
+                codes, scales = unit[j].numpy(), unit[2 + j].numpy()
+                for p in range(ppc):
+                    want_c, want_s = O.quantize_pages(pages[p], min(P, C - p * P))
+                    np.testing.assert_array_equal(codes[p], want_c, err_msg=f"h{h} p{p}, {desc}")
+                    assert np.float32(scales[p]) == want_s, (h, p, desc)
+        if ring:
+            w = cid % cache.window
+            assert torch.equal(cache.win_k[0][w].cpu(), k[0]), desc
+            assert torch.equal(cache.win_v[0][w].cpu(), v[0]), desc
+    cache.close()
