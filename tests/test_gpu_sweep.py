@@ -4,7 +4,7 @@ Every case draws its shape and options from its own seed, so a failure names a r
 configuration: the selection forward (dtypes, head dims 64 / 96 / 128, group sizes up to 192,
 block sizes 16..100, ragged tails, chunk-causal masks, -1 / out-of-range / duplicate ids,
 negative scales) against the float64 oracle at the BASELINE tolerances; its backward against the
-oracle's exact gradient; the paged cache's selection (bf16 / fp8 pages, host-resident units);
+oracle's exact gradient; the gated dense selection (branch mix in the epilogue); the paged cache's selection (bf16 / fp8 pages, host-resident units);
 the top-k selection from given scores (ties, -0, -inf, NaN) for topk 1..600 against the oracle's
 rule (path A to 128, path B past it); the fused pool + score + top-k call (MFMA and fmaf
 paths, causal and AR window masks); and the cache appends, bit-exact (pages, fp8 codes and
@@ -313,3 +313,32 @@ def test_paged_append_sweep(seed):
             assert torch.equal(cache.win_k[0][w].cpu(), k[0]), desc
             assert torch.equal(cache.win_v[0][w].cpu(), v[0]), desc
     cache.close()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sel_fwd_gated_sweep(seed):
+    """Dense selection with the NSA branch mix in its epilogue (bf16) over random shapes, against
+    g0 o_cmp + g1 o_slc + g2 o_swa from the float64 oracle's o_slc."""
+    from omnimem_amd.selection import sel_fwd_gated
+    c = _case(9300 + seed, 400, 1500, 12)
+    c["dtype"] = torch.bfloat16
+    if c["D"] not in (64, 128):  # the gated epilogue is on the MFMA paths only
+        c["D"], c["scale"] = 128, (1.0 if c["scale"] > 0 else -1.0) * 128 ** -0.5
+    q, k, v, ids = _inputs(c, seed)
+    gen = torch.Generator().manual_seed(seed + 100)
+    M, H, D = c["M"], c["H"], c["D"]
+    oc = torch.randn((1, M, H, D), generator=gen).to(torch.bfloat16)
+    ow = torch.randn((1, M, H, D), generator=gen).to(torch.bfloat16)
+    g = torch.sigmoid(torch.randn((1, M, H, 3), generator=gen) * 2).to(torch.bfloat16)
+    out = sel_fwd_gated(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), c["BS"], c["chunk"],
+                        c["scale"], c["causal"], c["G"], g.to(DEV), oc.to(DEV), ow.to(DEV))
+    slc, _ = O.selection_attention(
+        q.float().numpy(), k.float().numpy(), v.float().numpy(), ids.numpy(), c["G"], c["scale"],
+        O.dense_block_tokens(c["N"], c["BS"], c["chunk"], c["causal"]), chunk_size=c["chunk"],
+        causal=c["causal"])
+    gg = g.double().numpy()
+    want = gg[..., 0:1] * oc.double().numpy() + gg[..., 1:2] * slc + gg[..., 2:3] * ow.double().numpy()
+    err = np.abs(out.double().cpu().numpy() - want)
+    # the mix is O(1) (o_cmp, o_swa ~ N(0, 1)): its bf16 rounding alone is about 1e-3 mean-abs
+    assert err.max() <= 4e-2 and err.mean() <= 3e-3, (
+        f"{_desc(c)}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
