@@ -782,7 +782,8 @@ __global__ __launch_bounds__(kThreads) void topk_merge_kernel(const uint64_t* __
 // a stable descending segmented radix sort, so equal keys keep ascending column order; then
 // the first topk values, -1 past NC (topk.cu:563-581).  The key is the raw order code, unlike the
 // topk <= 128 rule: +0 ranks above -0, and visible -inf and NaN scores are ranked too (a NaN with
-// the sign bit clear above every number, one with it set level with the hidden columns).
+// the sign bit clear above every number, one with it set below -inf; the all-ones pattern has
+// code 0, level with the hidden columns).
 // One workgroup per row: the topk-th largest code by a 4-pass radix select (256-bin LDS
 // histograms over the row's codes), then the codes above it and the first codes equal to it in
 // column order, sorted in LDS by a bitonic network; their columns are written in that order.
