@@ -7,8 +7,8 @@ negative scales) against the float64 oracle at the BASELINE tolerances; its back
 oracle's exact gradient; the gated dense selection (branch mix in the epilogue); the paged cache's selection (bf16 / fp8 pages, host-resident units);
 the top-k selection from given scores (ties, -0, -inf, NaN) for topk 1..600 against the oracle's
 rule (path A to 128, path B past it); the fused pool + score + top-k call (MFMA and fmaf
-paths, causal and AR window masks); and the cache appends, bit-exact (pages, fp8 codes and
-scales, pooled rows, the window ring).
+paths, causal and AR window masks); the cache appends, bit-exact (pages, fp8 codes and
+scales, pooled rows, the window ring); and the window attention over pages or the ring.
 """
 import numpy as np
 import pytest
@@ -342,3 +342,54 @@ def test_sel_fwd_gated_sweep(seed):
     # the mix is O(1) (o_cmp, o_swa ~ N(0, 1)): its bf16 rounding alone is about 1e-3 mean-abs
     assert err.max() <= 4e-2 and err.mean() <= 3e-3, (
         f"{_desc(c)}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_window_attention_sweep(seed):
+    """Sliding-window attention over the paged cache (pages read in place, or the dense bf16 ring)
+    on random geometries against float64 softmax attention over every token of the last W chunks
+    (all of them while fewer than W exist)."""
+    from omnimem_amd.block_cache import PagedKVCache
+    r = np.random.default_rng(9800 + seed)
+    dtype = [torch.bfloat16, "fp8"][int(r.integers(0, 2))]
+    H, D = int(r.integers(1, 4)), int(r.choice([64, 128]))
+    P = int(r.choice([16, 32, 64]))
+    C = int(r.integers(P, 501))
+    n = int(r.integers(1, 6))
+    W = int(r.integers(1, 4))
+    ring = bool(r.integers(0, 2))
+    M = int(r.integers(1, 301))
+    fp8 = dtype == "fp8"
+    cache = PagedKVCache(1, H, D, max_chunks=n, chunk_len=C, page_tokens=P, dtype=dtype,
+                         window_chunks=W, keep_window_kv=ring)
+    g = torch.Generator().manual_seed(seed)
+    ks = [(torch.randn((1, C, H, D), generator=g) * 0.3).to(torch.bfloat16) for _ in range(n)]
+    vs = [torch.randn((1, C, H, D), generator=g).to(torch.bfloat16) for _ in range(n)]
+    for cid in range(n):
+        cache.append(0, ks[cid].to(DEV), vs[cid].to(DEV), cid)
+    q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16)
+    with torch.no_grad():
+        out = cache.window_attention(q.to(DEV), 0)
+    first = max(0, n - W)
+    if fp8 and not ring:  # pages hold codes: the kernel computes with codes times page scales
+        kk = np.zeros((1, (n - first) * C, H, D), np.float32)
+        vv = np.zeros_like(kk)
+        for i, cid in enumerate(range(first, n)):
+            for h in range(H):
+                kc, vc, sk, sv = cache.read_unit(0, h, cid)
+                for codes, sc, dst in ((kc, sk, kk), (vc, sv, vv)):
+                    deq = O.dequantize_pages(codes.numpy(), sc.numpy()[:, None, None])
+                    dst[0, i * C:(i + 1) * C, h] = deq.reshape(-1, D)[:C]
+    else:
+        kk = torch.cat(ks[first:], 1).float().numpy()
+        vv = torch.cat(vs[first:], 1).float().numpy()
+    Nw = kk.shape[1]
+    ids = np.broadcast_to(np.arange(-(-Nw // 64), dtype=np.int32), (1, -(-M // 64), H, -(-Nw // 64)))
+    want_o, _ = O.selection_attention(q.float().numpy(), kk, vv, ids, 64, D ** -0.5,
+                                      O.dense_block_tokens(Nw, 64, 1, False))
+    o = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(o - want_o)
+    desc = f"dtype={dtype} ring={ring} H={H} D={D} P={P} C={C} n={n} W={W} M={M}"
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3, (
+        f"{desc}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
+    cache.close()
