@@ -9,8 +9,11 @@ adapter).  Differences, all extensions that leave the reference's accepted input
 * ``blocks_per_chunk > 0`` selects chunk-aligned key blocks (block c lies in chunk
   c // blocks_per_chunk), the page layout of the paged KV cache.
 * ``allow_tf32`` and ``bt_chunk`` are accepted and ignored.  Scores are fp32 sums of exact
-  products: MFMA dot products for bf16 / f16 inputs with head dim 64 or 128 (the role of the
-  reference's TF32 WMMA), fmaf over d ascending otherwise.
+  products: MFMA dot products for bf16 / f16 inputs with head dim 64 or 128 and top-k <= 16 (the
+  role of the reference's TF32 WMMA), fmaf over d ascending otherwise.
+* Top-k up to 128 follows the reference's path-A ordering (cuda_backend/csrc/topk.cu:584,
+  648-660); 129 to 4096 its path-B ordering (topk.cu:741-807: raw order codes, so -0 below +0
+  and visible -inf / NaN scores ranked, hidden blocks last as -1).
 """
 from __future__ import annotations
 
