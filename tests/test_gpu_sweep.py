@@ -8,7 +8,9 @@ oracle's exact gradient; the gated dense selection (branch mix in the epilogue);
 the top-k selection from given scores (ties, -0, -inf, NaN) for topk 1..600 against the oracle's
 rule (path A to 128, path B past it); the fused pool + score + top-k call (MFMA and fmaf
 paths, causal and AR window masks); the cache appends, bit-exact (pages, fp8 codes and
-scales, pooled rows, the window ring); and the window attention over pages or the ring.
+scales, pooled rows, the window ring); the window attention over pages or the ring; and random
+sequences of appends, flushes, evictions, rewrites and snapshot / restore on a small cache, whose
+selections must equal an all-HBM cache's bit for bit.
 """
 import numpy as np
 import pytest
@@ -393,3 +395,78 @@ def test_window_attention_sweep(seed):
     assert err.max() <= 2e-2 and err.mean() <= 1e-3, (
         f"{desc}: max-abs {err.max():.3e}, mean-abs {err.mean():.3e}")
     cache.close()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_cache_residency_sequence_sweep(seed):
+    """A random sequence of cache operations on two caches fed the same data: one with every unit
+    in HBM, one whose small HBM pool forces evictions and promotions (asynchronous flushes, moves
+    pending across appends), plus evict_all, rewrites of earlier chunks and snapshot / rewrite /
+    restore of a chunk range.  After every step the two caches' selections must be bit-identical:
+    where a unit sits never changes what the kernel reads."""
+    from omnimem_amd.block_cache import PagedKVCache
+    r = np.random.default_rng(9600 + seed)
+    dtype = [torch.bfloat16, "fp8"][int(r.integers(0, 2))]
+    L, H = int(r.integers(1, 3)), int(r.integers(1, 3))
+    D = int(r.choice([64, 128]))
+    P = int(r.choice([32, 64]))
+    C = int(r.integers(P, 400))
+    n = int(r.integers(4, 8))
+    W = int(r.integers(0, 3))
+    G, M = 64, int(r.integers(1, 200))
+    fp8 = dtype == "fp8"
+    units = L * H * n
+    mk = lambda slots: PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P,
+                                    dtype=dtype, hbm_slots=slots, host_slots=2 * units,
+                                    window_chunks=W, keep_window_kv=fp8 and W > 0)
+    # the small pool holds the window's protected units plus the reserved next chunks
+    full, small = mk(2 * units), mk(L * H * int(r.integers(W + 3, max(W + 4, n))))
+    g = torch.Generator().manual_seed(seed)
+    desc = f"dtype={dtype} L={L} H={H} D={D} P={P} C={C} n={n} W={W} small={small.n_slots}"
+
+    def write(l, c):
+        k = (torch.randn((1, C, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+        v = torch.randn((1, C, H, D), generator=g).to(torch.bfloat16).to(DEV)
+        full.append(l, k, v, c)
+        small.append(l, k, v, c)
+
+    def compare(nc, step):
+        for l in range(L):
+            q = (torch.randn((1, M, H, D), generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+            ids = r.integers(-1, nc * small.ppc, size=(1, -(-M // G), H, int(r.integers(1, 12))))
+            ids = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+            a, la = full.select(q, ids, l, G, return_lse=True)
+            b, lb = small.select(q, ids, l, G, return_lse=True)
+            torch.cuda.synchronize()
+            assert torch.equal(a, b) and torch.equal(la, lb), f"{step}: {desc}"
+
+    snap = None
+    for cid in range(n):
+        for l in range(L):
+            write(l, cid)
+        compare(cid + 1, f"append {cid}")
+        full.flush()
+        small.flush()
+        compare(cid + 1, f"flush {cid}")
+        x = r.random()
+        if x < 0.25 and cid > 0:  # rewrite an earlier chunk (its units may be moving)
+            c = int(r.integers(0, cid))
+            for l in range(L):
+                write(l, c)
+            compare(cid + 1, f"rewrite {c}")
+        elif x < 0.4:
+            small.evict_all()
+            compare(cid + 1, "evict_all")
+        elif x < 0.6 and snap is None and cid >= 1:
+            lo = int(r.integers(0, cid))
+            snap = (full.snapshot_chunks(lo, cid + 1), small.snapshot_chunks(lo, cid + 1), lo, cid)
+            for l in range(L):
+                write(l, lo)
+            compare(cid + 1, f"snapshot + rewrite {lo}")
+        elif snap is not None:
+            full.restore_chunks(snap[0])
+            small.restore_chunks(snap[1])
+            compare(cid + 1, f"restore {snap[2]}..{snap[3]}")
+            snap = None
+    full.close()
+    small.close()
