@@ -41,18 +41,19 @@ def _case(seed, max_m, max_n, max_t):
     minus = float(r.choice([0.0, 0.1, 0.3]))
     dup = bool(r.integers(0, 2))
     sgn = float(r.choice([1.0, 1.0, -1.0]))
-    return dict(dtype=dtype, D=D, H=H, G=G, BS=BS, M=M, N=N, nb=nb, T=T, causal=causal,
+    B = int(r.choice([1, 1, 2]))
+    return dict(dtype=dtype, B=B, D=D, H=H, G=G, BS=BS, M=M, N=N, nb=nb, T=T, causal=causal,
                 chunk=chunk, minus=minus, dup=dup, scale=sgn * D ** -0.5)
 
 
 def _inputs(c, seed):
     gen = torch.Generator().manual_seed(seed)
-    M, N, H, D, dt = c["M"], c["N"], c["H"], c["D"], c["dtype"]
-    q = (torch.randn((1, M, H, D), generator=gen) * D ** -0.25).to(dt)
-    k = (torch.randn((1, N, H, D), generator=gen) * D ** -0.25).to(dt)
-    v = torch.randn((1, N, H, D), generator=gen).to(dt)
+    B, M, N, H, D, dt = c["B"], c["M"], c["N"], c["H"], c["D"], c["dtype"]
+    q = (torch.randn((B, M, H, D), generator=gen) * D ** -0.25).to(dt)
+    k = (torch.randn((B, N, H, D), generator=gen) * D ** -0.25).to(dt)
+    v = torch.randn((B, N, H, D), generator=gen).to(dt)
     MG = -(-M // c["G"])
-    ids = torch.randint(-1, c["nb"], (1, MG, H, c["T"]), generator=gen, dtype=torch.int32)
+    ids = torch.randint(-1, c["nb"], (B, MG, H, c["T"]), generator=gen, dtype=torch.int32)
     ids[torch.rand(ids.shape, generator=gen) < c["minus"]] = -1
     if c["dup"] and c["T"] > 1:
         ids[..., 1] = ids[..., 0]
@@ -328,10 +329,10 @@ def test_sel_fwd_gated_sweep(seed):
         c["D"], c["scale"] = 128, (1.0 if c["scale"] > 0 else -1.0) * 128 ** -0.5
     q, k, v, ids = _inputs(c, seed)
     gen = torch.Generator().manual_seed(seed + 100)
-    M, H, D = c["M"], c["H"], c["D"]
-    oc = torch.randn((1, M, H, D), generator=gen).to(torch.bfloat16)
-    ow = torch.randn((1, M, H, D), generator=gen).to(torch.bfloat16)
-    g = torch.sigmoid(torch.randn((1, M, H, 3), generator=gen) * 2).to(torch.bfloat16)
+    B, M, H, D = c["B"], c["M"], c["H"], c["D"]
+    oc = torch.randn((B, M, H, D), generator=gen).to(torch.bfloat16)
+    ow = torch.randn((B, M, H, D), generator=gen).to(torch.bfloat16)
+    g = torch.sigmoid(torch.randn((B, M, H, 3), generator=gen) * 2).to(torch.bfloat16)
     out = sel_fwd_gated(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), c["BS"], c["chunk"],
                         c["scale"], c["causal"], c["G"], g.to(DEV), oc.to(DEV), ow.to(DEV))
     slc, _ = O.selection_attention(
