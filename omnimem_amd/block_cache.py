@@ -366,9 +366,13 @@ class PagedKVCache:
                     sn["units"][u] = int(row[h])
                     row[h] = -1
         if (row < 0).any():
+            # making room may evict units of this very chunk (row is a view of the table), which
+            # then need a slot too: repeat until the free list covers every unit to place (at
+            # most H rounds; _make_room raises when it cannot free enough)
             need = int((row < 0).sum())
-            if len(self._free_hbm) < need:
+            while len(self._free_hbm) < need:
                 self._make_room(need)
+                need = int((row < 0).sum())
             changed = False
             for h in np.nonzero(row < 0)[0]:
                 if row[h] <= -2:  # host-resident unit being rewritten: bring it home

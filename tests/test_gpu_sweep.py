@@ -10,7 +10,7 @@ rule (path A to 128, path B past it); the fused pool + score + top-k call (MFMA 
 paths, causal and AR window masks); the cache appends, bit-exact (pages, fp8 codes and
 scales, pooled rows, the window ring); the window attention over pages or the ring; and random
 sequences of appends, flushes, evictions, rewrites and snapshot / restore on a small cache, whose
-selections must equal an all-HBM cache's bit for bit.
+selections (with or without staging its host pages first) must equal an all-HBM cache's bit for bit.
 """
 import numpy as np
 import pytest
@@ -437,9 +437,11 @@ def test_cache_residency_sequence_sweep(seed):
             ids = r.integers(-1, nc * small.ppc, size=(1, -(-M // G), H, int(r.integers(1, 12))))
             ids = torch.from_numpy(ids.astype(np.int32)).to(DEV)
             a, la = full.select(q, ids, l, G, return_lse=True)
-            b, lb = small.select(q, ids, l, G, return_lse=True)
+            # the small cache stages its host pages first half of the time (prefetch)
+            pf = small.prefetch(ids, l) if r.random() < 0.5 else None
+            b, lb = small.select(q, ids, l, G, return_lse=True, prefetch=pf)
             torch.cuda.synchronize()
-            assert torch.equal(a, b) and torch.equal(la, lb), f"{step}: {desc}"
+            assert torch.equal(a, b) and torch.equal(la, lb), f"{step} (prefetch {pf is not None}): {desc}"
 
     snap = None
     for cid in range(n):
