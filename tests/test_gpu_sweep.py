@@ -398,8 +398,10 @@ def test_window_attention_sweep(seed):
     cache.close()
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_cache_residency_sequence_sweep(seed):
+# (12, 3): a pool one chunk tighter, where making room for an append evicted units of the chunk
+# being written (regression case of the append fix)
+@pytest.mark.parametrize("seed,slack", [(s, 4) for s in range(48)] + [(12, 3)])
+def test_cache_residency_sequence_sweep(seed, slack):
     """A random sequence of cache operations on two caches fed the same data: one with every unit
     in HBM, one whose small HBM pool forces evictions and promotions (asynchronous flushes, moves
     pending across appends), plus evict_all, rewrites of earlier chunks and snapshot / rewrite /
@@ -420,8 +422,9 @@ def test_cache_residency_sequence_sweep(seed):
     mk = lambda slots: PagedKVCache(L, H, D, max_chunks=n, chunk_len=C, page_tokens=P,
                                     dtype=dtype, hbm_slots=slots, host_slots=2 * units,
                                     window_chunks=W, keep_window_kv=fp8 and W > 0)
-    # the small pool holds the window's protected units plus the reserved next chunks
-    full, small = mk(2 * units), mk(L * H * int(r.integers(W + 3, max(W + 4, n))))
+    # the small pool holds the window's protected units, the two reserved next chunks of an
+    # asynchronous flush and the chunk a snapshot keeps while it is rewritten
+    full, small = mk(2 * units), mk(L * H * int(r.integers(W + slack, max(W + slack + 1, n))))
     g = torch.Generator().manual_seed(seed)
     desc = f"dtype={dtype} L={L} H={H} D={D} P={P} C={C} n={n} W={W} small={small.n_slots}"
 
