@@ -404,8 +404,8 @@ def test_window_attention_sweep(seed):
 def test_cache_residency_sequence_sweep(seed, slack):
     """A random sequence of cache operations on two caches fed the same data: one with every unit
     in HBM, one whose small HBM pool forces evictions and promotions (asynchronous flushes, moves
-    pending across appends), plus evict_all, rewrites of earlier chunks and snapshot / rewrite /
-    restore of a chunk range.  After every step the two caches' selections must be bit-identical:
+    pending across appends), plus evict_all, rewrites of earlier chunks, snapshot / rewrite /
+    restore or discard of a chunk range, flushes without a reservation and a reset.  After every step the two caches' selections must be bit-identical:
     where a unit sits never changes what the kernel reads."""
     from omnimem_amd.block_cache import PagedKVCache
     r = np.random.default_rng(9600 + seed)
@@ -446,6 +446,9 @@ def test_cache_residency_sequence_sweep(seed, slack):
             torch.cuda.synchronize()
             assert torch.equal(a, b) and torch.equal(la, lb), f"{step} (prefetch {pf is not None}): {desc}"
 
+    # the pinned regression case runs its original sequence; the others also discard snapshots
+    # and flush without a reservation (drawn from a second generator)
+    extra, r2 = slack != 3, np.random.default_rng(19600 + seed)
     snap = None
     for cid in range(n):
         for l in range(L):
@@ -470,9 +473,27 @@ def test_cache_residency_sequence_sweep(seed, slack):
                 write(l, lo)
             compare(cid + 1, f"snapshot + rewrite {lo}")
         elif snap is not None:
-            full.restore_chunks(snap[0])
-            small.restore_chunks(snap[1])
-            compare(cid + 1, f"restore {snap[2]}..{snap[3]}")
+            if not extra or r2.random() < 0.7:
+                full.restore_chunks(snap[0])
+                small.restore_chunks(snap[1])
+                compare(cid + 1, f"restore {snap[2]}..{snap[3]}")
+            else:
+                full.discard_snapshot(snap[0])
+                small.discard_snapshot(snap[1])
+                compare(cid + 1, f"discard {snap[2]}..{snap[3]}")
             snap = None
+        if extra and r2.random() < 0.2:  # a flush that reserves nothing for the next chunk
+            full.flush(reserve_next_chunk=False)
+            small.flush(reserve_next_chunk=False)
+            compare(cid + 1, f"flush without reservation {cid}")
+    if snap is not None:
+        full.discard_snapshot(snap[0])
+        small.discard_snapshot(snap[1])
+    # after a reset both caches start over and must agree again
+    full.reset()
+    small.reset()
+    for l in range(L):
+        write(l, 0)
+    compare(1, "after reset")
     full.close()
     small.close()
