@@ -117,6 +117,7 @@ def test_sel_bwd_sweep(seed):
 def test_topk_from_scores_sweep(seed):
     from omnimem_amd.index_topk import topk_from_scores
     r = np.random.default_rng(9000 + seed)
+    r2 = np.random.default_rng(19000 + seed)
     MG, H, NC = int(r.integers(1, 101)), int(r.integers(1, 4)), int(r.integers(1, 3001))
     topk = int(r.choice([int(r.integers(1, 17)), int(r.integers(17, 65)),
                          int(r.integers(65, 129)), int(r.integers(129, 601))]))
@@ -124,7 +125,8 @@ def test_topk_from_scores_sweep(seed):
     chunk = int(bs * r.integers(1, 6))
     causal = bool(r.integers(0, 2))
     ex_win = int(r.integers(0, 3)) if not causal else 0
-    mk = dict(block_size=bs, group_size=1, chunk_q=chunk, chunk_k=chunk, causal=int(causal),
+    G = int(r2.choice([1, 1, 4, 16]))  # query tokens per row: the row chunk is chunk // G rows
+    mk = dict(block_size=bs, group_size=G, chunk_q=chunk * G, chunk_k=chunk, causal=int(causal),
               ex_win=ex_win, prog_excl=int(ex_win > 0), q_chunk_offset=int(r.integers(0, 3)) if ex_win else 0)
     s = r.integers(-20, 20, size=(1, MG, H, NC)).astype(np.float32) * 0.125
     s[r.random(s.shape) < 0.02] = -0.0
@@ -132,7 +134,7 @@ def test_topk_from_scores_sweep(seed):
     s[r.random(s.shape) < 0.005] = np.nan
     got = topk_from_scores(torch.from_numpy(s).to(DEV), topk, bs, chunk, chunk, causal,
                            ex_win=ex_win, prog_excl=bool(mk["prog_excl"]),
-                           q_chunk_offset=mk["q_chunk_offset"]).cpu().numpy()
+                           q_chunk_offset=mk["q_chunk_offset"], group_size=G).cpu().numpy()
     om = O.Mask(**mk)
     want = O.topk_select(s, topk, om) if topk <= 128 else O.topk_select_large(s, topk, om)
     np.testing.assert_array_equal(got, want, err_msg=f"MG={MG} H={H} NC={NC} topk={topk} {mk}")
